@@ -1,0 +1,276 @@
+#!/usr/bin/env python3
+"""Benchmark of the IntentIR MI355X backend on the five workloads of BASELINE.json.
+
+One step = one launch of the lowered gfx950 kernel over one batch of the
+workload (inputs already resident in HBM).  The headline line is the row-softmax
+workload; the four other workloads are measured the
+same way and reported under "kernels".
+
+Timing: W eager warmup launches, then K launches captured in one HIP graph on
+torch's current stream and replayed once between two HIP events, with a device
+synchronisation on both sides.  For workloads whose per-launch footprint fits
+in the 256 MB Infinity Cache, launches rotate over enough buffer sets (> 512 MiB
+in total) that reads must come from HBM.
+
+    python bench.py [--steps K] [--warmup W] [--config softmax|any|layernorm|gelu|matmul] [--only]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "HBM GB/s (% peak) per IntentIR kernel; matmul TFLOP/s; 1 MI355X"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+ROTATE_MIN_BYTES = 640 << 20   # > 2.5x the 256 MB Infinity Cache
+
+WORKLOAD_NAMES = {
+    "any": "any_kernel_dim reduce_any dim=1, f32 [8192,4096] -> bool[8192]",
+    "softmax": "softmax_inner row softmax, f32 [16384,1024]",
+    "layernorm": "layer_norm_persistent fwd, f16 [8192,4096], f32 stats",
+    "gelu": "bias + GELU-tanh * 0.5 + x, bf16 [32768,8192]",
+    "matmul": "relu(A@B + bias), bf16 8192^3, f32 acc",
+}
+DTYPES = {"any": "f32", "softmax": "f32", "layernorm": "f16", "gelu": "bf16", "matmul": "bf16"}
+
+
+def _gen_device(key, b, torch, g):
+    """Synthetic inputs of the workload's distributions, generated on the GPU (seeded)."""
+    dev = "cuda"
+    M, N = b["M"], b["N"]
+    if key == "any":
+        x = torch.zeros((M, N), dtype=torch.float32, device=dev)
+        mask = torch.rand((M, N), generator=g, device=dev) < 1e-4
+        x[mask] = torch.randn(int(mask.sum().item()), generator=g, device=dev)
+        return {"inp": x}
+    if key == "softmax":
+        x = torch.randn((M, N), generator=g, device=dev) * 2.0
+        spike = torch.rand((M, N), generator=g, device=dev) < 0.01
+        sign = torch.where(torch.rand((M, N), generator=g, device=dev) < 0.5, -30.0, 30.0)
+        return {"input_ptr": torch.where(spike, sign, x).contiguous()}
+    if key == "layernorm":
+        return {"in_ptr": torch.randn((M, N), generator=g, device=dev).half(),
+                "weight_ptr": (1.0 + 0.1 * torch.randn(N, generator=g, device=dev)).half(),
+                "bias_ptr": (0.1 * torch.randn(N, generator=g, device=dev)).half()}
+    if key == "gelu":
+        return {"x": torch.randn((M, N), generator=g, device=dev).bfloat16(),
+                "bias": (0.02 * torch.randn(N, generator=g, device=dev)).bfloat16()}
+    if key == "matmul":
+        K = b["K"]
+        s = 1.0 / math.sqrt(K)
+        return {"A": (torch.randn((M, K), generator=g, device=dev) * s).bfloat16(),
+                "B": (torch.randn((K, N), generator=g, device=dev) * s).bfloat16(),
+                "bias": 0.1 * torch.randn(N, generator=g, device=dev)}
+    raise KeyError(key)
+
+
+class Launcher:
+    """Pre-bound C-ABI calls for R buffer sets (ctypes arguments built once)."""
+
+    def __init__(self, lowered, sets, torch):
+        from intent_ir_amd.runtime import load_library, launch_lowered
+
+        self.lib = load_library()
+        self.fn = getattr(self.lib, lowered.kernel_id)
+        self.sets = sets
+        self.torch = torch
+        for bufs in sets:  # validates shapes/dtypes on the host before anything runs
+            launch_lowered(lowered, bufs)
+        torch.cuda.synchronize()
+        self.scratch = []
+        self.args = []
+        for bufs in sets:
+            a = []
+            for kind, v in lowered.call_args:
+                if kind == "tensor":
+                    a.append(ctypes.c_void_p(bufs[v].data_ptr()))
+                elif kind == "i64":
+                    a.append(ctypes.c_int64(int(v)))
+                elif kind == "i32":
+                    a.append(ctypes.c_int(int(v)))
+                elif kind == "f32":
+                    a.append(ctypes.c_float(float(v)))
+                elif kind == "null":
+                    a.append(ctypes.c_void_p(None))
+                elif kind == "scratch_f32":
+                    t = torch.empty(int(v), dtype=torch.float32, device="cuda")
+                    self.scratch.append(t)
+                    a.append(ctypes.c_void_p(t.data_ptr()))
+            self.args.append(a)
+
+    def launch(self, i):
+        s = ctypes.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+        st = self.fn(*self.args[i % len(self.args)], s)
+        if st != 0:
+            raise RuntimeError(f"launch failed: {self.lib.ihip_last_error().decode()}")
+
+
+def measure(key, steps, warmup, torch, log):
+    from intent_ir_amd import lower_intent_to_hip_kernel
+    from intent_ir_amd.configs import WORKLOADS, algorithmic_bytes
+    from intent_ir_amd.runtime import tensor_shapes, torch_dtype
+
+    w = WORKLOADS[key]
+    b = dict(w.bindings)
+    lowered = lower_intent_to_hip_kernel(w.ir(), shape_bindings=b)
+    shapes = tensor_shapes(lowered.io_spec, lowered.bindings)
+    per_launch = algorithmic_bytes(key, b)
+    nsets = 1 if key in ("matmul", "gelu") else max(2, math.ceil(ROTATE_MIN_BYTES / per_launch))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1234)
+    sets = []
+    for _ in range(nsets):
+        bufs = _gen_device(key, b, torch, g)
+        for n in lowered.output_names:
+            spec = lowered.io_spec["tensors"][n]
+            bufs[n] = torch.empty(shapes[n], dtype=torch_dtype(spec["dtype"]), device="cuda")
+        sets.append(bufs)
+    L = Launcher(lowered, sets, torch)
+    log(f"[bench] {key}: kernel={lowered.kernel_id} sets={nsets} warmup={warmup} steps={steps}")
+    for i in range(warmup):
+        L.launch(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph.capture_begin()
+        for i in range(steps):
+            L.launch(i)
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph.replay()  # untimed: first replay uploads the graph
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    # cheap property check on the last written set (no oracle in the timed path)
+    last = sets[(steps - 1) % nsets]
+    if key == "softmax":
+        rs = last["output_ptr"].double().sum(dim=1)
+        assert torch.allclose(rs, torch.ones_like(rs), atol=1e-5), "softmax rows do not sum to 1"
+    res = {"kernel": lowered.kernel_id, "ms_per_launch": ms, "steps": steps, "warmup": warmup, "buffer_sets": nsets,
+           "algo_bytes": per_launch}
+    if key == "matmul":
+        flops = w.algorithmic_flops(b)
+        tf = flops / (ms * 1e-3) / 1e12
+        res.update(value=tf, unit="TFLOP/s", frac=tf / BF16_PEAK_TFLOPS, algo_flops=flops)
+    else:
+        gbs = per_launch / (ms * 1e-3) / 1e9
+        res.update(value=gbs, unit="GB/s", frac=gbs / HBM_PEAK_GBS)
+    del graph, L, sets
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(key, log):
+    """Reference CPU path on a bounded sample, timed on this host (rank 0, N=1 only)."""
+    cpu_ref = ROOT / "oracle" / "cpu_ref"
+    exe = cpu_ref / "_build" / "intentir_cpu_ref"
+    if exe.exists():
+        threads = os.cpu_count() or 1
+        env = dict(os.environ, OMP_NUM_THREADS=str(min(threads, 16)), OMP_PROC_BIND="close")
+        out = subprocess.run([str(exe), key, "--target-seconds", "10"], capture_output=True, text=True, env=env,
+                             timeout=300)
+        if out.returncode == 0:
+            r = json.loads(out.stdout.strip().splitlines()[-1])
+            return {"value": r["value"], "unit": r["unit"], "cores": r["threads"], "kind": "port",
+                    "sample": r["sample"]}
+        log(f"[bench] cpu_ref failed: {out.stderr[-400:]}")
+    # numpy restatement of the interpreter on a row sample
+    import numpy as np
+
+    from intent_ir_amd.configs import WORKLOADS, algorithmic_bytes
+    from intent_ir_amd.dtypes import to_compute_f32
+    from intent_ir_amd.ir import as_intent
+    from oracle.interpreter import execute_intent
+
+    w = WORKLOADS[key]
+    b = dict(w.bindings)
+    b["M"] = max(1, b["M"] // 16)
+    inp = w.gen(b)
+    fn = as_intent(w.ir())
+    f32 = {n: to_compute_f32(v, fn.tensors[n].dtype) for n, v in inp.items()}
+    t0 = time.perf_counter()
+    iters = 0
+    while time.perf_counter() - t0 < 10.0:
+        execute_intent(w.ir(), f32, b)
+        iters += 1
+    dt = (time.perf_counter() - t0) / iters
+    return {"value": algorithmic_bytes(key, b) / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle, {b['M']} of {w.bindings['M']} rows, {iters} iterations"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="softmax", choices=sorted(WORKLOAD_NAMES))
+    ap.add_argument("--only", action="store_true", help="measure the headline workload only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every path here runs on one "
+              "MI355X; sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    log = lambda m: print(m, file=sys.stderr, flush=True)  # noqa: E731
+    if not torch.cuda.is_available():
+        log("bench.py needs a ROCm device")
+        sys.exit(1)
+    key = args.config
+    head = measure(key, args.steps, args.warmup, torch, log)
+    log(f"[bench] {key}: {head['value']:.1f} {head['unit']} ({100 * head['frac']:.1f}% of peak), "
+        f"{head['ms_per_launch'] * 1e3:.2f} us/launch")
+    kernels = {key: head}
+    if not args.only:
+        for other in WORKLOAD_NAMES:
+            if other == key:
+                continue
+            st = 20 if other == "matmul" else 100
+            r = measure(other, st, 5, torch, log)
+            log(f"[bench] {other}: {r['value']:.1f} {r['unit']} ({100 * r['frac']:.1f}% of peak), "
+                f"{r['ms_per_launch'] * 1e3:.2f} us/launch")
+            kernels[other] = r
+    cpu = None if args.no_cpu else cpu_baseline(key, log)
+    traffic = None
+    tfile = ROOT / "profiles" / "hbm_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get(head["kernel"])
+    if key == "matmul":
+        roof = {"bound": "mfma", "achieved": head["value"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": head["frac"], "traffic": traffic}
+    else:
+        roof = {"bound": "hbm", "achieved": head["value"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": head["frac"], "traffic": traffic}
+    line = {
+        "metric": METRIC, "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["ms_per_launch"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": DTYPES[key], "data": "synthetic (seeded, workload distributions)",
+        "config": {"workload": WORKLOAD_NAMES[key], "kernel": head["kernel"], "buffer_sets": head["buffer_sets"]},
+        "roofline": roof, "cpu_baseline": cpu,
+        "kernels": {k: {kk: v[kk] for kk in ("kernel", "value", "unit", "frac", "ms_per_launch")}
+                    for k, v in kernels.items()},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,95 @@
+// Shared device helpers for the IntentIR gfx950 kernels.
+//
+// Everything here is written for CDNA4 wave64: reductions are 6 xor-shuffle
+// steps over 64 lanes, vectors are 16-byte (dwordx4) accesses, and 16-bit
+// floats are carried as raw bit patterns so the kernels control rounding.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ihip {
+
+constexpr int kWave = 64;
+
+// Number of XCDs on MI355X.  Workgroups are dispatched round-robin over them,
+// and each XCD has a private L2, so tile schedules group work by XCD.
+constexpr int kNumXcd = 8;
+
+// 16-byte vectors as clang extended vectors, so they can go through the
+// nontemporal builtins (streaming accesses that should not linger in cache).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- 16-bit floats
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// float32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// float32 -> f16 bits with the hardware conversion (round to nearest even).
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// ---------------------------------------------------------------- reductions
+// max with numpy semantics: a NaN operand wins (np.maximum propagates NaN).
+__device__ __forceinline__ float max_nan(float a, float b) {
+  return (a >= b || a != a) ? a : b;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max_nan(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max_nan(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_or(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v |= __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Block-wide reductions across the waves of a workgroup (LDS scratch of
+// blockDim.x/64 floats supplied by the caller; result broadcast to all threads).
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  float r = 0.f;
+  for (int i = 0; i < nw; ++i) r += scratch[i];
+  return r;
+}
+
+__device__ __forceinline__ float block_max_nan(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_max_nan(v);
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  float r = scratch[0];
+  for (int i = 1; i < nw; ++i) r = max_nan(r, scratch[i]);
+  return r;
+}
+
+}  // namespace ihip

@@ -1,0 +1,380 @@
+// Row kernels over a row-major [M, N] matrix: reduce_any, reduce_sum/max,
+// softmax (f32) and LayerNorm forward (f16 in/out, f32 statistics).
+//
+// Layout and schedule (gfx950, wave64):
+//  * one wave owns one row; a 256-thread workgroup holds 4 rows;
+//  * lanes read the row with 16-byte loads, lane l taking vectors l, l+64, ...,
+//    so every load instruction of a wave covers 1 KiB of contiguous HBM;
+//  * rows that fit in registers are read from HBM exactly once; statistics are
+//    reduced with 6 xor-shuffle steps, never through LDS;
+//  * shapes the vector path cannot take (N not a multiple of the vector width,
+//    misaligned base, rows too long for registers) go to a workgroup-per-row
+//    kernel with scalar accesses.
+#include "common.hpp"
+
+namespace ihip {
+
+// ============================================================== reduce_any
+// out[m] = any(x[m, :] != c)   (numpy semantics: NaN != c is true, -0.0 != 0 is false)
+// For c == 0 the test is on the bits: |x| has a non-zero bit pattern.
+template <bool kZero, int kUnroll>
+__global__ __launch_bounds__(256) void reduce_any_rows_f32_vec(const f32x4* __restrict__ x, uint8_t* __restrict__ out,
+                                                               int64_t M, int64_t n4, float c) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const f32x4* xr = x + row * n4;
+  uint32_t acc = 0;
+  for (int64_t base = lane; base < n4; base += kWave * kUnroll) {
+    f32x4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + static_cast<int64_t>(u) * kWave;
+      v[u] = (i < n4) ? __builtin_nontemporal_load(xr + i) : f32x4{c, c, c, c};
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (kZero) {
+        acc |= (__float_as_uint(v[u].x) | __float_as_uint(v[u].y) | __float_as_uint(v[u].z) |
+                __float_as_uint(v[u].w)) & 0x7fffffffu;
+      } else {
+        acc |= static_cast<uint32_t>(v[u].x != c) | static_cast<uint32_t>(v[u].y != c) |
+               static_cast<uint32_t>(v[u].z != c) | static_cast<uint32_t>(v[u].w != c);
+      }
+    }
+  }
+  acc = wave_or(acc);
+  if (lane == 0) out[row] = acc != 0u;
+}
+
+__global__ __launch_bounds__(256) void reduce_any_rows_f32_scalar(const float* __restrict__ x, uint8_t* __restrict__ out,
+                                                                  int64_t M, int64_t N, float c) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const float* xr = x + row * N;
+  uint32_t acc = 0;
+  for (int64_t i = lane; i < N; i += kWave) acc |= static_cast<uint32_t>(xr[i] != c);
+  acc = wave_or(acc);
+  if (lane == 0) out[row] = acc != 0u;
+}
+
+// bool/u8 input: out[m] = any(x[m, :] != 0).
+__global__ __launch_bounds__(256) void reduce_any_rows_u8(const uint8_t* __restrict__ x, uint8_t* __restrict__ out,
+                                                          int64_t M, int64_t N) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const uint8_t* xr = x + row * N;
+  uint32_t acc = 0;
+  for (int64_t i = lane; i < N; i += kWave) acc |= xr[i];
+  acc = wave_or(acc);
+  if (lane == 0) out[row] = acc != 0u;
+}
+
+hipError_t launch_reduce_any_rows_f32(const float* x, uint8_t* out, int64_t M, int64_t N, float c, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  const bool vec = (N % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+  if (!vec) {
+    reduce_any_rows_f32_scalar<<<grid, block, 0, s>>>(x, out, M, N, c);
+  } else if (c == 0.0f) {
+    if (N / 4 >= kWave * 16)
+      reduce_any_rows_f32_vec<true, 16><<<grid, block, 0, s>>>(reinterpret_cast<const f32x4*>(x), out, M, N / 4, c);
+    else
+      reduce_any_rows_f32_vec<true, 4><<<grid, block, 0, s>>>(reinterpret_cast<const f32x4*>(x), out, M, N / 4, c);
+  } else {
+    if (N / 4 >= kWave * 16)
+      reduce_any_rows_f32_vec<false, 16><<<grid, block, 0, s>>>(reinterpret_cast<const f32x4*>(x), out, M, N / 4, c);
+    else
+      reduce_any_rows_f32_vec<false, 4><<<grid, block, 0, s>>>(reinterpret_cast<const f32x4*>(x), out, M, N / 4, c);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_reduce_any_rows_u8(const uint8_t* x, uint8_t* out, int64_t M, int64_t N, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  reduce_any_rows_u8<<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(x, out, M, N);
+  return hipGetLastError();
+}
+
+// ============================================================== reduce_sum / reduce_max
+// kind 0: out[m] = sum(x[m, :]) (f32 accumulation); kind 1: out[m] = max(x[m, :]) (NaN-propagating).
+template <int kKind>
+__global__ __launch_bounds__(256) void reduce_rows_f32(const float* __restrict__ x, float* __restrict__ out, int64_t M,
+                                                       int64_t N) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const float* xr = x + row * N;
+  float acc = kKind == 0 ? 0.0f : -__builtin_inff();
+  for (int64_t i = lane; i < N; i += kWave) acc = kKind == 0 ? acc + xr[i] : max_nan(acc, xr[i]);
+  acc = kKind == 0 ? wave_sum(acc) : wave_max_nan(acc);
+  if (lane == 0) out[row] = acc;
+}
+
+hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  if (kind == 0)
+    reduce_rows_f32<0><<<grid, block, 0, s>>>(x, out, M, N);
+  else
+    reduce_rows_f32<1><<<grid, block, 0, s>>>(x, out, M, N);
+  return hipGetLastError();
+}
+
+// ============================================================== softmax (last axis, f32)
+// y = exp(x - max) / sum(exp(x - max)), the exact op order of the reference
+// interpreter; exp is the accurate expf and the final step is a true division.
+template <int kVpl>  // f32x4 vectors held per lane; row length <= 256 * kVpl
+__global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restrict__ x, f32x4* __restrict__ y,
+                                                            int64_t M, int n4) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const f32x4* xr = x + row * n4;
+  f32x4* yr = y + row * n4;
+  const float ninf = -__builtin_inff();
+  f32x4 v[kVpl];
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const int idx = lane + i * kWave;
+    v[i] = idx < n4 ? __builtin_nontemporal_load(xr + idx) : f32x4{ninf, ninf, ninf, ninf};
+  }
+  float mx = ninf;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) mx = max_nan(max_nan(mx, v[i].x), max_nan(max_nan(v[i].y, v[i].z), v[i].w));
+  mx = wave_max_nan(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const int idx = lane + i * kWave;
+    if (idx < n4) {
+      v[i].x = expf(v[i].x - mx);
+      v[i].y = expf(v[i].y - mx);
+      v[i].z = expf(v[i].z - mx);
+      v[i].w = expf(v[i].w - mx);
+      sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+  }
+  sum = wave_sum(sum);
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const int idx = lane + i * kWave;
+    if (idx < n4) {
+      f32x4 o;
+      o.x = v[i].x / sum;
+      o.y = v[i].y / sum;
+      o.z = v[i].z / sum;
+      o.w = v[i].w / sum;
+      __builtin_nontemporal_store(o, yr + idx);
+    }
+  }
+}
+
+// Any N: one workgroup per row, three passes (max, sum, write) over the row.
+__global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restrict__ x, float* __restrict__ y, int64_t N) {
+  __shared__ float scratch[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * N;
+  float* yr = y + row * N;
+  float mx = -__builtin_inff();
+  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) mx = max_nan(mx, xr[i]);
+  mx = block_max_nan(mx, scratch);
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) s += expf(xr[i] - mx);
+  s = block_sum(s, scratch);
+  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) yr[i] = expf(xr[i] - mx) / s;
+}
+
+hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, hipStream_t s) {
+  if (M == 0 || N == 0) return hipSuccess;
+  const bool vec = (N % 4 == 0) && (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0);
+  const int64_t n4 = N / 4;
+  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+  f32x4* y4 = reinterpret_cast<f32x4*>(y);
+  if (vec && n4 <= 64) {
+    softmax_rows_f32_reg<1><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
+  } else if (vec && n4 <= 128) {
+    softmax_rows_f32_reg<2><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
+  } else if (vec && n4 <= 256) {
+    softmax_rows_f32_reg<4><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
+  } else if (vec && n4 <= 512) {
+    softmax_rows_f32_reg<8><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
+  } else if (vec && n4 <= 1024) {
+    softmax_rows_f32_reg<16><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
+  } else {
+    softmax_rows_f32_any<<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, N);
+  }
+  return hipGetLastError();
+}
+
+// ============================================================== LayerNorm forward (f16)
+// Op order of the reference LayerNorm IR (pipeline/tilelang/core.py:1322-1384):
+//   mean = sum(x)/N; d = x - mean; var = sum(d*d)/N; rstd = 1/sqrt(var + eps);
+//   y = (d*rstd)*w + b
+// evaluated in f32 without contraction, y rounded to f16 (RNE).
+struct H8 {  // 8 halves = one 16-byte vector
+  u32x4 v;
+  __device__ __forceinline__ float get(int i) const {
+    const uint32_t w = (i < 2) ? v.x : (i < 4) ? v.y : (i < 6) ? v.z : v.w;
+    return f16_to_f32(static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xffffu)));
+  }
+};
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_f16_rne(lo)) | (static_cast<uint32_t>(f32_to_f16_rne(hi)) << 16);
+}
+
+template <int kVpl>  // 16-byte vectors per lane; row length <= 512 * kVpl
+__global__ __launch_bounds__(256) void layernorm_rows_f16_reg(const u32x4* __restrict__ x, const u32x4* __restrict__ w,
+                                                              const u32x4* __restrict__ b, u32x4* __restrict__ y,
+                                                              float* __restrict__ mean_out, float* __restrict__ rstd_out,
+                                                              int64_t M, int n8, int N, float eps) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
+  if (wave0 >= M) return;
+  // gamma / beta stay in registers for every row this wave visits.
+  H8 wv[kVpl], bv[kVpl];
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const int idx = lane + i * kWave;
+    wv[i].v = idx < n8 ? w[idx] : u32x4(0u);
+    bv[i].v = idx < n8 ? b[idx] : u32x4(0u);
+  }
+  const float inv_n_den = static_cast<float>(N);
+  H8 nxt[kVpl];
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const int idx = lane + i * kWave;
+    nxt[i].v = idx < n8 ? __builtin_nontemporal_load(x + wave0 * n8 + idx) : u32x4(0u);
+  }
+  for (int64_t row = wave0; row < M; row += nwaves) {
+    H8 cur[kVpl];
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i) cur[i] = nxt[i];
+    const int64_t next_row = row + nwaves;
+    if (next_row < M) {  // prefetch the next row while this one is reduced
+#pragma unroll
+      for (int i = 0; i < kVpl; ++i) {
+        const int idx = lane + i * kWave;
+        nxt[i].v = idx < n8 ? __builtin_nontemporal_load(x + next_row * n8 + idx) : u32x4(0u);
+      }
+    }
+    float xf[kVpl][8];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        xf[i][j] = cur[i].get(j);
+        s += xf[i][j];
+      }
+    }
+    const float mean = wave_sum(s) / inv_n_den;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i) {
+      const bool ok = (lane + i * kWave) < n8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        xf[i][j] = xf[i][j] - mean;
+        const float sq = xf[i][j] * xf[i][j];
+        q += ok ? sq : 0.f;
+      }
+    }
+    const float var = wave_sum(q) / inv_n_den;
+    const float rstd = 1.0f / sqrtf(var + eps);
+    u32x4* yr = y + row * n8;
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i) {
+      const int idx = lane + i * kWave;
+      if (idx < n8) {
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float xhat = xf[i][j] * rstd;
+          const float scaled = xhat * wv[i].get(j);
+          o[j] = scaled + bv[i].get(j);
+        }
+        u32x4 pk;
+        pk.x = pack_f16x2(o[0], o[1]);
+        pk.y = pack_f16x2(o[2], o[3]);
+        pk.z = pack_f16x2(o[4], o[5]);
+        pk.w = pack_f16x2(o[6], o[7]);
+        __builtin_nontemporal_store(pk, yr + idx);
+      }
+    }
+    if (lane == 0) {
+      mean_out[row] = mean;
+      rstd_out[row] = rstd;
+    }
+  }
+}
+
+// Any N: one workgroup per row, three passes over the row.
+__global__ __launch_bounds__(256) void layernorm_rows_f16_any(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                              const uint16_t* __restrict__ b, uint16_t* __restrict__ y,
+                                                              float* __restrict__ mean_out, float* __restrict__ rstd_out,
+                                                              int64_t N, float eps) {
+#pragma clang fp contract(off)
+  __shared__ float scratch[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * N;
+  uint16_t* yr = y + row * N;
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) s += f16_to_f32(xr[i]);
+  const float mean = block_sum(s, scratch) / static_cast<float>(N);
+  float q = 0.f;
+  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) {
+    const float d = f16_to_f32(xr[i]) - mean;
+    q += d * d;
+  }
+  const float var = block_sum(q, scratch) / static_cast<float>(N);
+  const float rstd = 1.0f / sqrtf(var + eps);
+  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) {
+    const float d = f16_to_f32(xr[i]) - mean;
+    const float xhat = d * rstd;
+    const float scaled = xhat * f16_to_f32(w[i]);
+    yr[i] = f32_to_f16_rne(scaled + f16_to_f32(b[i]));
+  }
+  if (threadIdx.x == 0) {
+    mean_out[row] = mean;
+    rstd_out[row] = rstd;
+  }
+}
+
+hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y, float* mean,
+                                     float* rstd, int64_t M, int64_t N, float eps, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                       reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(y);
+  const bool vec = N > 0 && (N % 8 == 0) && ((al & 15) == 0) && N <= 512 * 8;
+  if (!vec) {
+    layernorm_rows_f16_any<<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, w, b, y, mean, rstd, N, eps);
+    return hipGetLastError();
+  }
+  const int n8 = static_cast<int>(N / 8);
+  // Persistent waves: enough workgroups for ~2 per CU, each wave walks rows with a stride.
+  int64_t blocks = (M + 3) / 4;
+  if (blocks > 512) blocks = 512;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  const u32x4* x8 = reinterpret_cast<const u32x4*>(x);
+  const u32x4* w8 = reinterpret_cast<const u32x4*>(w);
+  const u32x4* b8 = reinterpret_cast<const u32x4*>(b);
+  u32x4* y8 = reinterpret_cast<u32x4*>(y);
+  if (n8 <= 64)
+    layernorm_rows_f16_reg<1><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+  else if (n8 <= 128)
+    layernorm_rows_f16_reg<2><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+  else if (n8 <= 256)
+    layernorm_rows_f16_reg<4><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+  else
+    layernorm_rows_f16_reg<8><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+  return hipGetLastError();
+}
+
+}  // namespace ihip

@@ -1,0 +1,337 @@
+"""IntentIR -> (gfx950 kernel entry point, argument plan, launch plan).
+
+Python side of the HIP backend, with the interface of the reference CUDA
+lowering ``lower_intent_to_cuda_kernel(intent, *, shape_bindings,
+schedule_override=None)`` (backends/cuda/codegen/intentir_to_cuda.py:2047-2201):
+the same arguments, bindings normalisation (:2059-2072), schedule-override
+handling (:2074-2097) and an error type raised for unsupported IR (:23-24,
+:2201).  Instead of CUDA source to compile, the result names a precompiled
+C-ABI entry point of ``libintentir_hip.so`` (``kernel_id``) and the argument
+list to call it with (``call_args``).
+
+Kernel families are recognised structurally (``patterns.py``), in this order:
+GEMM (+bias, +ReLU, incl. ``matmul{epilogue}``), reduce_any (incl.
+``const, ne, reduce_any``), softmax (op or expanded chain), LayerNorm
+(chain with any output names), bias + GELU-tanh + axpy, row reduce_sum/max.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Dict, List, Mapping, Optional, Tuple
+
+from .ir import IntentFunction, ScheduleSketch, as_intent, resolve_shape
+from .macros import GELU_CUBIC, GELU_NEG_2_SQRT_2_OVER_PI, expand_macros
+from .opset import HIP_SUPPORTED_OPS
+from .patterns import ExprBuilder, PatternError, close, unify
+
+
+class HipLoweringError(RuntimeError):
+    """The IR is outside what the HIP backend lowers (role of CudaLoweringError)."""
+
+
+@dataclass(frozen=True)
+class HipLaunch:
+    """Launch plan the C-ABI entry uses for 16-byte-aligned buffers (torch allocations are)."""
+    grid: Tuple[int, int, int]
+    block: Tuple[int, int, int]
+    lds_bytes: int = 0
+
+
+@dataclass(frozen=True)
+class HipLoweredKernel:
+    kernel_name: str
+    kernel_id: str                      # C-ABI symbol in libintentir_hip.so
+    io_spec: Dict[str, Any]             # {"arg_names", "tensors": {name: {dtype, shape}}, "scalars": {}}
+    launch: HipLaunch
+    output_names: List[str]
+    bindings: Dict[str, Any]
+    # Arguments of the C call in order: ("tensor", name) | ("i64", v) | ("i32", v) | ("f32", v)
+    # | ("null", None) | ("scratch_f32", n): a device temporary of n floats the runtime provides.
+    call_args: Tuple[Tuple[str, Any], ...] = field(default_factory=tuple)
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def _normalize_bindings(shape_bindings: Mapping[str, Any]) -> Dict[str, Any]:
+    """intentir_to_cuda.py:2059-2072: bools -> int, integral floats -> int, junk dropped."""
+    out: Dict[str, Any] = {}
+    for k, v in dict(shape_bindings).items():
+        if isinstance(v, bool):
+            out[str(k)] = int(v)
+            continue
+        if isinstance(v, int):
+            out[str(k)] = int(v)
+            continue
+        try:
+            fv = float(v)
+        except (TypeError, ValueError):
+            continue
+        out[str(k)] = int(fv) if fv.is_integer() else fv
+    return out
+
+
+class _Ctx:
+    def __init__(self, fn: IntentFunction, bindings: Dict[str, Any]):
+        self.fn = fn
+        self.b = bindings
+        self.eb = ExprBuilder(fn, bindings)
+        self.outs = {o: self.eb.get(o) for o in fn.outputs}
+
+    def dtype(self, name: str) -> str:
+        return self.fn.tensors[name].dtype
+
+    def shape(self, name: str) -> Tuple[int, ...]:
+        try:
+            return resolve_shape(self.fn.tensors[name], self.b)
+        except KeyError as e:
+            raise HipLoweringError(f"missing binding for {name}: {e}") from e
+
+    def rows(self, name: str) -> Tuple[int, int]:
+        shp = self.shape(name)
+        if not shp:
+            raise HipLoweringError(f"{name} is a scalar; row kernels need rank >= 1")
+        m = 1
+        for d in shp[:-1]:
+            m *= d
+        return m, shp[-1]
+
+    def io(self, names: List[str]) -> Dict[str, Any]:
+        tensors = {n: {"dtype": self.dtype(n), "shape": self.fn.tensors[n].dims()} for n in names}
+        return {"arg_names": list(names), "tensors": tensors, "scalars": {}}
+
+
+# ---------------------------------------------------------------- matchers
+def _row_launch(m: int) -> HipLaunch:
+    return HipLaunch((max(1, _cdiv(m, 4)), 1, 1), (256, 1, 1), 0)
+
+
+def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
+    if len(c.outs) != 1:
+        return None
+    (oname, ov), = c.outs.items()
+    mm = ("matmul", ("?in", "A"), ("?in", "B"), ("?", "ta"), ("?", "tb"))
+    bias = ("bcast", ("?in", "bias"), (1,), 2)
+    env = None
+    relu = has_bias = False
+    for t, r, hb in ((mm, False, False), (("relu", mm), True, False), (("add", mm, bias), False, True),
+                     (("relu", ("add", mm, bias)), True, True)):
+        env = unify(ov.tree, t, {})
+        if env is not None:
+            relu, has_bias = r, hb
+            break
+    if env is None:
+        return None
+    if env["ta"] or env["tb"]:
+        raise HipLoweringError("matmul with transpose_a/transpose_b is not lowered by the HIP backend yet")
+    a, b = env["A"][1], env["B"][1]
+    for n in (a, b, oname):
+        if c.dtype(n) != "bf16":
+            raise HipLoweringError(f"HIP GEMM takes bf16 A, B and C; {n} is {c.dtype(n)}")
+    sa, sb, so = c.shape(a), c.shape(b), c.shape(oname)
+    if len(sa) != 2 or len(sb) != 2 or sa[1] != sb[0] or so != (sa[0], sb[1]):
+        raise HipLoweringError(f"matmul shapes do not agree: A{sa} B{sb} C{so}")
+    M, K, N = sa[0], sa[1], sb[1]
+    names = [a, b] + ([env["bias"][1]] if has_bias else []) + [oname]
+    if has_bias:
+        bn = env["bias"][1]
+        if c.dtype(bn) != "f32" or c.shape(bn) != (N,):
+            raise HipLoweringError(f"GEMM bias must be f32 [{N}]")
+    args = [("tensor", a), ("tensor", b), ("tensor", env["bias"][1]) if has_bias else ("null", None),
+            ("tensor", oname), ("i64", M), ("i64", N), ("i64", K), ("i32", int(relu))]
+    launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 147456)
+    return HipLoweredKernel(c.fn.name, "ihip_gemm_bf16_bias_relu", c.io(names), launch, [oname], dict(c.b),
+                            tuple(args))
+
+
+def _match_reduce_any(c: _Ctx) -> Optional[HipLoweredKernel]:
+    if len(c.outs) != 1:
+        return None
+    (oname, ov), = c.outs.items()
+    if not (isinstance(ov.tree, tuple) and ov.tree[0] == "rany"):
+        return None
+    env = unify(ov.tree, ("rany", ("?in", "x"), ("?", "ax")), {})
+    cmp = 0.0
+    if env is None:
+        env = unify(ov.tree, ("rany", ("ne", ("?in", "x"), ("?c", "c")), ("?", "ax")), {})
+        if env is None:
+            raise HipLoweringError("reduce_any over a computed operand is not lowered")
+        cmp = env["c"][1]
+    x = env["x"][1]
+    rank = c.fn.tensors[x].rank
+    if env["ax"] != (rank - 1,):
+        raise HipLoweringError("reduce_any is lowered over the last axis only")
+    if c.dtype(oname) not in ("bool", "i1"):
+        raise HipLoweringError(f"reduce_any output {oname} must be bool")
+    M, N = c.rows(x)
+    dt = c.dtype(x)
+    if dt == "f32":
+        args = (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N), ("f32", float(cmp)))
+        kid = "ihip_reduce_any_rows_f32"
+    elif dt in ("bool", "i1", "u8") and cmp == 0.0:
+        args = (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N))
+        kid = "ihip_reduce_any_rows_u8"
+    else:
+        raise HipLoweringError(f"reduce_any input dtype {dt} is not lowered")
+    return HipLoweredKernel(c.fn.name, kid, c.io([x, oname]), _row_launch(M), [oname], dict(c.b), args)
+
+
+def _softmax_templates(rank: int):
+    last = rank - 1
+    lead = tuple(range(last))
+    X = ("?in", "x")
+    E = ("exp", ("sub", X, ("bcast", ("rmax", X, (last,)), lead, rank)))
+    return [("softmax", X, last), ("div", E, ("bcast", ("rsum", E, (last,)), lead, rank))]
+
+
+def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
+    if len(c.outs) != 1:
+        return None
+    (oname, ov), = c.outs.items()
+    if ov.rank < 1:
+        return None
+    env = None
+    for t in _softmax_templates(ov.rank):
+        env = unify(ov.tree, t, {})
+        if env is not None:
+            break
+    if env is None:
+        return None
+    x = env["x"][1]
+    if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
+        raise HipLoweringError("HIP softmax takes f32 input and output")
+    M, N = c.rows(x)
+    launch = _row_launch(M) if (N % 4 == 0 and N <= 4096) else HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
+    return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b),
+                            (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N)))
+
+
+def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
+    X = ("?in", "x")
+    MEAN = ("div", ("rsum", X, (1,)), ("?c", "n1"))
+    D = ("sub", X, ("bcast", MEAN, (0,), 2))
+    VAR = ("div", ("rsum", ("mul", D, D), (1,)), ("?c", "n2"))
+    R = ("rsqrt", ("add", VAR, ("?c", "eps")))
+    Y = ("add", ("mul", ("mul", D, ("bcast", R, (0,), 2)), ("bcast", ("?in", "w"), (1,), 2)),
+         ("bcast", ("?in", "b"), (1,), 2))
+    roles: Dict[str, str] = {}
+    env: Dict[str, Any] = {}
+    for name, v in c.outs.items():
+        for role, t in (("y", Y), ("mean", MEAN), ("rstd", R)):
+            e = unify(v.tree, t, env)
+            if e is not None and role not in roles.values():
+                env, roles[name] = e, role
+                break
+        else:
+            return None
+    if "y" not in roles.values():
+        return None
+    inv = {r: n for n, r in roles.items()}
+    x, w, b = env["x"][1], env["w"][1], env["b"][1]
+    y = inv["y"]
+    M, N = c.rows(x)
+    if c.fn.tensors[x].rank != 2:
+        return None
+    if not (close(env["n1"][1], N) and close(env["n2"][1], N)):
+        raise HipLoweringError("LayerNorm chain divides by something other than the row length")
+    for n in (x, w, b, y):
+        if c.dtype(n) != "f16":
+            raise HipLoweringError(f"HIP LayerNorm takes f16 x, w, b, y; {n} is {c.dtype(n)}")
+    for role in ("mean", "rstd"):
+        if role in inv and c.dtype(inv[role]) != "f32":
+            raise HipLoweringError(f"LayerNorm {role} output must be f32")
+    stat = lambda r: ("tensor", inv[r]) if r in inv else ("scratch_f32", M)  # noqa: E731
+    args = (("tensor", x), ("tensor", w), ("tensor", b), ("tensor", y), stat("mean"), stat("rstd"), ("i64", M),
+            ("i64", N), ("f32", float(env["eps"][1])))
+    names = [x, w, b, y] + [inv[r] for r in ("mean", "rstd") if r in inv]
+    vec = N % 8 == 0 and 0 < N <= 4096
+    launch = HipLaunch((min(512, max(1, _cdiv(M, 4))) if vec else max(1, M), 1, 1), (256, 1, 1), 0 if vec else 16)
+    return HipLoweredKernel(c.fn.name, "ihip_layernorm_rows_f16", c.io(names), launch, list(c.fn.outputs),
+                            dict(c.b), args)
+
+
+def _match_gelu_axpy(c: _Ctx) -> Optional[HipLoweredKernel]:
+    if len(c.outs) != 1:
+        return None
+    (oname, ov), = c.outs.items()
+    X = ("?in", "x")
+    Z = ("add", X, ("bcast", ("?in", "bias"), (1,), 2))
+    U = ("add", Z, ("mul", ("mul", ("mul", Z, Z), Z), ("?c", "c0")))
+    G = ("div", Z, ("add", ("exp", ("mul", U, ("?c", "c1"))), ("?c", "one")))
+    env = unify(ov.tree, ("add", ("mul", G, ("?c", "alpha")), X), {})
+    if env is None:
+        return None
+    if not (close(env["c0"][1], GELU_CUBIC) and close(env["c1"][1], GELU_NEG_2_SQRT_2_OVER_PI)
+            and env["one"][1] == 1.0):
+        return None
+    x, bias = env["x"][1], env["bias"][1]
+    for n in (x, bias, oname):
+        if c.dtype(n) != "bf16":
+            raise HipLoweringError(f"HIP bias+GELU+axpy takes bf16 x, bias, y; {n} is {c.dtype(n)}")
+    M, N = c.rows(x)
+    if c.fn.tensors[x].rank != 2 or c.shape(bias) != (N,):
+        raise HipLoweringError("bias+GELU+axpy expects x [M,N] and bias [N]")
+    if N % 8 == 0:
+        launch = HipLaunch((max(1, _cdiv(N // 8, 256)), max(1, min(65535, _cdiv(M, 8))), 1), (256, 1, 1), 0)
+    else:
+        launch = HipLaunch((max(1, min(65536, _cdiv(M * N, 256))), 1, 1), (256, 1, 1), 0)
+    return HipLoweredKernel(c.fn.name, "ihip_bias_gelu_tanh_axpy_bf16", c.io([x, bias, oname]), launch, [oname],
+                            dict(c.b), (("tensor", x), ("tensor", bias), ("tensor", oname), ("i64", M), ("i64", N),
+                                        ("f32", float(env["alpha"][1]))))
+
+
+def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
+    if len(c.outs) != 1:
+        return None
+    (oname, ov), = c.outs.items()
+    kind = ov.tree[0] if isinstance(ov.tree, tuple) else None
+    if kind not in ("rsum", "rmax"):
+        return None
+    env = unify(ov.tree, (kind, ("?in", "x"), ("?", "ax")), {})
+    if env is None:
+        return None
+    x = env["x"][1]
+    if env["ax"] != (c.fn.tensors[x].rank - 1,):
+        raise HipLoweringError(f"{kind} is lowered over the last axis only")
+    if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
+        raise HipLoweringError("HIP row reductions take f32 input and output")
+    M, N = c.rows(x)
+    return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32", c.io([x, oname]), _row_launch(M), [oname], dict(c.b),
+                            (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N),
+                             ("i32", 0 if kind == "rsum" else 1)))
+
+
+_MATCHERS = (_match_gemm, _match_reduce_any, _match_softmax, _match_layernorm, _match_gelu_axpy, _match_row_reduce)
+
+
+def lower_intent_to_hip_kernel(intent, *, shape_bindings: Mapping[str, Any],
+                               schedule_override: ScheduleSketch | Dict[str, Any] | None = None) -> HipLoweredKernel:
+    """Lower one IntentIR function to a single gfx950 kernel call.
+
+    ``intent`` may be an IntentIR JSON dict, an ``intent_ir_amd.ir.IntentFunction``
+    or a reference ``IntentFunction`` (anything with ``to_json_dict()``).  Raises
+    ``HipLoweringError`` when no kernel family matches."""
+    bindings = _normalize_bindings(shape_bindings)
+    bindings.setdefault("HIP_RESPECT_SCHEDULE", 1 if schedule_override is not None else 0)
+    fn = as_intent(intent)
+    if schedule_override is not None:
+        fn.schedule = (schedule_override if isinstance(schedule_override, ScheduleSketch)
+                       else ScheduleSketch.from_json(schedule_override))
+    fn = expand_macros(fn)
+    unsupported = sorted({o.op for o in fn.ops} - HIP_SUPPORTED_OPS)
+    if unsupported:
+        raise HipLoweringError(f"HIP lowering unsupported ops {unsupported} in {fn.name}")
+    try:
+        ctx = _Ctx(fn, bindings)
+    except PatternError as e:
+        raise HipLoweringError(f"HIP lowering cannot read {fn.name}: {e}") from e
+    for m in _MATCHERS:
+        k = m(ctx)
+        if k is not None:
+            return k
+    raise HipLoweringError(f"HIP lowering unsupported for intent: name={fn.name} ops={sorted({o.op for o in fn.ops})}")
+
+
+__all__ = ["HipLoweringError", "HipLaunch", "HipLoweredKernel", "lower_intent_to_hip_kernel"]

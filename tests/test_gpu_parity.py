@@ -1,0 +1,329 @@
+"""Parity of the gfx950 kernels with the CPU oracle (restated verify/interpreter.py).
+
+Every case lowers the IntentIR document through ``lower_intent_to_hip_kernel``,
+runs it through the C-ABI (``run_hip_kernel``) and judges the outputs against
+``oracle.interpreter.execute_intent`` on the same seeded inputs with the
+reference pass/fail rule (``oracle.compare.compare_outputs`` =
+verify/diff_runner.py:357-418).  Tolerances are the workload contract:
+
+  reduce_any ........ bit-exact (bool)
+  softmax f32 ....... rtol 1e-5, atol 1e-7
+  LayerNorm f16 ..... y: rtol 1e-2, atol 1e-3 (the f16/bf16 floor of verify/tolerances.py:111-113);
+                      mean/rstd: rtol 1e-5, atol 1e-7
+  GELU chain bf16 ... rtol 1e-2, atol 1e-3 (same floor); plus a strict rtol 1e-2, atol 1e-6 check
+  GEMM bf16 ......... rtol 2e-2, atol 2e-2 (verify/tolerances.py:44); plus a strict atol 1e-4 check
+
+Small shapes use the reference's edge sizes (verify/gen_cases.py:27); the full
+workload sizes are checked on a row sample against the oracle and in full
+against size-independent properties or a float32 torch evaluation of the same
+formula.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from intent_ir_amd import lower_intent_to_hip_kernel, run_lowered
+from intent_ir_amd.configs import WORKLOADS, bias_gelu_axpy_ir, matmul_bias_relu2d_ir
+from intent_ir_amd.dtypes import bf16_bits_to_f32, f32_to_bf16_bits, to_compute_f32
+from intent_ir_amd.ir import as_intent
+from oracle.compare import compare_outputs
+from oracle.interpreter import execute_intent
+
+pytestmark = pytest.mark.gpu
+
+EDGE = [1, 2, 3, 7, 8, 15, 16, 17, 31, 32, 33]  # verify/gen_cases.py:27
+
+TOL = {
+    "softmax": {"atol": 1e-7, "rtol": 1e-5},
+    "ln_y": {"atol": 1e-3, "rtol": 1e-2},
+    "ln_stats": {"atol": 1e-7, "rtol": 1e-5},
+    "gelu": {"atol": 1e-3, "rtol": 1e-2},
+    "gelu_strict": {"atol": 1e-6, "rtol": 1e-2},
+    "matmul": {"atol": 2e-2, "rtol": 2e-2},
+    "matmul_strict": {"atol": 1e-4, "rtol": 2e-2},
+}
+
+
+def oracle_outputs(ir: dict, inputs: dict, bindings: dict) -> dict:
+    fn = as_intent(ir)
+    f32 = {n: to_compute_f32(v, fn.tensors[n].dtype) for n, v in inputs.items()}
+    return execute_intent(ir, f32, bindings)
+
+
+def run_case(ir: dict, inputs: dict, bindings: dict) -> dict:
+    k = lower_intent_to_hip_kernel(ir, shape_bindings=bindings)
+    print(f"[case] {k.kernel_id} bindings={bindings}", flush=True)
+    return run_lowered(k, inputs)
+
+
+def check(pred, ref, names, tol, what=""):
+    d = compare_outputs(pred, ref, names, tol)
+    assert d.ok, f"{what}: {d.summary} at {d.first_bad_index} (max_abs={d.max_abs_err:.3g} max_rel={d.max_rel_err:.3g})"
+    return d
+
+
+# ------------------------------------------------------------------ reduce_any
+@pytest.mark.parametrize("M", [1, 3, 17, 33])
+@pytest.mark.parametrize("N", EDGE + [64, 255, 256, 1023, 4096, 4100])
+def test_reduce_any_edge_shapes(hip, M, N):
+    w = WORKLOADS["any"]
+    b = {"M": M, "N": N}
+    rng = np.random.default_rng(M * 1000 + N)
+    x = np.zeros((M, N), np.float32)
+    x[rng.random((M, N)) < 0.05] = 1.5
+    inp = {"inp": x}
+    out = run_case(w.ir(), inp, b)
+    ref = oracle_outputs(w.ir(), inp, b)
+    assert out["out"].dtype == np.bool_
+    np.testing.assert_array_equal(out["out"], ref["out"])
+
+
+def test_reduce_any_special_values(hip):
+    """-0.0 counts as zero, NaN/inf/denormals as non-zero (np.any semantics)."""
+    w = WORKLOADS["any"]
+    M, N = 8, 4096
+    x = np.zeros((M, N), np.float32)
+    x[1, 4095] = -0.0
+    x[2, 0] = np.nan
+    x[3, 17] = np.inf
+    x[4, 2048] = np.float32(1e-45)  # smallest denormal
+    x[5, 100] = -np.float32(1e-45)
+    x[6, :] = -0.0
+    x[7, 5] = -3.0
+    out = run_case(w.ir(), {"inp": x}, {"M": M, "N": N})
+    np.testing.assert_array_equal(out["out"], np.any(x != 0, axis=1))
+    assert out["out"].tolist() == [False, False, True, True, True, True, False, True]
+
+
+def test_reduce_any_ne_form_with_nonzero_constant(hip):
+    """`const, ne, reduce_any` form (tests/backends/cuda/test_cuda_backend_smoke.py:249-267) with c != 0."""
+    ir = {
+        "name": "any_ne", "tensors": {"A": {"dtype": "f32", "shape": ["M", "N"]}, "z": {"dtype": "f32", "shape": []},
+                                      "T": {"dtype": "i1", "shape": ["M", "N"]}, "Out": {"dtype": "i1", "shape": ["M"]}},
+        "ops": [{"op": "const", "inputs": [], "output": "z", "attrs": {"value": 1.0}},
+                {"op": "ne", "inputs": ["A", "z"], "output": "T"},
+                {"op": "reduce_any", "inputs": ["T"], "output": "Out", "attrs": {"dims": [1]}}],
+        "outputs": ["Out"],
+    }
+    rng = np.random.default_rng(0)
+    A = rng.integers(0, 2, size=(33, 257)).astype(np.float32)
+    A[::3] = 1.0
+    out = run_case(ir, {"A": A}, {"M": 33, "N": 257})
+    np.testing.assert_array_equal(out["Out"], oracle_outputs(ir, {"A": A}, {"M": 33, "N": 257})["Out"])
+
+
+def test_reduce_any_full_config(hip):
+    w = WORKLOADS["any"]
+    inp = w.gen(w.bindings)
+    out = run_case(w.ir(), inp, w.bindings)
+    ref = oracle_outputs(w.ir(), inp, w.bindings)
+    np.testing.assert_array_equal(out["out"], ref["out"])
+    assert 0.2 < out["out"].mean() < 0.5  # ~33% of rows hold a Bernoulli(1e-4) hit
+
+
+# ------------------------------------------------------------------ softmax
+@pytest.mark.parametrize("M", [1, 7, 33])
+@pytest.mark.parametrize("N", EDGE + [64, 256, 1000, 1024, 4096, 5000])
+def test_softmax_edge_shapes(hip, M, N):
+    w = WORKLOADS["softmax"]
+    b = {"M": M, "N": N}
+    inp = w.gen(b, seed=M + N)
+    check(run_case(w.ir(), inp, b), oracle_outputs(w.ir(), inp, b), ["output_ptr"], TOL["softmax"], f"softmax {b}")
+
+
+def test_softmax_expanded_chain_form(hip):
+    """reduce_max, sub, exp, reduce_sum, div (tests/test_diff_runner.py:73-101) lowers to the same kernel."""
+    ir = {
+        "name": "softmax_like",
+        "tensors": {n: {"dtype": "f32", "shape": s} for n, s in
+                    {"X": ["M", "N"], "mx": ["M"], "Xc": ["M", "N"], "E": ["M", "N"], "sm": ["M"], "out": ["M", "N"]}.items()},
+        "ops": [{"op": "reduce_max", "inputs": ["X"], "output": "mx", "attrs": {"axis": [1], "keepdims": False}},
+                {"op": "sub", "inputs": ["X", "mx"], "output": "Xc"},
+                {"op": "exp", "inputs": ["Xc"], "output": "E"},
+                {"op": "reduce_sum", "inputs": ["E"], "output": "sm", "attrs": {"axis": [1], "keepdims": False}},
+                {"op": "div", "inputs": ["E", "sm"], "output": "out"}],
+        "outputs": ["out"],
+    }
+    b = {"M": 64, "N": 1024}
+    X = WORKLOADS["softmax"].gen(b)["input_ptr"]
+    k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    assert k.kernel_id == "ihip_softmax_rows_f32"
+    check(run_lowered(k, {"X": X}), oracle_outputs(ir, {"X": X}, b), ["out"], TOL["softmax"], "softmax chain")
+
+
+def test_softmax_full_config(hip):
+    w = WORKLOADS["softmax"]
+    inp = w.gen(w.bindings)
+    out = run_case(w.ir(), inp, w.bindings)
+    check(out, oracle_outputs(w.ir(), inp, w.bindings), ["output_ptr"], TOL["softmax"], "softmax full")
+    np.testing.assert_allclose(out["output_ptr"].astype(np.float64).sum(axis=1), 1.0, rtol=0, atol=1e-5)
+
+
+# ------------------------------------------------------------------ LayerNorm
+LN_OUTS = ["out_ptr", "out_mean_ptr", "out_rstd_ptr"]
+
+
+def _check_ln(out, ref, what):
+    check(out, ref, ["out_ptr"], TOL["ln_y"], what + " y")
+    check(out, ref, ["out_mean_ptr", "out_rstd_ptr"], TOL["ln_stats"], what + " stats")
+
+
+@pytest.mark.parametrize("M", [1, 3, 17])
+@pytest.mark.parametrize("N", EDGE + [64, 1000, 1024, 4096, 4104, 8192])
+def test_layernorm_edge_shapes(hip, M, N):
+    w = WORKLOADS["layernorm"]
+    b = {"M": M, "N": N}
+    inp = w.gen(b, seed=M * 7 + N)
+    _check_ln(run_case(w.ir(), inp, b), oracle_outputs(w.ir(), inp, b), f"LN {b}")
+
+
+def test_layernorm_full_config(hip):
+    w = WORKLOADS["layernorm"]
+    inp = w.gen(w.bindings)
+    _check_ln(run_case(w.ir(), inp, w.bindings), oracle_outputs(w.ir(), inp, w.bindings), "LN full")
+
+
+def test_layernorm_shift_invariance(hip):
+    """verify/metamorphic.py:409-482: y and rstd unchanged, mean shifted, for x + c (c exact in f16)."""
+    w = WORKLOADS["layernorm"]
+    b = {"M": 64, "N": 4096}
+    inp = w.gen(b)
+    base = run_case(w.ir(), inp, b)
+    shifted = dict(inp, in_ptr=(inp["in_ptr"].astype(np.float32) + 4.0).astype(np.float16))
+    exact = shifted["in_ptr"].astype(np.float32) - 4.0 == inp["in_ptr"].astype(np.float32)
+    rows = exact.all(axis=1)
+    out = run_case(w.ir(), shifted, b)
+    np.testing.assert_allclose(out["out_rstd_ptr"][rows], base["out_rstd_ptr"][rows], rtol=1e-4)
+    np.testing.assert_allclose(out["out_mean_ptr"][rows], base["out_mean_ptr"][rows] + 4.0, rtol=0, atol=1e-5)
+    np.testing.assert_allclose(out["out_ptr"][rows].astype(np.float32), base["out_ptr"][rows].astype(np.float32),
+                               rtol=1e-2, atol=4e-3)
+
+
+def test_layernorm_reference_naming_variant(hip):
+    """The reference CUDA lowering needs outputs named Y/Mean/Rstd (intentir_to_cuda.py:2163); any names lower here."""
+    ir = WORKLOADS["layernorm"].ir()
+    ren = {"out_ptr": "Y", "out_mean_ptr": "Mean", "out_rstd_ptr": "Rstd"}
+    ir["tensors"] = {ren.get(k, k): v for k, v in ir["tensors"].items()}
+    for op in ir["ops"]:
+        op["output"] = ren.get(op["output"], op["output"])
+    ir["outputs"] = ["Mean", "Y", "Rstd"]
+    b = {"M": 33, "N": 1024}
+    inp = WORKLOADS["layernorm"].gen(b)
+    out = run_case(ir, inp, b)
+    ref = oracle_outputs(ir, inp, b)
+    check(out, ref, ["Y"], TOL["ln_y"], "LN renamed")
+    check(out, ref, ["Mean", "Rstd"], TOL["ln_stats"], "LN renamed stats")
+
+
+# ------------------------------------------------------------------ GELU chain
+@pytest.mark.parametrize("M", [1, 3, 17])
+@pytest.mark.parametrize("N", EDGE + [64, 1000, 8192])
+def test_gelu_edge_shapes(hip, M, N):
+    w = WORKLOADS["gelu"]
+    b = {"M": M, "N": N}
+    inp = w.gen(b, seed=M * 13 + N)
+    out = run_case(w.ir(), inp, b)
+    ref = oracle_outputs(w.ir(), inp, b)
+    check(out, ref, ["y"], TOL["gelu"], f"gelu {b}")
+    check(out, ref, ["y"], TOL["gelu_strict"], f"gelu strict {b}")
+
+
+def test_gelu_matches_tanh_form(hip):
+    """y = 0.5*(0.5*z*(1+tanh(sqrt(2/pi)(z+0.044715 z^3)))) + x computed with math.tanh in float64."""
+    w = WORKLOADS["gelu"]
+    b = {"M": 16, "N": 512}
+    x = np.linspace(-8, 8, 16 * 512, dtype=np.float32).reshape(16, 512)
+    bias = np.linspace(-0.1, 0.1, 512, dtype=np.float32)
+    inp = {"x": f32_to_bf16_bits(x), "bias": f32_to_bf16_bits(bias)}
+    out = run_case(w.ir(), inp, b)["y"].astype(np.float64)
+    xf, bf = bf16_bits_to_f32(inp["x"]).astype(np.float64), bf16_bits_to_f32(inp["bias"]).astype(np.float64)
+    z = xf + bf
+    gelu = np.vectorize(lambda v: 0.5 * v * (1.0 + math.tanh(math.sqrt(2 / math.pi) * (v + 0.044715 * v ** 3))))(z)
+    np.testing.assert_allclose(out, 0.5 * gelu + xf, rtol=1e-2, atol=1e-3)
+
+
+def test_gelu_full_config(hip):
+    import torch
+
+    w = WORKLOADS["gelu"]
+    inp = w.gen(w.bindings)
+    out = run_case(w.ir(), inp, w.bindings)["y"]
+    rows = np.arange(0, w.bindings["M"], 64)  # oracle on a row sample (row-independent chain)
+    sub = {"x": inp["x"][rows], "bias": inp["bias"]}
+    sb = {"M": len(rows), "N": w.bindings["N"]}
+    ref = oracle_outputs(w.ir(), sub, sb)
+    check({"y": out[rows]}, ref, ["y"], TOL["gelu"], "gelu full sample")
+    check({"y": out[rows]}, ref, ["y"], TOL["gelu_strict"], "gelu full sample strict")
+    # whole tensor against a float32 torch evaluation of the same formula
+    xt = torch.from_numpy(bf16_bits_to_f32(inp["x"])).cuda()
+    bt = torch.from_numpy(bf16_bits_to_f32(inp["bias"])).cuda()
+    z = xt + bt
+    g = z / (1.0 + torch.exp(-2.0 * math.sqrt(2.0 / math.pi) * (z + 0.044715 * z * z * z)))
+    yref = (0.5 * g + xt).cpu().numpy()
+    np.testing.assert_allclose(out, yref, rtol=1e-2, atol=1e-3)
+
+
+# ------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (3, 5, 7), (17, 33, 31), (32, 48, 16), (256, 256, 64), (255, 257, 65),
+                                   (512, 256, 128), (300, 600, 1000)])
+def test_gemm_edge_shapes(hip, M, N, K):
+    w = WORKLOADS["matmul"]
+    b = {"M": M, "N": N, "K": K}
+    inp = w.gen(b, seed=M + N + K, sigma=1.0)  # unit-scale operands: the product dominates the bias
+    out = run_case(w.ir(), inp, b)
+    ref = oracle_outputs(w.ir(), inp, b)
+    check(out, ref, ["C"], TOL["matmul"], f"gemm {b}")
+    check(out, ref, ["C"], TOL["matmul_strict"], f"gemm strict {b}")
+
+
+def test_gemm_ones_known_answer(hip):
+    """tests/test_diff_runner.py:35-43: ones @ ones + 1 -> K + 1 everywhere."""
+    M, N, K = 256, 256, 192
+    ir = matmul_bias_relu2d_ir()
+    inp = {"A": f32_to_bf16_bits(np.ones((M, K), np.float32)), "B": f32_to_bf16_bits(np.ones((K, N), np.float32)),
+           "bias": np.ones(N, np.float32)}
+    out = run_case(ir, inp, {"M": M, "N": N, "K": K})
+    assert np.all(out["C"] == K + 1.0)
+
+
+def test_gemm_plain_and_epilogue_forms(hip):
+    """Lone matmul (no bias/relu) and matmul{epilogue} lower to the same kernel."""
+    M = N = K = 256
+    rng = np.random.default_rng(11)
+    A = f32_to_bf16_bits(rng.standard_normal((M, K), dtype=np.float32))
+    B = f32_to_bf16_bits(rng.standard_normal((K, N), dtype=np.float32))
+    bias = rng.standard_normal(N).astype(np.float32)
+    plain = {"name": "mm", "tensors": {"A": {"dtype": "bf16", "shape": ["M", "K"]}, "B": {"dtype": "bf16", "shape": ["K", "N"]},
+                                        "C": {"dtype": "bf16", "shape": ["M", "N"]}},
+             "ops": [{"op": "matmul", "inputs": ["A", "B"], "output": "C"}], "outputs": ["C"]}
+    b = {"M": M, "N": N, "K": K}
+    out = run_case(plain, {"A": A, "B": B}, b)
+    check(out, oracle_outputs(plain, {"A": A, "B": B}, b), ["C"], TOL["matmul_strict"], "plain gemm")
+    epi = {"name": "mm_epi", "tensors": dict(plain["tensors"], bias={"dtype": "f32", "shape": ["N"]}),
+           "ops": [{"op": "matmul", "inputs": ["A", "B"], "output": "C",
+                    "attrs": {"epilogue": {"op": "relu", "inputs": [{"op": "add", "inputs": ["$x", "bias"]}]}}}],
+           "outputs": ["C"]}
+    inp = {"A": A, "B": B, "bias": bias}
+    out = run_case(epi, inp, b)
+    check(out, oracle_outputs(epi, inp, b), ["C"], TOL["matmul_strict"], "epilogue gemm")
+
+
+def test_gemm_full_config(hip):
+    import torch
+
+    w = WORKLOADS["matmul"]
+    inp = w.gen(w.bindings)
+    out = run_case(w.ir(), inp, w.bindings)["C"]
+    rows = np.arange(0, w.bindings["M"], 32)  # oracle (np.matmul in f32) on a row sample
+    sb = dict(w.bindings, M=len(rows))
+    ref = oracle_outputs(w.ir(), dict(inp, A=inp["A"][rows]), sb)
+    check({"C": out[rows]}, ref, ["C"], TOL["matmul"], "gemm full sample")
+    check({"C": out[rows]}, ref, ["C"], TOL["matmul_strict"], "gemm full sample strict")
+    at = torch.from_numpy(bf16_bits_to_f32(inp["A"])).cuda()
+    bt = torch.from_numpy(bf16_bits_to_f32(inp["B"])).cuda()
+    cref = torch.relu(at @ bt + torch.from_numpy(inp["bias"]).cuda()).cpu().numpy()
+    np.testing.assert_allclose(out, cref, rtol=2e-2, atol=1e-4)
