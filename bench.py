@@ -45,36 +45,6 @@ WORKLOAD_NAMES = {
 DTYPES = {"any": "f32", "softmax": "f32", "layernorm": "f16", "gelu": "bf16", "matmul": "bf16"}
 
 
-def _gen_device(key, b, torch, g):
-    """Synthetic inputs of the workload's distributions, generated on the GPU (seeded)."""
-    dev = "cuda"
-    M, N = b["M"], b["N"]
-    if key == "any":
-        x = torch.zeros((M, N), dtype=torch.float32, device=dev)
-        mask = torch.rand((M, N), generator=g, device=dev) < 1e-4
-        x[mask] = torch.randn(int(mask.sum().item()), generator=g, device=dev)
-        return {"inp": x}
-    if key == "softmax":
-        x = torch.randn((M, N), generator=g, device=dev) * 2.0
-        spike = torch.rand((M, N), generator=g, device=dev) < 0.01
-        sign = torch.where(torch.rand((M, N), generator=g, device=dev) < 0.5, -30.0, 30.0)
-        return {"input_ptr": torch.where(spike, sign, x).contiguous()}
-    if key == "layernorm":
-        return {"in_ptr": torch.randn((M, N), generator=g, device=dev).half(),
-                "weight_ptr": (1.0 + 0.1 * torch.randn(N, generator=g, device=dev)).half(),
-                "bias_ptr": (0.1 * torch.randn(N, generator=g, device=dev)).half()}
-    if key == "gelu":
-        return {"x": torch.randn((M, N), generator=g, device=dev).bfloat16(),
-                "bias": (0.02 * torch.randn(N, generator=g, device=dev)).bfloat16()}
-    if key == "matmul":
-        K = b["K"]
-        s = 1.0 / math.sqrt(K)
-        return {"A": (torch.randn((M, K), generator=g, device=dev) * s).bfloat16(),
-                "B": (torch.randn((K, N), generator=g, device=dev) * s).bfloat16(),
-                "bias": 0.1 * torch.randn(N, generator=g, device=dev)}
-    raise KeyError(key)
-
-
 class Launcher:
     """Pre-bound C-ABI calls for R buffer sets (ctypes arguments built once)."""
 
@@ -118,7 +88,7 @@ class Launcher:
 
 def measure(key, steps, warmup, torch, log):
     from intent_ir_amd import lower_intent_to_hip_kernel
-    from intent_ir_amd.configs import WORKLOADS, algorithmic_bytes
+    from intent_ir_amd.configs import WORKLOADS, algorithmic_bytes, gen_device
     from intent_ir_amd.runtime import tensor_shapes, torch_dtype
 
     w = WORKLOADS[key]
@@ -131,7 +101,7 @@ def measure(key, steps, warmup, torch, log):
     g.manual_seed(1234)
     sets = []
     for _ in range(nsets):
-        bufs = _gen_device(key, b, torch, g)
+        bufs = gen_device(key, b, torch, g)
         for n in lowered.output_names:
             spec = lowered.io_spec["tensors"][n]
             bufs[n] = torch.empty(shapes[n], dtype=torch_dtype(spec["dtype"]), device="cuda")

@@ -187,6 +187,37 @@ def gen_matmul_bias_relu(b: Mapping[str, int], seed: int = 5, sigma: float | Non
     }
 
 
+def gen_device(key: str, b: Mapping[str, int], torch, g) -> Dict[str, "object"]:
+    """The workload's inputs with the same distributions, generated on the GPU (seeded
+    torch generator ``g``), for benchmarking without host-side generation or copies."""
+    dev = "cuda"
+    M, N = int(b["M"]), int(b["N"])
+    if key == "any":
+        x = torch.zeros((M, N), dtype=torch.float32, device=dev)
+        mask = torch.rand((M, N), generator=g, device=dev) < 1e-4
+        x[mask] = torch.randn(int(mask.sum().item()), generator=g, device=dev)
+        return {"inp": x}
+    if key == "softmax":
+        x = torch.randn((M, N), generator=g, device=dev) * 2.0
+        spike = torch.rand((M, N), generator=g, device=dev) < 0.01
+        sign = torch.where(torch.rand((M, N), generator=g, device=dev) < 0.5, -30.0, 30.0)
+        return {"input_ptr": torch.where(spike, sign, x).contiguous()}
+    if key == "layernorm":
+        return {"in_ptr": torch.randn((M, N), generator=g, device=dev).half(),
+                "weight_ptr": (1.0 + 0.1 * torch.randn(N, generator=g, device=dev)).half(),
+                "bias_ptr": (0.1 * torch.randn(N, generator=g, device=dev)).half()}
+    if key == "gelu":
+        return {"x": torch.randn((M, N), generator=g, device=dev).bfloat16(),
+                "bias": (0.02 * torch.randn(N, generator=g, device=dev)).bfloat16()}
+    if key == "matmul":
+        K = int(b["K"])
+        s = 1.0 / float(np.sqrt(K))
+        return {"A": (torch.randn((M, K), generator=g, device=dev) * s).bfloat16(),
+                "B": (torch.randn((K, N), generator=g, device=dev) * s).bfloat16(),
+                "bias": 0.1 * torch.randn(N, generator=g, device=dev)}
+    raise KeyError(key)
+
+
 @dataclass(frozen=True)
 class Workload:
     key: str

@@ -1,0 +1,273 @@
+// Full-tile bf16 GEMM for gfx950: C = act(A @ B + bias), A [M,K], B [K,N] row-major bf16,
+// f32 accumulation on v_mfma_f32_32x32x16_bf16, C bf16 (RNE).  Requires M % 256 == 0,
+// N % 256 == 0, K % DK == 0 and 16-byte aligned A, B, C; other shapes take the guarded
+// kernel in gemm.hip.
+//
+// Work decomposition
+//  * one 256x256 C tile per workgroup of 256 threads = 4 waves in a 2x2 grid; wave (wm, wn)
+//    owns rows wm*128 + [0,128) and the four 32-column blocks wn*32 + 64*ni, ni = 0..3
+//    (4x4 MFMA blocks, 256 f32 accumulators per lane, held in AGPRs);
+//  * tiles are remapped so each of the 8 XCDs (private L2) works on one contiguous range,
+//    rastered in groups of 8 tile-rows, so concurrently running tiles share A rows and
+//    B columns in L2.
+//
+// Operand staging
+//  * a ring of STAGES LDS stages, each holding a 256 x DK slice of A and a DK x 256 slice
+//    of B; the copy of K-slice kt+STAGES-1 is issued while slice kt is multiplied, so a
+//    copy has STAGES-1 slices of MFMA time to land;
+//  * copies use gfx950's direct-to-LDS loads (global_load_lds_dwordx4): lane l of a wave
+//    writes 16 bytes at LDS m0 + 16*l; no VGPR holds tile data;
+//  * because the LDS position is fixed by the lane, bank conflicts are avoided by choosing
+//    which global 16-byte chunk each lane fetches (XOR swizzles, 64-bank LDS):
+//      A row r (DK*2 bytes) stores logical k-chunk c in slot c ^ ((r / RPW) % CA), where
+//        CA = DK/8 chunks per row and RPW = 256 / (DK*2) rows per 256-byte bank window:
+//        the 16 rows one ds_read_b128 cycle serves cover all 16 bank positions;
+//      B row k (512 bytes) stores logical n-chunk c in slot c ^ 2*(k & 3) ^ 8*((c >> 1) & 1):
+//        the 4 rows x 2 column groups one 32-lane ds_read_b64_tr_b16 cycle serves land on
+//        8 distinct 32-byte windows;
+//  * B fragments come from ds_read_b64_tr_b16: lanes 4t+q of a 16-lane group address
+//    row k0+t, columns 4q..4q+3, and lane i receives column i of rows k0..k0+3, i.e. the
+//    k-contiguous operand layout, with no VALU transposition.
+//  * The MFMA is issued as D = B^T-block x A-block, so each lane's accumulators hold four
+//    consecutive n of one m: the epilogue adds bias, applies ReLU and stores 8 bytes.
+#include "common.hpp"
+
+namespace ihip {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x8_t __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+typedef __attribute__((address_space(3))) bf16x8_t lds_bf16x8_t;
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+constexpr int kTile = 256;   // M and N extent of a workgroup tile
+constexpr int kGroupRows = 8;  // tile-rows per raster group
+
+__device__ __forceinline__ float relu_keep_nan(float v) { return v < 0.0f ? 0.0f : v; }  // np.maximum(v, 0)
+
+template <int DK, int STAGES>
+struct FastGemm {
+  static constexpr int kRowA = DK * 2;             // bytes per A row in a stage
+  static constexpr int kChunksA = DK / 8;          // 16-byte chunks per A row
+  static constexpr int kRowsPerWindow = 256 / kRowA;
+  static constexpr int kStageA = kTile * kRowA;    // bytes
+  static constexpr int kStageB = DK * kTile * 2;   // bytes
+  static constexpr int kStage = kStageA + kStageB;
+  static constexpr int kInstrA = kStageA / 1024 / 4;  // direct-to-LDS instructions per wave per stage
+  static constexpr int kInstrB = kStageB / 1024 / 4;
+  static constexpr int kInstr = kInstrA + kInstrB;
+  static constexpr int kRowsPerInstrA = 1024 / kRowA;
+  static_assert(kStage * STAGES <= 160 * 1024, "stages exceed the 160 KiB LDS");
+  static_assert(kInstr * (STAGES - 2) <= 63, "vmcnt field");
+
+  static __device__ __forceinline__ int a_slot(int c, int r) { return c ^ ((r / kRowsPerWindow) % kChunksA); }
+  static __device__ __forceinline__ int b_slot(int c, int k) { return c ^ ((k & 3) << 1) ^ (((c >> 1) & 1) << 3); }
+  static __device__ __forceinline__ int b_logical(int p, int k) {
+    const int x = p ^ ((k & 3) << 1);
+    return x ^ (((x >> 1) & 1) << 3);
+  }
+
+  // Per-lane byte offsets of the copies, identical for every instruction and K slice.
+  struct Lane {
+    uint32_t a, b;
+    int ra[DK / 16];  // A fragment LDS offsets, per kk
+    int rb[4];        // B fragment LDS offsets, per ni
+  };
+
+  static __device__ __forceinline__ Lane lane_plan(int64_t N, int64_t K, int wave, int wm, int wn, int lane) {
+    Lane L;
+    // A: instruction j = 4i + wave holds rows j*RPI + lane / CA, slot lane % CA; the swizzle
+    // term (r / RPW) % CA does not depend on i.
+    const int ra0 = wave * kRowsPerInstrA + lane / kChunksA;
+    L.a = 2u * static_cast<uint32_t>((lane / kChunksA) * K + a_slot(lane % kChunksA, ra0) * 8);
+    // B: instruction j holds k-rows 2j, 2j+1; k & 3 == (2*wave + lane/32) & 3 for every i.
+    const int kb = 2 * wave + (lane >> 5);
+    L.b = 2u * static_cast<uint32_t>((lane >> 5) * N + b_logical(lane & 31, kb) * 8);
+    const int r = wm * 128 + (lane & 31);
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk) L.ra[kk] = r * kRowA + a_slot(2 * kk + (lane >> 5), r) * 16;
+    const int g = lane >> 4, i = lane & 15;
+    const int k = (g >> 1) * 8 + (i >> 2);
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      const int n = wn * 32 + ni * 64 + (g & 1) * 16 + 4 * (i & 3);
+      L.rb[ni] = kStageA + k * 512 + b_slot(n >> 3, k) * 16 + (n & 7) * 2;
+    }
+    return L;
+  }
+
+  static __device__ __forceinline__ void dma16(const uint16_t* sbase, uint32_t voff, uint32_t lds_addr) {
+    // Inline asm, so the compiler does not treat the copy as an LDS store that every later
+    // LDS read must wait for; the kernel waits for the copies itself before reading a stage.
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
+  }
+
+  static __device__ __forceinline__ void copy_slice(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                                    int64_t N, int64_t K, int64_t m0, int64_t n0, int64_t k0,
+                                                    uint32_t stage, int wave, const Lane& L) {
+#pragma unroll
+    for (int i = 0; i < kInstrA; ++i) {
+      const int j = 4 * i + wave;
+      dma16(A + (m0 + j * kRowsPerInstrA) * K + k0, L.a, stage + j * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < kInstrB; ++i) {
+      const int j = 4 * i + wave;
+      dma16(B + (k0 + 2 * j) * N + n0, L.b, stage + kStageA + j * 1024);
+    }
+  }
+
+  // Wait until at most `pending` slices of this wave's copies are still in flight
+  // (copies complete in issue order, kInstr instructions per slice).
+  static __device__ __forceinline__ void wait_copies(int pending) {
+    static_assert(STAGES <= 5, "wait_copies covers up to 4 pending slices");
+    if (pending >= 4) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kInstr < 63 ? 4 * kInstr : 63) : "memory");
+    } else if (pending == 3) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * kInstr < 63 ? 3 * kInstr : 63) : "memory");
+    } else if (pending == 2) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kInstr) : "memory");
+    } else if (pending == 1) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kInstr) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+  }
+
+  struct Frag {
+    bf16x8_t a[4], b[4];
+  };
+
+  static __device__ __forceinline__ void read(const lds_char_t* st, int kk, const Lane& L, Frag& f) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) f.a[mi] = *(const lds_bf16x8_t*)(st + L.ra[kk] + mi * 32 * kRowA);
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + L.rb[ni] + kk * 16 * 512));
+      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + L.rb[ni] + (kk * 16 + 4) * 512));
+      const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      f.b[ni] = __builtin_bit_cast(bf16x8_t, both);
+    }
+  }
+
+  static __device__ __forceinline__ void mfma(const Frag& f, f32x16_t (&acc)[4][4]) {
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+        acc[ni][mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[ni], f.a[mi], acc[ni][mi], 0, 0, 0);
+  }
+
+};
+
+template <int DK, int STAGES>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const float* __restrict__ bias,
+                           uint16_t* __restrict__ C, int64_t N, int64_t K, int relu, int tiles_m, int tiles_n) {
+  using G = FastGemm<DK, STAGES>;
+  __shared__ __attribute__((aligned(1024))) char lds_raw[STAGES * G::kStage];
+  const lds_char_t* lds = (const lds_char_t*)lds_raw;
+  const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+
+  int bid = blockIdx.x;
+  const int T = gridDim.x;
+  if (T % kNumXcd == 0) bid = (bid % kNumXcd) * (T / kNumXcd) + bid / kNumXcd;
+  const int per_group = kGroupRows * tiles_n;
+  const int grp = bid / per_group, first_m = grp * kGroupRows;
+  const int gsz = (tiles_m - first_m) < kGroupRows ? (tiles_m - first_m) : kGroupRows;
+  const int tm = first_m + (bid % per_group) % gsz, tn = (bid % per_group) / gsz;
+  const int64_t m0 = static_cast<int64_t>(tm) * kTile, n0 = static_cast<int64_t>(tn) * kTile;
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+
+  const typename G::Lane L = G::lane_plan(N, K, wave, wm, wn, lane);
+  const int KT = static_cast<int>(K / DK);
+  // Prologue: slices 0 .. STAGES-2 in flight, then slice 0 must land.
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < KT) G::copy_slice(A, B, N, K, m0, n0, static_cast<int64_t>(s) * DK, lds_addr + s * G::kStage, wave, L);
+  G::wait_copies((KT < STAGES - 1 ? KT : STAGES - 1) - 1);
+  __syncthreads();
+
+  for (int kt = 0; kt < KT; ++kt) {
+    // Slice kt+STAGES-1 goes to the stage read in iteration kt-1, which that iteration's
+    // barrier has released.
+    const int nt = kt + STAGES - 1;
+    if (nt < KT)
+      G::copy_slice(A, B, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage, wave, L);
+    const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk) {
+      typename G::Frag f;
+      G::read(st, kk, L, f);
+      G::mfma(f, acc);
+    }
+    // slice kt+1 must have landed before the barrier; later slices may stay in flight
+    const int last = nt < KT ? nt : KT - 1;
+    G::wait_copies(last > kt + 1 ? last - (kt + 1) : 0);
+    __syncthreads();
+  }
+
+  // Epilogue, one 32x32 block at a time (the empty asm keeps the compiler from pulling all
+  // 256 accumulators into VGPRs at once).
+  const bool has_bias = bias != nullptr;
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) {
+    float bv[4][4];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int64_t n = n0 + wn * 32 + ni * 64 + g4 * 8 + (lane >> 5) * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bv[g4][q] = has_bias ? bias[n + q] : 0.0f;
+    }
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      const int64_t m = m0 + wm * 128 + mi * 32 + (lane & 31);
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int64_t n = n0 + wn * 32 + ni * 64 + g4 * 8 + (lane >> 5) * 4;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float t = acc[ni][mi][g4 * 4 + q];
+          if (has_bias) t = t + bv[g4][q];
+          v[q] = relu ? relu_keep_nan(t) : t;
+        }
+        uint2 pk;
+        pk.x = f32_to_bf16_rne(v[0]) | (uint32_t(f32_to_bf16_rne(v[1])) << 16);
+        pk.y = f32_to_bf16_rne(v[2]) | (uint32_t(f32_to_bf16_rne(v[3])) << 16);
+        *reinterpret_cast<uint2*>(C + m * N + n) = pk;
+      }
+      asm volatile("" ::: "memory");
+    }
+  }
+}
+
+// K step and ring depth of the fast path.
+constexpr int kFastDK = 32;
+constexpr int kFastStages = 4;
+
+bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* C) {
+  const uintptr_t al = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
+  return M % kTile == 0 && N % kTile == 0 && K % kFastDK == 0 && (al & 15) == 0 && K * 16 < (int64_t(1) << 31) &&
+         N * 16 < (int64_t(1) << 31);
+}
+
+hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
+                            int64_t K, int relu, hipStream_t s) {
+  const int64_t tm = M / kTile, tn = N / kTile;
+  gemm_bf16_fast_kernel<kFastDK, kFastStages><<<dim3(static_cast<unsigned>(tm * tn)), dim3(256), 0, s>>>(
+      A, B, bias, C, N, K, relu, static_cast<int>(tm), static_cast<int>(tn));
+  return hipGetLastError();
+}
+
+}  // namespace ihip
