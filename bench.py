@@ -148,42 +148,58 @@ def measure(key, steps, warmup, torch, log):
     return res
 
 
-def cpu_baseline(key, log):
-    """Reference CPU path on a bounded sample, timed on this host (rank 0, N=1 only)."""
-    cpu_ref = ROOT / "oracle" / "cpu_ref"
-    exe = cpu_ref / "_build" / "intentir_cpu_ref"
-    if exe.exists():
-        threads = os.cpu_count() or 1
-        env = dict(os.environ, OMP_NUM_THREADS=str(min(threads, 16)), OMP_PROC_BIND="close")
-        out = subprocess.run([str(exe), key, "--target-seconds", "10"], capture_output=True, text=True, env=env,
-                             timeout=300)
-        if out.returncode == 0:
-            r = json.loads(out.stdout.strip().splitlines()[-1])
-            return {"value": r["value"], "unit": r["unit"], "cores": r["threads"], "kind": "port",
-                    "sample": r["sample"]}
-        log(f"[bench] cpu_ref failed: {out.stderr[-400:]}")
-    # numpy restatement of the interpreter on a row sample
+def cpu_baseline(key, log, target_s=10.0):
+    """Reference CPU path on a bounded sample of the workload, timed on this host's cores.
+
+    Preferred: the reference's own C path (oracle/_ref/<cfg>_sample, built from the reference
+    sources by oracle/build_ref.py), run on the sample's real inputs with OpenMP on up to 16
+    host threads; it also checks its result against the oracle.  Fallback when that build is
+    absent: the numpy oracle on the same sample, single-threaded."""
     import numpy as np
 
     from intent_ir_amd.configs import WORKLOADS, algorithmic_bytes
     from intent_ir_amd.dtypes import to_compute_f32
     from intent_ir_amd.ir import as_intent
+    from intent_ir_amd.macros import expand_macros
+    from oracle import ref_runner
     from oracle.interpreter import execute_intent
 
     w = WORKLOADS[key]
-    b = dict(w.bindings)
-    b["M"] = max(1, b["M"] // 16)
-    inp = w.gen(b)
-    fn = as_intent(w.ir())
-    f32 = {n: to_compute_f32(v, fn.tensors[n].dtype) for n, v in inp.items()}
+    if ref_runner.available(key, "sample"):
+        b = ref_runner.bindings(key, "sample")
+    else:
+        b = dict(w.bindings)
+        b["M"] = max(1, b["M"] // 16)
+    fn = expand_macros(as_intent(w.ir()))
+    raw = w.gen(b)
+    f32 = {n: to_compute_f32(v, fn.tensors[n].dtype) for n, v in raw.items()}
+    work = w.algorithmic_flops(b) if key == "matmul" else algorithmic_bytes(key, b)
+    unit = "TFLOP/s" if key == "matmul" else "GB/s"
+    scale = 1e12 if key == "matmul" else 1e9
+    sample = f"{b} slice of the {w.bindings} workload"
+    if ref_runner.available(key, "sample"):
+        ref = execute_intent(w.ir(), f32, b)
+        probe = ref_runner.run(key, "sample", fn, f32, ref, iters=1)
+        if probe.ns_per_iter:
+            iters = max(1, min(1000, int(target_s * 1e9 / probe.ns_per_iter)))
+            r = ref_runner.run(key, "sample", fn, f32, ref, iters=iters)
+            if r.ns_per_iter:
+                log(f"[bench] cpu reference path: {r.ns_per_iter / 1e6:.2f} ms/iter x {iters}, "
+                    f"{r.threads} threads, result {'PASS' if r.passed else 'FAIL'}")
+                return {"value": work / (r.ns_per_iter * 1e-9) / scale, "unit": unit, "cores": r.threads,
+                        "kind": "reference",
+                        "sample": f"reference spmd_rvv C path (codegen + runtime built from the reference sources, "
+                                  f"-O3 -fopenmp), {sample}, {iters} timed iterations after 1 warmup, "
+                                  f"result vs oracle {'PASS' if r.passed else 'FAIL'}"}
+        log(f"[bench] reference CPU path did not report timing: {probe.stdout[-300:]}")
     t0 = time.perf_counter()
     iters = 0
-    while time.perf_counter() - t0 < 10.0:
+    while time.perf_counter() - t0 < target_s:
         execute_intent(w.ir(), f32, b)
         iters += 1
     dt = (time.perf_counter() - t0) / iters
-    return {"value": algorithmic_bytes(key, b) / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle, {b['M']} of {w.bindings['M']} rows, {iters} iterations"}
+    return {"value": work / dt / scale, "unit": unit, "cores": 1, "kind": "port",
+            "sample": f"numpy oracle (restated interpreter), {sample}, {iters} iterations"}
 
 
 def main():
