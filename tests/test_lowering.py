@@ -1,0 +1,211 @@
+"""IR loading, macro expansion and structural lowering — CPU only (no kernel launches)."""
+
+from __future__ import annotations
+
+import copy
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from intent_ir_amd import HipLoweringError, lower_intent_to_hip_kernel
+from intent_ir_amd.configs import WORKLOADS, matmul_bias_relu2d_ir, softmax_inner_ir
+from intent_ir_amd.ir import IntentFunction, IntentIRValidationError, as_intent
+from intent_ir_amd.macros import expand_macros
+from intent_ir_amd.runtime import LIB_PATH, SIGNATURES
+
+ROOT = Path(__file__).resolve().parents[1]
+
+EXPECTED_KERNEL = {
+    "any": "ihip_reduce_any_rows_f32",
+    "softmax": "ihip_softmax_rows_f32",
+    "layernorm": "ihip_layernorm_rows_f16",
+    "gelu": "ihip_bias_gelu_tanh_axpy_bf16",
+    "matmul": "ihip_gemm_bf16_bias_relu",
+}
+
+
+@pytest.mark.parametrize("key", sorted(WORKLOADS))
+def test_workloads_lower_to_their_kernel(key):
+    w = WORKLOADS[key]
+    k = lower_intent_to_hip_kernel(w.ir(), shape_bindings=w.bindings)
+    assert k.kernel_id == EXPECTED_KERNEL[key]
+    assert k.kernel_id in SIGNATURES
+    # every tensor argument is declared in io_spec, and the arg count matches the C signature (+ stream)
+    for kind, v in k.call_args:
+        if kind == "tensor":
+            assert v in k.io_spec["tensors"]
+    assert len(k.call_args) + 1 == len(SIGNATURES[k.kernel_id][1])
+
+
+def test_json_round_trip_and_reference_object_duck_typing():
+    ir = WORKLOADS["layernorm"].ir()
+    fn = IntentFunction.from_json_dict(ir)
+    again = IntentFunction.from_json_dict(fn.to_json_dict())
+    assert again.to_json_dict() == fn.to_json_dict()
+
+    class RefLike:  # anything with to_json_dict(), like the reference IntentFunction
+        def to_json_dict(self):
+            return ir
+
+    assert as_intent(RefLike()).to_json_dict() == fn.to_json_dict()
+    k = lower_intent_to_hip_kernel(RefLike(), shape_bindings={"M": 8, "N": 64})
+    assert k.kernel_id == "ihip_layernorm_rows_f16"
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda ir: ir["ops"][0].__setitem__("inputs", ["nope"]), "undefined tensor"),
+    (lambda ir: ir["ops"][0]["attrs"].__setitem__("dims", "1"), "dims must be list"),
+    (lambda ir: ir.__setitem__("outputs", ["ghost"]), "not found"),
+    (lambda ir: ir["tensors"]["inp"].__setitem__("dtype", "f8"), "dtype unsupported"),
+    (lambda ir: ir["ops"][0].__setitem__("op", "frobnicate"), "unsupported"),
+])
+def test_validation_errors(mutate, msg):
+    ir = copy.deepcopy(WORKLOADS["any"].ir())
+    mutate(ir)
+    with pytest.raises(IntentIRValidationError, match=msg):
+        as_intent(ir)
+
+
+def test_outputs_default_to_last_op():
+    ir = softmax_inner_ir()
+    del ir["outputs"]
+    assert as_intent(ir).outputs == ["output_ptr"]
+
+
+def test_gelu_macro_expands_to_interpreter_ops():
+    fn = expand_macros(as_intent(WORKLOADS["gelu"].ir()))
+    ops = {o.op for o in fn.ops}
+    assert "gelu_tanh" not in ops
+    assert ops <= {"broadcast_in_dim", "add", "mul", "const", "exp", "div"}
+    assert all(o.attrs.get("dtype") == "f32" for o in fn.ops if o.op == "const")
+
+
+def test_bindings_normalisation_and_knobs():
+    w = WORKLOADS["softmax"]
+    k = lower_intent_to_hip_kernel(w.ir(), shape_bindings={"M": 16.0, "N": "1024", "junk": object(), "flag": True})
+    assert k.bindings["M"] == 16 and k.bindings["N"] == 1024 and k.bindings["flag"] == 1 and "junk" not in k.bindings
+    assert k.bindings["HIP_RESPECT_SCHEDULE"] == 0
+    k2 = lower_intent_to_hip_kernel(w.ir(), shape_bindings={"M": 16, "N": 1024}, schedule_override={"tile_m": 4})
+    assert k2.bindings["HIP_RESPECT_SCHEDULE"] == 1
+
+
+def test_softmax_expanded_chain_with_keepdims_forms():
+    base = {"X": {"dtype": "f32", "shape": ["M", "N"]}, "Xc": {"dtype": "f32", "shape": ["M", "N"]},
+            "E": {"dtype": "f32", "shape": ["M", "N"]}, "out": {"dtype": "f32", "shape": ["M", "N"]}}
+    for keep, rshape in ((False, ["M"]), (True, ["M", 1])):
+        ir = {"name": "sm", "tensors": dict(base, mx={"dtype": "f32", "shape": rshape}, sm={"dtype": "f32", "shape": rshape}),
+              "ops": [{"op": "reduce_max", "inputs": ["X"], "output": "mx", "attrs": {"dims": [1], "keepdims": keep}},
+                      {"op": "sub", "inputs": ["X", "mx"], "output": "Xc"},
+                      {"op": "exp", "inputs": ["Xc"], "output": "E"},
+                      {"op": "reduce_sum", "inputs": ["E"], "output": "sm", "attrs": {"dims": [1], "keepdims": keep}},
+                      {"op": "div", "inputs": ["E", "sm"], "output": "out"}], "outputs": ["out"]}
+        assert lower_intent_to_hip_kernel(ir, shape_bindings={"M": 4, "N": 8}).kernel_id == "ihip_softmax_rows_f32"
+
+
+def test_softmax_over_wrong_axis_is_not_softmax():
+    ir = softmax_inner_ir()
+    ir["ops"][0]["attrs"]["axis"] = 0
+    with pytest.raises(HipLoweringError):
+        lower_intent_to_hip_kernel(ir, shape_bindings={"M": 4, "N": 8})
+
+
+def test_trailing_alignment_is_not_mistaken_for_row_broadcast():
+    """reduce_max keepdims=False declared [N] (not [M]) broadcasts along the trailing axis: not softmax."""
+    ir = {"name": "notsm", "tensors": {"X": {"dtype": "f32", "shape": ["M", "N"]}, "mx": {"dtype": "f32", "shape": ["N"]},
+                                       "Xc": {"dtype": "f32", "shape": ["M", "N"]}, "E": {"dtype": "f32", "shape": ["M", "N"]},
+                                       "sm": {"dtype": "f32", "shape": ["N"]}, "out": {"dtype": "f32", "shape": ["M", "N"]}},
+          "ops": [{"op": "reduce_max", "inputs": ["X"], "output": "mx", "attrs": {"dims": [1]}},
+                  {"op": "sub", "inputs": ["X", "mx"], "output": "Xc"}, {"op": "exp", "inputs": ["Xc"], "output": "E"},
+                  {"op": "reduce_sum", "inputs": ["E"], "output": "sm", "attrs": {"dims": [1]}},
+                  {"op": "div", "inputs": ["E", "sm"], "output": "out"}], "outputs": ["out"]}
+    with pytest.raises(HipLoweringError):
+        lower_intent_to_hip_kernel(ir, shape_bindings={"M": 8, "N": 8})
+
+
+def test_layernorm_chain_with_wrong_divisor_is_rejected():
+    ir = WORKLOADS["layernorm"].ir()
+    ir["ops"][1]["attrs"]["divisor"] = "M"
+    with pytest.raises(HipLoweringError):
+        lower_intent_to_hip_kernel(ir, shape_bindings={"M": 8, "N": 64})
+
+
+def test_layernorm_without_stat_outputs_uses_scratch():
+    ir = WORKLOADS["layernorm"].ir()
+    ir["outputs"] = ["out_ptr"]
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 8, "N": 64})
+    assert [a for a in k.call_args if a[0] == "scratch_f32"] == [("scratch_f32", 8), ("scratch_f32", 8)]
+
+
+def test_gelu_with_wrong_constant_is_not_gelu():
+    ir = WORKLOADS["gelu"].ir()
+    fn = expand_macros(as_intent(ir)).to_json_dict()
+    for op in fn["ops"]:
+        if op["op"] == "const" and abs(op["attrs"]["value"] - 0.044715) < 1e-9:
+            op["attrs"]["value"] = 0.05
+    with pytest.raises(HipLoweringError):
+        lower_intent_to_hip_kernel(fn, shape_bindings={"M": 4, "N": 64})
+
+
+def test_gemm_forms_and_errors():
+    b = {"M": 256, "N": 256, "K": 64}
+    assert lower_intent_to_hip_kernel(matmul_bias_relu2d_ir(), shape_bindings=b).call_args[-1] == ("i32", 1)
+    ir = matmul_bias_relu2d_ir()
+    ir["ops"][0]["attrs"] = {"transpose_b": True}
+    with pytest.raises(HipLoweringError, match="transpose"):
+        lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    f32 = matmul_bias_relu2d_ir("f32")
+    with pytest.raises(HipLoweringError, match="bf16"):
+        lower_intent_to_hip_kernel(f32, shape_bindings=b)
+    # max(x, 0) is ReLU too
+    ir = matmul_bias_relu2d_ir()
+    ir["tensors"]["zero"] = {"dtype": "f32", "shape": []}
+    ir["ops"][-1] = {"op": "max", "inputs": ["mm_b", "zero"], "output": "C"}
+    ir["ops"].insert(0, {"op": "const", "inputs": [], "output": "zero", "attrs": {"value": 0.0, "dtype": "f32"}})
+    assert lower_intent_to_hip_kernel(ir, shape_bindings=b).call_args[-1] == ("i32", 1)
+
+
+def test_unsupported_ops_raise():
+    ir = {"name": "g", "tensors": {"x": {"dtype": "f32", "shape": ["N"]}, "i": {"dtype": "i32", "shape": ["N"]},
+                                   "y": {"dtype": "f32", "shape": ["N"]}},
+          "ops": [{"op": "gather", "inputs": ["x", "i"], "output": "y"}], "outputs": ["y"]}
+    with pytest.raises(HipLoweringError, match="unsupported"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={"N": 4})
+
+
+# ---------------------------------------------------------------- C-ABI library
+def _header_symbols():
+    text = (ROOT / "include" / "intentir_hip.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(ihip_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_every_runtime_signature():
+    assert _header_symbols() == sorted(SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    if not LIB_PATH.exists():
+        pytest.fail("libintentir_hip.so is not built: run python -m intent_ir_amd.build")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for sym in _header_symbols():
+        assert hasattr(lib, sym), sym
+    lib.ihip_abi_version.restype = ctypes.c_int
+    assert lib.ihip_abi_version() == 1
+    lib.ihip_last_error.restype = ctypes.c_char_p
+    assert lib.ihip_last_error() == b""
+
+
+def test_library_rejects_bad_arguments_without_a_device():
+    """Argument checks run on the host before any HIP call: no GPU needed to see them."""
+    from intent_ir_amd.runtime import load_library
+
+    lib = load_library()
+    st = lib.ihip_softmax_rows_f32(None, None, -1, 4, None)
+    assert st == -1 and b"invalid shape" in lib.ihip_last_error()
+    st = lib.ihip_reduce_rows_f32(None, None, 4, 4, 7, None)
+    assert st == -1 and b"unknown kind" in lib.ihip_last_error()
+    st = lib.ihip_gemm_bf16_bias_relu(None, None, None, None, 2, 2, 2, 1, None)
+    assert st == -1 and b"null" in lib.ihip_last_error()
+    st = lib.ihip_reduce_any_rows_f32(None, None, 1 << 62, 1 << 62, 0.0, None)
+    assert st == -1  # element count overflows int64
