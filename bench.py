@@ -86,7 +86,7 @@ class Launcher:
             raise RuntimeError(f"launch failed: {self.lib.ihip_last_error().decode()}")
 
 
-def measure(key, steps, warmup, torch, log):
+def measure(key, steps, warmup, torch, log, timing="eager"):
     from intent_ir_amd import lower_intent_to_hip_kernel
     from intent_ir_amd.configs import WORKLOADS, algorithmic_bytes, gen_device
     from intent_ir_amd.runtime import tensor_shapes, torch_dtype
@@ -111,23 +111,31 @@ def measure(key, steps, warmup, torch, log):
     for i in range(warmup):
         L.launch(i)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        graph.capture_begin()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if timing == "graph":
+        graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            graph.capture_begin()
+            for i in range(steps):
+                L.launch(i)
+            graph.capture_end()
+        torch.cuda.current_stream().wait_stream(stream)
+        graph.replay()  # untimed: first replay uploads the graph
+        torch.cuda.synchronize()
+        t0.record()
+        graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        del graph
+    else:
+        torch.cuda.synchronize()
+        t0.record()
         for i in range(steps):
             L.launch(i)
-        graph.capture_end()
-    torch.cuda.current_stream().wait_stream(stream)
-    graph.replay()  # untimed: first replay uploads the graph
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
-    graph.replay()
-    t1.record()
-    torch.cuda.synchronize()
+        t1.record()
+        torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
     # cheap property check on the last written set (no oracle in the timed path)
     last = sets[(steps - 1) % nsets]
@@ -135,6 +143,7 @@ def measure(key, steps, warmup, torch, log):
         rs = last["output_ptr"].double().sum(dim=1)
         assert torch.allclose(rs, torch.ones_like(rs), atol=1e-5), "softmax rows do not sum to 1"
     res = {"kernel": lowered.kernel_id, "ms_per_launch": ms, "steps": steps, "warmup": warmup, "buffer_sets": nsets,
+           "timing": timing,
            "algo_bytes": per_launch}
     if key == "matmul":
         flops = w.algorithmic_flops(b)
@@ -143,7 +152,7 @@ def measure(key, steps, warmup, torch, log):
     else:
         gbs = per_launch / (ms * 1e-3) / 1e9
         res.update(value=gbs, unit="GB/s", frac=gbs / HBM_PEAK_GBS)
-    del graph, L, sets
+    del L, sets
     torch.cuda.empty_cache()
     return res
 
@@ -210,6 +219,8 @@ def main():
     ap.add_argument("--config", default="softmax", choices=sorted(WORKLOAD_NAMES))
     ap.add_argument("--only", action="store_true", help="measure the headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--timing", default="graph", choices=["eager", "graph"],
+                    help="eager: K stream-ordered launches between two events; graph: one replay of K captured launches")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every path here runs on one "
@@ -222,7 +233,7 @@ def main():
         log("bench.py needs a ROCm device")
         sys.exit(1)
     key = args.config
-    head = measure(key, args.steps, args.warmup, torch, log)
+    head = measure(key, args.steps, args.warmup, torch, log, args.timing)
     log(f"[bench] {key}: {head['value']:.1f} {head['unit']} ({100 * head['frac']:.1f}% of peak), "
         f"{head['ms_per_launch'] * 1e3:.2f} us/launch")
     kernels = {key: head}
@@ -231,7 +242,7 @@ def main():
             if other == key:
                 continue
             st = 20 if other == "matmul" else 100
-            r = measure(other, st, 5, torch, log)
+            r = measure(other, st, 5, torch, log, args.timing)
             log(f"[bench] {other}: {r['value']:.1f} {r['unit']} ({100 * r['frac']:.1f}% of peak), "
                 f"{r['ms_per_launch'] * 1e3:.2f} us/launch")
             kernels[other] = r

@@ -162,11 +162,12 @@ struct FastGemm {
 
 };
 
-template <int DK, int STAGES>
+template <int DK, int STAGES, int SCHED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const float* __restrict__ bias,
                            uint16_t* __restrict__ C, int64_t N, int64_t K, int relu, int tiles_m, int tiles_n) {
   using G = FastGemm<DK, STAGES>;
+  static_assert(SCHED == 0 || STAGES >= 3, "the pipelined schedule keeps two slices ahead");
   __shared__ __attribute__((aligned(1024))) char lds_raw[STAGES * G::kStage];
   const lds_char_t* lds = (const lds_char_t*)lds_raw;
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
@@ -198,23 +199,64 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
   G::wait_copies((KT < STAGES - 1 ? KT : STAGES - 1) - 1);
   __syncthreads();
 
-  for (int kt = 0; kt < KT; ++kt) {
-    // Slice kt+STAGES-1 goes to the stage read in iteration kt-1, which that iteration's
-    // barrier has released.
-    const int nt = kt + STAGES - 1;
-    if (nt < KT)
-      G::copy_slice(A, B, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage, wave, L);
-    const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
+  if constexpr (SCHED == 0) {
+    for (int kt = 0; kt < KT; ++kt) {
+      // Slice kt+STAGES-1 goes to the stage read in iteration kt-1, which that iteration's
+      // barrier has released.
+      const int nt = kt + STAGES - 1;
+      if (nt < KT)
+        G::copy_slice(A, B, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage, wave, L);
+      const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk) {
-      typename G::Frag f;
-      G::read(st, kk, L, f);
-      G::mfma(f, acc);
+      for (int kk = 0; kk < DK / 16; ++kk) {
+        typename G::Frag f;
+        G::read(st, kk, L, f);
+        G::mfma(f, acc);
+      }
+      // slice kt+1 must have landed before the barrier; later slices may stay in flight
+      const int last = nt < KT ? nt : KT - 1;
+      G::wait_copies(last > kt + 1 ? last - (kt + 1) : 0);
+      __syncthreads();
     }
-    // slice kt+1 must have landed before the barrier; later slices may stay in flight
-    const int last = nt < KT ? nt : KT - 1;
-    G::wait_copies(last > kt + 1 ? last - (kt + 1) : 0);
-    __syncthreads();
+  } else {
+    // Software pipeline over k16 steps: the fragments of step s+1 are read while the 16 MFMAs
+    // of step s issue (one LDS read slotted after each MFMA), so no MFMA waits on LDS.  At the
+    // last step of a slice the wave first makes slice kt+1 ready (its copy + one barrier),
+    // refills the stage of slice kt-1 (every wave consumed it before reaching this barrier)
+    // and reads slice kt+1's first fragments under the slice's last MFMAs.
+    constexpr int NK = DK / 16;
+    typename G::Frag f[2];
+    if (KT > 0) G::read(lds, 0, L, f[0]);
+    int cur = 0;
+    for (int kt = 0; kt < KT; ++kt) {
+      const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) {
+        const bool more = kk + 1 < NK || kt + 1 < KT;
+        if (kk + 1 < NK) {
+          G::read(st, kk + 1, L, f[cur ^ 1]);
+        } else if (kt + 1 < KT) {
+          const int issued = (kt + STAGES - 2 < KT - 1) ? kt + STAGES - 2 : KT - 1;  // last slice copied so far
+          G::wait_copies(issued - (kt + 1));
+          __syncthreads();
+          const int nt = kt + STAGES - 1;
+          if (nt < KT)
+            G::copy_slice(A, B, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage,
+                          wave, L);
+          G::read(lds + ((kt + 1) % STAGES) * G::kStage, 0, L, f[cur ^ 1]);
+        }
+        G::mfma(f[cur], acc);
+        if (more) {
+#pragma unroll
+          for (int j = 0; j < 12; ++j) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        }
+        cur ^= 1;
+      }
+    }
   }
 
   // Epilogue, one 32x32 block at a time (the empty asm keeps the compiler from pulling all
@@ -255,6 +297,7 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
 // K step and ring depth of the fast path.
 constexpr int kFastDK = 32;
 constexpr int kFastStages = 4;
+constexpr int kFastSched = 0;
 
 bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* C) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
@@ -265,7 +308,7 @@ bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, const void* A, const void* 
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
                             int64_t K, int relu, hipStream_t s) {
   const int64_t tm = M / kTile, tn = N / kTile;
-  gemm_bf16_fast_kernel<kFastDK, kFastStages><<<dim3(static_cast<unsigned>(tm * tn)), dim3(256), 0, s>>>(
+  gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched><<<dim3(static_cast<unsigned>(tm * tn)), dim3(256), 0, s>>>(
       A, B, bias, C, N, K, relu, static_cast<int>(tm), static_cast<int>(tn));
   return hipGetLastError();
 }

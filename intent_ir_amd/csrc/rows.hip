@@ -21,7 +21,7 @@ template <bool kZero, int kUnroll>
 __global__ __launch_bounds__(256) void reduce_any_rows_f32_vec(const f32x4* __restrict__ x, uint8_t* __restrict__ out,
                                                                int64_t M, int64_t n4, float c) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
   const f32x4* xr = x + row * n4;
   uint32_t acc = 0;
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void reduce_any_rows_f32_vec(const f32x4* __re
 __global__ __launch_bounds__(256) void reduce_any_rows_f32_scalar(const float* __restrict__ x, uint8_t* __restrict__ out,
                                                                   int64_t M, int64_t N, float c) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
   const float* xr = x + row * N;
   uint32_t acc = 0;
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(256) void reduce_any_rows_f32_scalar(const float* _
 __global__ __launch_bounds__(256) void reduce_any_rows_u8(const uint8_t* __restrict__ x, uint8_t* __restrict__ out,
                                                           int64_t M, int64_t N) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
   const uint8_t* xr = x + row * N;
   uint32_t acc = 0;
@@ -72,9 +72,14 @@ __global__ __launch_bounds__(256) void reduce_any_rows_u8(const uint8_t* __restr
   if (lane == 0) out[row] = acc != 0u;
 }
 
+// Row kernels take the number of rows per workgroup from blockDim.x / 64.  Streaming kernels
+// launch one-wave workgroups (measured 2-3% faster than four-wave ones on MI355X at 128 MiB).
+constexpr int kStreamBlock = 64;
+
 hipError_t launch_reduce_any_rows_f32(const float* x, uint8_t* out, int64_t M, int64_t N, float c, hipStream_t s) {
   if (M == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row
+  const dim3 grid(static_cast<unsigned>(M)), block(kStreamBlock);
   const bool vec = (N % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
   if (!vec) {
     reduce_any_rows_f32_scalar<<<grid, block, 0, s>>>(x, out, M, N, c);
@@ -104,7 +109,7 @@ template <int kKind>
 __global__ __launch_bounds__(256) void reduce_rows_f32(const float* __restrict__ x, float* __restrict__ out, int64_t M,
                                                        int64_t N) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
   const float* xr = x + row * N;
   float acc = kKind == 0 ? 0.0f : -__builtin_inff();
@@ -130,7 +135,7 @@ template <int kVpl>  // f32x4 vectors held per lane; row length <= 256 * kVpl
 __global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restrict__ x, f32x4* __restrict__ y,
                                                             int64_t M, int n4) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
   const f32x4* xr = x + row * n4;
   f32x4* yr = y + row * n4;
@@ -189,9 +194,10 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restr
 
 hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
+  if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row
   const bool vec = (N % 4 == 0) && (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0);
   const int64_t n4 = N / 4;
-  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  const dim3 grid(static_cast<unsigned>(M)), block(kStreamBlock);
   const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
   f32x4* y4 = reinterpret_cast<f32x4*>(y);
   if (vec && n4 <= 64) {
@@ -227,91 +233,72 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_f16_rne(lo)) | (static_cast<uint32_t>(f32_to_f16_rne(hi)) << 16);
 }
 
-template <int kVpl>  // 16-byte vectors per lane; row length <= 512 * kVpl
-__global__ __launch_bounds__(256) void layernorm_rows_f16_reg(const u32x4* __restrict__ x, const u32x4* __restrict__ w,
-                                                              const u32x4* __restrict__ b, u32x4* __restrict__ y,
-                                                              float* __restrict__ mean_out, float* __restrict__ rstd_out,
-                                                              int64_t M, int n8, int N, float eps) {
+// One row per wave, no persistence: gamma/beta are re-read per row (they stay in L2), which
+// keeps the register footprint small enough for four or more waves per SIMD.
+template <int kVpl>
+__global__ __launch_bounds__(256) void layernorm_rows_f16_wave(const u32x4* __restrict__ x, const u32x4* __restrict__ w,
+                                                               const u32x4* __restrict__ b, u32x4* __restrict__ y,
+                                                               float* __restrict__ mean_out, float* __restrict__ rstd_out,
+                                                               int64_t M, int n8, int N, float eps) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const int64_t wave0 = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
-  if (wave0 >= M) return;
-  // gamma / beta stay in registers for every row this wave visits.
-  H8 wv[kVpl], bv[kVpl];
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= M) return;
+  H8 xv[kVpl];
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
     const int idx = lane + i * kWave;
-    wv[i].v = idx < n8 ? w[idx] : u32x4(0u);
-    bv[i].v = idx < n8 ? b[idx] : u32x4(0u);
+    xv[i].v = idx < n8 ? __builtin_nontemporal_load(x + row * n8 + idx) : u32x4(0u);
   }
-  const float inv_n_den = static_cast<float>(N);
-  H8 nxt[kVpl];
+  float xf[kVpl][8];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      xf[i][j] = xv[i].get(j);
+      s += xf[i][j];
+    }
+  const float mean = wave_sum(s) / static_cast<float>(N);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const bool ok = (lane + i * kWave) < n8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      xf[i][j] = xf[i][j] - mean;
+      const float sq = xf[i][j] * xf[i][j];
+      q += ok ? sq : 0.f;
+    }
+  }
+  const float var = wave_sum(q) / static_cast<float>(N);
+  const float rstd = 1.0f / sqrtf(var + eps);
+  u32x4* yr = y + row * n8;
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
     const int idx = lane + i * kWave;
-    nxt[i].v = idx < n8 ? __builtin_nontemporal_load(x + wave0 * n8 + idx) : u32x4(0u);
+    if (idx < n8) {
+      H8 wv, bv;
+      wv.v = w[idx];
+      bv.v = b[idx];
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xhat = xf[i][j] * rstd;
+        const float scaled = xhat * wv.get(j);
+        o[j] = scaled + bv.get(j);
+      }
+      u32x4 pk;
+      pk.x = pack_f16x2(o[0], o[1]);
+      pk.y = pack_f16x2(o[2], o[3]);
+      pk.z = pack_f16x2(o[4], o[5]);
+      pk.w = pack_f16x2(o[6], o[7]);
+      __builtin_nontemporal_store(pk, yr + idx);
+    }
   }
-  for (int64_t row = wave0; row < M; row += nwaves) {
-    H8 cur[kVpl];
-#pragma unroll
-    for (int i = 0; i < kVpl; ++i) cur[i] = nxt[i];
-    const int64_t next_row = row + nwaves;
-    if (next_row < M) {  // prefetch the next row while this one is reduced
-#pragma unroll
-      for (int i = 0; i < kVpl; ++i) {
-        const int idx = lane + i * kWave;
-        nxt[i].v = idx < n8 ? __builtin_nontemporal_load(x + next_row * n8 + idx) : u32x4(0u);
-      }
-    }
-    float xf[kVpl][8];
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < kVpl; ++i) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        xf[i][j] = cur[i].get(j);
-        s += xf[i][j];
-      }
-    }
-    const float mean = wave_sum(s) / inv_n_den;
-    float q = 0.f;
-#pragma unroll
-    for (int i = 0; i < kVpl; ++i) {
-      const bool ok = (lane + i * kWave) < n8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        xf[i][j] = xf[i][j] - mean;
-        const float sq = xf[i][j] * xf[i][j];
-        q += ok ? sq : 0.f;
-      }
-    }
-    const float var = wave_sum(q) / inv_n_den;
-    const float rstd = 1.0f / sqrtf(var + eps);
-    u32x4* yr = y + row * n8;
-#pragma unroll
-    for (int i = 0; i < kVpl; ++i) {
-      const int idx = lane + i * kWave;
-      if (idx < n8) {
-        float o[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float xhat = xf[i][j] * rstd;
-          const float scaled = xhat * wv[i].get(j);
-          o[j] = scaled + bv[i].get(j);
-        }
-        u32x4 pk;
-        pk.x = pack_f16x2(o[0], o[1]);
-        pk.y = pack_f16x2(o[2], o[3]);
-        pk.z = pack_f16x2(o[4], o[5]);
-        pk.w = pack_f16x2(o[6], o[7]);
-        __builtin_nontemporal_store(pk, yr + idx);
-      }
-    }
-    if (lane == 0) {
-      mean_out[row] = mean;
-      rstd_out[row] = rstd;
-    }
+  if (lane == 0) {
+    mean_out[row] = mean;
+    rstd_out[row] = rstd;
   }
 }
 
@@ -358,22 +345,19 @@ hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const
     return hipGetLastError();
   }
   const int n8 = static_cast<int>(N / 8);
-  // Persistent waves: enough workgroups for ~2 per CU, each wave walks rows with a stride.
-  int64_t blocks = (M + 3) / 4;
-  if (blocks > 512) blocks = 512;
-  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
   const u32x4* x8 = reinterpret_cast<const u32x4*>(x);
   const u32x4* w8 = reinterpret_cast<const u32x4*>(w);
   const u32x4* b8 = reinterpret_cast<const u32x4*>(b);
   u32x4* y8 = reinterpret_cast<u32x4*>(y);
   if (n8 <= 64)
-    layernorm_rows_f16_reg<1><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+    layernorm_rows_f16_wave<1><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
   else if (n8 <= 128)
-    layernorm_rows_f16_reg<2><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+    layernorm_rows_f16_wave<2><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
   else if (n8 <= 256)
-    layernorm_rows_f16_reg<4><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+    layernorm_rows_f16_wave<4><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
   else
-    layernorm_rows_f16_reg<8><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+    layernorm_rows_f16_wave<8><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
   return hipGetLastError();
 }
 

@@ -104,8 +104,8 @@ class _Ctx:
 
 
 # ---------------------------------------------------------------- matchers
-def _row_launch(m: int) -> HipLaunch:
-    return HipLaunch((max(1, _cdiv(m, 4)), 1, 1), (256, 1, 1), 0)
+def _row_launch(m: int, rows_per_block: int = 4) -> HipLaunch:
+    return HipLaunch((max(1, _cdiv(m, rows_per_block)), 1, 1), (64 * rows_per_block, 1, 1), 0)
 
 
 def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
@@ -141,7 +141,8 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
             raise HipLoweringError(f"GEMM bias must be f32 [{N}]")
     args = [("tensor", a), ("tensor", b), ("tensor", env["bias"][1]) if has_bias else ("null", None),
             ("tensor", oname), ("i64", M), ("i64", N), ("i64", K), ("i32", int(relu))]
-    launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 147456)
+    full = M % 256 == 0 and N % 256 == 0 and K % 32 == 0  # fast path (4-stage ring) vs guarded kernel
+    launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 131072 if full else 147456)
     return HipLoweredKernel(c.fn.name, "ihip_gemm_bf16_bias_relu", c.io(names), launch, [oname], dict(c.b),
                             tuple(args))
 
@@ -175,7 +176,8 @@ def _match_reduce_any(c: _Ctx) -> Optional[HipLoweredKernel]:
         kid = "ihip_reduce_any_rows_u8"
     else:
         raise HipLoweringError(f"reduce_any input dtype {dt} is not lowered")
-    return HipLoweredKernel(c.fn.name, kid, c.io([x, oname]), _row_launch(M), [oname], dict(c.b), args)
+    launch = _row_launch(M, 1) if kid == "ihip_reduce_any_rows_f32" else _row_launch(M)
+    return HipLoweredKernel(c.fn.name, kid, c.io([x, oname]), launch, [oname], dict(c.b), args)
 
 
 def _softmax_templates(rank: int):
@@ -203,7 +205,7 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
     if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
         raise HipLoweringError("HIP softmax takes f32 input and output")
     M, N = c.rows(x)
-    launch = _row_launch(M) if (N % 4 == 0 and N <= 4096) else HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
+    launch = _row_launch(M, 1) if (N % 4 == 0 and N <= 4096) else HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
     return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b),
                             (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N)))
 
@@ -247,7 +249,7 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
             ("i64", N), ("f32", float(env["eps"][1])))
     names = [x, w, b, y] + [inv[r] for r in ("mean", "rstd") if r in inv]
     vec = N % 8 == 0 and 0 < N <= 4096
-    launch = HipLaunch((min(512, max(1, _cdiv(M, 4))) if vec else max(1, M), 1, 1), (256, 1, 1), 0 if vec else 16)
+    launch = HipLaunch((max(1, _cdiv(M, 4)) if vec else max(1, M), 1, 1), (256, 1, 1), 0 if vec else 16)
     return HipLoweredKernel(c.fn.name, "ihip_layernorm_rows_f16", c.io(names), launch, list(c.fn.outputs),
                             dict(c.b), args)
 
