@@ -44,11 +44,26 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
+// ---------------------------------------------------------------- exp
+// e^d for d <= 0 or NaN (softmax arguments x - max).  t = d*log2(e) is carried as
+// a head RN(d*L) and a tail (its exact rounding error plus d*(log2 e - L)); the
+// head goes through the hardware 2^x and the tail through a first-order
+// correction, |tail| <= 2^-24 |t|.  Relative error about 2 ulp for d >= -87;
+// below that the result is under 1e-38.
+__device__ __forceinline__ float exp_nonpos(float d) {
+  constexpr float kL = 1.44269502f;        // RN(log2 e)
+  constexpr float kLlo = 1.92596303e-08f;  // log2 e - kL
+  constexpr float kLn2 = 0.693147182f;
+  const float t = d * kL;
+  const float tail = __builtin_fmaf(d, kLlo, __builtin_fmaf(d, kL, -t));
+  const float e = __builtin_amdgcn_exp2f(t);
+  return __builtin_fmaf(e, tail * kLn2, e);
+}
+
 // ---------------------------------------------------------------- reductions
 // max with numpy semantics: a NaN operand wins (np.maximum propagates NaN).
-__device__ __forceinline__ float max_nan(float a, float b) {
-  return (a >= b || a != a) ? a : b;
-}
+// gfx950 has an IEEE 754-2019 maximum (v_maximum3_f32): NaN in, NaN out.
+__device__ __forceinline__ float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

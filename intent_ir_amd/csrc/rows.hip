@@ -129,9 +129,12 @@ hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t
 }
 
 // ============================================================== softmax (last axis, f32)
-// y = exp(x - max) / sum(exp(x - max)), the exact op order of the reference
-// interpreter; exp is the accurate expf and the final step is a true division.
-template <int kVpl>  // f32x4 vectors held per lane; row length <= 256 * kVpl
+// y = exp(x - max) * (1 / sum(exp(x - max))).  The reference interpreter divides
+// every element by the sum; multiplying by the row's correctly rounded
+// reciprocal adds at most one rounding (|rel. diff| < 2.4e-7).  max propagates
+// NaN (v_maximum3_f32), so a row holding a NaN comes out all NaN, as in numpy.
+// About 14 VALU instructions per element, so the kernel stays HBM-bound.
+template <int kVpl, bool kFull>  // f32x4 vectors held per lane; kFull: n4 == 64 * kVpl
 __global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restrict__ x, f32x4* __restrict__ y,
                                                             int64_t M, int n4) {
   const int lane = threadIdx.x & 63;
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restr
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
     const int idx = lane + i * kWave;
-    v[i] = idx < n4 ? __builtin_nontemporal_load(xr + idx) : f32x4{ninf, ninf, ninf, ninf};
+    v[i] = (kFull || idx < n4) ? __builtin_nontemporal_load(xr + idx) : f32x4{ninf, ninf, ninf, ninf};
   }
   float mx = ninf;
 #pragma unroll
@@ -153,25 +156,23 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restr
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
-    const int idx = lane + i * kWave;
-    if (idx < n4) {
-      v[i].x = expf(v[i].x - mx);
-      v[i].y = expf(v[i].y - mx);
-      v[i].z = expf(v[i].z - mx);
-      v[i].w = expf(v[i].w - mx);
-      sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    }
+    v[i].x = exp_nonpos(v[i].x - mx);
+    v[i].y = exp_nonpos(v[i].y - mx);
+    v[i].z = exp_nonpos(v[i].z - mx);
+    v[i].w = exp_nonpos(v[i].w - mx);
+    if (kFull || lane + i * kWave < n4) sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
   }
   sum = wave_sum(sum);
+  const float inv = 1.0f / sum;
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
     const int idx = lane + i * kWave;
-    if (idx < n4) {
+    if (kFull || idx < n4) {
       f32x4 o;
-      o.x = v[i].x / sum;
-      o.y = v[i].y / sum;
-      o.z = v[i].z / sum;
-      o.w = v[i].w / sum;
+      o.x = v[i].x * inv;
+      o.y = v[i].y * inv;
+      o.z = v[i].z * inv;
+      o.w = v[i].w * inv;
       __builtin_nontemporal_store(o, yr + idx);
     }
   }
@@ -192,83 +193,90 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restr
   for (int64_t i = threadIdx.x; i < N; i += blockDim.x) yr[i] = expf(xr[i] - mx) / s;
 }
 
+template <int kVpl>
+static void launch_softmax_reg(const f32x4* x4, f32x4* y4, int64_t M, int n4, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  if (n4 == kVpl * kWave)
+    softmax_rows_f32_reg<kVpl, true><<<grid, block, 0, s>>>(x4, y4, M, n4);
+  else
+    softmax_rows_f32_reg<kVpl, false><<<grid, block, 0, s>>>(x4, y4, M, n4);
+}
+
 hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row
+  if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // grid.x limit of the row-per-workgroup fallback
   const bool vec = (N % 4 == 0) && (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0);
   const int64_t n4 = N / 4;
-  const dim3 grid(static_cast<unsigned>(M)), block(kStreamBlock);
   const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
   f32x4* y4 = reinterpret_cast<f32x4*>(y);
-  if (vec && n4 <= 64) {
-    softmax_rows_f32_reg<1><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
-  } else if (vec && n4 <= 128) {
-    softmax_rows_f32_reg<2><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
-  } else if (vec && n4 <= 256) {
-    softmax_rows_f32_reg<4><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
-  } else if (vec && n4 <= 512) {
-    softmax_rows_f32_reg<8><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
-  } else if (vec && n4 <= 1024) {
-    softmax_rows_f32_reg<16><<<grid, block, 0, s>>>(x4, y4, M, static_cast<int>(n4));
-  } else {
+  const int n4i = static_cast<int>(n4 < 0x7fffffff ? n4 : 0x7fffffff);
+  if (vec && n4 <= 64)
+    launch_softmax_reg<1>(x4, y4, M, n4i, s);
+  else if (vec && n4 <= 128)
+    launch_softmax_reg<2>(x4, y4, M, n4i, s);
+  else if (vec && n4 <= 256)
+    launch_softmax_reg<4>(x4, y4, M, n4i, s);
+  else if (vec && n4 <= 512)
+    launch_softmax_reg<8>(x4, y4, M, n4i, s);
+  else if (vec && n4 <= 1024)
+    launch_softmax_reg<16>(x4, y4, M, n4i, s);
+  else
     softmax_rows_f32_any<<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, N);
-  }
   return hipGetLastError();
 }
 
 // ============================================================== LayerNorm forward (f16)
 // Op order of the reference LayerNorm IR (pipeline/tilelang/core.py:1322-1384):
 //   mean = sum(x)/N; d = x - mean; var = sum(d*d)/N; rstd = 1/sqrt(var + eps);
-//   y = (d*rstd)*w + b
-// evaluated in f32 without contraction, y rounded to f16 (RNE).
-struct H8 {  // 8 halves = one 16-byte vector
-  u32x4 v;
-  __device__ __forceinline__ float get(int i) const {
-    const uint32_t w = (i < 2) ? v.x : (i < 4) ? v.y : (i < 6) ? v.z : v.w;
-    return f16_to_f32(static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xffffu)));
-  }
-};
+//   y = (d*rstd)*w + b, rounded to f16 (RNE).
+// Statistics are accumulated in f32 from the exact f16 values.  The vector kernel
+// uses gfx950's mixed-precision instructions so a row costs ~7 VALU per element:
+// v_dot2_f32_f16 for sum(x), v_fma_mix_f32 (f16 operand, f32 math) for
+// d = x*1 - mean and for d*rstd*w + b, and v_cvt_pk_f16_f32 for the packed store.
+// The last step is one fused multiply-add instead of a multiply and an add
+// (a difference of at most one f32 rounding before the f16 rounding).
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_f16_rne(lo)) | (static_cast<uint32_t>(f32_to_f16_rne(hi)) << 16);
-}
-
-// One row per wave, no persistence: gamma/beta are re-read per row (they stay in L2), which
-// keeps the register footprint small enough for four or more waves per SIMD.
-template <int kVpl>
+// One wave per row; the row is held in registers (kVpl 16-byte vectors per lane)
+// and read from HBM once.  kFull: n8 == 64 * kVpl, no tail masks.
+template <int kVpl, bool kFull>
 __global__ __launch_bounds__(256) void layernorm_rows_f16_wave(const u32x4* __restrict__ x, const u32x4* __restrict__ w,
                                                                const u32x4* __restrict__ b, u32x4* __restrict__ y,
                                                                float* __restrict__ mean_out, float* __restrict__ rstd_out,
                                                                int64_t M, int n8, int N, float eps) {
-#pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
-  H8 xv[kVpl];
+  f16x8_t xv[kVpl];
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
     const int idx = lane + i * kWave;
-    xv[i].v = idx < n8 ? __builtin_nontemporal_load(x + row * n8 + idx) : u32x4(0u);
+    xv[i] = __builtin_bit_cast(f16x8_t, (kFull || idx < n8) ? __builtin_nontemporal_load(x + row * n8 + idx) : u32x4(0u));
   }
-  float xf[kVpl][8];
   float s = 0.f;
+  const f16x2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 #pragma unroll
   for (int i = 0; i < kVpl; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      xf[i][j] = xv[i].get(j);
-      s += xf[i][j];
+    for (int j = 0; j < 4; ++j) {
+      const f16x2_t p = {xv[i][2 * j], xv[i][2 * j + 1]};
+      s = __builtin_amdgcn_fdot2(p, one, s, false);  // padding lanes hold +0
     }
   const float mean = wave_sum(s) / static_cast<float>(N);
+  // 1.0 the compiler cannot fold away, so x*unit - mean stays one v_fma_mix_f32
+  // (f16 operand widened inside the instruction) instead of a convert and a subtract.
+  float unit;
+  asm volatile("v_mov_b32 %0, 1.0" : "=v"(unit));
+  float d[kVpl][8];
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
-    const bool ok = (lane + i * kWave) < n8;
+    const bool ok = kFull || (lane + i * kWave) < n8;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      xf[i][j] = xf[i][j] - mean;
-      const float sq = xf[i][j] * xf[i][j];
-      q += ok ? sq : 0.f;
+      d[i][j] = __builtin_fmaf(static_cast<float>(xv[i][j]), unit, -mean);
+      q = __builtin_fmaf(d[i][j], ok ? d[i][j] : 0.f, q);
     }
   }
   const float var = wave_sum(q) / static_cast<float>(N);
@@ -277,23 +285,15 @@ __global__ __launch_bounds__(256) void layernorm_rows_f16_wave(const u32x4* __re
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
     const int idx = lane + i * kWave;
-    if (idx < n8) {
-      H8 wv, bv;
-      wv.v = w[idx];
-      bv.v = b[idx];
-      float o[8];
+    if (kFull || idx < n8) {
+      const f16x8_t wv = __builtin_bit_cast(f16x8_t, w[idx]);
+      const f16x8_t bv = __builtin_bit_cast(f16x8_t, b[idx]);
+      f16x8_t o;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float xhat = xf[i][j] * rstd;
-        const float scaled = xhat * wv.get(j);
-        o[j] = scaled + bv.get(j);
-      }
-      u32x4 pk;
-      pk.x = pack_f16x2(o[0], o[1]);
-      pk.y = pack_f16x2(o[2], o[3]);
-      pk.z = pack_f16x2(o[4], o[5]);
-      pk.w = pack_f16x2(o[6], o[7]);
-      __builtin_nontemporal_store(pk, yr + idx);
+      for (int j = 0; j < 8; ++j)
+        o[j] = static_cast<_Float16>(
+            __builtin_fmaf(d[i][j] * rstd, static_cast<float>(wv[j]), static_cast<float>(bv[j])));
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), yr + idx);
     }
   }
   if (lane == 0) {
@@ -334,9 +334,20 @@ __global__ __launch_bounds__(256) void layernorm_rows_f16_any(const uint16_t* __
   }
 }
 
+template <int kVpl>
+static void launch_layernorm_wave(const u32x4* x8, const u32x4* w8, const u32x4* b8, u32x4* y8, float* mean, float* rstd,
+                                  int64_t M, int n8, int N, float eps, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  if (n8 == kVpl * kWave)
+    layernorm_rows_f16_wave<kVpl, true><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, N, eps);
+  else
+    layernorm_rows_f16_wave<kVpl, false><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, N, eps);
+}
+
 hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y, float* mean,
                                      float* rstd, int64_t M, int64_t N, float eps, hipStream_t s) {
   if (M == 0) return hipSuccess;
+  if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // grid.x limit of the row-per-workgroup fallback
   const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                        reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(y);
   const bool vec = N > 0 && (N % 8 == 0) && ((al & 15) == 0) && N <= 512 * 8;
@@ -345,19 +356,18 @@ hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const
     return hipGetLastError();
   }
   const int n8 = static_cast<int>(N / 8);
-  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
   const u32x4* x8 = reinterpret_cast<const u32x4*>(x);
   const u32x4* w8 = reinterpret_cast<const u32x4*>(w);
   const u32x4* b8 = reinterpret_cast<const u32x4*>(b);
   u32x4* y8 = reinterpret_cast<u32x4*>(y);
   if (n8 <= 64)
-    layernorm_rows_f16_wave<1><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+    launch_layernorm_wave<1>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
   else if (n8 <= 128)
-    layernorm_rows_f16_wave<2><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+    launch_layernorm_wave<2>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
   else if (n8 <= 256)
-    layernorm_rows_f16_wave<4><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+    launch_layernorm_wave<4>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
   else
-    layernorm_rows_f16_wave<8><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps);
+    launch_layernorm_wave<8>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
   return hipGetLastError();
 }
 

@@ -205,7 +205,7 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
     if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
         raise HipLoweringError("HIP softmax takes f32 input and output")
     M, N = c.rows(x)
-    launch = _row_launch(M, 1) if (N % 4 == 0 and N <= 4096) else HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
+    launch = _row_launch(M) if (N % 4 == 0 and N <= 4096) else HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
     return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b),
                             (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N)))
 
