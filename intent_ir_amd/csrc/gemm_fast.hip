@@ -32,6 +32,8 @@
 //    consecutive n of one m: the epilogue adds bias, applies ReLU and stores 8 bytes.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace ihip {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -45,7 +47,7 @@ typedef __attribute__((address_space(3))) char lds_char_t;
 constexpr int kTile = 256;   // M and N extent of a workgroup tile
 constexpr int kGroupRows = 8;  // tile-rows per raster group
 
-__device__ __forceinline__ float relu_keep_nan(float v) { return v < 0.0f ? 0.0f : v; }  // np.maximum(v, 0)
+typedef __bf16 bf16x2_pk_t __attribute__((ext_vector_type(2)));
 
 template <int DK, int STAGES>
 struct FastGemm {
@@ -168,6 +170,7 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
                            uint16_t* __restrict__ C, int64_t N, int64_t K, int relu, int tiles_m, int tiles_n) {
   using G = FastGemm<DK, STAGES>;
   static_assert(SCHED == 0 || STAGES >= 3, "the pipelined schedule keeps two slices ahead");
+  // SCHED 1 needs KT >= STAGES - 1 (the prologue fills STAGES - 1 stages); the launcher checks.
   __shared__ __attribute__((aligned(1024))) char lds_raw[STAGES * G::kStage];
   const lds_char_t* lds = (const lds_char_t*)lds_raw;
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
@@ -221,32 +224,41 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
   } else {
     // Software pipeline over k16 steps: the fragments of step s+1 are read while the 16 MFMAs
     // of step s issue (one LDS read slotted after each MFMA), so no MFMA waits on LDS.  At the
-    // last step of a slice the wave first makes slice kt+1 ready (its copy + one barrier),
-    // refills the stage of slice kt-1 (every wave consumed it before reaching this barrier)
-    // and reads slice kt+1's first fragments under the slice's last MFMAs.
+    // last step of slice kt the wave makes slice kt+1 ready (its copies + one barrier), copies
+    // slice kt+STAGES-1 into the stage slice kt-1 used (every wave finished reading it before
+    // the barrier), and reads slice kt+1's first fragments under slice kt's last MFMAs.
+    // The loops are split so every body is straight-line code: the steady loop always copies
+    // and waits for a fixed number of slices, the tail copies nothing.  (Merged control flow
+    // makes the compiler's LDS wait counts conservative and stalls the MFMAs on reads of the
+    // next slice.)
     constexpr int NK = DK / 16;
     typename G::Frag f[2];
-    if (KT > 0) G::read(lds, 0, L, f[0]);
-    int cur = 0;
-    for (int kt = 0; kt < KT; ++kt) {
+    G::read(lds, 0, L, f[0]);
+    auto slice = [&](int kt, auto copy_tag, int pending) {
+      constexpr bool kCopy = decltype(copy_tag)::value;
       const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
-        const bool more = kk + 1 < NK || kt + 1 < KT;
+        typename G::Frag& cur = f[kk & 1];
+        typename G::Frag& nxt = f[(kk & 1) ^ 1];
+        // Step kk starts after every instruction of step kk-1: the barrier of a slice boundary
+        // cannot be hoisted above the previous step's MFMAs, whose slack lets this wave's LDS
+        // reads finish before the barrier waits for them.
+        __builtin_amdgcn_sched_barrier(0);
         if (kk + 1 < NK) {
-          G::read(st, kk + 1, L, f[cur ^ 1]);
-        } else if (kt + 1 < KT) {
-          const int issued = (kt + STAGES - 2 < KT - 1) ? kt + STAGES - 2 : KT - 1;  // last slice copied so far
-          G::wait_copies(issued - (kt + 1));
+          G::read(st, kk + 1, L, nxt);
+        } else if (pending >= 0) {  // a next slice exists
+          G::wait_copies(pending);
           __syncthreads();
-          const int nt = kt + STAGES - 1;
-          if (nt < KT)
+          G::read(lds + ((kt + 1) % STAGES) * G::kStage, 0, L, nxt);
+          if constexpr (kCopy) {  // after the reads: the copies are ordered asm the reads cannot pass
+            const int nt = kt + STAGES - 1;
             G::copy_slice(A, B, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage,
                           wave, L);
-          G::read(lds + ((kt + 1) % STAGES) * G::kStage, 0, L, f[cur ^ 1]);
+          }
         }
-        G::mfma(f[cur], acc);
-        if (more) {
+        G::mfma(cur, acc);
+        if (kk + 1 < NK || pending >= 0) {
 #pragma unroll
           for (int j = 0; j < 12; ++j) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
@@ -254,14 +266,22 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
           }
           __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         }
-        cur ^= 1;
       }
-    }
+    };
+    static_assert((DK / 16) % 2 == 0, "fragment double buffer alternates within a slice");
+    int kt = 0;
+    // steady state: slices up to kt+STAGES-2 are in flight; slice kt+1 must land
+    for (; kt + STAGES - 1 < KT; ++kt) slice(kt, std::true_type{}, STAGES - 3);
+    // tail: everything is issued; slice kt+1 must land, later ones may stay in flight
+    for (; kt < KT; ++kt) slice(kt, std::false_type{}, kt + 1 < KT ? KT - 2 - kt : -1);
   }
 
   // Epilogue, one 32x32 block at a time (the empty asm keeps the compiler from pulling all
-  // 256 accumulators into VGPRs at once).
+  // 256 accumulators into VGPRs at once).  Branch-free: no bias adds +0, ReLU is
+  // maximum(t, 0) (NaN stays NaN) and no ReLU is maximum(t, -inf); v_cvt_pk_bf16_f32 rounds
+  // two values to nearest even in one instruction.
   const bool has_bias = bias != nullptr;
+  const float floor_v = relu ? 0.0f : -__builtin_inff();
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni) {
     float bv[4][4];
@@ -279,15 +299,11 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
         const int64_t n = n0 + wn * 32 + ni * 64 + g4 * 8 + (lane >> 5) * 4;
         float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float t = acc[ni][mi][g4 * 4 + q];
-          if (has_bias) t = t + bv[g4][q];
-          v[q] = relu ? relu_keep_nan(t) : t;
-        }
-        uint2 pk;
-        pk.x = f32_to_bf16_rne(v[0]) | (uint32_t(f32_to_bf16_rne(v[1])) << 16);
-        pk.y = f32_to_bf16_rne(v[2]) | (uint32_t(f32_to_bf16_rne(v[3])) << 16);
-        *reinterpret_cast<uint2*>(C + m * N + n) = pk;
+        for (int q = 0; q < 4; ++q) v[q] = __builtin_elementwise_maximum(acc[ni][mi][g4 * 4 + q] + bv[g4][q], floor_v);
+        const bf16x2_pk_t lo = {static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1])};
+        const bf16x2_pk_t hi = {static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
+        const u32x2 pk = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        *reinterpret_cast<u32x2*>(C + m * N + n) = pk;
       }
       asm volatile("" ::: "memory");
     }
@@ -297,7 +313,7 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
 // K step and ring depth of the fast path.
 constexpr int kFastDK = 32;
 constexpr int kFastStages = 4;
-constexpr int kFastSched = 0;
+constexpr int kFastSched = 1;
 
 bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* C) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
