@@ -16,8 +16,9 @@
  *    uint16_t bit patterns; bool outputs are one byte (0/1) per element.
  *  - ``stream`` is a hipStream_t passed as void* (NULL = the default stream).
  *    Work is enqueued on it; nothing synchronises the host.
- *  - The caller owns every buffer.  The library allocates nothing and keeps no
- *    state besides a thread-local error message; it is re-entrant.
+ *  - The caller owns every buffer.  The library allocates no device memory.  Its only
+ *    state is a thread-local error message and, for element-wise programs, a cache of
+ *    compiled code behind a mutex; it is re-entrant.
  *  - Return: IHIP_OK (0); a negative IHIP_ERR_* for rejected arguments; or a
  *    positive hipError_t value when the launch itself failed.  On failure
  *    ihip_last_error() describes it (thread-local, valid until the next call).
@@ -87,6 +88,108 @@ int ihip_bias_gelu_tanh_axpy_bf16(const uint16_t* x, const uint16_t* bias, uint1
  * only as a lone op (:2137-2140). */
 int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                              int64_t N, int64_t K, int relu, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Generic element-wise program: any chain of element-wise ops over inputs that
+ * broadcast, transpose or repeat along the axes of one iteration space (rank <= 4).
+ * Replaces the reference's fused element-wise lowering, which generates and
+ * compiles one CUDA kernel per chain (backends/cuda/codegen/intentir_to_cuda.py:229-534;
+ * C++ emitter intentir_cuda_codegen.cpp:4057-4195).  Here one precompiled kernel runs a
+ * short register program that the host passes by value: every wave executes the
+ * same instruction stream (uniform branches), on 4 consecutive elements per lane.
+ * Values are f32 inside the program; bool is 0.0 / 1.0.
+ * ------------------------------------------------------------------------- */
+#define IHIP_EW_MAX_CODE 64
+#define IHIP_EW_MAX_REGS 8
+#define IHIP_EW_MAX_INPUTS 8
+#define IHIP_EW_MAX_OUTPUTS 4
+#define IHIP_EW_MAX_RANK 4
+
+/* Operand element types. */
+#define IHIP_DT_F32 0
+#define IHIP_DT_F16 1  /* IEEE half, 16-bit pattern */
+#define IHIP_DT_BF16 2 /* bfloat16, 16-bit pattern */
+#define IHIP_DT_BOOL 3 /* one byte; stored as 0/1, read as non-zero */
+#define IHIP_DT_I32 4  /* exact while |x| < 2^24 inside the program */
+
+/* Opcodes.  r[x] is register x; numpy float32 semantics (NaN propagates through
+ * max/min/relu; comparisons with NaN are false except ne). */
+#define IHIP_EW_LOAD 1       /* r[dst] = input[a] at the current coordinates */
+#define IHIP_EW_IMM 2        /* r[dst] = imm */
+#define IHIP_EW_IOTA 3       /* r[dst] = coordinate along axis a (0 = outermost of rank 4) */
+#define IHIP_EW_STORE 4      /* output[b] = r[a], converted to the output type (RNE) */
+#define IHIP_EW_MOV 5        /* r[dst] = r[a] */
+#define IHIP_EW_ADD 10       /* binary: r[dst] = r[a] op r[b] */
+#define IHIP_EW_SUB 11
+#define IHIP_EW_MUL 12
+#define IHIP_EW_DIV 13       /* IEEE division */
+#define IHIP_EW_MAX 14       /* np.maximum */
+#define IHIP_EW_MIN 15       /* np.minimum */
+#define IHIP_EW_NE 20        /* comparisons give 0.0 / 1.0 */
+#define IHIP_EW_LT 21
+#define IHIP_EW_LE 22
+#define IHIP_EW_GT 23
+#define IHIP_EW_GE 24
+#define IHIP_EW_EQ 25
+#define IHIP_EW_AND 30       /* logical, operands tested != 0 */
+#define IHIP_EW_OR 31
+#define IHIP_EW_NOT 32       /* unary: r[dst] = op(r[a]) */
+#define IHIP_EW_RELU 40      /* np.maximum(x, 0) */
+#define IHIP_EW_EXP 41
+#define IHIP_EW_RSQRT 42     /* 1 / sqrt(x), both correctly rounded */
+#define IHIP_EW_ABS 43
+#define IHIP_EW_FLOOR 44
+#define IHIP_EW_NEG 45
+#define IHIP_EW_WHERE 50     /* r[dst] = r[a] != 0 ? r[b] : r[c] */
+#define IHIP_EW_CAST_F16 60  /* round to f16 (RNE) and back */
+#define IHIP_EW_CAST_BF16 61 /* round to bf16 (RNE) and back */
+#define IHIP_EW_CAST_BOOL 62 /* x != 0 */
+#define IHIP_EW_CAST_I32 63  /* truncate toward zero */
+
+typedef struct ihip_ew_instr {
+  uint8_t op, dst, a, b, c;
+  uint8_t reserved[3];
+  float imm;
+} ihip_ew_instr;
+
+/* One input or output.  Inputs: element stride per axis of the rank-4 iteration
+ * space (0 = broadcast along that axis); any strides are accepted.  Outputs are
+ * dense row-major tensors of the iteration shape (strides ignored). */
+typedef struct ihip_ew_operand {
+  const void* ptr;
+  int32_t dtype;
+  int32_t reserved;
+  int64_t stride[IHIP_EW_MAX_RANK];
+} ihip_ew_operand;
+
+/* Run `code` (host memory, copied into the launch) over the iteration space
+ * `shape[0..rank-1]` (rank 0..4).  The program is checked before launch: known
+ * opcodes, registers and operand indices in range, every register written before
+ * it is read, every output stored exactly once. */
+int ihip_elementwise_program(const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,
+                             int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs,
+                             const int64_t* shape, int32_t rank, void* stream);
+
+/* How ihip_elementwise_program executes a program (process-wide):
+ *  AUTO   - native code specialised for the program and its operand types, compiled with
+ *           hiprtc on first use and cached (per device) for the life of the process; the
+ *           interpreter kernel when that compilation fails.  The default.
+ *  INTERP - always the interpreter kernel (no compilation).
+ *  NATIVE - specialised code only; a failed compilation is returned as an error.
+ * The first call of a new program in AUTO/NATIVE mode blocks the host for the compile
+ * (~0.3-3 s); later calls only launch. */
+#define IHIP_EW_MODE_AUTO 0
+#define IHIP_EW_MODE_INTERP 1
+#define IHIP_EW_MODE_NATIVE 2
+
+/* Set the mode when mode >= 0; return the previous mode (-1 for an unknown mode, unchanged). */
+int ihip_elementwise_mode(int mode);
+
+/* Compile the native code of a program for the given operand types ahead of its first launch
+ * (for example before capturing a graph).  Needs no device.  Checks the program like
+ * ihip_elementwise_program; returns IHIP_OK, or an error whose message holds the compiler log. */
+int ihip_elementwise_prepare(const ihip_ew_instr* code, int32_t n_code, const int32_t* input_dtypes, int32_t n_inputs,
+                             const int32_t* output_dtypes, int32_t n_outputs);
 
 #ifdef __cplusplus
 }

@@ -14,7 +14,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libintentir_hip.so"
-SOURCES = ["capi.hip", "rows.hip", "elementwise.hip", "gemm.hip", "gemm_fast.hip"]
+SOURCES = ["capi.hip", "rows.hip", "elementwise.hip", "gemm.hip", "gemm_fast.hip", "ewprog.hip", "ewjit.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -27,6 +27,8 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
 ]
+# hiprtc specialises element-wise programs at run time (ewjit.hip).
+LINK_FLAGS = ["-L/opt/rocm/lib", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"]
 
 
 def hipcc() -> str:
@@ -39,7 +41,7 @@ def hipcc() -> str:
 def build_library(verbose: bool = False) -> Path:
     """Compile every kernel source into one shared library (always recompiles)."""
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", str(tmp), *[str(CSRC / s) for s in SOURCES]]
+    cmd = [hipcc(), *HIPCC_FLAGS, "-o", str(tmp), *[str(CSRC / s) for s in SOURCES], *LINK_FLAGS]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -11,6 +11,9 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+#include <string>
+
 #include "../../include/intentir_hip.h"
 #include "common.hpp"
 
@@ -25,11 +28,17 @@ hipError_t launch_bias_gelu_axpy_bf16(const uint16_t*, const uint16_t*, uint16_t
                                       hipStream_t);
 hipError_t launch_gemm_bf16_bias_relu(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t,
                                       int64_t, int, hipStream_t);
+hipError_t launch_elementwise_program(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*,
+                                      int, const int64_t (&)[4], hipStream_t);
+hipError_t launch_elementwise_jit(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*, int,
+                                  const int64_t (&)[4], hipStream_t, std::string*);
+bool prepare_elementwise_jit(const ihip_ew_instr*, int, int, const int*, int, const int*, std::string*);
 }  // namespace ihip
 
 namespace {
 
 thread_local char g_last_error[512] = "";
+std::atomic<int> g_ew_mode{IHIP_EW_MODE_AUTO};
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -52,10 +61,81 @@ int64_t numel2(int64_t a, int64_t b) {
   return a * b;
 }
 
+// Operand shape of one element-wise program instruction: which fields name registers.
+enum EwForm { kEwBad, kEwLoad, kEwImm, kEwIota, kEwStore, kEwUnary, kEwBinary, kEwWhere };
+
+EwForm ew_form(int op) {
+  switch (op) {
+    case IHIP_EW_LOAD: return kEwLoad;
+    case IHIP_EW_IMM: return kEwImm;
+    case IHIP_EW_IOTA: return kEwIota;
+    case IHIP_EW_STORE: return kEwStore;
+    case IHIP_EW_MOV: case IHIP_EW_NOT: case IHIP_EW_RELU: case IHIP_EW_EXP: case IHIP_EW_RSQRT: case IHIP_EW_ABS:
+    case IHIP_EW_FLOOR: case IHIP_EW_NEG: case IHIP_EW_CAST_F16: case IHIP_EW_CAST_BF16: case IHIP_EW_CAST_BOOL:
+    case IHIP_EW_CAST_I32:
+      return kEwUnary;
+    case IHIP_EW_ADD: case IHIP_EW_SUB: case IHIP_EW_MUL: case IHIP_EW_DIV: case IHIP_EW_MAX: case IHIP_EW_MIN:
+    case IHIP_EW_NE: case IHIP_EW_LT: case IHIP_EW_LE: case IHIP_EW_GT: case IHIP_EW_GE: case IHIP_EW_EQ:
+    case IHIP_EW_AND: case IHIP_EW_OR:
+      return kEwBinary;
+    case IHIP_EW_WHERE: return kEwWhere;
+    default: return kEwBad;
+  }
+}
+
+bool ew_dtype_ok(int dt) { return dt >= IHIP_DT_F32 && dt <= IHIP_DT_I32; }
+
 #define IHIP_REQUIRE(cond, ...)                               \
   do {                                                        \
     if (!(cond)) return fail(IHIP_ERR_INVALID_ARG, __VA_ARGS__); \
   } while (0)
+
+// Data-flow check of an element-wise program: known opcodes, registers in range and written
+// before read, operands in range, every output stored exactly once.  0 or a failure code.
+int check_program(const ihip_ew_instr* code, int n_code, int n_inputs, int n_outputs) {
+  bool written[IHIP_EW_MAX_REGS] = {};
+  int stored[IHIP_EW_MAX_OUTPUTS] = {};
+  for (int pc = 0; pc < n_code; ++pc) {
+    const ihip_ew_instr& in = code[pc];
+    const EwForm f = ew_form(in.op);
+    IHIP_REQUIRE(f != kEwBad, "elementwise_program: instruction %d has unknown opcode %d", pc, (int)in.op);
+    const auto reg_ok = [&](int r) { return r < IHIP_EW_MAX_REGS && written[r]; };
+    switch (f) {
+      case kEwLoad:
+        IHIP_REQUIRE(in.a < n_inputs, "elementwise_program: instruction %d loads input %d of %d", pc, (int)in.a,
+                     (int)n_inputs);
+        break;
+      case kEwIota:
+        IHIP_REQUIRE(in.a < 4, "elementwise_program: instruction %d: iota axis %d outside 0..3", pc, (int)in.a);
+        break;
+      case kEwStore:
+        IHIP_REQUIRE(reg_ok(in.a), "elementwise_program: instruction %d stores unwritten register %d", pc, (int)in.a);
+        IHIP_REQUIRE(in.b < n_outputs, "elementwise_program: instruction %d stores output %d of %d", pc, (int)in.b,
+                     (int)n_outputs);
+        ++stored[in.b];
+        break;
+      case kEwWhere:
+        IHIP_REQUIRE(reg_ok(in.c), "elementwise_program: instruction %d reads unwritten register %d", pc, (int)in.c);
+        [[fallthrough]];
+      case kEwBinary:
+        IHIP_REQUIRE(reg_ok(in.b), "elementwise_program: instruction %d reads unwritten register %d", pc, (int)in.b);
+        [[fallthrough]];
+      case kEwUnary:
+        IHIP_REQUIRE(reg_ok(in.a), "elementwise_program: instruction %d reads unwritten register %d", pc, (int)in.a);
+        break;
+      default:
+        break;
+    }
+    if (f != kEwStore) {
+      IHIP_REQUIRE(in.dst < IHIP_EW_MAX_REGS, "elementwise_program: instruction %d writes register %d of %d", pc,
+                   (int)in.dst, IHIP_EW_MAX_REGS);
+      written[in.dst] = true;
+    }
+  }
+  for (int k = 0; k < n_outputs; ++k)
+    IHIP_REQUIRE(stored[k] == 1, "elementwise_program: output %d is stored %d times (must be once)", k, stored[k]);
+  return 0;
+}
 
 }  // namespace
 
@@ -128,6 +208,84 @@ int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* 
   IHIP_REQUIRE(M == 0 || N == 0 || K == 0 || (A != nullptr && B != nullptr), "gemm_bf16_bias_relu: A or B is null");
   return finish(ihip::launch_gemm_bf16_bias_relu(A, B, bias, C, M, N, K, relu, static_cast<hipStream_t>(stream)),
                 "gemm_bf16_bias_relu");
+}
+
+int ihip_elementwise_program(const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,
+                             int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs,
+                             const int64_t* shape, int32_t rank, void* stream) {
+  IHIP_REQUIRE(code != nullptr && n_code >= 1 && n_code <= IHIP_EW_MAX_CODE,
+               "elementwise_program: need 1..%d instructions, got %d", IHIP_EW_MAX_CODE, (int)n_code);
+  IHIP_REQUIRE(n_inputs >= 0 && n_inputs <= IHIP_EW_MAX_INPUTS && (n_inputs == 0 || inputs != nullptr),
+               "elementwise_program: need 0..%d inputs, got %d", IHIP_EW_MAX_INPUTS, (int)n_inputs);
+  IHIP_REQUIRE(n_outputs >= 1 && n_outputs <= IHIP_EW_MAX_OUTPUTS && outputs != nullptr,
+               "elementwise_program: need 1..%d outputs, got %d", IHIP_EW_MAX_OUTPUTS, (int)n_outputs);
+  IHIP_REQUIRE(rank >= 0 && rank <= IHIP_EW_MAX_RANK && (rank == 0 || shape != nullptr),
+               "elementwise_program: rank %d outside 0..%d", (int)rank, IHIP_EW_MAX_RANK);
+  int64_t sh[4] = {1, 1, 1, 1};
+  int64_t total = 1;
+  for (int i = 0; i < rank; ++i) {
+    sh[4 - rank + i] = shape[i];
+    total = numel2(total, shape[i]);
+    IHIP_REQUIRE(total >= 0, "elementwise_program: invalid shape (axis %d = %lld)", i, (long long)shape[i]);
+  }
+  for (int k = 0; k < n_inputs; ++k) {
+    IHIP_REQUIRE(ew_dtype_ok(inputs[k].dtype), "elementwise_program: input %d has unknown dtype %d", k,
+                 (int)inputs[k].dtype);
+    IHIP_REQUIRE(total == 0 || inputs[k].ptr != nullptr, "elementwise_program: input %d is null", k);
+  }
+  for (int k = 0; k < n_outputs; ++k) {
+    IHIP_REQUIRE(ew_dtype_ok(outputs[k].dtype), "elementwise_program: output %d has unknown dtype %d", k,
+                 (int)outputs[k].dtype);
+    IHIP_REQUIRE(total == 0 || outputs[k].ptr != nullptr, "elementwise_program: output %d is null", k);
+  }
+  const int bad = check_program(code, n_code, n_inputs, n_outputs);
+  if (bad) return bad;
+  if (total == 0) return finish(hipSuccess, "elementwise_program");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int mode = g_ew_mode.load();
+  if (mode != IHIP_EW_MODE_INTERP) {
+    std::string why;
+    const hipError_t e = ihip::launch_elementwise_jit(code, n_code, inputs, n_inputs, outputs, n_outputs, sh, s, &why);
+    if (e != hipErrorNotSupported || why.empty()) return finish(e, "elementwise_program (native)");
+    if (mode == IHIP_EW_MODE_NATIVE)
+      return fail(static_cast<int>(e), "elementwise_program: native code unavailable: %s", why.c_str());
+  }
+  return finish(ihip::launch_elementwise_program(code, n_code, inputs, n_inputs, outputs, n_outputs, sh, s),
+                "elementwise_program");
+}
+
+int ihip_elementwise_prepare(const ihip_ew_instr* code, int32_t n_code, const int32_t* input_dtypes, int32_t n_inputs,
+                             const int32_t* output_dtypes, int32_t n_outputs) {
+  IHIP_REQUIRE(code != nullptr && n_code >= 1 && n_code <= IHIP_EW_MAX_CODE,
+               "elementwise_prepare: need 1..%d instructions, got %d", IHIP_EW_MAX_CODE, (int)n_code);
+  IHIP_REQUIRE(n_inputs >= 0 && n_inputs <= IHIP_EW_MAX_INPUTS && (n_inputs == 0 || input_dtypes != nullptr),
+               "elementwise_prepare: need 0..%d inputs, got %d", IHIP_EW_MAX_INPUTS, (int)n_inputs);
+  IHIP_REQUIRE(n_outputs >= 1 && n_outputs <= IHIP_EW_MAX_OUTPUTS && output_dtypes != nullptr,
+               "elementwise_prepare: need 1..%d outputs, got %d", IHIP_EW_MAX_OUTPUTS, (int)n_outputs);
+  int in_dt[IHIP_EW_MAX_INPUTS] = {}, out_dt[IHIP_EW_MAX_OUTPUTS] = {};
+  for (int k = 0; k < n_inputs; ++k) {
+    IHIP_REQUIRE(ew_dtype_ok(input_dtypes[k]), "elementwise_prepare: input %d has unknown dtype %d", k,
+                 (int)input_dtypes[k]);
+    in_dt[k] = input_dtypes[k];
+  }
+  for (int k = 0; k < n_outputs; ++k) {
+    IHIP_REQUIRE(ew_dtype_ok(output_dtypes[k]), "elementwise_prepare: output %d has unknown dtype %d", k,
+                 (int)output_dtypes[k]);
+    out_dt[k] = output_dtypes[k];
+  }
+  const int bad = check_program(code, n_code, n_inputs, n_outputs);
+  if (bad) return bad;
+  std::string why;
+  if (!ihip::prepare_elementwise_jit(code, n_code, n_inputs, in_dt, n_outputs, out_dt, &why))
+    return fail(static_cast<int>(hipErrorNotSupported), "elementwise_prepare: %s", why.c_str());
+  g_last_error[0] = '\0';
+  return IHIP_OK;
+}
+
+int ihip_elementwise_mode(int mode) {
+  if (mode > IHIP_EW_MODE_NATIVE) return -1;
+  if (mode < 0) return g_ew_mode.load();
+  return g_ew_mode.exchange(mode);
 }
 
 }  // extern "C"

@@ -1,0 +1,417 @@
+// Native code for element-wise programs: the instruction list of ihip_elementwise_program
+// (include/intentir_hip.h) is turned into straight-line gfx950 code with hiprtc, once per
+// distinct program and operand types, and cached for the life of the process.
+//
+// The interpreter kernel (ewprog.hip) pays a uniform dispatch, operand moves through the
+// indexed register file and an instruction fetch for every program instruction, which
+// costs several times the HBM time of a chain longer than three or four instructions.
+// Specialised code has none of that: registers are plain variables and every operand type
+// is known, so a chain runs at the rate of its loads and stores.  This mirrors what the
+// reference does per chain (CUDA source generated and compiled at first use,
+// frontends/cuda/runtime.py:621-808), with the difference that the source is derived here
+// from the already validated instruction list, inside the library, behind the same C call.
+//
+// Layout and schedule follow the interpreter kernel: a lane owns V consecutive elements of
+// the innermost axis (V = 8 when all operands are 16-bit or narrower, so each access is one
+// 16-byte vector; else 4), grid.y strides over outer rows, inputs carry per-axis strides,
+// and V-wide, 4-wide or element-wise access per operand is chosen from uniform flags.
+#include <hip/hiprtc.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/intentir_hip.h"
+#include "common.hpp"
+
+namespace ihip {
+
+struct EwJitArgs {
+  const void* in_ptr[IHIP_EW_MAX_INPUTS];
+  int64_t in_stride[IHIP_EW_MAX_INPUTS][4];
+  void* out_ptr[IHIP_EW_MAX_OUTPUTS];
+  int64_t shape[4];
+  int64_t rows;
+  int64_t nvec;      // ceil(D3 / V): lanes own V = 4 or 8 elements
+  uint32_t in_vec4;  // bit k: input k is read with 4-element vectors
+  uint32_t in_vec8;  // bit k: input k is read with 8-element vectors
+  uint32_t out_vec4;
+  uint32_t out_vec8;
+};
+
+namespace {
+
+// Device prelude of every generated kernel; the struct must match EwJitArgs above.
+const char* kPrelude = R"JIT(
+typedef unsigned int u32;
+typedef unsigned short u16;
+typedef unsigned char u8;
+typedef long long i64;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+typedef u32 u32x2 __attribute__((ext_vector_type(2)));
+struct EwJitArgs {
+  const void* in_ptr[8];
+  i64 in_stride[8][4];
+  void* out_ptr[4];
+  i64 shape[4];
+  i64 rows;
+  i64 nvec;
+  u32 in_vec4;
+  u32 in_vec8;
+  u32 out_vec4;
+  u32 out_vec8;
+};
+__device__ __forceinline__ float h2f(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ float b2f(u16 b) { return __builtin_bit_cast(float, ((u32)b) << 16); }
+__device__ __forceinline__ u16 f2h(float x) { return __builtin_bit_cast(u16, (_Float16)x); }
+__device__ __forceinline__ u16 f2b(float x) { return __builtin_bit_cast(u16, (__bf16)x); }
+template <int DT> __device__ __forceinline__ float ld1(const void* p, i64 i) {
+  if (DT == 0) return ((const float*)p)[i];
+  if (DT == 1) return h2f(((const u16*)p)[i]);
+  if (DT == 2) return b2f(((const u16*)p)[i]);
+  if (DT == 3) return (float)((const u8*)p)[i];
+  return (float)((const int*)p)[i];
+}
+template <int DT> __device__ __forceinline__ void ld4(const void* p, i64 i, float* v) {
+  if (DT == 0) {
+    const f32x4 q = *(const f32x4*)((const float*)p + i);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else if (DT == 1 || DT == 2) {
+    const u32x2 q = *(const u32x2*)((const u16*)p + i);
+    const u16 h[4] = {(u16)(q.x & 0xffffu), (u16)(q.x >> 16), (u16)(q.y & 0xffffu), (u16)(q.y >> 16)};
+    for (int j = 0; j < 4; ++j) v[j] = DT == 1 ? h2f(h[j]) : b2f(h[j]);
+  } else if (DT == 3) {
+    const u32 q = *(const u32*)((const u8*)p + i);
+    for (int j = 0; j < 4; ++j) v[j] = (float)((q >> (8 * j)) & 0xffu);
+  } else {
+    const u32x4 q = *(const u32x4*)((const int*)p + i);
+    v[0] = (float)(int)q.x; v[1] = (float)(int)q.y; v[2] = (float)(int)q.z; v[3] = (float)(int)q.w;
+  }
+}
+template <int DT> __device__ __forceinline__ void st1(void* p, i64 i, float x) {
+  if (DT == 0) ((float*)p)[i] = x;
+  else if (DT == 1) ((u16*)p)[i] = f2h(x);
+  else if (DT == 2) ((u16*)p)[i] = f2b(x);
+  else if (DT == 3) ((u8*)p)[i] = x != 0.0f ? 1 : 0;
+  else ((int*)p)[i] = (int)x;
+}
+template <int DT> __device__ __forceinline__ void st4(void* p, i64 i, const float* v) {
+  if (DT == 0) {
+    *(f32x4*)((float*)p + i) = f32x4{v[0], v[1], v[2], v[3]};
+  } else if (DT == 1 || DT == 2) {
+    u16 h[4];
+    for (int j = 0; j < 4; ++j) h[j] = DT == 1 ? f2h(v[j]) : f2b(v[j]);
+    *(u32x2*)((u16*)p + i) = u32x2{h[0] | ((u32)h[1] << 16), h[2] | ((u32)h[3] << 16)};
+  } else if (DT == 3) {
+    u32 q = 0;
+    for (int j = 0; j < 4; ++j) q |= (v[j] != 0.0f ? 1u : 0u) << (8 * j);
+    *(u32*)((u8*)p + i) = q;
+  } else {
+    *(u32x4*)((int*)p + i) = u32x4{(u32)(int)v[0], (u32)(int)v[1], (u32)(int)v[2], (u32)(int)v[3]};
+  }
+}
+// 8 consecutive elements at offset i (i % 8 == 0, base aligned to 8 elements): one 16-byte
+// access for 16-bit types, two for 32-bit ones.
+template <int DT> __device__ __forceinline__ void ld8(const void* p, i64 i, float* v) {
+  if (DT == 1 || DT == 2) {
+    const u32x4 q = *(const u32x4*)((const u16*)p + i);
+    const u32 w[4] = {q.x, q.y, q.z, q.w};
+    for (int j = 0; j < 4; ++j) {
+      const u16 lo = (u16)(w[j] & 0xffffu), hi = (u16)(w[j] >> 16);
+      v[2 * j] = DT == 1 ? h2f(lo) : b2f(lo);
+      v[2 * j + 1] = DT == 1 ? h2f(hi) : b2f(hi);
+    }
+  } else if (DT == 3) {
+    const u32x2 q = *(const u32x2*)((const u8*)p + i);
+    for (int j = 0; j < 4; ++j) v[j] = (float)((q.x >> (8 * j)) & 0xffu);
+    for (int j = 0; j < 4; ++j) v[4 + j] = (float)((q.y >> (8 * j)) & 0xffu);
+  } else {
+    ld4<DT>(p, i, v);
+    ld4<DT>(p, i + 4, v + 4);
+  }
+}
+template <int DT> __device__ __forceinline__ void st8(void* p, i64 i, const float* v) {
+  if (DT == 1 || DT == 2) {
+    u32 w[4];
+    for (int j = 0; j < 4; ++j) {
+      const u16 lo = DT == 1 ? f2h(v[2 * j]) : f2b(v[2 * j]);
+      const u16 hi = DT == 1 ? f2h(v[2 * j + 1]) : f2b(v[2 * j + 1]);
+      w[j] = lo | ((u32)hi << 16);
+    }
+    *(u32x4*)((u16*)p + i) = u32x4{w[0], w[1], w[2], w[3]};
+  } else if (DT == 3) {
+    u32 q0 = 0, q1 = 0;
+    for (int j = 0; j < 4; ++j) q0 |= (v[j] != 0.0f ? 1u : 0u) << (8 * j);
+    for (int j = 0; j < 4; ++j) q1 |= (v[4 + j] != 0.0f ? 1u : 0u) << (8 * j);
+    *(u32x2*)((u8*)p + i) = u32x2{q0, q1};
+  } else {
+    st4<DT>(p, i, v);
+    st4<DT>(p, i + 4, v + 4);
+  }
+}
+// EW_V (4 or 8) elements per lane, defined by the generated source.
+template <int DT> __device__ __forceinline__ void load_op(const EwJitArgs& a, int k, i64 c0, i64 c1, i64 c2, i64 c3,
+                                                          int valid, float* v) {
+  const void* p = a.in_ptr[k];
+  const i64 base = c0 * a.in_stride[k][0] + c1 * a.in_stride[k][1] + c2 * a.in_stride[k][2];
+  const i64 s3 = a.in_stride[k][3];
+  if (EW_V == 8 && ((a.in_vec8 >> k) & 1u)) {
+    ld8<DT>(p, base + c3, v);
+  } else if ((a.in_vec4 >> k) & 1u) {
+    ld4<DT>(p, base + c3, v);
+    if (EW_V == 8) {
+      if (valid > 4) ld4<DT>(p, base + c3 + 4, v + 4);
+      else for (int j = 4; j < EW_V; ++j) v[j] = 0.0f;
+    }
+  } else if (s3 == 0) {
+    const float x = ld1<DT>(p, base);
+    for (int j = 0; j < EW_V; ++j) v[j] = x;
+  } else {
+    for (int j = 0; j < EW_V; ++j) v[j] = j < valid ? ld1<DT>(p, base + (c3 + j) * s3) : 0.0f;
+  }
+}
+template <int DT> __device__ __forceinline__ void store_op(const EwJitArgs& a, int k, i64 off, int valid,
+                                                           const float* v) {
+  void* p = a.out_ptr[k];
+  if (EW_V == 8 && ((a.out_vec8 >> k) & 1u)) {
+    st8<DT>(p, off, v);
+  } else if ((a.out_vec4 >> k) & 1u) {
+    st4<DT>(p, off, v);
+    if (EW_V == 8 && valid > 4) st4<DT>(p, off + 4, v + 4);
+  } else {
+    for (int j = 0; j < EW_V; ++j)
+      if (j < valid) st1<DT>(p, off + j, v[j]);
+  }
+}
+)JIT";
+
+// Element expression of one instruction in terms of x = r[a][j], y = r[b][j], z = r[c][j].
+const char* expr_of(int op) {
+  switch (op) {
+    case IHIP_EW_MOV: return "x";
+    case IHIP_EW_ADD: return "x + y";
+    case IHIP_EW_SUB: return "x - y";
+    case IHIP_EW_MUL: return "x * y";
+    case IHIP_EW_DIV: return "x / y";
+    case IHIP_EW_MAX: return "__builtin_elementwise_maximum(x, y)";
+    case IHIP_EW_MIN: return "__builtin_elementwise_minimum(x, y)";
+    case IHIP_EW_NE: return "x != y ? 1.0f : 0.0f";
+    case IHIP_EW_LT: return "x < y ? 1.0f : 0.0f";
+    case IHIP_EW_LE: return "x <= y ? 1.0f : 0.0f";
+    case IHIP_EW_GT: return "x > y ? 1.0f : 0.0f";
+    case IHIP_EW_GE: return "x >= y ? 1.0f : 0.0f";
+    case IHIP_EW_EQ: return "x == y ? 1.0f : 0.0f";
+    case IHIP_EW_AND: return "(x != 0.0f && y != 0.0f) ? 1.0f : 0.0f";
+    case IHIP_EW_OR: return "(x != 0.0f || y != 0.0f) ? 1.0f : 0.0f";
+    case IHIP_EW_NOT: return "x == 0.0f ? 1.0f : 0.0f";
+    case IHIP_EW_RELU: return "__builtin_elementwise_maximum(x, 0.0f)";
+    case IHIP_EW_EXP: return "expf(x)";
+    case IHIP_EW_RSQRT: return "1.0f / sqrtf(x)";
+    case IHIP_EW_ABS: return "fabsf(x)";
+    case IHIP_EW_FLOOR: return "floorf(x)";
+    case IHIP_EW_NEG: return "-x";
+    case IHIP_EW_WHERE: return "x != 0.0f ? y : z";
+    case IHIP_EW_CAST_F16: return "h2f(f2h(x))";
+    case IHIP_EW_CAST_BF16: return "b2f(f2b(x))";
+    case IHIP_EW_CAST_BOOL: return "x != 0.0f ? 1.0f : 0.0f";
+    case IHIP_EW_CAST_I32: return "truncf(x)";
+    default: return nullptr;
+  }
+}
+
+std::string fmt(const char* f, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, f);
+  vsnprintf(buf, sizeof(buf), f, ap);
+  va_end(ap);
+  return buf;
+}
+
+}  // namespace
+
+// Kernel source of a validated program (registers < IHIP_EW_MAX_REGS, operands in range).
+// Elements per lane: 8 when every operand is 16-bit or narrower (one 16-byte access each),
+// else 4 (16-byte f32/i32 accesses).
+int ew_jit_width(int n_inputs, const int* in_dt, int n_outputs, const int* out_dt) {
+  for (int k = 0; k < n_inputs; ++k)
+    if (in_dt[k] == IHIP_DT_F32 || in_dt[k] == IHIP_DT_I32) return 4;
+  for (int k = 0; k < n_outputs; ++k)
+    if (out_dt[k] == IHIP_DT_F32 || out_dt[k] == IHIP_DT_I32) return 4;
+  return 8;
+}
+
+std::string ew_jit_source(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
+                          const int* out_dt) {
+  const int V = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt);
+  std::string s = fmt("#define EW_V %d\n", V);
+  s += kPrelude;
+  s += "extern \"C\" __global__ __launch_bounds__(256) void ihip_ew_jit(const EwJitArgs a) {\n"
+       "  const i64 D1 = a.shape[1], D2 = a.shape[2], D3 = a.shape[3];\n"
+       "  for (i64 row = blockIdx.y; row < a.rows; row += gridDim.y) {\n"
+       "    i64 c0 = 0, c1 = 0, c2 = row;\n"
+       "    if (row >= D2) { c2 = row % D2; const i64 t = row / D2; c1 = t % D1; c0 = t / D1; }\n"
+       "    for (i64 vec = (i64)blockIdx.x * blockDim.x + threadIdx.x; vec < a.nvec; vec += (i64)gridDim.x * blockDim.x) {\n"
+       "      const i64 c3 = vec * EW_V;\n"
+       "      const int valid = D3 - c3 < EW_V ? (int)(D3 - c3) : EW_V;\n"
+       "      float r[8][EW_V];\n";
+  for (int pc = 0; pc < n_code; ++pc) {
+    const ihip_ew_instr& in = code[pc];
+    switch (in.op) {
+      case IHIP_EW_LOAD:
+        s += fmt("      load_op<%d>(a, %d, c0, c1, c2, c3, valid, r[%d]);\n", in_dt[in.a], in.a, in.dst);
+        break;
+      case IHIP_EW_IMM:
+        s += fmt("      for (int j = 0; j < EW_V; ++j) r[%d][j] = __builtin_bit_cast(float, %uu);\n", in.dst,
+                 __builtin_bit_cast(uint32_t, in.imm));
+        break;
+      case IHIP_EW_IOTA:
+        s += fmt("      for (int j = 0; j < EW_V; ++j) r[%d][j] = (float)(%s);\n", in.dst,
+                 in.a == 0 ? "c0" : in.a == 1 ? "c1" : in.a == 2 ? "c2" : "c3 + j");
+        break;
+      case IHIP_EW_STORE:
+        s += fmt("      store_op<%d>(a, %d, row * D3 + c3, valid, r[%d]);\n", out_dt[in.b], in.b, in.a);
+        break;
+      default: {
+        // read only the operands the opcode uses (the others may be unwritten registers)
+        const bool two = in.op >= IHIP_EW_ADD && in.op <= IHIP_EW_OR;
+        const bool three = in.op == IHIP_EW_WHERE;
+        s += fmt("      { float t[EW_V]; for (int j = 0; j < EW_V; ++j) { const float x = r[%d][j];", in.a);
+        if (two || three) s += fmt(" const float y = r[%d][j];", in.b);
+        if (three) s += fmt(" const float z = r[%d][j];", in.c);
+        s += fmt(" t[j] = %s; } for (int j = 0; j < EW_V; ++j) r[%d][j] = t[j]; }\n", expr_of(in.op), in.dst);
+      }
+    }
+  }
+  s += "    }\n  }\n}\n";
+  return s;
+}
+
+namespace {
+
+// One specialised program: its code object, and the module loaded from it on each device.
+struct JitEntry {
+  std::string object;  // code object from hiprtc; empty when compilation failed
+  std::string error;
+  std::unordered_map<int, hipFunction_t> fn;  // device -> kernel
+};
+
+std::mutex g_jit_mu;
+std::unordered_map<std::string, JitEntry> g_jit;  // key: generated source
+
+void compile(const std::string& src, JitEntry& e) {
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, src.c_str(), "ihip_ew_jit.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
+    e.error = "hiprtcCreateProgram failed";
+    return;
+  }
+  // gfx950 only; packed-FP32 instructions stay off as in the library's own kernels.
+  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  const hiprtcResult r = hiprtcCompileProgram(prog, 6, opts);
+  if (r != HIPRTC_SUCCESS) {
+    size_t n = 0;
+    hiprtcGetProgramLogSize(prog, &n);
+    std::string log(n, '\0');
+    if (n) hiprtcGetProgramLog(prog, &log[0]);
+    e.error = std::string("hiprtc: ") + hiprtcGetErrorString(r) + ": " + log.substr(0, 300);
+    hiprtcDestroyProgram(&prog);
+    return;
+  }
+  size_t n = 0;
+  hiprtcGetCodeSize(prog, &n);
+  e.object.assign(n, '\0');
+  hiprtcGetCode(prog, &e.object[0]);
+  hiprtcDestroyProgram(&prog);
+}
+
+// Cache entry of a source, compiled on first request (caller holds g_jit_mu).
+JitEntry& entry(const std::string& src) {
+  auto it = g_jit.find(src);
+  if (it == g_jit.end()) {
+    it = g_jit.emplace(src, JitEntry{}).first;
+    compile(src, it->second);
+  }
+  return it->second;
+}
+
+}  // namespace
+
+// Compile (once) the native code of a validated program for the given operand types; no
+// device is needed.  Returns false with *why set when compilation fails.
+bool prepare_elementwise_jit(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
+                             const int* out_dt, std::string* why) {
+  const std::string src = ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt);
+  std::lock_guard<std::mutex> lock(g_jit_mu);
+  JitEntry& e = entry(src);
+  if (!e.error.empty() && why) *why = e.error;
+  return e.error.empty();
+}
+
+// Launch the specialised kernel of a validated program; compiles on first use.  Returns
+// hipErrorNotSupported with *why set when the program cannot be compiled.
+hipError_t launch_elementwise_jit(const ihip_ew_instr* code, int n_code, const ihip_ew_operand* inputs, int n_inputs,
+                                  const ihip_ew_operand* outputs, int n_outputs, const int64_t (&shape)[4],
+                                  hipStream_t s, std::string* why) {
+  EwJitArgs a{};
+  for (int d = 0; d < 4; ++d) a.shape[d] = shape[d];
+  int in_dt[IHIP_EW_MAX_INPUTS] = {}, out_dt[IHIP_EW_MAX_OUTPUTS] = {};
+  for (int k = 0; k < n_inputs; ++k) in_dt[k] = inputs[k].dtype;
+  for (int k = 0; k < n_outputs; ++k) out_dt[k] = outputs[k].dtype;
+  const int V = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt);
+  a.rows = shape[0] * shape[1] * shape[2];
+  a.nvec = (shape[3] + V - 1) / V;
+  if (a.rows == 0 || a.nvec == 0) return hipSuccess;
+  const auto esize = [](int dt) -> int64_t { return dt == IHIP_DT_F32 || dt == IHIP_DT_I32 ? 4 : dt == IHIP_DT_BOOL ? 1 : 2; };
+  // W-element vectors need every row to start at a multiple of W elements and an aligned base.
+  const auto vec_ok = [&](const void* ptr, const int64_t* st, int dt, int64_t w) {
+    const bool rows = (st == nullptr) || ((st[0] % w == 0 || shape[0] == 1) && (st[1] % w == 0 || shape[1] == 1) &&
+                                          (st[2] % w == 0 || shape[2] == 1) && st[3] == 1);
+    return shape[3] % w == 0 && rows && reinterpret_cast<uintptr_t>(ptr) % (w * esize(dt)) == 0;
+  };
+  for (int k = 0; k < n_inputs; ++k) {
+    a.in_ptr[k] = inputs[k].ptr;
+    for (int d = 0; d < 4; ++d) a.in_stride[k][d] = inputs[k].stride[d];
+    if (V == 8 && vec_ok(inputs[k].ptr, inputs[k].stride, in_dt[k], 8)) a.in_vec8 |= 1u << k;
+    else if (vec_ok(inputs[k].ptr, inputs[k].stride, in_dt[k], 4)) a.in_vec4 |= 1u << k;
+  }
+  for (int k = 0; k < n_outputs; ++k) {
+    a.out_ptr[k] = const_cast<void*>(outputs[k].ptr);
+    if (V == 8 && vec_ok(outputs[k].ptr, nullptr, out_dt[k], 8)) a.out_vec8 |= 1u << k;
+    else if (vec_ok(outputs[k].ptr, nullptr, out_dt[k], 4)) a.out_vec4 |= 1u << k;
+  }
+  int dev = 0;
+  hipError_t he = hipGetDevice(&dev);
+  if (he != hipSuccess) return he;
+  const std::string src = ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt);
+  hipFunction_t fn = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_jit_mu);
+    JitEntry& e = entry(src);
+    if (!e.error.empty()) {
+      if (why) *why = e.error;
+      return hipErrorNotSupported;
+    }
+    auto f = e.fn.find(dev);
+    if (f == e.fn.end()) {  // first launch on this device: load the module (kept until the process ends)
+      hipModule_t mod = nullptr;
+      he = hipModuleLoadData(&mod, e.object.data());
+      if (he == hipSuccess) he = hipModuleGetFunction(&fn, mod, "ihip_ew_jit");
+      if (he != hipSuccess) return he;
+      e.fn.emplace(dev, fn);
+    } else {
+      fn = f->second;
+    }
+  }
+  const int64_t bx = (a.nvec + 255) / 256;
+  const unsigned gx = static_cast<unsigned>(bx < 1024 ? bx : 1024);
+  int64_t gy = (4096 + gx - 1) / gx;
+  if (gy > a.rows) gy = a.rows;
+  if (gy > 65535) gy = 65535;
+  void* params[] = {&a};
+  return hipModuleLaunchKernel(fn, gx, static_cast<unsigned>(gy), 1, 256, 1, 1, 0, s, params, nullptr);
+}
+
+}  // namespace ihip

@@ -12,7 +12,8 @@ list to call it with (``call_args``).
 Kernel families are recognised structurally (``patterns.py``), in this order:
 GEMM (+bias, +ReLU, incl. ``matmul{epilogue}``), reduce_any (incl.
 ``const, ne, reduce_any``), softmax (op or expanded chain), LayerNorm
-(chain with any output names), bias + GELU-tanh + axpy, row reduce_sum/max.
+(chain with any output names), bias + GELU-tanh + axpy, row reduce_sum/max,
+and last any other element-wise chain (a register program, ``ewprogram.py``).
 """
 
 from __future__ import annotations
@@ -23,6 +24,8 @@ from typing import Any, Dict, List, Mapping, Optional, Tuple
 from .ir import IntentFunction, ScheduleSketch, as_intent, resolve_shape
 from .macros import GELU_CUBIC, GELU_NEG_2_SQRT_2_OVER_PI, expand_macros
 from .opset import HIP_SUPPORTED_OPS
+from .ewprogram import BINARY as EW_BINARY, DTYPE_CODE as EW_DTYPE_CODE, UNARY as EW_UNARY
+from .ewprogram import EwCompileError, compile_elementwise
 from .patterns import ExprBuilder, PatternError, close, unify
 
 
@@ -47,7 +50,8 @@ class HipLoweredKernel:
     output_names: List[str]
     bindings: Dict[str, Any]
     # Arguments of the C call in order: ("tensor", name) | ("i64", v) | ("i32", v) | ("f32", v)
-    # | ("null", None) | ("scratch_f32", n): a device temporary of n floats the runtime provides.
+    # | ("null", None) | ("scratch_f32", n): a device temporary of n floats the runtime provides
+    # | ("ew_program", EwProgram): the program, operand table and shape of ihip_elementwise_program.
     call_args: Tuple[Tuple[str, Any], ...] = field(default_factory=tuple)
 
 
@@ -305,7 +309,68 @@ def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
                              ("i32", 0 if kind == "rsum" else 1)))
 
 
-_MATCHERS = (_match_gemm, _match_reduce_any, _match_softmax, _match_layernorm, _match_gelu_axpy, _match_row_reduce)
+_EW_KINDS = frozenset({"in", "const", "bcast", "transpose", "iota", "cast", "where"}) | frozenset(EW_BINARY) | frozenset(
+    EW_UNARY)
+
+
+def _is_elementwise(tree: Any) -> bool:
+    if not isinstance(tree, tuple) or not tree or tree[0] not in _EW_KINDS:
+        return False
+    k = tree[0]
+    if k in ("in", "const", "iota"):
+        return True
+    if k in ("bcast", "transpose", "cast"):
+        return _is_elementwise(tree[1])
+    return all(_is_elementwise(t) for t in tree[1:])
+
+
+def _leaves(tree: Any, out: List[str]) -> None:
+    if isinstance(tree, tuple) and tree:
+        if tree[0] == "in":
+            if tree[1] not in out:
+                out.append(tree[1])
+            return
+        for t in tree[1:]:
+            _leaves(t, out)
+
+
+def _match_elementwise(c: _Ctx) -> Optional[HipLoweredKernel]:
+    """Any remaining chain of element-wise ops: one register program on ihip_elementwise_program
+    (the reference's fused element-wise lowering, intentir_to_cuda.py:229-534, dispatched at :2170-2199)."""
+    outs = list(c.fn.outputs)
+    if not all(_is_elementwise(c.outs[o].tree) for o in outs):
+        return None
+    shp = c.shape(outs[0])
+    for o in outs:
+        if c.shape(o) != shp:
+            raise HipLoweringError(f"element-wise outputs of different shapes: {outs}")
+    names: List[str] = []
+    for o in outs:
+        _leaves(c.outs[o].tree, names)
+    for n in names + outs:
+        if c.dtype(n) not in EW_DTYPE_CODE:
+            raise HipLoweringError(f"element-wise program does not take {c.dtype(n)} ({n})")
+    try:
+        prog = compile_elementwise([(o, c.outs[o].tree) for o in outs], shp, {n: c.shape(n) for n in names},
+                                   {n: c.eb.get(n).unit for n in names})
+    except EwCompileError as e:
+        raise HipLoweringError(f"element-wise chain of {c.fn.name}: {e}") from e
+    used = []
+    for n, _ in prog.inputs:
+        if n not in used:
+            used.append(n)
+    d3 = shp[-1] if shp else 1
+    rows = 1
+    for d in shp[:-1]:
+        rows *= d
+    gx = max(1, min(1024, _cdiv(_cdiv(d3, 4), 256)))
+    launch = HipLaunch((gx, max(1, min(rows, 65535, _cdiv(4096, gx))), 1), (256, 1, 1), 0)
+    return HipLoweredKernel(c.fn.name, "ihip_elementwise_program", c.io(used + outs), launch, outs, dict(c.b),
+                            (("ew_program", prog),))
+
+
+_MATCHERS = (_match_gemm, _match_reduce_any, _match_softmax, _match_layernorm, _match_gelu_axpy, _match_row_reduce,
+             _match_elementwise)
 
 
 def lower_intent_to_hip_kernel(intent, *, shape_bindings: Mapping[str, Any],

@@ -29,12 +29,12 @@ MACRO_OPS: frozenset = frozenset({"upsample_bicubic2d_aa", "gelu_tanh"})
 SUPPORTED_OPS: frozenset = CORE_OPS | EXPERIMENTAL_OPS | MACRO_OPS
 
 # Shape-only ops: no arithmetic, the backend folds them into index maps.
-VIEW_OPS: frozenset = frozenset({"identity", "reshape", "layout_cast", "broadcast_in_dim"})
+VIEW_OPS: frozenset = frozenset({"identity", "reshape", "layout_cast", "broadcast_in_dim", "transpose"})
 
 # Element-wise ops the fused chain kernels evaluate.
 ELEMENTWISE_OPS: frozenset = frozenset({
     "const", "add", "sub", "mul", "div", "max", "min", "exp", "relu", "rsqrt", "abs", "floor",
-    "ne", "lt", "le", "gt", "ge", "and", "or", "not", "where", "cast",
+    "ne", "lt", "le", "gt", "ge", "and", "or", "not", "where", "cast", "iota",
 }) | VIEW_OPS
 
 HIP_SUPPORTED_OPS: frozenset = ELEMENTWISE_OPS | frozenset({

@@ -217,6 +217,23 @@ class ExprBuilder:
         if name in UNARY:
             a = self.get(ins[0])
             return Val((name, a.tree), a.rank, a.unit)
+        if name == "cast":  # interpreter.py:270-273
+            a = self.get(ins[0])
+            return Val(("cast", a.tree, str(at.get("to"))), a.rank, a.unit)
+        if name == "where":  # interpreter.py:292-302
+            return self._where(ins)
+        if name == "transpose":  # interpreter.py:258-263
+            a = self.get(ins[0])
+            perm = tuple(int(p) for p in at.get("perm") or [])
+            if sorted(perm) != list(range(a.rank)):
+                raise PatternError(f"transpose perm {perm} does not fit rank {a.rank}")
+            return Val(("transpose", a.full(), perm), a.rank)
+        if name == "iota":  # interpreter.py:274-283
+            shp = at.get("shape") or []
+            axis = int(at.get("axis", 0))
+            if not 0 <= axis < len(shp):
+                raise PatternError(f"iota axis {axis} out of range")
+            return Val(("iota", axis, len(shp)), len(shp))
         if name in ("reduce_sum", "reduce_max", "reduce_any"):
             a = self.get(ins[0])
             axes = self._norm_axes(reduce_dims_attr(at), a.rank)
@@ -239,6 +256,26 @@ class ExprBuilder:
             ep = at.get("epilogue")
             return self._epilogue(ep, mm) if ep else mm
         raise PatternError(f"op {name} has no structural form")
+
+    def _where(self, ins: Sequence[str]) -> Val:
+        """np.where after the interpreter's pairwise name-based alignment: 1-D operands go
+        on the axis of a full-rank operand whose declared symbol they name, else the
+        trailing axis; scalars broadcast."""
+        if len(ins) != 3:
+            raise PatternError("where takes (cond, x, y)")
+        vals = [self.get(n) for n in ins]
+        rank = max(v.rank for v in vals)
+        big = next(n for n, v in zip(ins, vals) if v.rank == rank)
+        trees = []
+        for n, v in zip(ins, vals):
+            if v.rank == rank or v.rank == 0:
+                trees.append(v.full())
+            elif v.rank == 1 and not v.unit:
+                ax = self._match_axis(n, big, rank)
+                trees.append(("bcast", v.tree, (rank - 1 if ax is None else ax,), rank))
+            else:
+                raise PatternError("where operands of mixed rank > 1")
+        return Val(("where", *trees), rank)
 
     def _epilogue(self, node: Any, x: Val) -> Val:
         """matmul epilogue trees (interpreter.py:567-591): plain numpy broadcasting."""

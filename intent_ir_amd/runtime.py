@@ -45,7 +45,44 @@ SIGNATURES: Dict[str, Tuple[Any, Tuple[Any, ...]]] = {
     "ihip_layernorm_rows_f16": (_I32, (_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _P)),
     "ihip_bias_gelu_tanh_axpy_bf16": (_I32, (_P, _P, _P, _I64, _I64, _F32, _P)),
     "ihip_gemm_bf16_bias_relu": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _P)),
+    "ihip_elementwise_program": (_I32, (_P, _I32, _P, _I32, _P, _I32, _P, _I32, _P)),
+    "ihip_elementwise_mode": (_I32, (_I32,)),
+    "ihip_elementwise_prepare": (_I32, (_P, _I32, _P, _I32, _P, _I32)),
 }
+EW_MODE_AUTO, EW_MODE_INTERP, EW_MODE_NATIVE = 0, 1, 2
+
+
+class EwInstr(ctypes.Structure):
+    """ihip_ew_instr (include/intentir_hip.h)."""
+    _fields_ = [("op", ctypes.c_uint8), ("dst", ctypes.c_uint8), ("a", ctypes.c_uint8), ("b", ctypes.c_uint8),
+                ("c", ctypes.c_uint8), ("reserved", ctypes.c_uint8 * 3), ("imm", ctypes.c_float)]
+
+
+class EwOperand(ctypes.Structure):
+    """ihip_ew_operand (include/intentir_hip.h)."""
+    _fields_ = [("ptr", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("stride", ctypes.c_int64 * 4)]
+
+
+def ew_program_args(prog, ptrs: Mapping[str, int], dtypes: Mapping[str, str]) -> list:
+    """ctypes arguments of ihip_elementwise_program (minus the stream) for an EwProgram."""
+    from .ewprogram import DTYPE_CODE  # noqa: PLC0415
+
+    code = (EwInstr * len(prog.code))()
+    for i, (op, d, a, b, c, imm) in enumerate(prog.code):
+        code[i].op, code[i].dst, code[i].a, code[i].b, code[i].c, code[i].imm = op, d, a, b, c, imm
+    ins = (EwOperand * max(1, len(prog.inputs)))()
+    for i, (name, st) in enumerate(prog.inputs):
+        ins[i].ptr, ins[i].dtype = ptrs[name], DTYPE_CODE[dtypes[name]]
+        for j in range(4):
+            ins[i].stride[j] = int(st[j])
+    outs = (EwOperand * len(prog.outputs))()
+    for i, name in enumerate(prog.outputs):
+        outs[i].ptr, outs[i].dtype = ptrs[name], DTYPE_CODE[dtypes[name]]
+    shape = (ctypes.c_int64 * max(1, len(prog.shape)))(*[int(d) for d in prog.shape])
+    return [ctypes.cast(code, _P), _I32(len(prog.code)), ctypes.cast(ins, _P), _I32(len(prog.inputs)),
+            ctypes.cast(outs, _P), _I32(len(prog.outputs)), ctypes.cast(shape, _P), _I32(len(prog.shape)),
+            (code, ins, outs, shape)]
 ABI_VERSION = 1
 
 _lock = threading.Lock()
@@ -134,11 +171,16 @@ def _check_buffer(name: str, t, dtype: str, shape: Sequence[int]) -> None:
         raise HipRuntimeError(f"{name}: tensor must be contiguous")
 
 
-def _ctype_args(call_args: Iterable[Tuple[str, Any]], buffers: Mapping[str, Any], scratch: list):
+def _ctype_args(call_args: Iterable[Tuple[str, Any]], buffers: Mapping[str, Any], scratch: list,
+                dtypes: Optional[Mapping[str, str]] = None):
     torch = _torch()
     out = []
     for kind, v in call_args:
-        if kind == "tensor":
+        if kind == "ew_program":
+            args = ew_program_args(v, {n: buffers[n].data_ptr() for n in buffers}, dtypes or {})
+            scratch.append(args.pop())  # keep the ctypes arrays alive through the call
+            out.extend(args)
+        elif kind == "tensor":
             out.append(_P(buffers[v].data_ptr()))
         elif kind == "i64":
             out.append(_I64(int(v)))
@@ -175,10 +217,11 @@ def launch_lowered(lowered, buffers: Mapping[str, Any], stream=None) -> None:
         _check_buffer(n, buffers[n], spec["dtype"], shapes[n])
     s = stream if stream is not None else torch.cuda.current_stream()
     scratch: list = []
-    args = _ctype_args(lowered.call_args, buffers, scratch)
+    dtypes = {n: spec["dtype"] for n, spec in lowered.io_spec["tensors"].items()}
+    args = _ctype_args(lowered.call_args, buffers, scratch, dtypes)
     call(lowered.kernel_id, *args, _P(s.cuda_stream))
-    if scratch:
-        s.synchronize()  # temporaries must outlive the kernel
+    if any(isinstance(t, torch.Tensor) for t in scratch):
+        s.synchronize()  # device temporaries must outlive the kernel (host arrays are copied at launch)
 
 
 def run_hip_kernel(*, kernel_name: str, kernel_id: str, io_spec: Mapping[str, Any], launch: Any,
@@ -220,5 +263,5 @@ def run_lowered(lowered, inputs_np: Mapping[str, np.ndarray]) -> Dict[str, np.nd
                           output_names=lowered.output_names, call_args=lowered.call_args)
 
 
-__all__ = ["HipRuntimeError", "SIGNATURES", "LIB_PATH", "load_library", "call", "launch_lowered", "run_hip_kernel",
+__all__ = ["HipRuntimeError", "SIGNATURES", "EwInstr", "EwOperand", "ew_program_args", "LIB_PATH", "load_library", "call", "launch_lowered", "run_hip_kernel",
            "run_lowered", "to_device", "to_host", "torch_dtype", "tensor_shapes"]
