@@ -89,6 +89,13 @@ int ihip_bias_gelu_tanh_axpy_bf16(const uint16_t* x, const uint16_t* bias, uint1
 int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                              int64_t N, int64_t K, int relu, void* stream);
 
+/* The same with matmul's transpose flags (verify/interpreter.py:507-520): when transpose_a,
+ * A is given as [K, M] and the product uses its transpose; when transpose_b, B is given as
+ * [N, K].  Every layout runs the same MFMA schedule and accumulates in the same order, so a
+ * transposed operand gives bit-identical C. */
+int ihip_gemm_bf16_bias_relu_t(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                               int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Generic element-wise program: any chain of element-wise ops over inputs that
  * broadcast, transpose or repeat along the axes of one iteration space (rank <= 4).

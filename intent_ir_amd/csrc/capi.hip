@@ -27,7 +27,7 @@ hipError_t launch_layernorm_rows_f16(const uint16_t*, const uint16_t*, const uin
 hipError_t launch_bias_gelu_axpy_bf16(const uint16_t*, const uint16_t*, uint16_t*, int64_t, int64_t, float,
                                       hipStream_t);
 hipError_t launch_gemm_bf16_bias_relu(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t,
-                                      int64_t, int, hipStream_t);
+                                      int64_t, bool, bool, int, hipStream_t);
 hipError_t launch_elementwise_program(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*,
                                       int, const int64_t (&)[4], hipStream_t);
 hipError_t launch_elementwise_jit(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*, int,
@@ -200,14 +200,20 @@ int ihip_bias_gelu_tanh_axpy_bf16(const uint16_t* x, const uint16_t* bias, uint1
                 "bias_gelu_tanh_axpy_bf16");
 }
 
-int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
-                             int64_t N, int64_t K, int relu, void* stream) {
+int ihip_gemm_bf16_bias_relu_t(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                               int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, void* stream) {
   IHIP_REQUIRE(numel2(M, K) >= 0 && numel2(K, N) >= 0 && numel2(M, N) >= 0,
                "gemm_bf16_bias_relu: invalid shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
   IHIP_REQUIRE(M == 0 || N == 0 || C != nullptr, "gemm_bf16_bias_relu: C is null");
   IHIP_REQUIRE(M == 0 || N == 0 || K == 0 || (A != nullptr && B != nullptr), "gemm_bf16_bias_relu: A or B is null");
-  return finish(ihip::launch_gemm_bf16_bias_relu(A, B, bias, C, M, N, K, relu, static_cast<hipStream_t>(stream)),
+  return finish(ihip::launch_gemm_bf16_bias_relu(A, B, bias, C, M, N, K, transpose_a != 0, transpose_b != 0, relu,
+                                                 static_cast<hipStream_t>(stream)),
                 "gemm_bf16_bias_relu");
+}
+
+int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                             int64_t N, int64_t K, int relu, void* stream) {
+  return ihip_gemm_bf16_bias_relu_t(A, B, bias, C, M, N, K, 0, 0, relu, stream);
 }
 
 int ihip_elementwise_program(const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,

@@ -1,5 +1,6 @@
-// C = relu?(A @ B + bias?) with A [M,K] bf16, B [K,N] bf16 (both row-major),
-// bias f32 [N], f32 accumulation on CDNA4 MFMA, C bf16 (RNE) — any shape.
+// C = relu?(op(A) @ op(B) + bias?) with A [M,K] (or [K,M] transposed) and B [K,N] (or
+// [N,K] transposed), bf16 row-major, bias f32 [N], f32 accumulation on CDNA4 MFMA,
+// C bf16 (RNE) — any shape.
 //
 // Entry point of the GEMM family: full 256x256 tiles with K a multiple of the fast
 // path's K step and 16-byte aligned operands go to gemm_fast.hip; every other shape
@@ -11,7 +12,9 @@
 //  * B is transposed on the way into LDS: each thread loads an 8(k) x 8(n) block and
 //    writes eight 16-byte [n][k] rows;
 //  * loads are element-wise with zero fill outside [M, N, K] and stores element-wise,
-//    so any M, N, K and any alignment are handled.
+//    so any M, N, K and any alignment are handled;
+//  * a transposed operand swaps roles: A given as [K,M] is loaded like B and transposed into
+//    the [m][k] tile, B given as [N,K] is loaded like A straight into the [n][k] tile.
 #include "common.hpp"
 
 namespace ihip {
@@ -101,7 +104,27 @@ __device__ __forceinline__ void store_bt(uint16_t* lds_b, int tid, const uint4 (
 
 __device__ __forceinline__ float relu_np(float v) { return v < 0.0f ? 0.0f : v; }  // keeps -0.0 and NaN
 
-template <bool kGuard>
+// One K slice of both operands into registers, then into the [m][k] / [n][k] LDS tiles.
+template <bool kGuard, bool kTA, bool kTB>
+__device__ __forceinline__ void load_slice(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, int64_t M,
+                                           int64_t N, int64_t K, int64_t m0, int64_t n0, int64_t k0, int tid,
+                                           uint4 (&ra)[8], uint4 (&rb)[8]) {
+  if (!kTA) load_a<kGuard>(A, M, K, m0, k0, tid, ra);
+  else load_b<kGuard>(A, K, M, k0, m0, tid, ra);
+  if (!kTB) load_b<kGuard>(B, K, N, k0, n0, tid, rb);
+  else load_a<kGuard>(B, N, K, n0, k0, tid, rb);
+}
+
+template <bool kTA, bool kTB>
+__device__ __forceinline__ void store_slice(uint16_t* lds_a, uint16_t* lds_b, int tid, const uint4 (&ra)[8],
+                                            const uint4 (&rb)[8]) {
+  if (!kTA) store_a(lds_a, tid, ra);
+  else store_bt(lds_a, tid, ra);
+  if (!kTB) store_bt(lds_b, tid, rb);
+  else store_a(lds_b, tid, rb);
+}
+
+template <bool kGuard, bool kTA, bool kTB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                 const float* __restrict__ bias, uint16_t* __restrict__ C, int64_t M, int64_t N,
@@ -129,10 +152,8 @@ void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* 
   const int KT = static_cast<int>((K + kBK - 1) / kBK);
   uint4 ra[8], rb[8];
   if (KT > 0) {
-    load_a<kGuard>(A, M, K, m0, 0, tid, ra);
-    load_b<kGuard>(B, K, N, 0, n0, tid, rb);
-    store_a(lds, tid, ra);
-    store_bt(lds + kTileHalves, tid, rb);
+    load_slice<kGuard, kTA, kTB>(A, B, M, N, K, m0, n0, 0, tid, ra, rb);
+    store_slice<kTA, kTB>(lds, lds + kTileHalves, tid, ra, rb);
   }
   __syncthreads();
 
@@ -141,10 +162,7 @@ void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* 
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < KT;
-    if (more) {
-      load_a<kGuard>(A, M, K, m0, static_cast<int64_t>(kt + 1) * kBK, tid, ra);
-      load_b<kGuard>(B, K, N, static_cast<int64_t>(kt + 1) * kBK, n0, tid, rb);
-    }
+    if (more) load_slice<kGuard, kTA, kTB>(A, B, M, N, K, m0, n0, static_cast<int64_t>(kt + 1) * kBK, tid, ra, rb);
     const uint16_t* la = lds + cur * 2 * kTileHalves + a_off;
     const uint16_t* lb = lds + cur * 2 * kTileHalves + kTileHalves + b_off;
 #pragma unroll
@@ -163,8 +181,7 @@ void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* 
     }
     if (more) {
       uint16_t* nxt = lds + (cur ^ 1) * 2 * kTileHalves;
-      store_a(nxt, tid, ra);
-      store_bt(nxt + kTileHalves, tid, rb);
+      store_slice<kTA, kTB>(nxt, nxt + kTileHalves, tid, ra, rb);
     }
     __syncthreads();
   }
@@ -202,16 +219,27 @@ void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* 
 
 bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* C);
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
-                            int64_t K, int relu, hipStream_t s);
+                            int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s);
+
+template <bool kTA, bool kTB>
+static void launch_guarded(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
+                           int64_t K, int relu, int tm, int tn, hipStream_t s) {
+  gemm_bf16_bias_relu_kernel<true, kTA, kTB><<<dim3(static_cast<unsigned>(tm) * tn), dim3(256), 0, s>>>(
+      A, B, bias, C, M, N, K, relu, tm, tn);
+}
 
 hipError_t launch_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
-                                      int64_t N, int64_t K, int relu, hipStream_t s) {
+                                      int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu,
+                                      hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (gemm_fast_fits(M, N, K, A, B, C)) return launch_gemm_fast(A, B, bias, C, M, N, K, relu, s);
+  if (gemm_fast_fits(M, N, K, A, B, C)) return launch_gemm_fast(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
   const int64_t tm = (M + kBM - 1) / kBM, tn = (N + kBN - 1) / kBN;
   if (tm * tn > 0x7fffffffLL) return hipErrorInvalidValue;
-  gemm_bf16_bias_relu_kernel<true><<<dim3(static_cast<unsigned>(tm * tn)), dim3(256), 0, s>>>(
-      A, B, bias, C, M, N, K, relu, static_cast<int>(tm), static_cast<int>(tn));
+  const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);
+  if (!transpose_a && !transpose_b) launch_guarded<false, false>(A, B, bias, C, M, N, K, relu, itm, itn, s);
+  else if (!transpose_a) launch_guarded<false, true>(A, B, bias, C, M, N, K, relu, itm, itn, s);
+  else if (!transpose_b) launch_guarded<true, false>(A, B, bias, C, M, N, K, relu, itm, itn, s);
+  else launch_guarded<true, true>(A, B, bias, C, M, N, K, relu, itm, itn, s);
   return hipGetLastError();
 }
 

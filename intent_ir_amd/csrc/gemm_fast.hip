@@ -49,13 +49,18 @@ constexpr int kGroupRows = 8;  // tile-rows per raster group
 
 typedef __bf16 bf16x2_pk_t __attribute__((ext_vector_type(2)));
 
-template <int DK, int STAGES>
+// AKM / BKM select the global layout of each operand: false = K-contiguous rows (A [M,K],
+// or B given transposed as [N,K]), true = K-major (A given transposed as [K,M], or B [K,N]).  A K-contiguous operand
+// is staged as [256 rows][DK] and read with ds_read_b128; a K-major one as [DK][256] and read
+// with the transposing ds_read_b64_tr_b16.  Either way the MFMA sees the same fragments, so
+// every layout accumulates in the same order and gives identical results.
+template <int DK, int STAGES, bool AKM = false, bool BKM = true>
 struct FastGemm {
-  static constexpr int kRowA = DK * 2;             // bytes per A row in a stage
-  static constexpr int kChunksA = DK / 8;          // 16-byte chunks per A row
+  static constexpr int kRowA = DK * 2;             // bytes per K-contiguous tile row
+  static constexpr int kChunksA = DK / 8;          // 16-byte chunks per row
   static constexpr int kRowsPerWindow = 256 / kRowA;
-  static constexpr int kStageA = kTile * kRowA;    // bytes
-  static constexpr int kStageB = DK * kTile * 2;   // bytes
+  static constexpr int kStageA = kTile * kRowA;    // bytes per operand tile (either layout)
+  static constexpr int kStageB = DK * kTile * 2;
   static constexpr int kStage = kStageA + kStageB;
   static constexpr int kInstrA = kStageA / 1024 / 4;  // direct-to-LDS instructions per wave per stage
   static constexpr int kInstrB = kStageB / 1024 / 4;
@@ -71,32 +76,50 @@ struct FastGemm {
     return x ^ (((x >> 1) & 1) << 3);
   }
 
-  // Per-lane byte offsets of the copies, identical for every instruction and K slice.
+  // Per-lane offsets: copy offsets (bytes from the copy's scalar base) and fragment LDS
+  // offsets.  K-contiguous operand: off[kk], blocks at a fixed stride; K-major: off[block].
   struct Lane {
     uint32_t a, b;
-    int ra[DK / 16];  // A fragment LDS offsets, per kk
-    int rb[4];        // B fragment LDS offsets, per ni
+    int fa[4], fb[4];
   };
 
-  static __device__ __forceinline__ Lane lane_plan(int64_t N, int64_t K, int wave, int wm, int wn, int lane) {
-    Lane L;
-    // A: instruction j = 4i + wave holds rows j*RPI + lane / CA, slot lane % CA; the swizzle
-    // term (r / RPW) % CA does not depend on i.
-    const int ra0 = wave * kRowsPerInstrA + lane / kChunksA;
-    L.a = 2u * static_cast<uint32_t>((lane / kChunksA) * K + a_slot(lane % kChunksA, ra0) * 8);
-    // B: instruction j holds k-rows 2j, 2j+1; k & 3 == (2*wave + lane/32) & 3 for every i.
-    const int kb = 2 * wave + (lane >> 5);
-    L.b = 2u * static_cast<uint32_t>((lane >> 5) * N + b_logical(lane & 31, kb) * 8);
-    const int r = wm * 128 + (lane & 31);
-#pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk) L.ra[kk] = r * kRowA + a_slot(2 * kk + (lane >> 5), r) * 16;
-    const int g = lane >> 4, i = lane & 15;
-    const int k = (g >> 1) * 8 + (i >> 2);
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
-      const int n = wn * 32 + ni * 64 + (g & 1) * 16 + 4 * (i & 3);
-      L.rb[ni] = kStageA + k * 512 + b_slot(n >> 3, k) * 16 + (n & 7) * 2;
+  // Copy offset of a lane: K-contiguous rows (leading dim K) or K-major rows (leading dim ld).
+  static __device__ __forceinline__ uint32_t copy_off(bool kmajor, int64_t ld, int64_t K, int wave, int lane) {
+    if (!kmajor) {
+      // instruction j = 4i + wave holds rows j*RPI + lane / CA, slot lane % CA; the swizzle
+      // term (r / RPW) % CA does not depend on i
+      const int r0 = wave * kRowsPerInstrA + lane / kChunksA;
+      return 2u * static_cast<uint32_t>((lane / kChunksA) * K + a_slot(lane % kChunksA, r0) * 8);
     }
+    // instruction j holds k-rows 2j, 2j+1; k & 3 == (2*wave + lane/32) & 3 for every i
+    const int kb = 2 * wave + (lane >> 5);
+    return 2u * static_cast<uint32_t>((lane >> 5) * ld + b_logical(lane & 31, kb) * 8);
+  }
+
+  // Fragment offsets of an operand whose wave rows start at `base` with blocks `step` apart.
+  static __device__ __forceinline__ void frag_off(bool kmajor, int region, int base, int step, int lane, int (&o)[4]) {
+    if (!kmajor) {
+      const int r = base + (lane & 31);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) o[kk] = kk < DK / 16 ? region + r * kRowA + a_slot(2 * kk + (lane >> 5), r) * 16 : 0;
+    } else {
+      const int g = lane >> 4, i = lane & 15;
+      const int k = (g >> 1) * 8 + (i >> 2);
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const int x = base + blk * step + (g & 1) * 16 + 4 * (i & 3);
+        o[blk] = region + k * 512 + b_slot(x >> 3, k) * 16 + (x & 7) * 2;
+      }
+    }
+  }
+
+  static __device__ __forceinline__ Lane lane_plan(int64_t M, int64_t N, int64_t K, int wave, int wm, int wn,
+                                                   int lane) {
+    Lane L;
+    L.a = copy_off(AKM, M, K, wave, lane);
+    L.b = copy_off(BKM, N, K, wave, lane);
+    frag_off(AKM, 0, wm * 128, 32, lane, L.fa);
+    frag_off(BKM, kStageA, wn * 32, 64, lane, L.fb);
     return L;
   }
 
@@ -106,19 +129,25 @@ struct FastGemm {
     asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
   }
 
+  // One operand's share of a K slice: tile rows x0.. (K-contiguous) or k-rows k0.. (K-major).
+  template <bool kKMajor, int kInstrOp>
+  static __device__ __forceinline__ void copy_operand(const uint16_t* __restrict__ X, int64_t ld, int64_t K,
+                                                      int64_t x0, int64_t k0, uint32_t dst, int wave, uint32_t off) {
+#pragma unroll
+    for (int i = 0; i < kInstrOp; ++i) {
+      const int j = 4 * i + wave;
+      if (!kKMajor)
+        dma16(X + (x0 + j * kRowsPerInstrA) * K + k0, off, dst + j * 1024);
+      else
+        dma16(X + (k0 + 2 * j) * ld + x0, off, dst + j * 1024);
+    }
+  }
+
   static __device__ __forceinline__ void copy_slice(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-                                                    int64_t N, int64_t K, int64_t m0, int64_t n0, int64_t k0,
-                                                    uint32_t stage, int wave, const Lane& L) {
-#pragma unroll
-    for (int i = 0; i < kInstrA; ++i) {
-      const int j = 4 * i + wave;
-      dma16(A + (m0 + j * kRowsPerInstrA) * K + k0, L.a, stage + j * 1024);
-    }
-#pragma unroll
-    for (int i = 0; i < kInstrB; ++i) {
-      const int j = 4 * i + wave;
-      dma16(B + (k0 + 2 * j) * N + n0, L.b, stage + kStageA + j * 1024);
-    }
+                                                    int64_t M, int64_t N, int64_t K, int64_t m0, int64_t n0,
+                                                    int64_t k0, uint32_t stage, int wave, const Lane& L) {
+    copy_operand<AKM, kInstrA>(A, M, K, m0, k0, stage, wave, L.a);
+    copy_operand<BKM, kInstrB>(B, N, K, n0, k0, stage + kStageA, wave, L.b);
   }
 
   // Wait until at most `pending` slices of this wave's copies are still in flight
@@ -142,16 +171,25 @@ struct FastGemm {
     bf16x8_t a[4], b[4];
   };
 
-  static __device__ __forceinline__ void read(const lds_char_t* st, int kk, const Lane& L, Frag& f) {
+  template <bool kKMajor>
+  static __device__ __forceinline__ void read_operand(const lds_char_t* st, int kk, const int (&o)[4], int blk_stride,
+                                                      bf16x8_t (&f)[4]) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) f.a[mi] = *(const lds_bf16x8_t*)(st + L.ra[kk] + mi * 32 * kRowA);
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
-      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + L.rb[ni] + kk * 16 * 512));
-      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + L.rb[ni] + (kk * 16 + 4) * 512));
-      const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      f.b[ni] = __builtin_bit_cast(bf16x8_t, both);
+    for (int blk = 0; blk < 4; ++blk) {
+      if (!kKMajor) {
+        f[blk] = *(const lds_bf16x8_t*)(st + o[kk] + blk * blk_stride);
+      } else {
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + kk * 16 * 512));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + (kk * 16 + 4) * 512));
+        const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        f[blk] = __builtin_bit_cast(bf16x8_t, both);
+      }
     }
+  }
+
+  static __device__ __forceinline__ void read(const lds_char_t* st, int kk, const Lane& L, Frag& f) {
+    read_operand<AKM>(st, kk, L.fa, 32 * kRowA, f.a);
+    read_operand<BKM>(st, kk, L.fb, 64 * kRowA, f.b);
   }
 
   static __device__ __forceinline__ void mfma(const Frag& f, f32x16_t (&acc)[4][4]) {
@@ -161,14 +199,14 @@ struct FastGemm {
       for (int mi = 0; mi < 4; ++mi)
         acc[ni][mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[ni], f.a[mi], acc[ni][mi], 0, 0, 0);
   }
-
 };
 
-template <int DK, int STAGES, int SCHED>
+template <int DK, int STAGES, int SCHED, bool AKM = false, bool BKM = true>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const float* __restrict__ bias,
-                           uint16_t* __restrict__ C, int64_t N, int64_t K, int relu, int tiles_m, int tiles_n) {
-  using G = FastGemm<DK, STAGES>;
+                           uint16_t* __restrict__ C, int64_t M, int64_t N, int64_t K, int relu, int tiles_m,
+                           int tiles_n) {
+  using G = FastGemm<DK, STAGES, AKM, BKM>;
   static_assert(SCHED == 0 || STAGES >= 3, "the pipelined schedule keeps two slices ahead");
   // SCHED 1 needs KT >= STAGES - 1 (the prologue fills STAGES - 1 stages); the launcher checks.
   __shared__ __attribute__((aligned(1024))) char lds_raw[STAGES * G::kStage];
@@ -193,12 +231,12 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
 
-  const typename G::Lane L = G::lane_plan(N, K, wave, wm, wn, lane);
+  const typename G::Lane L = G::lane_plan(M, N, K, wave, wm, wn, lane);
   const int KT = static_cast<int>(K / DK);
   // Prologue: slices 0 .. STAGES-2 in flight, then slice 0 must land.
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
-    if (s < KT) G::copy_slice(A, B, N, K, m0, n0, static_cast<int64_t>(s) * DK, lds_addr + s * G::kStage, wave, L);
+    if (s < KT) G::copy_slice(A, B, M, N, K, m0, n0, static_cast<int64_t>(s) * DK, lds_addr + s * G::kStage, wave, L);
   G::wait_copies((KT < STAGES - 1 ? KT : STAGES - 1) - 1);
   __syncthreads();
 
@@ -208,7 +246,7 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
       // barrier has released.
       const int nt = kt + STAGES - 1;
       if (nt < KT)
-        G::copy_slice(A, B, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage, wave, L);
+        G::copy_slice(A, B, M, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage, wave, L);
       const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
 #pragma unroll
       for (int kk = 0; kk < DK / 16; ++kk) {
@@ -253,7 +291,7 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
           G::read(lds + ((kt + 1) % STAGES) * G::kStage, 0, L, nxt);
           if constexpr (kCopy) {  // after the reads: the copies are ordered asm the reads cannot pass
             const int nt = kt + STAGES - 1;
-            G::copy_slice(A, B, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage,
+            G::copy_slice(A, B, M, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage,
                           wave, L);
           }
         }
@@ -317,15 +355,25 @@ constexpr int kFastSched = 1;
 
 bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* C) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
-  return M % kTile == 0 && N % kTile == 0 && K % kFastDK == 0 && (al & 15) == 0 && K * 16 < (int64_t(1) << 31) &&
-         N * 16 < (int64_t(1) << 31);
+  const int64_t lim = int64_t(1) << 31;  // per-lane copy offsets are 32-bit
+  return M % kTile == 0 && N % kTile == 0 && K % kFastDK == 0 && (al & 15) == 0 && K * 16 < lim && N * 16 < lim &&
+         M * 16 < lim;
 }
 
+// transpose_a: A is given as [K, M]; transpose_b: B is given as [N, K].
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
-                            int64_t K, int relu, hipStream_t s) {
+                            int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s) {
   const int64_t tm = M / kTile, tn = N / kTile;
-  gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched><<<dim3(static_cast<unsigned>(tm * tn)), dim3(256), 0, s>>>(
-      A, B, bias, C, N, K, relu, static_cast<int>(tm), static_cast<int>(tn));
+  const dim3 grid(static_cast<unsigned>(tm * tn)), block(256);
+  const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);
+  if (!transpose_a && !transpose_b)
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched, false, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+  else if (!transpose_a)
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched, false, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+  else if (!transpose_b)
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched, true, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+  else
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched, true, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
   return hipGetLastError();
 }
 

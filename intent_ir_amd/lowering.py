@@ -128,27 +128,30 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
             break
     if env is None:
         return None
-    if env["ta"] or env["tb"]:
-        raise HipLoweringError("matmul with transpose_a/transpose_b is not lowered by the HIP backend yet")
+    ta, tb = bool(env["ta"]), bool(env["tb"])
     a, b = env["A"][1], env["B"][1]
     for n in (a, b, oname):
         if c.dtype(n) != "bf16":
             raise HipLoweringError(f"HIP GEMM takes bf16 A, B and C; {n} is {c.dtype(n)}")
     sa, sb, so = c.shape(a), c.shape(b), c.shape(oname)
-    if len(sa) != 2 or len(sb) != 2 or sa[1] != sb[0] or so != (sa[0], sb[1]):
-        raise HipLoweringError(f"matmul shapes do not agree: A{sa} B{sb} C{so}")
-    M, K, N = sa[0], sa[1], sb[1]
+    if len(sa) != 2 or len(sb) != 2:
+        raise HipLoweringError(f"HIP GEMM takes rank-2 operands: A{sa} B{sb}")
+    (M, K), (K2, N) = (sa[::-1] if ta else sa), (sb[::-1] if tb else sb)  # interpreter.py:510-515
+    if K != K2 or so != (M, N):
+        raise HipLoweringError(f"matmul shapes do not agree: A{sa} B{sb} C{so} (transpose_a={ta}, transpose_b={tb})")
     names = [a, b] + ([env["bias"][1]] if has_bias else []) + [oname]
     if has_bias:
         bn = env["bias"][1]
         if c.dtype(bn) != "f32" or c.shape(bn) != (N,):
             raise HipLoweringError(f"GEMM bias must be f32 [{N}]")
     args = [("tensor", a), ("tensor", b), ("tensor", env["bias"][1]) if has_bias else ("null", None),
-            ("tensor", oname), ("i64", M), ("i64", N), ("i64", K), ("i32", int(relu))]
+            ("tensor", oname), ("i64", M), ("i64", N), ("i64", K)]
+    args += [("i32", int(ta)), ("i32", int(tb))] if (ta or tb) else []
+    args += [("i32", int(relu))]
     full = M % 256 == 0 and N % 256 == 0 and K % 32 == 0  # fast path (4-stage ring) vs guarded kernel
     launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 131072 if full else 147456)
-    return HipLoweredKernel(c.fn.name, "ihip_gemm_bf16_bias_relu", c.io(names), launch, [oname], dict(c.b),
-                            tuple(args))
+    kid = "ihip_gemm_bf16_bias_relu_t" if (ta or tb) else "ihip_gemm_bf16_bias_relu"
+    return HipLoweredKernel(c.fn.name, kid, c.io(names), launch, [oname], dict(c.b), tuple(args))
 
 
 def _match_reduce_any(c: _Ctx) -> Optional[HipLoweredKernel]:

@@ -45,6 +45,7 @@ SIGNATURES: Dict[str, Tuple[Any, Tuple[Any, ...]]] = {
     "ihip_layernorm_rows_f16": (_I32, (_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _P)),
     "ihip_bias_gelu_tanh_axpy_bf16": (_I32, (_P, _P, _P, _I64, _I64, _F32, _P)),
     "ihip_gemm_bf16_bias_relu": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _P)),
+    "ihip_gemm_bf16_bias_relu_t": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _P)),
     "ihip_elementwise_program": (_I32, (_P, _I32, _P, _I32, _P, _I32, _P, _I32, _P)),
     "ihip_elementwise_mode": (_I32, (_I32,)),
     "ihip_elementwise_prepare": (_I32, (_P, _I32, _P, _I32, _P, _I32)),

@@ -312,6 +312,33 @@ def test_gemm_plain_and_epilogue_forms(hip):
     check(out, oracle_outputs(epi, inp, b), ["C"], TOL["matmul_strict"], "epilogue gemm")
 
 
+def _transposed_ir(ta: bool, tb: bool) -> dict:
+    ir = matmul_bias_relu2d_ir()
+    ir["tensors"]["A"]["shape"] = ["K", "M"] if ta else ["M", "K"]
+    ir["tensors"]["B"]["shape"] = ["N", "K"] if tb else ["K", "N"]
+    ir["ops"][0]["attrs"] = {"transpose_a": ta, "transpose_b": tb}
+    return ir
+
+
+@pytest.mark.parametrize("ta,tb", [(False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(512, 256, 96), (256, 512, 8192), (17, 33, 31), (300, 260, 100)])
+def test_gemm_transposed_operands(hip, ta, tb, M, N, K):
+    """matmul{transpose_a, transpose_b} (interpreter.py:507-520): parity with the oracle, and the
+    same bits as the plain layout on explicitly transposed copies (same MFMA order)."""
+    w = WORKLOADS["matmul"]
+    b = {"M": M, "N": N, "K": K}
+    inp = w.gen(b, seed=M + 2 * N + 3 * K, sigma=1.0)
+    tin = {"A": np.ascontiguousarray(inp["A"].T) if ta else inp["A"],
+           "B": np.ascontiguousarray(inp["B"].T) if tb else inp["B"], "bias": inp["bias"]}
+    ir = _transposed_ir(ta, tb)
+    k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    assert k.kernel_id == "ihip_gemm_bf16_bias_relu_t"
+    out = run_case(ir, tin, b)
+    check(out, oracle_outputs(ir, tin, b), ["C"], TOL["matmul_strict"], f"gemm ta={ta} tb={tb} {b}")
+    plain = run_case(w.ir(), inp, b)
+    np.testing.assert_array_equal(out["C"], plain["C"])
+
+
 def test_gemm_full_config(hip):
     import torch
 

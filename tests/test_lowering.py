@@ -154,9 +154,11 @@ def test_gemm_forms_and_errors():
     b = {"M": 256, "N": 256, "K": 64}
     assert lower_intent_to_hip_kernel(matmul_bias_relu2d_ir(), shape_bindings=b).call_args[-1] == ("i32", 1)
     ir = matmul_bias_relu2d_ir()
-    ir["ops"][0]["attrs"] = {"transpose_b": True}
-    with pytest.raises(HipLoweringError, match="transpose"):
-        lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    ir["ops"][0]["attrs"] = {"transpose_b": True}  # B declared [K, N] read as [N, K]: fine when N == K
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 256, "N": 64, "K": 64})
+    assert k.kernel_id == "ihip_gemm_bf16_bias_relu_t" and k.call_args[-3:] == (("i32", 0), ("i32", 1), ("i32", 1))
+    with pytest.raises(HipLoweringError, match="transpose_b=True"):
+        lower_intent_to_hip_kernel(ir, shape_bindings=b | {"N": 128})
     f32 = matmul_bias_relu2d_ir("f32")
     with pytest.raises(HipLoweringError, match="bf16"):
         lower_intent_to_hip_kernel(f32, shape_bindings=b)
