@@ -14,10 +14,11 @@ from .ir import IntentFunction, IntentIRValidationError, as_intent  # noqa: F401
 from .lowering import HipLaunch, HipLoweredKernel, HipLoweringError, lower_intent_to_hip_kernel  # noqa: F401
 from .macros import expand_macros  # noqa: F401
 from .opset import HIP_SUPPORTED_OPS  # noqa: F401
-from .runtime import HipRuntimeError, launch_lowered, load_library, run_hip_kernel, run_lowered  # noqa: F401
+from .runtime import (HipRuntimeError, launch_lowered, load_library, make_hip_ref_fn, run_hip_kernel,  # noqa: F401
+                      run_lowered)
 
 __all__ = [
     "HIP_SUPPORTED_OPS", "HipLaunch", "HipLoweredKernel", "HipLoweringError", "HipRuntimeError", "IntentFunction",
-    "IntentIRValidationError", "as_intent", "expand_macros", "launch_lowered", "load_library",
+    "IntentIRValidationError", "as_intent", "expand_macros", "launch_lowered", "load_library", "make_hip_ref_fn",
     "lower_intent_to_hip_kernel", "run_hip_kernel", "run_lowered",
 ]

@@ -258,11 +258,33 @@ def run_hip_kernel(*, kernel_name: str, kernel_id: str, io_spec: Mapping[str, An
     return result
 
 
+def make_hip_ref_fn(intent, make_inputs):
+    """``run_ref_fn`` for the reference's ``run_diff(intent, run_ref_fn, cases)``
+    (verify/diff_runner.py:37-44): per case, lower ``intent`` for ``case.shapes``, run it
+    through the C-ABI on ``case.inputs`` (or ``make_inputs(case)``) and return every
+    external input and every output under its IR name, 16-bit floats widened to float32
+    so the interpreter computes in float32 (inputs are exact widenings of what the
+    kernel read)."""
+    from .dtypes import to_compute_f32  # noqa: PLC0415
+    from .ir import as_intent  # noqa: PLC0415
+    from .lowering import lower_intent_to_hip_kernel  # noqa: PLC0415
+
+    fn = as_intent(intent)
+
+    def run_ref_fn(case):
+        k = lower_intent_to_hip_kernel(intent, shape_bindings=dict(case.shapes))
+        inputs = dict(case.inputs) if case.inputs else make_inputs(case)
+        out = run_lowered(k, inputs)
+        return {n: (to_compute_f32(v, fn.tensors[n].dtype) if n in fn.tensors else v) for n, v in out.items()}
+
+    return run_ref_fn
+
+
 def run_lowered(lowered, inputs_np: Mapping[str, np.ndarray]) -> Dict[str, np.ndarray]:
     return run_hip_kernel(kernel_name=lowered.kernel_name, kernel_id=lowered.kernel_id, io_spec=lowered.io_spec,
                           launch=lowered.launch, bindings=lowered.bindings, inputs_np=inputs_np,
                           output_names=lowered.output_names, call_args=lowered.call_args)
 
 
-__all__ = ["HipRuntimeError", "SIGNATURES", "EwInstr", "EwOperand", "ew_program_args", "LIB_PATH", "load_library", "call", "launch_lowered", "run_hip_kernel",
+__all__ = ["HipRuntimeError", "SIGNATURES", "EwInstr", "EwOperand", "ew_program_args", "make_hip_ref_fn", "LIB_PATH", "load_library", "call", "launch_lowered", "run_hip_kernel",
            "run_lowered", "to_device", "to_host", "torch_dtype", "tensor_shapes"]
