@@ -192,23 +192,80 @@ struct FastGemm {
     read_operand<BKM>(st, kk, L.fb, 64 * kRowA, f.b);
   }
 
-  static __device__ __forceinline__ void mfma(const Frag& f, f32x16_t (&acc)[4][4]) {
+  // The fragment reads of one k16 step as a flat list of LDS instructions ("slots"): A's
+  // first, then B's; a K-contiguous operand takes one ds_read_b128 per block, a K-major one
+  // two ds_read_b64_tr_b16 (low and high four k) per block.
+  static constexpr int kSlotsA = AKM ? 8 : 4;
+  static constexpr int kSlots = kSlotsA + (BKM ? 8 : 4);
+
+  template <bool kKMajor>
+  static __device__ __forceinline__ void read_operand_slot(const lds_char_t* st, int kk, const int (&o)[4],
+                                                           int blk_stride, bf16x8_t (&f)[4], int slot) {
+    if (!kKMajor) {
+      f[slot] = *(const lds_bf16x8_t*)(st + o[kk] + slot * blk_stride);
+    } else {
+      const int blk = slot >> 1, half = slot & 1;
+      const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + (kk * 16 + half * 4) * 512));
+      i16x8_t w = __builtin_bit_cast(i16x8_t, f[blk]);
+      if (half == 0) {
+        w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
+      } else {
+        w[4] = v[0], w[5] = v[1], w[6] = v[2], w[7] = v[3];
+      }
+      f[blk] = __builtin_bit_cast(bf16x8_t, w);
+    }
+  }
+
+  static __device__ __forceinline__ void read_slot(const lds_char_t* st, int kk, const Lane& L, Frag& f, int slot) {
+    if (slot < kSlotsA)
+      read_operand_slot<AKM>(st, kk, L.fa, 32 * kRowA, f.a, slot);
+    else
+      read_operand_slot<BKM>(st, kk, L.fb, 64 * kRowA, f.b, slot - kSlotsA);
+  }
+
+  // The MFMAs of B block ni against A blocks lo .. hi-1.
+  static __device__ __forceinline__ void mfma_range(const Frag& f, f32x16_t (&acc)[4][4], int ni, int lo, int hi) {
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 4; ++mi)
+      if (mi >= lo && mi < hi)
         acc[ni][mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[ni], f.a[mi], acc[ni][mi], 0, 0, 0);
   }
+
+  // Copy instruction i (0 .. kInstr-1) of a K slice: A's instructions first, then B's.
+  static __device__ __forceinline__ void copy_instr(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                                    int64_t M, int64_t N, int64_t K, int64_t m0, int64_t n0,
+                                                    int64_t k0, uint32_t stage, int wave, const Lane& L, int i) {
+    if (i < kInstrA) {
+      const int j = 4 * i + wave;
+      if (!AKM)
+        dma16(A + (m0 + j * kRowsPerInstrA) * K + k0, L.a, stage + j * 1024);
+      else
+        dma16(A + (k0 + 2 * j) * M + m0, L.a, stage + j * 1024);
+    } else {
+      const int j = 4 * (i - kInstrA) + wave;
+      if (!BKM)
+        dma16(B + (n0 + j * kRowsPerInstrA) * K + k0, L.b, stage + kStageA + j * 1024);
+      else
+        dma16(B + (k0 + 2 * j) * N + n0, L.b, stage + kStageA + j * 1024);
+    }
+  }
+
+  // s_waitcnt vmcnt(n) for a compile-time n.
+  template <int n>
+  static __device__ __forceinline__ void wait_vm() {
+    static_assert(n >= 0 && n <= 63, "vmcnt field");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+  }
+
 };
 
-template <int DK, int STAGES, int SCHED, bool AKM = false, bool BKM = true>
+template <int DK, int STAGES, bool AKM = false, bool BKM = true>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const float* __restrict__ bias,
                            uint16_t* __restrict__ C, int64_t M, int64_t N, int64_t K, int relu, int tiles_m,
                            int tiles_n) {
   using G = FastGemm<DK, STAGES, AKM, BKM>;
-  static_assert(SCHED == 0 || STAGES >= 3, "the pipelined schedule keeps two slices ahead");
-  // SCHED 1 needs KT >= STAGES - 1 (the prologue fills STAGES - 1 stages); the launcher checks.
+  static_assert(STAGES >= 3, "the pipeline keeps two slices ahead");
   __shared__ __attribute__((aligned(1024))) char lds_raw[STAGES * G::kStage];
   const lds_char_t* lds = (const lds_char_t*)lds_raw;
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
@@ -233,86 +290,94 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
 
   const typename G::Lane L = G::lane_plan(M, N, K, wave, wm, wn, lane);
   const int KT = static_cast<int>(K / DK);
-  // Prologue: slices 0 .. STAGES-2 in flight, then slice 0 must land.
+  // Slice kt's copies fill the stage slice kt-1 used, so a copy is issued kLead slices ahead.
+  constexpr int kLead = STAGES - 1;
+  // Prologue: slices 0 .. kLead-1 in flight, then slice 0 must land.
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
+  for (int s = 0; s < kLead; ++s)
     if (s < KT) G::copy_slice(A, B, M, N, K, m0, n0, static_cast<int64_t>(s) * DK, lds_addr + s * G::kStage, wave, L);
-  G::wait_copies((KT < STAGES - 1 ? KT : STAGES - 1) - 1);
+  G::wait_copies((KT < kLead ? KT : kLead) - 1);
   __syncthreads();
 
-  if constexpr (SCHED == 0) {
-    for (int kt = 0; kt < KT; ++kt) {
-      // Slice kt+STAGES-1 goes to the stage read in iteration kt-1, which that iteration's
-      // barrier has released.
-      const int nt = kt + STAGES - 1;
-      if (nt < KT)
-        G::copy_slice(A, B, M, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage, wave, L);
-      const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
+  // Main loop, software-pipelined per k16 step.  A step is four quarters of four MFMAs (one
+  // B block against the four A blocks); the next step's fragment reads are slotted between a
+  // quarter's MFMAs (sched_group_barrier), so no MFMA waits on LDS, and one copy instruction of
+  // slice kt+kLead follows each of the first kPerStep quarters, so a wave never issues its
+  // copies in a burst (a burst of copies stalls the issuing wave and skews the waves against
+  // the slice barrier).  At the last step of slice kt the wave issues kPre MFMAs, waits for
+  // its copies of slice kt+1, passes the barrier and reads slice kt+1's first fragments under
+  // the remaining MFMAs.  The barrier is fenced: every wave's LDS reads of slice kt-1 are
+  // complete once it passes the barrier ending slice kt-1, so slice kt may refill that stage.
+  // The steady loop and the tail are separate straight-line loops: with merged control flow
+  // the compiler's LDS wait counts become conservative and stall the MFMAs on reads of the
+  // next slice.
+  constexpr int NK = DK / 16;
+  constexpr int kPerStep = G::kInstr / NK;
+  static_assert(G::kInstr % NK == 0 && kPerStep <= 4, "at most one copy per quarter");
+  constexpr int kPerQ = G::kSlots / 4;
+  static_assert(G::kSlots % 4 == 0, "reads split evenly over quarters");
+  static_assert(NK % 2 == 0, "fragment double buffer alternates within a slice");
+  constexpr int kPre = 1;
+  // copies in flight when slice kt+1 must have landed: slices kt+2 .. kt+kLead-1 and the part
+  // of slice kt+kLead issued before the last step
+  constexpr int kSteadyPending = (kLead - 2) * G::kInstr + (NK - 1) * kPerStep;
+  typename G::Frag f[2];
+  G::read(lds, 0, L, f[0]);
+  auto slice = [&](int kt, auto copy_tag, int pending) {
+    constexpr bool kCopy = decltype(copy_tag)::value;
+    const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
+    const int nt = kt + kLead;
+    const uint32_t cdst = lds_addr + (nt % STAGES) * G::kStage;
+    const int64_t ck0 = static_cast<int64_t>(nt) * DK;
 #pragma unroll
-      for (int kk = 0; kk < DK / 16; ++kk) {
-        typename G::Frag f;
-        G::read(st, kk, L, f);
-        G::mfma(f, acc);
-      }
-      // slice kt+1 must have landed before the barrier; later slices may stay in flight
-      const int last = nt < KT ? nt : KT - 1;
-      G::wait_copies(last > kt + 1 ? last - (kt + 1) : 0);
-      __syncthreads();
-    }
-  } else {
-    // Software pipeline over k16 steps: the fragments of step s+1 are read while the 16 MFMAs
-    // of step s issue (one LDS read slotted after each MFMA), so no MFMA waits on LDS.  At the
-    // last step of slice kt the wave makes slice kt+1 ready (its copies + one barrier), copies
-    // slice kt+STAGES-1 into the stage slice kt-1 used (every wave finished reading it before
-    // the barrier), and reads slice kt+1's first fragments under slice kt's last MFMAs.
-    // The loops are split so every body is straight-line code: the steady loop always copies
-    // and waits for a fixed number of slices, the tail copies nothing.  (Merged control flow
-    // makes the compiler's LDS wait counts conservative and stalls the MFMAs on reads of the
-    // next slice.)
-    constexpr int NK = DK / 16;
-    typename G::Frag f[2];
-    G::read(lds, 0, L, f[0]);
-    auto slice = [&](int kt, auto copy_tag, int pending) {
-      constexpr bool kCopy = decltype(copy_tag)::value;
-      const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
+    for (int kk = 0; kk < NK; ++kk) {
+      typename G::Frag& cur = f[kk & 1];
+      typename G::Frag& nxt = f[(kk & 1) ^ 1];
+      const bool boundary = kk + 1 == NK;
+      const bool more = !boundary || pending >= 0;  // a next step exists
+      const lds_char_t* rs = boundary ? lds + ((kt + 1) % STAGES) * G::kStage : st;
+      const int rk = boundary ? 0 : kk + 1;
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) {
-        typename G::Frag& cur = f[kk & 1];
-        typename G::Frag& nxt = f[(kk & 1) ^ 1];
-        // Step kk starts after every instruction of step kk-1: the barrier of a slice boundary
-        // cannot be hoisted above the previous step's MFMAs, whose slack lets this wave's LDS
-        // reads finish before the barrier waits for them.
+      for (int q = 0; q < 4; ++q) {
+        // every quarter starts after all instructions of the previous one
         __builtin_amdgcn_sched_barrier(0);
-        if (kk + 1 < NK) {
-          G::read(st, kk + 1, L, nxt);
-        } else if (pending >= 0) {  // a next slice exists
-          G::wait_copies(pending);
+        const bool pre = boundary && q == 0 && more;
+        if (pre) {
+          G::mfma_range(cur, acc, 0, 0, kPre);
+          if constexpr (kCopy)
+            G::template wait_vm<kSteadyPending>();
+          else
+            G::wait_copies(pending);
           __syncthreads();
-          G::read(lds + ((kt + 1) % STAGES) * G::kStage, 0, L, nxt);
-          if constexpr (kCopy) {  // after the reads: the copies are ordered asm the reads cannot pass
-            const int nt = kt + STAGES - 1;
-            G::copy_slice(A, B, M, N, K, m0, n0, static_cast<int64_t>(nt) * DK, lds_addr + (nt % STAGES) * G::kStage,
-                          wave, L);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const int from = pre ? kPre : 0;
+        if (more) {
+#pragma unroll
+          for (int r = 0; r < kPerQ; ++r) G::read_slot(rs, rk, L, nxt, q * kPerQ + r);
+        }
+        G::mfma_range(cur, acc, q, from, 4);
+        if (more) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (j < 4 - from) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            if (j < kPerQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // one LDS read
           }
         }
-        G::mfma(cur, acc);
-        if (kk + 1 < NK || pending >= 0) {
-#pragma unroll
-          for (int j = 0; j < 12; ++j) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        if constexpr (kCopy) {
+          if (q < kPerStep) {
+            __builtin_amdgcn_sched_barrier(0);
+            G::copy_instr(A, B, M, N, K, m0, n0, ck0, cdst, wave, L, kk * kPerStep + q);
           }
-          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         }
       }
-    };
-    static_assert((DK / 16) % 2 == 0, "fragment double buffer alternates within a slice");
-    int kt = 0;
-    // steady state: slices up to kt+STAGES-2 are in flight; slice kt+1 must land
-    for (; kt + STAGES - 1 < KT; ++kt) slice(kt, std::true_type{}, STAGES - 3);
-    // tail: everything is issued; slice kt+1 must land, later ones may stay in flight
-    for (; kt < KT; ++kt) slice(kt, std::false_type{}, kt + 1 < KT ? KT - 2 - kt : -1);
-  }
+    }
+  };
+  int kt = 0;
+  // steady state: every slice copies, and waits for a fixed number of copies
+  for (; kt + kLead < KT; ++kt) slice(kt, std::true_type{}, 0);
+  // tail: everything is issued; slice kt+1 must land, later ones may stay in flight
+  for (; kt < KT; ++kt) slice(kt, std::false_type{}, kt + 1 < KT ? KT - 2 - kt : -1);
 
   // Epilogue, one 32x32 block at a time (the empty asm keeps the compiler from pulling all
   // 256 accumulators into VGPRs at once).  Branch-free: no bias adds +0, ReLU is
@@ -351,7 +416,6 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
 // K step and ring depth of the fast path.
 constexpr int kFastDK = 32;
 constexpr int kFastStages = 4;
-constexpr int kFastSched = 1;
 
 bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* C) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
@@ -367,13 +431,13 @@ hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* b
   const dim3 grid(static_cast<unsigned>(tm * tn)), block(256);
   const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);
   if (!transpose_a && !transpose_b)
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched, false, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, false, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
   else if (!transpose_a)
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched, false, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, false, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
   else if (!transpose_b)
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched, true, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, true, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
   else
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, kFastSched, true, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, true, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
   return hipGetLastError();
 }
 
