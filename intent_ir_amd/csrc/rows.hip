@@ -238,21 +238,43 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 
-// One wave per row; the row is held in registers (kVpl 16-byte vectors per lane)
-// and read from HBM once.  kFull: n8 == 64 * kVpl, no tail masks.
-template <int kVpl, bool kFull>
-__global__ __launch_bounds__(256) void layernorm_rows_f16_wave(const u32x4* __restrict__ x, const u32x4* __restrict__ w,
-                                                               const u32x4* __restrict__ b, u32x4* __restrict__ y,
-                                                               float* __restrict__ mean_out, float* __restrict__ rstd_out,
-                                                               int64_t M, int n8, int N, float eps) {
+// One wave per row, kLnRows rows per workgroup.  The row is held in registers (kVpl
+// 16-byte vectors per lane) and read from HBM once; w and b are staged in LDS once per
+// workgroup instead of being read by every row (16 KiB of L1/L2 traffic per 8 KiB row), and
+// the row's loads are issued before the staging loads.  The centred values are recomputed
+// in the last pass rather than kept live (the same FMA, so the same bits).
+// Measured on [8192, 4096]: 24.9 us with 4 rows per workgroup and w/b read per row, 22.6 us
+// like this (a plain copy of the same bytes takes 22.4 us).  The kernel must stay within 64
+// VGPRs so that two workgroups fit on a CU (at one per CU it ran ~12% slower): the row loads
+// share one base address, and the arithmetic runs on every lane with only the stores
+// predicated (with the arithmetic inside the store branch the compiler kept f32 copies of x
+// live across the reduction).  kExact (n8 == 64 * kVpl and M % kLnRows == 0) drops the tail
+// masks.
+constexpr int kLnRows = 16;
+template <int kVpl, bool kExact>
+__global__ __launch_bounds__(64 * kLnRows) void layernorm_rows_f16_wave(
+    const u32x4* __restrict__ x, const u32x4* __restrict__ w, const u32x4* __restrict__ b, u32x4* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t M, int n8, int N, float eps) {
+  static_assert(kVpl * kWave <= 64 * kLnRows, "one staging load per thread");
+  __shared__ u32x4 w_lds[kVpl * kWave], b_lds[kVpl * kWave];
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (row >= M) return;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kLnRows + (threadIdx.x >> 6);
+  // Waves past the last row read row M-1 (M > 0), stage w/b, pass the barrier and store nothing.
+  const bool live = kExact || row0 < M;
+  const int64_t row = live ? row0 : M - 1;
+  // The address is written base + lane + i*kWave so that every load shares one base register
+  // and takes i*1 KiB as an immediate offset; with the index precomputed, each load got its
+  // own 64-bit address (+16 VGPRs, which cost the second workgroup per CU).
+  const u32x4* xr = x + row * n8 + lane;
   f16x8_t xv[kVpl];
 #pragma unroll
-  for (int i = 0; i < kVpl; ++i) {
-    const int idx = lane + i * kWave;
-    xv[i] = __builtin_bit_cast(f16x8_t, (kFull || idx < n8) ? __builtin_nontemporal_load(x + row * n8 + idx) : u32x4(0u));
+  for (int i = 0; i < kVpl; ++i)
+    xv[i] = __builtin_bit_cast(f16x8_t, (kExact || lane + i * kWave < n8) ? __builtin_nontemporal_load(xr + i * kWave)
+                                                                         : u32x4(0u));
+  if (threadIdx.x < (kExact ? kVpl * kWave : n8)) {
+    const u32x4 wt = w[threadIdx.x], bt = b[threadIdx.x];
+    w_lds[threadIdx.x] = wt;
+    b_lds[threadIdx.x] = bt;
   }
   float s = 0.f;
   const f16x2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
@@ -264,39 +286,38 @@ __global__ __launch_bounds__(256) void layernorm_rows_f16_wave(const u32x4* __re
       s = __builtin_amdgcn_fdot2(p, one, s, false);  // padding lanes hold +0
     }
   const float mean = wave_sum(s) / static_cast<float>(N);
+  float q = 0.f;
   // 1.0 the compiler cannot fold away, so x*unit - mean stays one v_fma_mix_f32
   // (f16 operand widened inside the instruction) instead of a convert and a subtract.
   float unit;
   asm volatile("v_mov_b32 %0, 1.0" : "=v"(unit));
-  float d[kVpl][8];
-  float q = 0.f;
 #pragma unroll
-  for (int i = 0; i < kVpl; ++i) {
-    const bool ok = kFull || (lane + i * kWave) < n8;
+  for (int i = 0; i < kVpl; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      d[i][j] = __builtin_fmaf(static_cast<float>(xv[i][j]), unit, -mean);
-      q = __builtin_fmaf(d[i][j], ok ? d[i][j] : 0.f, q);
+      const float d = __builtin_fmaf(static_cast<float>(xv[i][j]), unit, -mean);
+      q = __builtin_fmaf(d, (kExact || (lane + i * kWave) < n8) ? d : 0.f, q);
     }
-  }
   const float var = wave_sum(q) / static_cast<float>(N);
   const float rstd = 1.0f / sqrtf(var + eps);
+  float unit2;  // a second opaque 1.0: d is recomputed below, not kept live across the reduction
+  asm volatile("v_mov_b32 %0, 1.0" : "=v"(unit2));
+  __syncthreads();  // w/b staged
   u32x4* yr = y + row * n8;
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
-    const int idx = lane + i * kWave;
-    if (kFull || idx < n8) {
-      const f16x8_t wv = __builtin_bit_cast(f16x8_t, w[idx]);
-      const f16x8_t bv = __builtin_bit_cast(f16x8_t, b[idx]);
-      f16x8_t o;
+    const int idx = lane + i * kWave;  // lanes past n8 read LDS entries never staged and store nothing
+    const f16x8_t wv = __builtin_bit_cast(f16x8_t, w_lds[idx]);
+    const f16x8_t bv = __builtin_bit_cast(f16x8_t, b_lds[idx]);
+    f16x8_t o;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        o[j] = static_cast<_Float16>(
-            __builtin_fmaf(d[i][j] * rstd, static_cast<float>(wv[j]), static_cast<float>(bv[j])));
-      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), yr + idx);
+    for (int j = 0; j < 8; ++j) {
+      const float d = __builtin_fmaf(static_cast<float>(xv[i][j]), unit2, -mean);
+      o[j] = static_cast<_Float16>(__builtin_fmaf(d * rstd, static_cast<float>(wv[j]), static_cast<float>(bv[j])));
     }
+    if (kExact || (live && idx < n8)) __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), yr + idx);
   }
-  if (lane == 0) {
+  if ((kExact || live) && lane == 0) {
     mean_out[row] = mean;
     rstd_out[row] = rstd;
   }
@@ -337,8 +358,8 @@ __global__ __launch_bounds__(256) void layernorm_rows_f16_any(const uint16_t* __
 template <int kVpl>
 static void launch_layernorm_wave(const u32x4* x8, const u32x4* w8, const u32x4* b8, u32x4* y8, float* mean, float* rstd,
                                   int64_t M, int n8, int N, float eps, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
-  if (n8 == kVpl * kWave)
+  const dim3 grid(static_cast<unsigned>((M + kLnRows - 1) / kLnRows)), block(64 * kLnRows);
+  if (n8 == kVpl * kWave && M % kLnRows == 0)
     layernorm_rows_f16_wave<kVpl, true><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, N, eps);
   else
     layernorm_rows_f16_wave<kVpl, false><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, N, eps);
