@@ -157,6 +157,19 @@ def measure(key, steps, warmup, torch, log, timing="eager"):
     return res
 
 
+def measure_in_child(key, steps, warmup, timing, log):
+    """measure() in a fresh process (a child; its log lines are passed through)."""
+    cmd = [sys.executable, str(ROOT / "bench.py"), "--config", key, "--only", "--no-cpu", "--steps", str(steps),
+           "--warmup", str(warmup), "--timing", timing, "--kernel-json"]
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    for line in p.stderr.splitlines():
+        if line.startswith("[bench]"):
+            log(line)
+    if p.returncode != 0:
+        raise RuntimeError(f"bench child for {key} failed ({p.returncode}):\n{p.stderr[-2000:]}")
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
 def cpu_baseline(key, log, target_s=10.0):
     """Reference CPU path on a bounded sample of the workload, timed on this host's cores.
 
@@ -221,6 +234,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--timing", default="graph", choices=["eager", "graph"],
                     help="eager: K stream-ordered launches between two events; graph: one replay of K captured launches")
+    ap.add_argument("--kernel-json", action="store_true",
+                    help="(internal) measure --config only and print its result as one JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every path here runs on one "
@@ -234,6 +249,9 @@ def main():
         sys.exit(1)
     key = args.config
     head = measure(key, args.steps, args.warmup, torch, log, args.timing)
+    if args.kernel_json:
+        print(json.dumps(head), flush=True)
+        return
     log(f"[bench] {key}: {head['value']:.1f} {head['unit']} ({100 * head['frac']:.1f}% of peak), "
         f"{head['ms_per_launch'] * 1e3:.2f} us/launch")
     kernels = {key: head}
@@ -241,8 +259,13 @@ def main():
         for other in WORKLOAD_NAMES:
             if other == key:
                 continue
-            st = 20 if other == "matmul" else 100
-            r = measure(other, st, 5, torch, log, args.timing)
+            # Each workload runs in a process of its own: buffers allocated after an earlier
+            # workload's were freed measured up to ~7% slower for the same kernel (physical
+            # placement the kernel does not control), which would make each number depend on the
+            # order of the list.  The memory-bound kernels (~20-180 us) get the headline's warmup
+            # and step count.
+            st, wu = (20, 5) if other == "matmul" else (args.steps, args.warmup)
+            r = measure_in_child(other, st, wu, args.timing, log)
             log(f"[bench] {other}: {r['value']:.1f} {r['unit']} ({100 * r['frac']:.1f}% of peak), "
                 f"{r['ms_per_launch'] * 1e3:.2f} us/launch")
             kernels[other] = r
