@@ -181,6 +181,21 @@ def test_layernorm_edge_shapes(hip, M, N):
     _check_ln(run_case(w.ir(), inp, b), oracle_outputs(w.ir(), inp, b), f"LN {b}")
 
 
+@pytest.mark.parametrize("N", [512, 1024, 2048, 4096])
+def test_layernorm_exact_and_tail_paths_agree(hip, N):
+    """Rows per workgroup: M % 16 == 0 with full-width rows takes the unmasked kernel, M = 31 the
+    masked one (its last workgroup has a wave past the last row).  Shared rows must be identical."""
+    w = WORKLOADS["layernorm"]
+    inp = w.gen({"M": 32, "N": N}, seed=N)
+    full = run_case(w.ir(), inp, {"M": 32, "N": N})
+    part_in = dict(inp, in_ptr=np.ascontiguousarray(inp["in_ptr"][:31]))
+    part = run_case(w.ir(), part_in, {"M": 31, "N": N})
+    for name in ("out_ptr", "out_mean_ptr", "out_rstd_ptr"):
+        np.testing.assert_array_equal(part[name], full[name][:31], err_msg=name)
+    _check_ln(full, oracle_outputs(w.ir(), inp, {"M": 32, "N": N}), f"LN exact N={N}")
+    _check_ln(part, oracle_outputs(w.ir(), part_in, {"M": 31, "N": N}), f"LN tail N={N}")
+
+
 def test_layernorm_full_config(hip):
     w = WORKLOADS["layernorm"]
     inp = w.gen(w.bindings)
