@@ -148,8 +148,9 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
             ("tensor", oname), ("i64", M), ("i64", N), ("i64", K)]
     args += [("i32", int(ta)), ("i32", int(tb))] if (ta or tb) else []
     args += [("i32", int(relu))]
-    full = M % 256 == 0 and N % 256 == 0 and K % 32 == 0  # fast path (4-stage ring) vs guarded kernel
-    launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 131072 if full else 147456)
+    full = M % 256 == 0 and N % 256 == 0 and K % 32 == 0  # fast path vs guarded kernel
+    # fast path LDS: max(4-stage ring 131072, bf16 C tile 256 x 528) + 256 f32 bias values
+    launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 136192 if full else 147456)
     kid = "ihip_gemm_bf16_bias_relu_t" if (ta or tb) else "ihip_gemm_bf16_bias_relu"
     return HipLoweredKernel(c.fn.name, kid, c.io(names), launch, [oname], dict(c.b), tuple(args))
 
@@ -256,7 +257,11 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
             ("i64", N), ("f32", float(env["eps"][1])))
     names = [x, w, b, y] + [inv[r] for r in ("mean", "rstd") if r in inv]
     vec = N % 8 == 0 and 0 < N <= 4096
-    launch = HipLaunch((max(1, _cdiv(M, 4)) if vec else max(1, M), 1, 1), (256, 1, 1), 0 if vec else 16)
+    if vec:  # 16 rows per 1024-thread workgroup; w and b staged in LDS (kVpl 16-byte vectors per lane)
+        kvpl = next(v for v in (1, 2, 4, 8) if N // 8 <= 64 * v)
+        launch = HipLaunch((max(1, _cdiv(M, 16)), 1, 1), (1024, 1, 1), 2 * kvpl * 64 * 16)
+    else:
+        launch = HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
     return HipLoweredKernel(c.fn.name, "ihip_layernorm_rows_f16", c.io(names), launch, list(c.fn.outputs),
                             dict(c.b), args)
 
