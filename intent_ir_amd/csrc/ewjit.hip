@@ -39,6 +39,7 @@ struct EwJitArgs {
   uint32_t in_vec8;  // bit k: input k is read with 8-element vectors
   uint32_t out_vec4;
   uint32_t out_vec8;
+  uint32_t in_stage_vec;  // bit k: staged input k is read into the LDS tile with 16-byte vectors
 };
 
 namespace {
@@ -63,6 +64,7 @@ struct EwJitArgs {
   u32 in_vec8;
   u32 out_vec4;
   u32 out_vec8;
+  u32 in_stage_vec;
 };
 __device__ __forceinline__ float h2f(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ float b2f(u16 b) { return __builtin_bit_cast(float, ((u32)b) << 16); }
@@ -223,12 +225,15 @@ const char* expr_of(int op) {
 }
 
 std::string fmt(const char* f, ...) {
-  char buf[512];
-  va_list ap;
+  va_list ap, ap2;
   va_start(ap, f);
-  vsnprintf(buf, sizeof(buf), f, ap);
+  va_copy(ap2, ap);
+  const int n = vsnprintf(nullptr, 0, f, ap);
   va_end(ap);
-  return buf;
+  std::string out(n > 0 ? static_cast<size_t>(n) : 0, '\0');
+  if (n > 0) vsnprintf(&out[0], static_cast<size_t>(n) + 1, f, ap2);
+  va_end(ap2);
+  return out;
 }
 
 }  // namespace
@@ -244,49 +249,124 @@ int ew_jit_width(int n_inputs, const int* in_dt, int n_outputs, const int* out_d
   return 8;
 }
 
-std::string ew_jit_source(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
-                          const int* out_dt) {
-  const int V = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt);
-  std::string s = fmt("#define EW_V %d\n", V);
-  s += kPrelude;
-  s += "extern \"C\" __global__ __launch_bounds__(256) void ihip_ew_jit(const EwJitArgs a) {\n"
-       "  const i64 D1 = a.shape[1], D2 = a.shape[2], D3 = a.shape[3];\n"
-       "  for (i64 row = blockIdx.y; row < a.rows; row += gridDim.y) {\n"
-       "    i64 c0 = 0, c1 = 0, c2 = row;\n"
-       "    if (row >= D2) { c2 = row % D2; const i64 t = row / D2; c1 = t % D1; c0 = t / D1; }\n"
-       "    for (i64 vec = (i64)blockIdx.x * blockDim.x + threadIdx.x; vec < a.nvec; vec += (i64)gridDim.x * blockDim.x) {\n"
-       "      const i64 c3 = vec * EW_V;\n"
-       "      const int valid = D3 - c3 < EW_V ? (int)(D3 - c3) : EW_V;\n"
-       "      float r[8][EW_V];\n";
+// Program body: the instruction list as straight-line code over r[8][EW_V].  `tiled`: inputs
+// in tile_mask are read from the LDS tile (slot = their rank among the staged inputs).
+static std::string ew_jit_body(const ihip_ew_instr* code, int n_code, const int* in_dt, const int* out_dt,
+                               uint32_t tile_mask, const char* ind) {
+  std::string s;
   for (int pc = 0; pc < n_code; ++pc) {
     const ihip_ew_instr& in = code[pc];
     switch (in.op) {
       case IHIP_EW_LOAD:
-        s += fmt("      load_op<%d>(a, %d, c0, c1, c2, c3, valid, r[%d]);\n", in_dt[in.a], in.a, in.dst);
+        if ((tile_mask >> in.a) & 1u) {
+          const int slot = __builtin_popcount(tile_mask & ((1u << in.a) - 1u));
+          s += fmt("%sfor (int j = 0; j < EW_V; ++j) r[%d][j] = tile[%d][l3 + j][l2];\n", ind, in.dst, slot);
+        } else {
+          s += fmt("%sload_op<%d>(a, %d, c0, c1, c2, c3, valid, r[%d]);\n", ind, in_dt[in.a], in.a, in.dst);
+        }
         break;
       case IHIP_EW_IMM:
-        s += fmt("      for (int j = 0; j < EW_V; ++j) r[%d][j] = __builtin_bit_cast(float, %uu);\n", in.dst,
+        s += fmt("%sfor (int j = 0; j < EW_V; ++j) r[%d][j] = __builtin_bit_cast(float, %uu);\n", ind, in.dst,
                  __builtin_bit_cast(uint32_t, in.imm));
         break;
       case IHIP_EW_IOTA:
-        s += fmt("      for (int j = 0; j < EW_V; ++j) r[%d][j] = (float)(%s);\n", in.dst,
+        s += fmt("%sfor (int j = 0; j < EW_V; ++j) r[%d][j] = (float)(%s);\n", ind, in.dst,
                  in.a == 0 ? "c0" : in.a == 1 ? "c1" : in.a == 2 ? "c2" : "c3 + j");
         break;
       case IHIP_EW_STORE:
-        s += fmt("      store_op<%d>(a, %d, row * D3 + c3, valid, r[%d]);\n", out_dt[in.b], in.b, in.a);
+        s += fmt("%sstore_op<%d>(a, %d, row * D3 + c3, valid, r[%d]);\n", ind, out_dt[in.b], in.b, in.a);
         break;
       default: {
         // read only the operands the opcode uses (the others may be unwritten registers)
         const bool two = in.op >= IHIP_EW_ADD && in.op <= IHIP_EW_OR;
         const bool three = in.op == IHIP_EW_WHERE;
-        s += fmt("      { float t[EW_V]; for (int j = 0; j < EW_V; ++j) { const float x = r[%d][j];", in.a);
+        s += fmt("%s{ float t[EW_V]; for (int j = 0; j < EW_V; ++j) { const float x = r[%d][j];", ind, in.a);
         if (two || three) s += fmt(" const float y = r[%d][j];", in.b);
         if (three) s += fmt(" const float z = r[%d][j];", in.c);
         s += fmt(" t[j] = %s; } for (int j = 0; j < EW_V; ++j) r[%d][j] = t[j]; }\n", expr_of(in.op), in.dst);
       }
     }
   }
-  s += "    }\n  }\n}\n";
+  return s;
+}
+
+std::string ew_jit_source(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
+                          const int* out_dt, uint32_t tile_mask) {
+  const int V = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt);
+  std::string s = fmt("#define EW_V %d\n", V);
+  s += kPrelude;
+  if (tile_mask == 0) {
+    s += "extern \"C\" __global__ __launch_bounds__(256) void ihip_ew_jit(const EwJitArgs a) {\n"
+         "  const i64 D1 = a.shape[1], D2 = a.shape[2], D3 = a.shape[3];\n"
+         "  for (i64 row = blockIdx.y; row < a.rows; row += gridDim.y) {\n"
+         "    i64 c0 = 0, c1 = 0, c2 = row;\n"
+         "    if (row >= D2) { c2 = row % D2; const i64 t = row / D2; c1 = t % D1; c0 = t / D1; }\n"
+         "    for (i64 vec = (i64)blockIdx.x * blockDim.x + threadIdx.x; vec < a.nvec; vec += (i64)gridDim.x * blockDim.x) {\n"
+         "      const i64 c3 = vec * EW_V;\n"
+         "      const int valid = D3 - c3 < EW_V ? (int)(D3 - c3) : EW_V;\n"
+         "      float r[8][EW_V];\n";
+    s += ew_jit_body(code, n_code, in_dt, out_dt, 0, "      ");
+    s += "    }\n  }\n}\n";
+    return s;
+  }
+  // Tiled form for inputs read across their unit-stride axis (axis 2 contiguous, axis 3
+  // strided, e.g. a transpose): a workgroup takes 64 rows (axis 2) x 64 columns (axis 3).
+  // Each staged input is read into LDS with consecutive threads on consecutive addresses of
+  // its axis 2.  Then 64/EW_V consecutive threads cover one row's 64 columns (EW_V each), so
+  // stores and the other operands' accesses stay contiguous, in 16/EW_V passes of 4*EW_V
+  // rows.  The 65-float tile pitch keeps both the staging writes and the reads conflict-free.
+  const int nt = __builtin_popcount(tile_mask);
+  s += fmt("#define EW_NT %d\n", nt);
+  s += "extern \"C\" __global__ __launch_bounds__(256) void ihip_ew_jit(const EwJitArgs a) {\n"
+       "  __shared__ float tile[EW_NT][64][65];\n"
+       "  const i64 D0 = a.shape[0], D1 = a.shape[1], D2 = a.shape[2], D3 = a.shape[3];\n"
+       "  const i64 T2 = (D2 + 63) / 64, ytiles = D0 * D1 * T2;\n"
+       "  const int tid = threadIdx.x, l3 = (tid % (64 / EW_V)) * EW_V;\n"
+       "  for (i64 y = blockIdx.y; y < ytiles; y += gridDim.y) {\n"
+       "    const i64 u = y / T2, c2_0 = (y % T2) * 64, c1 = u % D1, c0 = u / D1;\n"
+       "    for (i64 c3_0 = (i64)blockIdx.x * 64; c3_0 < D3; c3_0 += (i64)gridDim.x * 64) {\n"
+       "      __syncthreads();  // the previous tile is consumed\n";
+  int slot = 0;
+  for (int k = 0; k < n_inputs; ++k) {
+    if (!((tile_mask >> k) & 1u)) continue;
+    // 16-byte staging reads: VS elements of axis 2 per thread, 64/VS threads per tile row
+    const int vs = (in_dt[k] == IHIP_DT_F32 || in_dt[k] == IHIP_DT_I32) ? 4 : 8;
+    s += fmt("      {\n"
+             "        const void* p = a.in_ptr[%d];\n"
+             "        const i64 base = c0 * a.in_stride[%d][0] + c1 * a.in_stride[%d][1], s3 = a.in_stride[%d][3];\n"
+             "        if ((a.in_stage_vec >> %d) & 1u) {\n"
+             "          const int cc = (tid %% (64 / %d)) * %d;\n"
+             "          const i64 g2 = c2_0 + cc;\n"
+             "          for (int i = 0; i < 16 / %d; ++i) {\n"
+             "            const int r3 = i * 4 * %d + tid / (64 / %d);\n"
+             "            const i64 g3 = c3_0 + r3;\n"
+             "            float v[%d];\n"
+             "            if (g2 < D2 && g3 < D3) ld%d<%d>(p, base + g2 + g3 * s3, v);\n"
+             "            else for (int e = 0; e < %d; ++e) v[e] = 0.0f;\n"
+             "            for (int e = 0; e < %d; ++e) tile[%d][r3][cc + e] = v[e];\n"
+             "          }\n"
+             "        } else {\n"
+             "          const i64 g2 = c2_0 + (tid & 63);\n"
+             "          for (int i = 0; i < 16; ++i) {\n"
+             "            const int r3 = (tid >> 6) + 4 * i;\n"
+             "            const i64 g3 = c3_0 + r3;\n"
+             "            tile[%d][r3][tid & 63] = (g2 < D2 && g3 < D3) ? ld1<%d>(p, base + g2 + g3 * s3) : 0.0f;\n"
+             "          }\n"
+             "        }\n"
+             "      }\n",
+             k, k, k, k, k, vs, vs, vs, vs, vs, vs, vs, in_dt[k], vs, vs, slot, slot, in_dt[k]);
+    ++slot;
+  }
+  s += "      __syncthreads();\n"
+       "      const i64 c3 = c3_0 + l3;\n"
+       "      const int valid = D3 - c3 < EW_V ? (int)(D3 - c3) : EW_V;\n"
+       "      for (int pass = 0; pass < 16 / EW_V && c3 < D3; ++pass) {\n"
+       "        const int l2 = pass * 4 * EW_V + tid / (64 / EW_V);\n"
+       "        const i64 c2 = c2_0 + l2, row = (c0 * D1 + c1) * D2 + c2;\n"
+       "        if (c2 < D2) {\n"
+       "          float r[8][EW_V];\n";
+  s += ew_jit_body(code, n_code, in_dt, out_dt, tile_mask, "          ");
+  s += "        }\n      }\n    }\n  }\n}\n";
   return s;
 }
 
@@ -343,7 +423,7 @@ JitEntry& entry(const std::string& src) {
 // device is needed.  Returns false with *why set when compilation fails.
 bool prepare_elementwise_jit(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
                              const int* out_dt, std::string* why) {
-  const std::string src = ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt);
+  const std::string src = ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt, 0);
   std::lock_guard<std::mutex> lock(g_jit_mu);
   JitEntry& e = entry(src);
   if (!e.error.empty() && why) *why = e.error;
@@ -382,10 +462,27 @@ hipError_t launch_elementwise_jit(const ihip_ew_instr* code, int n_code, const i
     if (V == 8 && vec_ok(outputs[k].ptr, nullptr, out_dt[k], 8)) a.out_vec8 |= 1u << k;
     else if (vec_ok(outputs[k].ptr, nullptr, out_dt[k], 4)) a.out_vec4 |= 1u << k;
   }
+  // Inputs read across their unit-stride axis (axis 2 contiguous, axis 3 strided) are staged
+  // through LDS tiles, at most kMaxTiled of them (16.6 KiB each).
+  constexpr int kMaxTiled = 4;
+  uint32_t tile_mask = 0;
+  if (shape[2] > 1 && shape[3] > 1)
+    for (int k = 0; k < n_inputs && __builtin_popcount(tile_mask) < kMaxTiled; ++k)
+      if (inputs[k].stride[2] == 1 && inputs[k].stride[3] != 0 && inputs[k].stride[3] != 1) tile_mask |= 1u << k;
+  // A staged input is read in 16-byte vectors when every vector starts at a multiple of its
+  // width and stays inside axis 2.
+  for (int k = 0; k < n_inputs; ++k) {
+    if (!((tile_mask >> k) & 1u)) continue;
+    const int64_t vs = (in_dt[k] == IHIP_DT_F32 || in_dt[k] == IHIP_DT_I32) ? 4 : 8;
+    const int64_t* st = inputs[k].stride;
+    if (shape[2] % vs == 0 && st[3] % vs == 0 && (st[0] % vs == 0 || shape[0] == 1) &&
+        (st[1] % vs == 0 || shape[1] == 1) && reinterpret_cast<uintptr_t>(inputs[k].ptr) % 16 == 0)
+      a.in_stage_vec |= 1u << k;
+  }
   int dev = 0;
   hipError_t he = hipGetDevice(&dev);
   if (he != hipSuccess) return he;
-  const std::string src = ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt);
+  const std::string src = ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt, tile_mask);
   hipFunction_t fn = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_jit_mu);
@@ -405,12 +502,18 @@ hipError_t launch_elementwise_jit(const ihip_ew_instr* code, int n_code, const i
       fn = f->second;
     }
   }
+  void* params[] = {&a};
+  if (tile_mask != 0) {  // one workgroup per 64 x 64 tile (grid-strided beyond the grid limits)
+    const int64_t tx = (shape[3] + 63) / 64, ty = shape[0] * shape[1] * ((shape[2] + 63) / 64);
+    const unsigned gx = static_cast<unsigned>(tx < 65535 ? tx : 65535);
+    const unsigned gy = static_cast<unsigned>(ty < 65535 ? ty : 65535);
+    return hipModuleLaunchKernel(fn, gx, gy, 1, 256, 1, 1, 0, s, params, nullptr);
+  }
   const int64_t bx = (a.nvec + 255) / 256;
   const unsigned gx = static_cast<unsigned>(bx < 1024 ? bx : 1024);
   int64_t gy = (4096 + gx - 1) / gx;
   if (gy > a.rows) gy = a.rows;
   if (gy > 65535) gy = 65535;
-  void* params[] = {&a};
   return hipModuleLaunchKernel(fn, gx, static_cast<unsigned>(gy), 1, 256, 1, 1, 0, s, params, nullptr);
 }
 

@@ -114,6 +114,20 @@ case("transpose_add", {
     "ops": [op("transpose", ["x"], "xt", perm=[1, 0]), op("add", ["xt", "b"], "y")], "outputs": ["y"]},
     {"M": 17, "N": 32}, lambda r, b: {"x": _f(r, b["M"], b["N"]), "b": _f(r, b["M"])})
 
+# transposes staged through LDS tiles: 16-bit operands (8-wide lanes, 16-byte staging reads),
+# a batched 3-D transpose (batch axis outside the tile), tails on both tile axes
+case("transpose_half_bf16_out", {
+    "tensors": {"x": T("f16", "M", "N"), "xt": T("f16", "N", "M"), "w": T("bf16", "M"), "t": T("f32", "N", "M"),
+                "y": T("bf16", "N", "M")},
+    "ops": [op("transpose", ["x"], "xt", perm=[1, 0]), op("mul", ["xt", "w"], "t"), op("add", ["t"], "y", addend=0.25)],
+    "outputs": ["y"]},
+    {"M": 24, "N": 40}, lambda r, b: {"x": _f(r, b["M"], b["N"]).astype(np.float16), "w": _f(r, b["M"])})
+
+case("transpose_batched_3d", {
+    "tensors": {"x": T("f32", "A", "M", "N"), "xt": T("f32", "A", "N", "M"), "y": T("f32", "A", "N", "M")},
+    "ops": [op("transpose", ["x"], "xt", perm=[0, 2, 1]), op("relu", ["xt"], "y")], "outputs": ["y"]},
+    {"A": 3, "M": 70, "N": 66}, lambda r, b: {"x": _f(r, b["A"], b["M"], b["N"])})
+
 # iota along the inner axis
 case("iota_inner", {
     "tensors": {"x": T("f32", "M", "N"), "i": T("i32", "M", "N"), "y": T("f32", "M", "N")},

@@ -58,6 +58,9 @@ BIG = [
     ("rank4_broadcast", {"A": 4, "B": 8, "C": 64, "D": 256}),
     ("gelu_f32_chain", {"M": 256, "N": 8192}),
     ("two_outputs_shared", {"M": 70000, "N": 4}),  # more rows than grid.y: the row loop strides
+    ("transpose_half_bf16_out", {"M": 1000, "N": 1024}),  # LDS-staged transpose, 16-byte staging reads
+    ("transpose_half_bf16_out", {"M": 999, "N": 1001}),  # staging falls back to element reads
+    ("transpose_batched_3d", {"A": 4, "M": 256, "N": 520}),
 ]
 
 
