@@ -194,7 +194,10 @@ int ihip_elementwise_mode(int mode);
 
 /* Compile the native code of a program for the given operand types ahead of its first launch
  * (for example before capturing a graph).  Needs no device.  Checks the program like
- * ihip_elementwise_program; returns IHIP_OK, or an error whose message holds the compiler log. */
+ * ihip_elementwise_program; returns IHIP_OK, or an error whose message holds the compiler log.
+ * This prepares the row form.  Operands read across their unit-stride axis (axis 2 contiguous,
+ * axis 3 strided, as a transpose) select a tiled form at launch, which compiles on its first
+ * launch. */
 int ihip_elementwise_prepare(const ihip_ew_instr* code, int32_t n_code, const int32_t* input_dtypes, int32_t n_inputs,
                              const int32_t* output_dtypes, int32_t n_outputs);
 
