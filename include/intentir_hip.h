@@ -195,11 +195,22 @@ int ihip_elementwise_mode(int mode);
 /* Compile the native code of a program for the given operand types ahead of its first launch
  * (for example before capturing a graph).  Needs no device.  Checks the program like
  * ihip_elementwise_program; returns IHIP_OK, or an error whose message holds the compiler log.
- * This prepares the row form.  Operands read across their unit-stride axis (axis 2 contiguous,
- * axis 3 strided, as a transpose) select a tiled form at launch, which compiles on its first
- * launch. */
+ * The generated code fixes each operand's access form, so this prepares the form that dense
+ * operands select: every input and output 16-byte aligned, read and written in full vectors
+ * (inner size a multiple of 8 elements when all operands are 16-bit or narrower, else of 4).
+ * Other layouts (broadcast scalars and [M,1] columns, strided or unaligned operands, operands
+ * read across their unit-stride axis such as a transpose) compile on their first launch, or
+ * ahead of it through ihip_elementwise_prepare_operands. */
 int ihip_elementwise_prepare(const ihip_ew_instr* code, int32_t n_code, const int32_t* input_dtypes, int32_t n_inputs,
                              const int32_t* output_dtypes, int32_t n_outputs);
+
+/* Compile exactly the native code that ihip_elementwise_program would run for these operands
+ * and shape (same arguments, without the stream), ahead of the launch.  Needs no device:
+ * the pointers are only inspected for their alignment.  Returns IHIP_OK, or an error as
+ * ihip_elementwise_prepare. */
+int ihip_elementwise_prepare_operands(const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,
+                                      int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs,
+                                      const int64_t* shape, int32_t rank);
 
 #ifdef __cplusplus
 }

@@ -33,6 +33,8 @@ hipError_t launch_elementwise_program(const ihip_ew_instr*, int, const ihip_ew_o
 hipError_t launch_elementwise_jit(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*, int,
                                   const int64_t (&)[4], hipStream_t, std::string*);
 bool prepare_elementwise_jit(const ihip_ew_instr*, int, int, const int*, int, const int*, std::string*);
+bool prepare_elementwise_jit_operands(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*,
+                                      int, const int64_t (&)[4], std::string*);
 }  // namespace ihip
 
 namespace {
@@ -216,35 +218,43 @@ int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* 
   return ihip_gemm_bf16_bias_relu_t(A, B, bias, C, M, N, K, 0, 0, relu, stream);
 }
 
+// Checks the arguments of an element-wise launch (also those of its operand-aware prepare)
+// and right-aligns the shape into sh[4]; *total = element count.  Returns IHIP_OK or an error.
+static int check_ew_launch(const char* who, const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,
+                           int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs, const int64_t* shape,
+                           int32_t rank, int64_t (&sh)[4], int64_t* total) {
+  IHIP_REQUIRE(code != nullptr && n_code >= 1 && n_code <= IHIP_EW_MAX_CODE,
+               "%s: need 1..%d instructions, got %d", who, IHIP_EW_MAX_CODE, (int)n_code);
+  IHIP_REQUIRE(n_inputs >= 0 && n_inputs <= IHIP_EW_MAX_INPUTS && (n_inputs == 0 || inputs != nullptr),
+               "%s: need 0..%d inputs, got %d", who, IHIP_EW_MAX_INPUTS, (int)n_inputs);
+  IHIP_REQUIRE(n_outputs >= 1 && n_outputs <= IHIP_EW_MAX_OUTPUTS && outputs != nullptr,
+               "%s: need 1..%d outputs, got %d", who, IHIP_EW_MAX_OUTPUTS, (int)n_outputs);
+  IHIP_REQUIRE(rank >= 0 && rank <= IHIP_EW_MAX_RANK && (rank == 0 || shape != nullptr),
+               "%s: rank %d outside 0..%d", who, (int)rank, IHIP_EW_MAX_RANK);
+  for (int d = 0; d < 4; ++d) sh[d] = 1;
+  *total = 1;
+  for (int i = 0; i < rank; ++i) {
+    sh[4 - rank + i] = shape[i];
+    *total = numel2(*total, shape[i]);
+    IHIP_REQUIRE(*total >= 0, "%s: invalid shape (axis %d = %lld)", who, i, (long long)shape[i]);
+  }
+  for (int k = 0; k < n_inputs; ++k) {
+    IHIP_REQUIRE(ew_dtype_ok(inputs[k].dtype), "%s: input %d has unknown dtype %d", who, k, (int)inputs[k].dtype);
+    IHIP_REQUIRE(*total == 0 || inputs[k].ptr != nullptr, "%s: input %d is null", who, k);
+  }
+  for (int k = 0; k < n_outputs; ++k) {
+    IHIP_REQUIRE(ew_dtype_ok(outputs[k].dtype), "%s: output %d has unknown dtype %d", who, k, (int)outputs[k].dtype);
+    IHIP_REQUIRE(*total == 0 || outputs[k].ptr != nullptr, "%s: output %d is null", who, k);
+  }
+  return check_program(code, n_code, n_inputs, n_outputs);
+}
+
 int ihip_elementwise_program(const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,
                              int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs,
                              const int64_t* shape, int32_t rank, void* stream) {
-  IHIP_REQUIRE(code != nullptr && n_code >= 1 && n_code <= IHIP_EW_MAX_CODE,
-               "elementwise_program: need 1..%d instructions, got %d", IHIP_EW_MAX_CODE, (int)n_code);
-  IHIP_REQUIRE(n_inputs >= 0 && n_inputs <= IHIP_EW_MAX_INPUTS && (n_inputs == 0 || inputs != nullptr),
-               "elementwise_program: need 0..%d inputs, got %d", IHIP_EW_MAX_INPUTS, (int)n_inputs);
-  IHIP_REQUIRE(n_outputs >= 1 && n_outputs <= IHIP_EW_MAX_OUTPUTS && outputs != nullptr,
-               "elementwise_program: need 1..%d outputs, got %d", IHIP_EW_MAX_OUTPUTS, (int)n_outputs);
-  IHIP_REQUIRE(rank >= 0 && rank <= IHIP_EW_MAX_RANK && (rank == 0 || shape != nullptr),
-               "elementwise_program: rank %d outside 0..%d", (int)rank, IHIP_EW_MAX_RANK);
-  int64_t sh[4] = {1, 1, 1, 1};
-  int64_t total = 1;
-  for (int i = 0; i < rank; ++i) {
-    sh[4 - rank + i] = shape[i];
-    total = numel2(total, shape[i]);
-    IHIP_REQUIRE(total >= 0, "elementwise_program: invalid shape (axis %d = %lld)", i, (long long)shape[i]);
-  }
-  for (int k = 0; k < n_inputs; ++k) {
-    IHIP_REQUIRE(ew_dtype_ok(inputs[k].dtype), "elementwise_program: input %d has unknown dtype %d", k,
-                 (int)inputs[k].dtype);
-    IHIP_REQUIRE(total == 0 || inputs[k].ptr != nullptr, "elementwise_program: input %d is null", k);
-  }
-  for (int k = 0; k < n_outputs; ++k) {
-    IHIP_REQUIRE(ew_dtype_ok(outputs[k].dtype), "elementwise_program: output %d has unknown dtype %d", k,
-                 (int)outputs[k].dtype);
-    IHIP_REQUIRE(total == 0 || outputs[k].ptr != nullptr, "elementwise_program: output %d is null", k);
-  }
-  const int bad = check_program(code, n_code, n_inputs, n_outputs);
+  int64_t sh[4], total = 0;
+  const int bad = check_ew_launch("elementwise_program", code, n_code, inputs, n_inputs, outputs, n_outputs, shape,
+                                  rank, sh, &total);
   if (bad) return bad;
   if (total == 0) return finish(hipSuccess, "elementwise_program");
   const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -284,6 +294,21 @@ int ihip_elementwise_prepare(const ihip_ew_instr* code, int32_t n_code, const in
   std::string why;
   if (!ihip::prepare_elementwise_jit(code, n_code, n_inputs, in_dt, n_outputs, out_dt, &why))
     return fail(static_cast<int>(hipErrorNotSupported), "elementwise_prepare: %s", why.c_str());
+  g_last_error[0] = '\0';
+  return IHIP_OK;
+}
+
+int ihip_elementwise_prepare_operands(const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,
+                                      int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs,
+                                      const int64_t* shape, int32_t rank) {
+  int64_t sh[4], total = 0;
+  const int bad = check_ew_launch("elementwise_prepare_operands", code, n_code, inputs, n_inputs, outputs, n_outputs,
+                                  shape, rank, sh, &total);
+  if (bad) return bad;
+  std::string why;
+  if (total != 0 &&
+      !ihip::prepare_elementwise_jit_operands(code, n_code, inputs, n_inputs, outputs, n_outputs, sh, &why))
+    return fail(static_cast<int>(hipErrorNotSupported), "elementwise_prepare_operands: %s", why.c_str());
   g_last_error[0] = '\0';
   return IHIP_OK;
 }

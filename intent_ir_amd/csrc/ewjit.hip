@@ -13,12 +13,15 @@
 //
 // Layout and schedule follow the interpreter kernel: a lane owns V consecutive elements of
 // the innermost axis (V = 8 when all operands are 16-bit or narrower, so each access is one
-// 16-byte vector; else 4), grid.y strides over outer rows, inputs carry per-axis strides,
-// and V-wide, 4-wide or element-wise access per operand is chosen from uniform flags.
+// 16-byte vector; else 4), grid.y strides over outer rows, inputs carry per-axis strides.
+// The access form of every operand (V-wide or 4-wide vectors, a broadcast element, strided
+// elements, an LDS tile) is fixed in the generated source, so the code holds only the paths
+// a launch takes; each distinct combination compiles once.
 #include <hip/hiprtc.h>
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -34,12 +37,7 @@ struct EwJitArgs {
   void* out_ptr[IHIP_EW_MAX_OUTPUTS];
   int64_t shape[4];
   int64_t rows;
-  int64_t nvec;      // ceil(D3 / V): lanes own V = 4 or 8 elements
-  uint32_t in_vec4;  // bit k: input k is read with 4-element vectors
-  uint32_t in_vec8;  // bit k: input k is read with 8-element vectors
-  uint32_t out_vec4;
-  uint32_t out_vec8;
-  uint32_t in_stage_vec;  // bit k: staged input k is read into the LDS tile with 16-byte vectors
+  int64_t nvec;  // ceil(D3 / V): lanes own V = 4 or 8 elements
 };
 
 namespace {
@@ -60,12 +58,43 @@ struct EwJitArgs {
   i64 shape[4];
   i64 rows;
   i64 nvec;
-  u32 in_vec4;
-  u32 in_vec8;
-  u32 out_vec4;
-  u32 out_vec8;
-  u32 in_stage_vec;
 };
+// exp, division and 1/sqrt on the hardware approximations, each refined to within ~2 ulp of
+// the correctly rounded result (the numpy float32 forms the interpreter uses round once or
+// twice); non-finite inputs and results take the IEEE value.
+__device__ __forceinline__ float ew_exp(float x) {
+  // 2^(x*log2 e): the product carried as head t + tail, v_exp_f32 on the head, first-order
+  // correction e*(1 + tail*ln 2) for the tail.
+  const float t = x * 1.44269502f;
+  const float tail = __builtin_fmaf(x, 1.92596303e-08f, __builtin_fmaf(x, 1.44269502f, -t));
+  const float e = __builtin_amdgcn_exp2f(t);
+  return __builtin_isfinite(tail) ? __builtin_fmaf(e, tail * 0.693147182f, e) : e;
+}
+// x / y as v_rcp_f32 and one Newton step on the quotient.  `bad` is set where that form
+// does not hold (zero, infinite or NaN reciprocal or quotient); those elements take ew_div,
+// which falls back to IEEE division for exactly them, so a lane branches once per vector.
+__device__ __forceinline__ float ew_div_fast(float x, float y, bool& bad) {
+  const float r = __builtin_amdgcn_rcpf(y);
+  const float q = x * r;
+  bad |= !__builtin_isfinite(q) || r == 0.0f || !__builtin_isfinite(r);
+  return __builtin_fmaf(__builtin_fmaf(-y, q, x), r, q);
+}
+__device__ __forceinline__ float ew_div(float x, float y) {
+  bool bad = false;
+  const float q = ew_div_fast(x, y, bad);
+  return bad ? x / y : q;
+}
+// 1/sqrt(x) as v_rsq_f32 and one Newton step r + r/2 (1 - x r^2); `bad` as for division.
+__device__ __forceinline__ float ew_rsqrt_fast(float x, bool& bad) {
+  const float r = __builtin_amdgcn_rsqf(x);
+  bad |= !(x > 0.0f) || !__builtin_isfinite(x) || !__builtin_isfinite(r);
+  return __builtin_fmaf(r * 0.5f, __builtin_fmaf(-x * r, r, 1.0f), r);
+}
+__device__ __forceinline__ float ew_rsqrt(float x) {
+  bool bad = false;
+  const float r = ew_rsqrt_fast(x, bad);
+  return bad ? 1.0f / sqrtf(x) : r;
+}
 __device__ __forceinline__ float h2f(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ float b2f(u16 b) { return __builtin_bit_cast(float, ((u32)b) << 16); }
 __device__ __forceinline__ u16 f2h(float x) { return __builtin_bit_cast(u16, (_Float16)x); }
@@ -154,33 +183,31 @@ template <int DT> __device__ __forceinline__ void st8(void* p, i64 i, const floa
     st4<DT>(p, i + 4, v + 4);
   }
 }
-// EW_V (4 or 8) elements per lane, defined by the generated source.
-template <int DT> __device__ __forceinline__ void load_op(const EwJitArgs& a, int k, i64 c0, i64 c1, i64 c2, i64 c3,
-                                                          int valid, float* v) {
-  const void* p = a.in_ptr[k];
-  const i64 base = c0 * a.in_stride[k][0] + c1 * a.in_stride[k][1] + c2 * a.in_stride[k][2];
-  const i64 s3 = a.in_stride[k][3];
-  if (EW_V == 8 && ((a.in_vec8 >> k) & 1u)) {
+// EW_V (4 or 8) elements per lane, defined by the generated source.  The access form K of
+// each operand is fixed when the source is generated: '8' / '4' = 8- / 4-element vectors at
+// base + c3 (row starts and base aligned, inner size a multiple of the width), 'b' = one
+// element broadcast along axis 3, 's' = element-wise at base + (c3 + j) * s3.
+template <int DT, char K> __device__ __forceinline__ void ldk(const void* p, i64 base, i64 c3, i64 s3, int valid,
+                                                            float* v) {
+  if (K == '8') {
     ld8<DT>(p, base + c3, v);
-  } else if ((a.in_vec4 >> k) & 1u) {
+  } else if (K == '4') {
     ld4<DT>(p, base + c3, v);
     if (EW_V == 8) {
       if (valid > 4) ld4<DT>(p, base + c3 + 4, v + 4);
       else for (int j = 4; j < EW_V; ++j) v[j] = 0.0f;
     }
-  } else if (s3 == 0) {
+  } else if (K == 'b') {
     const float x = ld1<DT>(p, base);
     for (int j = 0; j < EW_V; ++j) v[j] = x;
   } else {
     for (int j = 0; j < EW_V; ++j) v[j] = j < valid ? ld1<DT>(p, base + (c3 + j) * s3) : 0.0f;
   }
 }
-template <int DT> __device__ __forceinline__ void store_op(const EwJitArgs& a, int k, i64 off, int valid,
-                                                           const float* v) {
-  void* p = a.out_ptr[k];
-  if (EW_V == 8 && ((a.out_vec8 >> k) & 1u)) {
+template <int DT, char K> __device__ __forceinline__ void stk(void* p, i64 off, int valid, const float* v) {
+  if (K == '8') {
     st8<DT>(p, off, v);
-  } else if ((a.out_vec4 >> k) & 1u) {
+  } else if (K == '4') {
     st4<DT>(p, off, v);
     if (EW_V == 8 && valid > 4) st4<DT>(p, off + 4, v + 4);
   } else {
@@ -197,7 +224,7 @@ const char* expr_of(int op) {
     case IHIP_EW_ADD: return "x + y";
     case IHIP_EW_SUB: return "x - y";
     case IHIP_EW_MUL: return "x * y";
-    case IHIP_EW_DIV: return "x / y";
+    case IHIP_EW_DIV: return "ew_div(x, y)";
     case IHIP_EW_MAX: return "__builtin_elementwise_maximum(x, y)";
     case IHIP_EW_MIN: return "__builtin_elementwise_minimum(x, y)";
     case IHIP_EW_NE: return "x != y ? 1.0f : 0.0f";
@@ -210,8 +237,8 @@ const char* expr_of(int op) {
     case IHIP_EW_OR: return "(x != 0.0f || y != 0.0f) ? 1.0f : 0.0f";
     case IHIP_EW_NOT: return "x == 0.0f ? 1.0f : 0.0f";
     case IHIP_EW_RELU: return "__builtin_elementwise_maximum(x, 0.0f)";
-    case IHIP_EW_EXP: return "expf(x)";
-    case IHIP_EW_RSQRT: return "1.0f / sqrtf(x)";
+    case IHIP_EW_EXP: return "ew_exp(x)";
+    case IHIP_EW_RSQRT: return "ew_rsqrt(x)";
     case IHIP_EW_ABS: return "fabsf(x)";
     case IHIP_EW_FLOOR: return "floorf(x)";
     case IHIP_EW_NEG: return "-x";
@@ -249,20 +276,30 @@ int ew_jit_width(int n_inputs, const int* in_dt, int n_outputs, const int* out_d
   return 8;
 }
 
-// Program body: the instruction list as straight-line code over r[8][EW_V].  `tiled`: inputs
-// in tile_mask are read from the LDS tile (slot = their rank among the staged inputs).
+static bool is_tiled(char kind) { return kind == 'v' || kind == 't'; }
+
+// Program body: the instruction list as straight-line code over r[8][EW_V].  Inputs and
+// outputs are accessed in their form (in_kind / out_kind, see ldk); in the tiled form
+// (`tiled`) staged inputs ('v', 't') are read from their LDS tile (slot = their rank among
+// the staged inputs) and the other inputs from the registers they were prefetched into.
 static std::string ew_jit_body(const ihip_ew_instr* code, int n_code, const int* in_dt, const int* out_dt,
-                               uint32_t tile_mask, const char* ind) {
+                               const char* in_kind, const char* out_kind, bool tiled, const char* ind) {
   std::string s;
   for (int pc = 0; pc < n_code; ++pc) {
     const ihip_ew_instr& in = code[pc];
     switch (in.op) {
       case IHIP_EW_LOAD:
-        if ((tile_mask >> in.a) & 1u) {
-          const int slot = __builtin_popcount(tile_mask & ((1u << in.a) - 1u));
+        if (tiled && is_tiled(in_kind[in.a])) {
+          int slot = 0;
+          for (int k = 0; k < in.a; ++k) slot += is_tiled(in_kind[k]);
           s += fmt("%sfor (int j = 0; j < EW_V; ++j) r[%d][j] = tile[%d][l3 + j][l2];\n", ind, in.dst, slot);
+        } else if (tiled) {
+          s += fmt("%sfor (int j = 0; j < EW_V; ++j) r[%d][j] = pre%d[pass][j];\n", ind, in.dst, in.a);
         } else {
-          s += fmt("%sload_op<%d>(a, %d, c0, c1, c2, c3, valid, r[%d]);\n", ind, in_dt[in.a], in.a, in.dst);
+          const int k = in.a;
+          s += fmt("%sldk<%d, '%c'>(a.in_ptr[%d], c0 * a.in_stride[%d][0] + c1 * a.in_stride[%d][1] + c2 * "
+                   "a.in_stride[%d][2], c3, a.in_stride[%d][3], valid, r[%d]);\n",
+                   ind, in_dt[k], in_kind[k], k, k, k, k, k, in.dst);
         }
         break;
       case IHIP_EW_IMM:
@@ -274,15 +311,27 @@ static std::string ew_jit_body(const ihip_ew_instr* code, int n_code, const int*
                  in.a == 0 ? "c0" : in.a == 1 ? "c1" : in.a == 2 ? "c2" : "c3 + j");
         break;
       case IHIP_EW_STORE:
-        s += fmt("%sstore_op<%d>(a, %d, row * D3 + c3, valid, r[%d]);\n", ind, out_dt[in.b], in.b, in.a);
+        s += fmt("%sstk<%d, '%c'>(a.out_ptr[%d], row * D3 + c3, valid, r[%d]);\n", ind, out_dt[in.b],
+                 out_kind[in.b], in.b, in.a);
         break;
       default: {
         // read only the operands the opcode uses (the others may be unwritten registers)
         const bool two = in.op >= IHIP_EW_ADD && in.op <= IHIP_EW_OR;
         const bool three = in.op == IHIP_EW_WHERE;
-        s += fmt("%s{ float t[EW_V]; for (int j = 0; j < EW_V; ++j) { const float x = r[%d][j];", ind, in.a);
-        if (two || three) s += fmt(" const float y = r[%d][j];", in.b);
-        if (three) s += fmt(" const float z = r[%d][j];", in.c);
+        std::string xs = fmt(" const float x = r[%d][j];", in.a);
+        if (two || three) xs += fmt(" const float y = r[%d][j];", in.b);
+        if (three) xs += fmt(" const float z = r[%d][j];", in.c);
+        if (in.op == IHIP_EW_DIV || in.op == IHIP_EW_RSQRT) {
+          // fast form over the whole vector, one (rarely taken) branch to the checked form
+          const bool div = in.op == IHIP_EW_DIV;
+          s += fmt("%s{ float t[EW_V]; bool bad = false; for (int j = 0; j < EW_V; ++j) {%s t[j] = %s; }"
+                   " if (bad) for (int j = 0; j < EW_V; ++j) {%s t[j] = %s; }"
+                   " for (int j = 0; j < EW_V; ++j) r[%d][j] = t[j]; }\n",
+                   ind, xs.c_str(), div ? "ew_div_fast(x, y, bad)" : "ew_rsqrt_fast(x, bad)", xs.c_str(),
+                   expr_of(in.op), in.dst);
+          break;
+        }
+        s += fmt("%s{ float t[EW_V]; for (int j = 0; j < EW_V; ++j) {%s", ind, xs.c_str());
         s += fmt(" t[j] = %s; } for (int j = 0; j < EW_V; ++j) r[%d][j] = t[j]; }\n", expr_of(in.op), in.dst);
       }
     }
@@ -291,11 +340,13 @@ static std::string ew_jit_body(const ihip_ew_instr* code, int n_code, const int*
 }
 
 std::string ew_jit_source(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
-                          const int* out_dt, uint32_t tile_mask) {
+                          const int* out_dt, const char* in_kind, const char* out_kind) {
   const int V = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt);
   std::string s = fmt("#define EW_V %d\n", V);
   s += kPrelude;
-  if (tile_mask == 0) {
+  int nt = 0;
+  for (int k = 0; k < n_inputs; ++k) nt += is_tiled(in_kind[k]);
+  if (nt == 0) {
     s += "extern \"C\" __global__ __launch_bounds__(256) void ihip_ew_jit(const EwJitArgs a) {\n"
          "  const i64 D1 = a.shape[1], D2 = a.shape[2], D3 = a.shape[3];\n"
          "  for (i64 row = blockIdx.y; row < a.rows; row += gridDim.y) {\n"
@@ -305,67 +356,116 @@ std::string ew_jit_source(const ihip_ew_instr* code, int n_code, int n_inputs, c
          "      const i64 c3 = vec * EW_V;\n"
          "      const int valid = D3 - c3 < EW_V ? (int)(D3 - c3) : EW_V;\n"
          "      float r[8][EW_V];\n";
-    s += ew_jit_body(code, n_code, in_dt, out_dt, 0, "      ");
+    s += ew_jit_body(code, n_code, in_dt, out_dt, in_kind, out_kind, false, "      ");
     s += "    }\n  }\n}\n";
     return s;
   }
   // Tiled form for inputs read across their unit-stride axis (axis 2 contiguous, axis 3
   // strided, e.g. a transpose): a workgroup takes 64 rows (axis 2) x 64 columns (axis 3).
-  // Each staged input is read into LDS with consecutive threads on consecutive addresses of
-  // its axis 2.  Then 64/EW_V consecutive threads cover one row's 64 columns (EW_V each), so
-  // stores and the other operands' accesses stay contiguous, in 16/EW_V passes of 4*EW_V
-  // rows.  The 65-float tile pitch keeps both the staging writes and the reads conflict-free.
-  const int nt = __builtin_popcount(tile_mask);
-  s += fmt("#define EW_NT %d\n", nt);
+  // Each staged input is read with consecutive threads on consecutive addresses of its axis 2
+  // (16-byte vectors for kind 'v', elements for 't') and written to an LDS tile.  Then 64/EW_V
+  // consecutive threads cover one row's 64 columns (EW_V each), so stores and the other
+  // operands' accesses stay contiguous, in 16/EW_V passes of 4*EW_V rows.  The 65-float tile
+  // pitch keeps both the staging writes and the reads conflict-free.
+  // Every global load of a tile (staging, and the other inputs for all passes) is issued
+  // before the first wait: lanes outside the tensor load from a clamped, valid address, so no
+  // load sits behind a branch.  Such values only reach elements that are never stored.
+  // Tile order: workgroups are dispatched in order of their linear id, and EW_GROUP
+  // consecutive ids take consecutive axis-2 tiles at the same axis-3 tile.  With EW_GROUP =
+  // 64 / element size, their staging reads cover 4 KiB of each source row; measured on
+  // 8192^2 transposes: 4.9 TB/s (f32) and 4.6 TB/s (f16), against 4.3 and 3.7 with the
+  // axis-3 tiles consecutive.
+  int esz = 1;
+  for (int k = 0; k < n_inputs; ++k)
+    if (is_tiled(in_kind[k])) esz = std::max(esz, (in_dt[k] == IHIP_DT_F32 || in_dt[k] == IHIP_DT_I32) ? 4 : 2);
+  s += fmt("#define EW_NT %d\n#define EW_GROUP %d\n", nt, 64 / esz);
   s += "extern \"C\" __global__ __launch_bounds__(256) void ihip_ew_jit(const EwJitArgs a) {\n"
        "  __shared__ float tile[EW_NT][64][65];\n"
        "  const i64 D0 = a.shape[0], D1 = a.shape[1], D2 = a.shape[2], D3 = a.shape[3];\n"
        "  const i64 T2 = (D2 + 63) / 64, ytiles = D0 * D1 * T2;\n"
        "  const int tid = threadIdx.x, l3 = (tid % (64 / EW_V)) * EW_V;\n"
-       "  for (i64 y = blockIdx.y; y < ytiles; y += gridDim.y) {\n"
-       "    const i64 u = y / T2, c2_0 = (y % T2) * 64, c1 = u % D1, c0 = u / D1;\n"
-       "    for (i64 c3_0 = (i64)blockIdx.x * 64; c3_0 < D3; c3_0 += (i64)gridDim.x * 64) {\n"
-       "      __syncthreads();  // the previous tile is consumed\n";
+       "  const i64 TX = (D3 + 63) / 64, ntiles = ytiles * TX;\n"
+       "  for (i64 t = blockIdx.x + (i64)gridDim.x * blockIdx.y; t < ntiles; t += (i64)gridDim.x * gridDim.y) {\n"
+       "    const i64 g = t / (EW_GROUP * TX), w = t % (EW_GROUP * TX);\n"
+       "    const i64 gs = ytiles - g * EW_GROUP < EW_GROUP ? ytiles - g * EW_GROUP : EW_GROUP;\n"
+       "    const i64 y = g * EW_GROUP + w % gs, u = y / T2, c2_0 = (y % T2) * 64, c1 = u % D1, c0 = u / D1;\n"
+       "    {\n"
+       "      const i64 c3_0 = (w / gs) * 64;\n";
+  for (int k = 0; k < n_inputs; ++k) {
+    if (in_kind[k] == 'v') {
+      // VS elements of axis 2 per thread, 64/VS threads per tile row, 16/VS rows per thread
+      const int vs = (in_dt[k] == IHIP_DT_F32 || in_dt[k] == IHIP_DT_I32) ? 4 : 8;
+      s += fmt("      float sv%d[16 / %d][%d];\n"
+               "      {\n"
+               "        const void* p = a.in_ptr[%d];\n"
+               "        const i64 base = c0 * a.in_stride[%d][0] + c1 * a.in_stride[%d][1], s3 = a.in_stride[%d][3];\n"
+               "        const i64 g2 = c2_0 + (tid %% (64 / %d)) * %d;\n"
+               "#pragma unroll\n"
+               "        for (int i = 0; i < 16 / %d; ++i) {\n"
+               "          const i64 g3 = c3_0 + i * 4 * %d + tid / (64 / %d);\n"
+               "          ld%d<%d>(p, g2 < D2 && g3 < D3 ? base + g2 + g3 * s3 : base, sv%d[i]);\n"
+               "        }\n"
+               "      }\n",
+               k, vs, vs, k, k, k, k, vs, vs, vs, vs, vs, vs, in_dt[k], k);
+    } else if (in_kind[k] == 't') {
+      s += fmt("      float sv%d[16];\n"
+               "      {\n"
+               "        const void* p = a.in_ptr[%d];\n"
+               "        const i64 base = c0 * a.in_stride[%d][0] + c1 * a.in_stride[%d][1], s3 = a.in_stride[%d][3];\n"
+               "        const i64 g2 = c2_0 + (tid & 63);\n"
+               "#pragma unroll\n"
+               "        for (int i = 0; i < 16; ++i) {\n"
+               "          const i64 g3 = c3_0 + (tid >> 6) + 4 * i;\n"
+               "          sv%d[i] = ld1<%d>(p, g2 < D2 && g3 < D3 ? base + g2 + g3 * s3 : base);\n"
+               "        }\n"
+               "      }\n",
+               k, k, k, k, k, k, in_dt[k]);
+    }
+  }
+  // the other inputs the program loads, for every pass, at clamped coordinates
+  s += "      const i64 c3 = c3_0 + l3, c3c = c3 < D3 ? c3 : 0;\n"
+       "      const int valid = D3 - c3 < EW_V ? (int)(D3 - c3) : EW_V;\n";
+  uint32_t loaded = 0;
+  for (int pc = 0; pc < n_code; ++pc)
+    if (code[pc].op == IHIP_EW_LOAD && !is_tiled(in_kind[code[pc].a])) loaded |= 1u << code[pc].a;
+  for (int k = 0; k < n_inputs; ++k)
+    if ((loaded >> k) & 1u) s += fmt("      float pre%d[16 / EW_V][EW_V];\n", k);
+  if (loaded) {
+    s += "#pragma unroll\n"
+         "      for (int pass = 0; pass < 16 / EW_V; ++pass) {\n"
+         "        const i64 c2 = c2_0 + pass * 4 * EW_V + tid / (64 / EW_V), c2c = c2 < D2 ? c2 : D2 - 1;\n";
+    for (int k = 0; k < n_inputs; ++k)
+      if ((loaded >> k) & 1u)
+        s += fmt("        ldk<%d, '%c'>(a.in_ptr[%d], c0 * a.in_stride[%d][0] + c1 * a.in_stride[%d][1] + c2c * "
+                 "a.in_stride[%d][2], c3c, a.in_stride[%d][3], valid, pre%d[pass]);\n",
+                 in_dt[k], in_kind[k], k, k, k, k, k, k);
+    s += "      }\n";
+  }
+  s += "      __syncthreads();  // the previous tile is consumed\n";
   int slot = 0;
   for (int k = 0; k < n_inputs; ++k) {
-    if (!((tile_mask >> k) & 1u)) continue;
-    // 16-byte staging reads: VS elements of axis 2 per thread, 64/VS threads per tile row
-    const int vs = (in_dt[k] == IHIP_DT_F32 || in_dt[k] == IHIP_DT_I32) ? 4 : 8;
-    s += fmt("      {\n"
-             "        const void* p = a.in_ptr[%d];\n"
-             "        const i64 base = c0 * a.in_stride[%d][0] + c1 * a.in_stride[%d][1], s3 = a.in_stride[%d][3];\n"
-             "        if ((a.in_stage_vec >> %d) & 1u) {\n"
-             "          const int cc = (tid %% (64 / %d)) * %d;\n"
-             "          const i64 g2 = c2_0 + cc;\n"
-             "          for (int i = 0; i < 16 / %d; ++i) {\n"
-             "            const int r3 = i * 4 * %d + tid / (64 / %d);\n"
-             "            const i64 g3 = c3_0 + r3;\n"
-             "            float v[%d];\n"
-             "            if (g2 < D2 && g3 < D3) ld%d<%d>(p, base + g2 + g3 * s3, v);\n"
-             "            else for (int e = 0; e < %d; ++e) v[e] = 0.0f;\n"
-             "            for (int e = 0; e < %d; ++e) tile[%d][r3][cc + e] = v[e];\n"
-             "          }\n"
-             "        } else {\n"
-             "          const i64 g2 = c2_0 + (tid & 63);\n"
-             "          for (int i = 0; i < 16; ++i) {\n"
-             "            const int r3 = (tid >> 6) + 4 * i;\n"
-             "            const i64 g3 = c3_0 + r3;\n"
-             "            tile[%d][r3][tid & 63] = (g2 < D2 && g3 < D3) ? ld1<%d>(p, base + g2 + g3 * s3) : 0.0f;\n"
-             "          }\n"
-             "        }\n"
-             "      }\n",
-             k, k, k, k, k, vs, vs, vs, vs, vs, vs, vs, in_dt[k], vs, vs, slot, slot, in_dt[k]);
-    ++slot;
+    if (in_kind[k] == 'v') {
+      const int vs = (in_dt[k] == IHIP_DT_F32 || in_dt[k] == IHIP_DT_I32) ? 4 : 8;
+      s += fmt("#pragma unroll\n"
+               "      for (int i = 0; i < 16 / %d; ++i)\n"
+               "        for (int e = 0; e < %d; ++e)\n"
+               "          tile[%d][i * 4 * %d + tid / (64 / %d)][(tid %% (64 / %d)) * %d + e] = sv%d[i][e];\n",
+               vs, vs, slot, vs, vs, vs, vs, k);
+      ++slot;
+    } else if (in_kind[k] == 't') {
+      s += fmt("#pragma unroll\n"
+               "      for (int i = 0; i < 16; ++i) tile[%d][(tid >> 6) + 4 * i][tid & 63] = sv%d[i];\n", slot, k);
+      ++slot;
+    }
   }
   s += "      __syncthreads();\n"
-       "      const i64 c3 = c3_0 + l3;\n"
-       "      const int valid = D3 - c3 < EW_V ? (int)(D3 - c3) : EW_V;\n"
-       "      for (int pass = 0; pass < 16 / EW_V && c3 < D3; ++pass) {\n"
+       "#pragma unroll\n"
+       "      for (int pass = 0; pass < 16 / EW_V; ++pass) {\n"
        "        const int l2 = pass * 4 * EW_V + tid / (64 / EW_V);\n"
        "        const i64 c2 = c2_0 + l2, row = (c0 * D1 + c1) * D2 + c2;\n"
-       "        if (c2 < D2) {\n"
+       "        if (c2 < D2 && c3 < D3) {\n"
        "          float r[8][EW_V];\n";
-  s += ew_jit_body(code, n_code, in_dt, out_dt, tile_mask, "          ");
+  s += ew_jit_body(code, n_code, in_dt, out_dt, in_kind, out_kind, true, "          ");
   s += "        }\n      }\n    }\n  }\n}\n";
   return s;
 }
@@ -419,23 +519,21 @@ JitEntry& entry(const std::string& src) {
 
 }  // namespace
 
-// Compile (once) the native code of a validated program for the given operand types; no
-// device is needed.  Returns false with *why set when compilation fails.
-bool prepare_elementwise_jit(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
-                             const int* out_dt, std::string* why) {
-  const std::string src = ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt, 0);
-  std::lock_guard<std::mutex> lock(g_jit_mu);
-  JitEntry& e = entry(src);
-  if (!e.error.empty() && why) *why = e.error;
-  return e.error.empty();
-}
+namespace {
 
-// Launch the specialised kernel of a validated program; compiles on first use.  Returns
-// hipErrorNotSupported with *why set when the program cannot be compiled.
-hipError_t launch_elementwise_jit(const ihip_ew_instr* code, int n_code, const ihip_ew_operand* inputs, int n_inputs,
-                                  const ihip_ew_operand* outputs, int n_outputs, const int64_t (&shape)[4],
-                                  hipStream_t s, std::string* why) {
+// Kernel arguments, generated source and grid of one launch of a validated program.
+struct JitPlan {
   EwJitArgs a{};
+  std::string src;
+  unsigned gx = 0, gy = 0;
+};
+
+// Plans a launch: the access form of every operand (see ldk), the LDS-staged inputs, the
+// arguments and the grid.  Returns false for an empty iteration space (nothing to launch).
+// Pointers are only inspected for alignment, so this needs no device.
+bool plan_jit(const ihip_ew_instr* code, int n_code, const ihip_ew_operand* inputs, int n_inputs,
+              const ihip_ew_operand* outputs, int n_outputs, const int64_t (&shape)[4], JitPlan& pl) {
+  EwJitArgs& a = pl.a;
   for (int d = 0; d < 4; ++d) a.shape[d] = shape[d];
   int in_dt[IHIP_EW_MAX_INPUTS] = {}, out_dt[IHIP_EW_MAX_OUTPUTS] = {};
   for (int k = 0; k < n_inputs; ++k) in_dt[k] = inputs[k].dtype;
@@ -443,7 +541,7 @@ hipError_t launch_elementwise_jit(const ihip_ew_instr* code, int n_code, const i
   const int V = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt);
   a.rows = shape[0] * shape[1] * shape[2];
   a.nvec = (shape[3] + V - 1) / V;
-  if (a.rows == 0 || a.nvec == 0) return hipSuccess;
+  if (a.rows == 0 || a.nvec == 0) return false;
   const auto esize = [](int dt) -> int64_t { return dt == IHIP_DT_F32 || dt == IHIP_DT_I32 ? 4 : dt == IHIP_DT_BOOL ? 1 : 2; };
   // W-element vectors need every row to start at a multiple of W elements and an aligned base.
   const auto vec_ok = [&](const void* ptr, const int64_t* st, int dt, int64_t w) {
@@ -451,17 +549,6 @@ hipError_t launch_elementwise_jit(const ihip_ew_instr* code, int n_code, const i
                                           (st[2] % w == 0 || shape[2] == 1) && st[3] == 1);
     return shape[3] % w == 0 && rows && reinterpret_cast<uintptr_t>(ptr) % (w * esize(dt)) == 0;
   };
-  for (int k = 0; k < n_inputs; ++k) {
-    a.in_ptr[k] = inputs[k].ptr;
-    for (int d = 0; d < 4; ++d) a.in_stride[k][d] = inputs[k].stride[d];
-    if (V == 8 && vec_ok(inputs[k].ptr, inputs[k].stride, in_dt[k], 8)) a.in_vec8 |= 1u << k;
-    else if (vec_ok(inputs[k].ptr, inputs[k].stride, in_dt[k], 4)) a.in_vec4 |= 1u << k;
-  }
-  for (int k = 0; k < n_outputs; ++k) {
-    a.out_ptr[k] = const_cast<void*>(outputs[k].ptr);
-    if (V == 8 && vec_ok(outputs[k].ptr, nullptr, out_dt[k], 8)) a.out_vec8 |= 1u << k;
-    else if (vec_ok(outputs[k].ptr, nullptr, out_dt[k], 4)) a.out_vec4 |= 1u << k;
-  }
   // Inputs read across their unit-stride axis (axis 2 contiguous, axis 3 strided) are staged
   // through LDS tiles, at most kMaxTiled of them (16.6 KiB each).
   constexpr int kMaxTiled = 4;
@@ -469,24 +556,92 @@ hipError_t launch_elementwise_jit(const ihip_ew_instr* code, int n_code, const i
   if (shape[2] > 1 && shape[3] > 1)
     for (int k = 0; k < n_inputs && __builtin_popcount(tile_mask) < kMaxTiled; ++k)
       if (inputs[k].stride[2] == 1 && inputs[k].stride[3] != 0 && inputs[k].stride[3] != 1) tile_mask |= 1u << k;
-  // A staged input is read in 16-byte vectors when every vector starts at a multiple of its
-  // width and stays inside axis 2.
-  for (int k = 0; k < n_inputs; ++k) {
-    if (!((tile_mask >> k) & 1u)) continue;
+  // A staged input is read in 16-byte vectors ('v', else element-wise 't') when every vector
+  // starts at a multiple of its width and stays inside axis 2.
+  const auto stage_vec = [&](int k) {
     const int64_t vs = (in_dt[k] == IHIP_DT_F32 || in_dt[k] == IHIP_DT_I32) ? 4 : 8;
     const int64_t* st = inputs[k].stride;
-    if (shape[2] % vs == 0 && st[3] % vs == 0 && (st[0] % vs == 0 || shape[0] == 1) &&
-        (st[1] % vs == 0 || shape[1] == 1) && reinterpret_cast<uintptr_t>(inputs[k].ptr) % 16 == 0)
-      a.in_stage_vec |= 1u << k;
+    return shape[2] % vs == 0 && st[3] % vs == 0 && (st[0] % vs == 0 || shape[0] == 1) &&
+           (st[1] % vs == 0 || shape[1] == 1) && reinterpret_cast<uintptr_t>(inputs[k].ptr) % 16 == 0;
+  };
+  char in_kind[IHIP_EW_MAX_INPUTS + 1] = {}, out_kind[IHIP_EW_MAX_OUTPUTS + 1] = {};
+  for (int k = 0; k < n_inputs; ++k) {
+    a.in_ptr[k] = inputs[k].ptr;
+    for (int d = 0; d < 4; ++d) a.in_stride[k][d] = inputs[k].stride[d];
+    const int64_t* st = inputs[k].stride;
+    in_kind[k] = ((tile_mask >> k) & 1u)                          ? (stage_vec(k) ? 'v' : 't')
+                 : (V == 8 && vec_ok(inputs[k].ptr, st, in_dt[k], 8)) ? '8'
+                 : vec_ok(inputs[k].ptr, st, in_dt[k], 4)               ? '4'
+                 : st[3] == 0                                           ? 'b'
+                                                                        : 's';
   }
+  for (int k = 0; k < n_outputs; ++k) {
+    a.out_ptr[k] = const_cast<void*>(outputs[k].ptr);
+    out_kind[k] = (V == 8 && vec_ok(outputs[k].ptr, nullptr, out_dt[k], 8)) ? '8'
+                  : vec_ok(outputs[k].ptr, nullptr, out_dt[k], 4)            ? '4'
+                                                                             : 's';
+  }
+  pl.src = ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt, in_kind, out_kind);
+  if (tile_mask != 0) {  // one workgroup per 64 x 64 tile (linear id; grid-strided beyond the grid limits)
+    const int64_t tx = (shape[3] + 63) / 64, ty = shape[0] * shape[1] * ((shape[2] + 63) / 64);
+    pl.gx = static_cast<unsigned>(tx < 65535 ? tx : 65535);
+    pl.gy = static_cast<unsigned>(ty < 65535 ? ty : 65535);
+  } else {  // a few thousand 256-lane workgroups, grid-strided over rows and vectors
+    const int64_t bx = (a.nvec + 255) / 256;
+    pl.gx = static_cast<unsigned>(bx < 1024 ? bx : 1024);
+    int64_t gy = (4096 + pl.gx - 1) / pl.gx;
+    if (gy > a.rows) gy = a.rows;
+    if (gy > 65535) gy = 65535;
+    pl.gy = static_cast<unsigned>(gy);
+  }
+  return true;
+}
+
+bool compile_checked(const std::string& src, std::string* why) {
+  std::lock_guard<std::mutex> lock(g_jit_mu);
+  JitEntry& e = entry(src);
+  if (!e.error.empty() && why) *why = e.error;
+  return e.error.empty();
+}
+
+}  // namespace
+
+// Compile (once) the native code of a validated program for the given operand types, in the
+// form that dense operands select (every input and output read and written in full-width
+// vectors); no device is needed.  Returns false with *why set when compilation fails.
+bool prepare_elementwise_jit(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
+                             const int* out_dt, std::string* why) {
+  const char w = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt) == 8 ? '8' : '4';
+  char in_kind[IHIP_EW_MAX_INPUTS + 1] = {}, out_kind[IHIP_EW_MAX_OUTPUTS + 1] = {};
+  for (int k = 0; k < n_inputs; ++k) in_kind[k] = w;
+  for (int k = 0; k < n_outputs; ++k) out_kind[k] = w;
+  return compile_checked(ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt, in_kind, out_kind), why);
+}
+
+// Compile (once) exactly the code that launch_elementwise_jit would run for these operands and
+// shape; no device is needed.
+bool prepare_elementwise_jit_operands(const ihip_ew_instr* code, int n_code, const ihip_ew_operand* inputs,
+                                      int n_inputs, const ihip_ew_operand* outputs, int n_outputs,
+                                      const int64_t (&shape)[4], std::string* why) {
+  JitPlan pl;
+  if (!plan_jit(code, n_code, inputs, n_inputs, outputs, n_outputs, shape, pl)) return true;
+  return compile_checked(pl.src, why);
+}
+
+// Launch the specialised kernel of a validated program; compiles on first use.  Returns
+// hipErrorNotSupported with *why set when the program cannot be compiled.
+hipError_t launch_elementwise_jit(const ihip_ew_instr* code, int n_code, const ihip_ew_operand* inputs, int n_inputs,
+                                  const ihip_ew_operand* outputs, int n_outputs, const int64_t (&shape)[4],
+                                  hipStream_t s, std::string* why) {
+  JitPlan pl;
+  if (!plan_jit(code, n_code, inputs, n_inputs, outputs, n_outputs, shape, pl)) return hipSuccess;
   int dev = 0;
   hipError_t he = hipGetDevice(&dev);
   if (he != hipSuccess) return he;
-  const std::string src = ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt, tile_mask);
   hipFunction_t fn = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_jit_mu);
-    JitEntry& e = entry(src);
+    JitEntry& e = entry(pl.src);
     if (!e.error.empty()) {
       if (why) *why = e.error;
       return hipErrorNotSupported;
@@ -502,19 +657,8 @@ hipError_t launch_elementwise_jit(const ihip_ew_instr* code, int n_code, const i
       fn = f->second;
     }
   }
-  void* params[] = {&a};
-  if (tile_mask != 0) {  // one workgroup per 64 x 64 tile (grid-strided beyond the grid limits)
-    const int64_t tx = (shape[3] + 63) / 64, ty = shape[0] * shape[1] * ((shape[2] + 63) / 64);
-    const unsigned gx = static_cast<unsigned>(tx < 65535 ? tx : 65535);
-    const unsigned gy = static_cast<unsigned>(ty < 65535 ? ty : 65535);
-    return hipModuleLaunchKernel(fn, gx, gy, 1, 256, 1, 1, 0, s, params, nullptr);
-  }
-  const int64_t bx = (a.nvec + 255) / 256;
-  const unsigned gx = static_cast<unsigned>(bx < 1024 ? bx : 1024);
-  int64_t gy = (4096 + gx - 1) / gx;
-  if (gy > a.rows) gy = a.rows;
-  if (gy > 65535) gy = 65535;
-  return hipModuleLaunchKernel(fn, gx, static_cast<unsigned>(gy), 1, 256, 1, 1, 0, s, params, nullptr);
+  void* params[] = {&pl.a};
+  return hipModuleLaunchKernel(fn, pl.gx, pl.gy, 1, 256, 1, 1, 0, s, params, nullptr);
 }
 
 }  // namespace ihip

@@ -49,6 +49,7 @@ SIGNATURES: Dict[str, Tuple[Any, Tuple[Any, ...]]] = {
     "ihip_elementwise_program": (_I32, (_P, _I32, _P, _I32, _P, _I32, _P, _I32, _P)),
     "ihip_elementwise_mode": (_I32, (_I32,)),
     "ihip_elementwise_prepare": (_I32, (_P, _I32, _P, _I32, _P, _I32)),
+    "ihip_elementwise_prepare_operands": (_I32, (_P, _I32, _P, _I32, _P, _I32, _P, _I32)),
 }
 EW_MODE_AUTO, EW_MODE_INTERP, EW_MODE_NATIVE = 0, 1, 2
 

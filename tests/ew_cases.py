@@ -213,6 +213,24 @@ case("special_values", {
             op("ne", ["x", "z"], "ne")], "outputs": ["mx", "ne"]},
     {"N": 8}, lambda r, b: {"x": np.array([np.nan, -0.0, 0.0, np.inf, -np.inf, -1.0, 1e-45, 3.0], np.float32)})
 
+# division and rsqrt where the reciprocal form fails (zero, inf, NaN, denormal and huge
+# divisors, overflowing quotients), mixed into vectors of ordinary values
+def _div_special(r, b):
+    n = b["N"]
+    x, y = _f(r, n), _f(r, n)
+    sx = [1.0, 3e38, -2.0, np.inf, np.nan, 1e-30, 0.0, -1.0, 5.0, 1e-45, 2.0, -np.inf]
+    sy = [0.0, 1e-3, -0.0, 2.0, 1.0, 1e10, 0.0, np.inf, 1e-40, 3e-39, 1e38, np.nan]
+    for i, (a, c) in enumerate(zip(sx, sy)):
+        if 5 * i + 1 < n:
+            x[5 * i + 1], y[5 * i + 1] = a, c
+    return {"x": x, "y": y}
+
+
+case("div_rsqrt_special", {
+    "tensors": {"x": T("f32", "N"), "y": T("f32", "N"), "q": T("f32", "N"), "s": T("f32", "N")},
+    "ops": [op("div", ["x", "y"], "q"), op("rsqrt", ["y"], "s")], "outputs": ["q", "s"]},
+    {"N": 67}, _div_special)
+
 # empty iteration space
 case("empty", {
     "tensors": {"x": T("f32", "M", "N"), "y": T("f32", "M", "N")},

@@ -237,6 +237,26 @@ def test_native_code_compiles(name, ir, bindings, gen):
     assert st == 0, lib.ihip_last_error().decode()
 
 
+@pytest.mark.parametrize("misalign", [0, 4], ids=["aligned", "misaligned"])
+@pytest.mark.parametrize("name,ir,bindings,gen", CASES, ids=[c[0] for c in CASES])
+def test_native_code_compiles_for_launch_operands(name, ir, bindings, gen, misalign):
+    """ihip_elementwise_prepare_operands compiles the form a launch with these operands runs: the
+    access form of each operand follows its strides and alignment (4 bytes off 16 selects narrower
+    or element-wise accesses), transposed operands select the LDS-tiled form.  No device needed:
+    the pointers are only inspected for alignment."""
+    from intent_ir_amd.runtime import ew_program_args, load_library
+
+    lib = load_library()
+    k = lower_intent_to_hip_kernel(ir, shape_bindings=bindings)
+    prog = k.call_args[0][1]
+    dt = {n: t["dtype"] for n, t in k.io_spec["tensors"].items()}
+    names = [n for n, _ in prog.inputs] + list(prog.outputs)
+    ptrs = {n: 0x100000 * (i + 1) + misalign for i, n in enumerate(names)}
+    args = ew_program_args(prog, ptrs, dt)
+    st = lib.ihip_elementwise_prepare_operands(*args[:8])
+    assert st == 0, lib.ihip_last_error().decode()
+
+
 def test_prepare_rejects_bad_programs():
     from intent_ir_amd.runtime import EwInstr, load_library
 

@@ -70,6 +70,11 @@ def test_run_diff_elementwise_chains(hip, name, ir, bindings, gen):
     axes = sorted(bindings)
     if not axes or 0 in bindings.values() or name == "special_values":
         pytest.skip("no symbolic axis to sweep (fixed-size inputs)")
+    if name == "div_rsqrt_special":
+        # its outputs hold NaN, and the reference's rule (diff_runner.py:390-391) compares
+        # non-finite values with np.array_equal, false for NaN; tests/test_gpu_ewprogram.py judges
+        # this case with NaN equal to NaN
+        pytest.skip("NaN outputs: the reference diff rule cannot pass by construction")
     # 16-bit outputs come back widened to f32, so the reference would infer f32 tolerances for
     # them; judge them at their own resolution instead
     out16 = [ir["tensors"][o]["dtype"] for o in ir["outputs"] if ir["tensors"][o]["dtype"] in ("f16", "bf16")]
