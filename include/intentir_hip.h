@@ -85,7 +85,9 @@ int ihip_bias_gelu_tanh_axpy_bf16(const uint16_t* x, const uint16_t* bias, uint1
  * (round to nearest even).  Replaces _kernel_matmul_f32 / wmma_matmul_f32_tf32
  * (backends/cuda/codegen/intentir_to_cuda.py:537-985,
  * backends/cuda/runtime/kernels/wmma_matmul.cuh:124-565), which lower matmul
- * only as a lone op (:2137-2140). */
+ * only as a lone op (:2137-2140).  Any shape: rows that all start 16-byte aligned
+ * (N % 8 == 0, K % 8 == 0, 16-byte aligned A, B, C) run the tiled MFMA kernel at any
+ * M, N, K; other shapes a slower guarded kernel with the same accumulation order. */
 int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                              int64_t N, int64_t K, int relu, void* stream);
 

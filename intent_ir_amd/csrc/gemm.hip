@@ -2,9 +2,10 @@
 // [N,K] transposed), bf16 row-major, bias f32 [N], f32 accumulation on CDNA4 MFMA,
 // C bf16 (RNE) — any shape.
 //
-// Entry point of the GEMM family: full 256x256 tiles with K a multiple of the fast
-// path's K step and 16-byte aligned operands go to gemm_fast.hip; every other shape
-// runs the guarded kernel below, which stages operands through registers:
+// Entry point of the GEMM family: shapes whose rows are all 16-byte aligned (N % 8 == 0,
+// M % 8 == 0 for a transposed A) with K a multiple of the fast path's K step and 16-byte
+// aligned operands go to gemm_fast.hip, for any M and N; every other shape runs the
+// guarded kernel below, which stages operands through registers:
 //  * workgroup tile 256(M) x 256(N), K step 64; 256 threads = 4 waves in a 2x2 grid,
 //    each wave owning a 128x128 sub-tile = 4x4 blocks of v_mfma_f32_32x32x16_bf16;
 //  * LDS double buffer: A tile as [m][k] and B tile transposed to [n][k] (rows padded
@@ -217,7 +218,7 @@ void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* 
   }
 }
 
-bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* C);
+bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, const void* A, const void* B, const void* C);
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
                             int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s);
 
@@ -232,7 +233,7 @@ hipError_t launch_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, cons
                                       int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu,
                                       hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (gemm_fast_fits(M, N, K, A, B, C)) return launch_gemm_fast(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
+  if (gemm_fast_fits(M, N, K, transpose_a, A, B, C)) return launch_gemm_fast(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
   const int64_t tm = (M + kBM - 1) / kBM, tn = (N + kBN - 1) / kBN;
   if (tm * tn > 0x7fffffffLL) return hipErrorInvalidValue;
   const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);

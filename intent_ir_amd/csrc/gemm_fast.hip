@@ -1,7 +1,10 @@
-// Full-tile bf16 GEMM for gfx950: C = act(A @ B + bias), A [M,K], B [K,N] row-major bf16,
-// f32 accumulation on v_mfma_f32_32x32x16_bf16, C bf16 (RNE).  Requires M % 256 == 0,
-// N % 256 == 0, K % DK == 0 and 16-byte aligned A, B, C; other shapes take the guarded
-// kernel in gemm.hip.
+// Tiled bf16 GEMM for gfx950: C = act(A @ B + bias), A [M,K], B [K,N] row-major bf16,
+// f32 accumulation on v_mfma_f32_32x32x16_bf16, C bf16 (RNE).  Any M and N; requires
+// K % DK == 0, every row of A, B and C 16-byte aligned (N % 8 == 0, and M % 8 == 0 when A
+// is given as [K,M]) and 16-byte aligned bases; other shapes take the guarded kernel in
+// gemm.hip.  Edge tiles: copies read through a range-checked buffer descriptor (zeros past
+// the end of a tensor), and what an edge tile reads outside [M) x [N) only reaches C rows
+// >= M or columns >= N, which are never stored.
 //
 // Work decomposition
 //  * one 256x256 C tile per workgroup of 256 threads = 4 waves in a 2x2 grid; wave (wm, wn)
@@ -15,8 +18,8 @@
 //  * a ring of STAGES LDS stages, each holding a 256 x DK slice of A and a DK x 256 slice
 //    of B; the copy of K-slice kt+STAGES-1 is issued while slice kt is multiplied, so a
 //    copy has STAGES-1 slices of MFMA time to land;
-//  * copies use gfx950's direct-to-LDS loads (global_load_lds_dwordx4): lane l of a wave
-//    writes 16 bytes at LDS m0 + 16*l; no VGPR holds tile data;
+//  * copies use gfx950's direct-to-LDS loads (buffer_load_dwordx4 ... lds): lane l of a
+//    wave writes 16 bytes at LDS m0 + 16*l; no VGPR holds tile data;
 //  * because the LDS position is fixed by the lane, bank conflicts are avoided by choosing
 //    which global 16-byte chunk each lane fetches (XOR swizzles, 64-bank LDS):
 //      A row r (DK*2 bytes) stores logical k-chunk c in slot c ^ ((r / RPW) % CA), where
@@ -39,6 +42,7 @@ namespace ihip {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x8_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
@@ -58,7 +62,9 @@ typedef __bf16 bf16x2_pk_t __attribute__((ext_vector_type(2)));
 // is staged as [256 rows][DK] and read with ds_read_b128; a K-major one as [DK][256] and read
 // with the transposing ds_read_b64_tr_b16.  Either way the MFMA sees the same fragments, so
 // every layout accumulates in the same order and gives identical results.
-template <int DK, int STAGES, bool AKM = false, bool BKM = true>
+// EDGE: the tile reaches past M or N; its copies go through range-checked buffer descriptors
+// (interior tiles use global_load_lds, which measured ~14% faster on full 8192^3 GEMMs).
+template <int DK, int STAGES, bool AKM = false, bool BKM = true, bool EDGE = false>
 struct FastGemm {
   static constexpr int kRowA = DK * 2;             // bytes per K-contiguous tile row
   static constexpr int kChunksA = DK / 8;          // 16-byte chunks per row
@@ -84,6 +90,7 @@ struct FastGemm {
   // offsets.  K-contiguous operand: off[kk], blocks at a fixed stride; K-major: off[block].
   struct Lane {
     uint32_t a, b;
+    int ka, kb;  // first k (within a slice) of the lane's 16-byte chunk; 0 for a K-major operand
     int fa[4], fb[4];
   };
 
@@ -98,6 +105,12 @@ struct FastGemm {
     // instruction j holds k-rows 2j, 2j+1; k & 3 == (2*wave + lane/32) & 3 for every i
     const int kb = 2 * wave + (lane >> 5);
     return 2u * static_cast<uint32_t>((lane >> 5) * ld + b_logical(lane & 31, kb) * 8);
+  }
+
+  // First k within the slice of the chunk a lane copies (K-contiguous operand; the swizzle
+  // term does not depend on the instruction).
+  static __device__ __forceinline__ int copy_k(bool kmajor, int wave, int lane) {
+    return kmajor ? 0 : a_slot(lane % kChunksA, wave * kRowsPerInstrA + lane / kChunksA) * 8;
   }
 
   // Fragment offsets of an operand whose wave rows start at `base` with blocks `step` apart.
@@ -122,36 +135,88 @@ struct FastGemm {
     Lane L;
     L.a = copy_off(AKM, M, K, wave, lane);
     L.b = copy_off(BKM, N, K, wave, lane);
+    L.ka = copy_k(AKM, wave, lane);
+    L.kb = copy_k(BKM, wave, lane);
     frag_off(AKM, 0, wm * 128, 32, lane, L.fa);
     frag_off(BKM, kStageA, wn * 32, 64, lane, L.fb);
     return L;
   }
 
+  // Raw buffer descriptor of the bytes from `base` to `end` (one past a tensor's last
+  // element): a lane whose offset reaches past the end reads zeros and touches no memory,
+  // which is what makes edge tiles (rows >= M, columns >= N) safe to copy.  The range check
+  // covers the VGPR offset (not the SGPR one), so every offset beyond `base` goes there.
+  static __device__ __forceinline__ i32x4_t rsrc_of(const uint16_t* base, const uint16_t* end) {
+    const int64_t left = (end - base) * 2;
+    const uint32_t records = left <= 0 ? 0u : left >= 0xffffffffll ? 0xffffffffu : static_cast<uint32_t>(left);
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    // word1: base address bits 47:32, stride 0; word3: 32-bit data format, raw (untyped) access
+    return i32x4_t{static_cast<int>(addr & 0xffffffffu), static_cast<int>((addr >> 32) & 0xffffu),
+                   static_cast<int>(records), 0x00020000};
+  }
+
+  // 16 bytes per lane into LDS at m0 + 16 * lane, from sbase + voff (global_load_lds) or
+  // from the descriptor's base + voff (buffer_load ... lds).  Inline asm, so the compiler does
+  // not treat a copy as an LDS store that every later LDS read must wait for; the kernel waits
+  // for the copies itself before reading a stage.
   static __device__ __forceinline__ void dma16(const uint16_t* sbase, uint32_t voff, uint32_t lds_addr) {
-    // Inline asm, so the compiler does not treat the copy as an LDS store that every later
-    // LDS read must wait for; the kernel waits for the copies itself before reading a stage.
     asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
+  }
+  static __device__ __forceinline__ void dma16(const i32x4_t& rsrc, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds_addr) : "memory");
+  }
+
+  // Lane offset that no descriptor covers (operands of a ragged-K launch are < 2 GiB).
+  static constexpr uint32_t kNoRecord = 0x80000000u;
+
+  // Copy instruction j of an operand slice starting at `base` (`end`: one past the tensor's
+  // last element; lane offset `off`).  In an edge tile, the lanes of a K-contiguous operand
+  // whose chunk starts at or past K (k_left = K - k0 elements remain from the slice start,
+  // chunk_k = the chunk's first k) take an offset past every record and load zeros; a
+  // K-major operand's k-rows past K lie past the tensor's end.
+  template <bool kKMajor>
+  static __device__ __forceinline__ void copy_one(const uint16_t* base, const uint16_t* end, int64_t ld, int64_t K,
+                                                  int j, uint32_t off, int64_t k_left, int chunk_k, uint32_t dst) {
+    if constexpr (EDGE)
+      dma16(rsrc_of(base, end), kKMajor || chunk_k < k_left ? off + instr_off<kKMajor>(j, ld, K) : kNoRecord, dst);
+    else
+      dma16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(base) + instr_off<kKMajor>(j, ld, K)), off,
+            dst);
+  }
+
+  // Byte offset of copy instruction j from its operand's slice base: tile rows j*RPI.. of a
+  // K-contiguous operand (leading dim K), k-rows 2j, 2j+1 of a K-major one (leading dim ld).
+  template <bool kKMajor>
+  static __device__ __forceinline__ uint32_t instr_off(int j, int64_t ld, int64_t K) {
+    return static_cast<uint32_t>(kKMajor ? 2 * j * ld * 2 : j * kRowsPerInstrA * K * 2);
+  }
+
+  // Slice base of an operand: tile rows x0.. at k0 (K-contiguous) or k-row k0 at column x0
+  // (K-major).
+  template <bool kKMajor>
+  static __device__ __forceinline__ const uint16_t* slice_base(const uint16_t* X, int64_t ld, int64_t K, int64_t x0,
+                                                               int64_t k0) {
+    return kKMajor ? X + k0 * ld + x0 : X + x0 * K + k0;
   }
 
   // One operand's share of a K slice: tile rows x0.. (K-contiguous) or k-rows k0.. (K-major).
   template <bool kKMajor, int kInstrOp>
-  static __device__ __forceinline__ void copy_operand(const uint16_t* __restrict__ X, int64_t ld, int64_t K,
-                                                      int64_t x0, int64_t k0, uint32_t dst, int wave, uint32_t off) {
+  static __device__ __forceinline__ void copy_operand(const uint16_t* __restrict__ X, const uint16_t* end, int64_t ld,
+                                                      int64_t K, int64_t x0, int64_t k0, uint32_t dst, int wave,
+                                                      uint32_t off, int chunk_k) {
+    const uint16_t* base = slice_base<kKMajor>(X, ld, K, x0, k0);
 #pragma unroll
     for (int i = 0; i < kInstrOp; ++i) {
       const int j = 4 * i + wave;
-      if (!kKMajor)
-        dma16(X + (x0 + j * kRowsPerInstrA) * K + k0, off, dst + j * 1024);
-      else
-        dma16(X + (k0 + 2 * j) * ld + x0, off, dst + j * 1024);
+      copy_one<kKMajor>(base, end, ld, K, j, off, K - k0, chunk_k, dst + j * 1024);
     }
   }
 
   static __device__ __forceinline__ void copy_slice(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                     int64_t M, int64_t N, int64_t K, int64_t m0, int64_t n0,
                                                     int64_t k0, uint32_t stage, int wave, const Lane& L) {
-    copy_operand<AKM, kInstrA>(A, M, K, m0, k0, stage, wave, L.a);
-    copy_operand<BKM, kInstrB>(B, N, K, n0, k0, stage + kStageA, wave, L.b);
+    copy_operand<AKM, kInstrA>(A, A + M * K, M, K, m0, k0, stage, wave, L.a, L.ka);
+    copy_operand<BKM, kInstrB>(B, B + K * N, N, K, n0, k0, stage + kStageA, wave, L.b, L.kb);
   }
 
   // Wait until at most `pending` slices of this wave's copies are still in flight
@@ -241,16 +306,11 @@ struct FastGemm {
                                                     int64_t k0, uint32_t stage, int wave, const Lane& L, int i) {
     if (i < kInstrA) {
       const int j = 4 * i + wave;
-      if (!AKM)
-        dma16(A + (m0 + j * kRowsPerInstrA) * K + k0, L.a, stage + j * 1024);
-      else
-        dma16(A + (k0 + 2 * j) * M + m0, L.a, stage + j * 1024);
+      copy_one<AKM>(slice_base<AKM>(A, M, K, m0, k0), A + M * K, M, K, j, L.a, K - k0, L.ka, stage + j * 1024);
     } else {
       const int j = 4 * (i - kInstrA) + wave;
-      if (!BKM)
-        dma16(B + (n0 + j * kRowsPerInstrA) * K + k0, L.b, stage + kStageA + j * 1024);
-      else
-        dma16(B + (k0 + 2 * j) * N + n0, L.b, stage + kStageA + j * 1024);
+      copy_one<BKM>(slice_base<BKM>(B, N, K, n0, k0), B + K * N, N, K, j, L.b, K - k0, L.kb,
+                    stage + kStageA + j * 1024);
     }
   }
 
@@ -263,32 +323,28 @@ struct FastGemm {
 
 };
 
-template <int DK, int STAGES, bool AKM = false, bool BKM = true>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const float* __restrict__ bias,
-                           uint16_t* __restrict__ C, int64_t M, int64_t N, int64_t K, int relu, int tiles_m,
-                           int tiles_n) {
-  using G = FastGemm<DK, STAGES, AKM, BKM>;
+constexpr int kCPitch = kTile * 2 + 16;  // bytes per staged C row (16 bytes of padding)
+
+// LDS bytes of the stage ring, which after the main loop holds the bf16 C tile.
+template <int DK, int STAGES>
+constexpr int fast_lds_bytes() {
+  return STAGES * FastGemm<DK, STAGES>::kStage > kTile * kCPitch ? STAGES * FastGemm<DK, STAGES>::kStage
+                                                                  : kTile * kCPitch;
+}
+
+// One 256x256 C tile at (m0, n0); lds_raw / bias_lds are the kernel's LDS.
+template <int DK, int STAGES, bool AKM, bool BKM, bool EDGE>
+__device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                               const float* __restrict__ bias, uint16_t* __restrict__ C, int64_t M,
+                                               int64_t N, int64_t K, int relu, int64_t m0, int64_t n0, char* lds_raw,
+                                               float* bias_lds) {
+  using G = FastGemm<DK, STAGES, AKM, BKM, EDGE>;
   static_assert(STAGES >= 3, "the pipeline keeps two slices ahead");
-  // The stage ring; after the main loop the same memory holds the bf16 C tile.
-  constexpr int kCPitch = kTile * 2 + 16;  // bytes per staged C row (16 bytes of padding)
-  constexpr int kLdsBytes = STAGES * G::kStage > kTile * kCPitch ? STAGES * G::kStage : kTile * kCPitch;
-  static_assert(kLdsBytes + kTile * 4 <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) char lds_raw[kLdsBytes];
   const lds_char_t* lds = (const lds_char_t*)lds_raw;
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave & 1, wn = wave >> 1;
-
-  int bid = blockIdx.x;
-  const int T = gridDim.x;
-  if (T % kNumXcd == 0) bid = (bid % kNumXcd) * (T / kNumXcd) + bid / kNumXcd;
-  const int per_group = kGroupRows * tiles_n;
-  const int grp = bid / per_group, first_m = grp * kGroupRows;
-  const int gsz = (tiles_m - first_m) < kGroupRows ? (tiles_m - first_m) : kGroupRows;
-  const int tm = first_m + (bid % per_group) % gsz, tn = (bid % per_group) / gsz;
-  const int64_t m0 = static_cast<int64_t>(tm) * kTile, n0 = static_cast<int64_t>(tn) * kTile;
 
   f32x16_t acc[4][4];
 #pragma unroll
@@ -298,11 +354,10 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
 
   // The tile's 256 bias values are staged in LDS now, so the epilogue does not wait on global
   // loads (their latency hides behind the prologue copies; the prologue barrier publishes them).
-  __shared__ float bias_lds[kTile];
-  bias_lds[threadIdx.x] = bias != nullptr ? bias[n0 + threadIdx.x] : 0.0f;
+  bias_lds[threadIdx.x] = bias != nullptr && (!EDGE || n0 + threadIdx.x < N) ? bias[n0 + threadIdx.x] : 0.0f;
 
   const typename G::Lane L = G::lane_plan(M, N, K, wave, wm, wn, lane);
-  const int KT = static_cast<int>(K / DK);
+  const int KT = static_cast<int>((K + DK - 1) / DK);  // a ragged last slice only in edge instances
   // Slice kt's copies fill the stage slice kt-1 used, so a copy is issued kLead slices ahead.
   constexpr int kLead = STAGES - 1;
   // Prologue: slices 0 .. kLead-1 in flight, then slice 0 must land.
@@ -426,30 +481,67 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     }
   }
   __syncthreads();
-  // 256 rows of 512 bytes; one store instruction covers two rows (32 lanes x 16 bytes each)
+  // 256 rows of 512 bytes; one store instruction covers two rows (32 lanes x 16 bytes each).
+  // An edge tile stores only rows < M and 16-byte chunks of columns < N (N % 8 == 0).
+  const bool col_ok = n0 + (lane & 31) * 8 < N;
 #pragma unroll 4
   for (int i = 0; i < kTile / 8; ++i) {
     const int row = (i * 4 + wave) * 2 + (lane >> 5);
     const u32x4 v = *(const lds_u32x4_t*)(ct + row * kCPitch + (lane & 31) * 16);
-    *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + (lane & 31) * 8) = v;
+    if (!EDGE || (col_ok && m0 + row < M)) *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + (lane & 31) * 8) = v;
   }
+}
+
+template <int DK, int STAGES, bool AKM = false, bool BKM = true>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const float* __restrict__ bias,
+                           uint16_t* __restrict__ C, int64_t M, int64_t N, int64_t K, int relu, int tiles_m,
+                           int tiles_n) {
+  constexpr int kLdsBytes = fast_lds_bytes<DK, STAGES>();
+  static_assert(kLdsBytes + kTile * 4 <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) char lds_raw[kLdsBytes];
+  __shared__ float bias_lds[kTile];
+
+  int bid = blockIdx.x;
+  const int T = gridDim.x;
+  if (T % kNumXcd == 0) bid = (bid % kNumXcd) * (T / kNumXcd) + bid / kNumXcd;
+  const int per_group = kGroupRows * tiles_n;
+  const int grp = bid / per_group, first_m = grp * kGroupRows;
+  const int gsz = (tiles_m - first_m) < kGroupRows ? (tiles_m - first_m) : kGroupRows;
+  const int tm = first_m + (bid % per_group) % gsz, tn = (bid % per_group) / gsz;
+  const int64_t m0 = static_cast<int64_t>(tm) * kTile, n0 = static_cast<int64_t>(tn) * kTile;
+
+  // Uniform per workgroup: edge tiles (and every tile when K is not a whole number of K steps)
+  // run the range-checked instance of the tile code.
+  if (m0 + kTile <= M && n0 + kTile <= N && K % DK == 0)
+    gemm_fast_tile<DK, STAGES, AKM, BKM, false>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
+  else
+    gemm_fast_tile<DK, STAGES, AKM, BKM, true>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
 }
 
 // K step and ring depth of the fast path.
 constexpr int kFastDK = 32;
 constexpr int kFastStages = 4;
 
-bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* C) {
+// Any M, N and K (edge tiles are copied through the descriptor's range check and stored under
+// masks) as long as every row of A, B and C starts 16 bytes aligned: N % 8 == 0, K % 8 == 0,
+// and M % 8 == 0 when A is given as [K, M].  When K is not a whole number of K steps, A and B
+// must be below 2 GiB each (the ragged k-chunks are pointed past every record).
+bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, const void* A, const void* B, const void* C) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
-  const int64_t lim = int64_t(1) << 31;  // per-lane copy offsets are 32-bit
-  return M % kTile == 0 && N % kTile == 0 && K % kFastDK == 0 && (al & 15) == 0 && K * 16 < lim && N * 16 < lim &&
-         M * 16 < lim;
+  // per-lane copy offsets from a slice base are 32-bit: up to 256 rows of K elements, or
+  // 64 k-rows of M or N elements
+  const int64_t lim = int64_t(1) << 32;
+  const bool sizes = K * 512 < lim && N * 128 < lim && M * 128 < lim;
+  const bool ragged_k_ok = K % kFastDK == 0 || (M * K * 2 < (int64_t(1) << 31) && K * N * 2 < (int64_t(1) << 31));
+  return M > 0 && N > 0 && K > 0 && N % 8 == 0 && K % 8 == 0 && (!transpose_a || M % 8 == 0) && (al & 15) == 0 &&
+         sizes && ragged_k_ok;
 }
 
 // transpose_a: A is given as [K, M]; transpose_b: B is given as [N, K].
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
                             int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s) {
-  const int64_t tm = M / kTile, tn = N / kTile;
+  const int64_t tm = (M + kTile - 1) / kTile, tn = (N + kTile - 1) / kTile;
   const dim3 grid(static_cast<unsigned>(tm * tn)), block(256);
   const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);
   if (!transpose_a && !transpose_b)

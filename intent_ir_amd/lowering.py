@@ -148,7 +148,12 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
             ("tensor", oname), ("i64", M), ("i64", N), ("i64", K)]
     args += [("i32", int(ta)), ("i32", int(tb))] if (ta or tb) else []
     args += [("i32", int(relu))]
-    full = M % 256 == 0 and N % 256 == 0 and K % 32 == 0  # fast path vs guarded kernel
+    # tiled fast path (any M and N; rows 16-byte aligned) vs guarded kernel, as gemm_fast_fits
+    # decides for 16-byte aligned tensors
+    lim = 1 << 32
+    ragged_k_ok = K % 32 == 0 or (M * K * 2 < (1 << 31) and K * N * 2 < (1 << 31))
+    full = (M > 0 and N > 0 and K > 0 and N % 8 == 0 and K % 8 == 0 and (not ta or M % 8 == 0)
+            and K * 512 < lim and N * 128 < lim and M * 128 < lim and ragged_k_ok)
     # fast path LDS: max(4-stage ring 131072, bf16 C tile 256 x 528) + 256 f32 bias values
     launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 136192 if full else 147456)
     kid = "ihip_gemm_bf16_bias_relu_t" if (ta or tb) else "ihip_gemm_bf16_bias_relu"

@@ -295,6 +295,54 @@ def test_gemm_edge_shapes(hip, M, N, K):
     check(out, ref, ["C"], TOL["matmul_strict"], f"gemm strict {b}")
 
 
+def _gemm_abi(hip, A, B, bias, M, N, K, ta=False, tb=False, offset=0):
+    """C (bf16 bits) through ihip_gemm_bf16_bias_relu_t on device copies of A and B placed `offset`
+    elements past a 256-byte aligned allocation (offset 1: 2-byte aligned, so the guarded
+    kernel runs instead of the tiled fast path)."""
+    import ctypes
+
+    import torch
+
+    def dev(bits):
+        t = torch.empty(bits.size + offset, dtype=torch.int16, device="cuda")
+        t[offset:] = torch.from_numpy(bits.reshape(-1).view(np.int16)).cuda()
+        return t
+
+    a, b = dev(A), dev(B)
+    bt = torch.from_numpy(bias).cuda()
+    c = torch.empty(M * N, dtype=torch.int16, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    st = hip.ihip_gemm_bf16_bias_relu_t(ctypes.c_void_p(a.data_ptr() + 2 * offset), ctypes.c_void_p(b.data_ptr() + 2 * offset),
+                                        ctypes.c_void_p(bt.data_ptr()), ctypes.c_void_p(c.data_ptr()), M, N, K,
+                                        int(ta), int(tb), 1, ctypes.c_void_p(s))
+    assert st == 0, hip.ihip_last_error().decode()
+    torch.cuda.synchronize()
+    return c.cpu().numpy().view(np.uint16).reshape(M, N)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(300, 264, 64), (8, 8, 32), (257, 8, 32), (513, 520, 96), (1000, 1000, 256),
+                                   (2000, 136, 4096), (300, 264, 1000), (257, 136, 40), (64, 64, 8), (512, 512, 264)])
+def test_gemm_edge_tiles_fast_path(hip, M, N, K, ta, tb):
+    """Shapes that are not multiples of the 256x256 tile or of the 32-deep K step, with 16-byte
+    aligned rows (N % 8 == 0, K % 8 == 0; M % 8 != 0 sends a transposed A to the guarded
+    kernel), run the tiled fast kernel with range-checked copies, k-chunks past K loaded as
+    zeros and masked edge stores.  Judged against the oracle, and bit for bit against the
+    guarded kernel (same MFMA over the same k order) run on 2-byte aligned copies."""
+    w = WORKLOADS["matmul"]
+    b = {"M": M, "N": N, "K": K}
+    inp = w.gen(b, seed=M + 3 * N + 5 * K, sigma=1.0)
+    A = np.ascontiguousarray(inp["A"].T) if ta else inp["A"]
+    B = np.ascontiguousarray(inp["B"].T) if tb else inp["B"]
+    print(f"[case] gemm edge tiles M={M} N={N} K={K} ta={ta} tb={tb}", flush=True)
+    fast = _gemm_abi(hip, A, B, inp["bias"], M, N, K, ta, tb)
+    ref = oracle_outputs(w.ir(), inp, b)
+    check({"C": bf16_bits_to_f32(fast)}, ref, ["C"], TOL["matmul"], f"fast {b}")
+    check({"C": bf16_bits_to_f32(fast)}, ref, ["C"], TOL["matmul_strict"], f"fast strict {b}")
+    guarded = _gemm_abi(hip, A, B, inp["bias"], M, N, K, ta, tb, offset=1)
+    assert np.array_equal(fast, guarded), f"fast and guarded kernels differ in {int((fast != guarded).sum())} elements"
+
+
 def test_gemm_ones_known_answer(hip):
     """tests/test_diff_runner.py:35-43: ones @ ones + 1 -> K + 1 everywhere."""
     M, N, K = 256, 256, 192

@@ -170,6 +170,18 @@ def test_gemm_forms_and_errors():
     assert lower_intent_to_hip_kernel(ir, shape_bindings=b).call_args[-1] == ("i32", 1)
 
 
+@pytest.mark.parametrize("M,N,K,tiled", [(256, 256, 64, True), (300, 264, 1000, True), (8, 8, 8, True),
+                                         (256, 250, 64, False), (256, 256, 60, False), (65536, 16384, 40960, True),
+                                         (65536, 16384, 40968, False)])
+def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tiled):
+    """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N (its LDS:
+    max(4-stage ring, staged C tile) + 256 bias floats); otherwise the guarded kernel.  A ragged
+    K needs operands below 2 GiB."""
+    k = lower_intent_to_hip_kernel(matmul_bias_relu2d_ir(), shape_bindings={"M": M, "N": N, "K": K})
+    assert k.launch.grid == (-(-M // 256) * -(-N // 256), 1, 1)
+    assert k.launch.lds_bytes == (136192 if tiled else 147456)
+
+
 def test_unsupported_ops_raise():
     ir = {"name": "g", "tensors": {"x": {"dtype": "f32", "shape": ["N"]}, "i": {"dtype": "i32", "shape": ["N"]},
                                    "y": {"dtype": "f32", "shape": ["N"]}},
