@@ -1,6 +1,7 @@
 // Native code for element-wise programs: the instruction list of ihip_elementwise_program
 // (include/intentir_hip.h) is turned into straight-line gfx950 code with hiprtc, once per
-// distinct program and operand types, and cached for the life of the process.
+// distinct program, operand types and operand access forms, and cached for the life of the
+// process.
 //
 // The interpreter kernel (ewprog.hip) pays a uniform dispatch, operand moves through the
 // indexed register file and an instruction fetch for every program instruction, which

@@ -2,10 +2,10 @@
 // [N,K] transposed), bf16 row-major, bias f32 [N], f32 accumulation on CDNA4 MFMA,
 // C bf16 (RNE) — any shape.
 //
-// Entry point of the GEMM family: shapes whose rows are all 16-byte aligned (N % 8 == 0,
-// M % 8 == 0 for a transposed A) with K a multiple of the fast path's K step and 16-byte
-// aligned operands go to gemm_fast.hip, for any M and N; every other shape runs the
-// guarded kernel below, which stages operands through registers:
+// Entry point of the GEMM family: shapes whose rows all start 16-byte aligned (N % 8 == 0,
+// K % 8 == 0, M % 8 == 0 for a transposed A) with 16-byte aligned operands go to
+// gemm_fast.hip, for any M, N and K; every other shape runs the guarded kernel below, which
+// stages operands through registers:
 //  * workgroup tile 256(M) x 256(N), K step 64; 256 threads = 4 waves in a 2x2 grid,
 //    each wave owning a 128x128 sub-tile = 4x4 blocks of v_mfma_f32_32x32x16_bf16;
 //  * LDS double buffer: A tile as [m][k] and B tile transposed to [n][k] (rows padded

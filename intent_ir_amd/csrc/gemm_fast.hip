@@ -1,10 +1,11 @@
 // Tiled bf16 GEMM for gfx950: C = act(A @ B + bias), A [M,K], B [K,N] row-major bf16,
-// f32 accumulation on v_mfma_f32_32x32x16_bf16, C bf16 (RNE).  Any M and N; requires
-// K % DK == 0, every row of A, B and C 16-byte aligned (N % 8 == 0, and M % 8 == 0 when A
-// is given as [K,M]) and 16-byte aligned bases; other shapes take the guarded kernel in
-// gemm.hip.  Edge tiles: copies read through a range-checked buffer descriptor (zeros past
-// the end of a tensor), and what an edge tile reads outside [M) x [N) only reaches C rows
-// >= M or columns >= N, which are never stored.
+// f32 accumulation on v_mfma_f32_32x32x16_bf16, C bf16 (RNE).  Any M, N and K as long as
+// every row of A, B and C starts 16-byte aligned (N % 8 == 0, K % 8 == 0, and M % 8 == 0
+// when A is given as [K,M]) and the bases are 16-byte aligned; other shapes take the
+// guarded kernel in gemm.hip.  Edge tiles (past M or N, or all tiles when K is not a
+// multiple of DK) copy through range-checked buffer descriptors: reads past the end of a
+// tensor and k-chunks past K load zeros, and what an edge tile reads outside [M) x [N) only
+// reaches C rows >= M or columns >= N, which are never stored.
 //
 // Work decomposition
 //  * one 256x256 C tile per workgroup of 256 threads = 4 waves in a 2x2 grid; wave (wm, wn)
@@ -18,8 +19,9 @@
 //  * a ring of STAGES LDS stages, each holding a 256 x DK slice of A and a DK x 256 slice
 //    of B; the copy of K-slice kt+STAGES-1 is issued while slice kt is multiplied, so a
 //    copy has STAGES-1 slices of MFMA time to land;
-//  * copies use gfx950's direct-to-LDS loads (buffer_load_dwordx4 ... lds): lane l of a
-//    wave writes 16 bytes at LDS m0 + 16*l; no VGPR holds tile data;
+//  * copies use gfx950's direct-to-LDS loads (global_load_lds_dwordx4 in interior tiles,
+//    buffer_load_dwordx4 ... lds in edge tiles): lane l of a wave writes 16 bytes at LDS
+//    m0 + 16*l; no VGPR holds tile data;
 //  * because the LDS position is fixed by the lane, bank conflicts are avoided by choosing
 //    which global 16-byte chunk each lane fetches (XOR swizzles, 64-bank LDS):
 //      A row r (DK*2 bytes) stores logical k-chunk c in slot c ^ ((r / RPW) % CA), where
@@ -32,7 +34,8 @@
 //    row k0+t, columns 4q..4q+3, and lane i receives column i of rows k0..k0+3, i.e. the
 //    k-contiguous operand layout, with no VALU transposition.
 //  * The MFMA is issued as D = B^T-block x A-block, so each lane's accumulators hold four
-//    consecutive n of one m: the epilogue adds bias, applies ReLU and stores 8 bytes.
+//    consecutive n of one m: the epilogue adds bias, applies ReLU, packs 8 bytes of bf16 per
+//    lane into the C tile staged in LDS, and writes the tile out in full 512-byte rows.
 #include "common.hpp"
 
 #include <type_traits>
@@ -58,10 +61,11 @@ constexpr int kGroupRows = 8;  // tile-rows per raster group
 typedef __bf16 bf16x2_pk_t __attribute__((ext_vector_type(2)));
 
 // AKM / BKM select the global layout of each operand: false = K-contiguous rows (A [M,K],
-// or B given transposed as [N,K]), true = K-major (A given transposed as [K,M], or B [K,N]).  A K-contiguous operand
-// is staged as [256 rows][DK] and read with ds_read_b128; a K-major one as [DK][256] and read
-// with the transposing ds_read_b64_tr_b16.  Either way the MFMA sees the same fragments, so
-// every layout accumulates in the same order and gives identical results.
+// or B given transposed as [N,K]), true = K-major (A given transposed as [K,M], or B
+// [K,N]).  A K-contiguous operand is staged as [256 rows][DK] and read with ds_read_b128; a
+// K-major one as [DK][256] and read with the transposing ds_read_b64_tr_b16.  Either way the
+// MFMA sees the same fragments, so every layout accumulates in the same order and gives
+// identical results.
 // EDGE: the tile reaches past M or N; its copies go through range-checked buffer descriptors
 // (interior tiles use global_load_lds, which measured ~14% faster on full 8192^3 GEMMs).
 template <int DK, int STAGES, bool AKM = false, bool BKM = true, bool EDGE = false>
