@@ -2,7 +2,8 @@
 // softmax (f32) and LayerNorm forward (f16 in/out, f32 statistics).
 //
 // Layout and schedule (gfx950, wave64):
-//  * one wave owns one row; a 256-thread workgroup holds 4 rows;
+//  * one wave owns one row (the row reductions spread few long rows over 16 waves);
+//    workgroups hold 1 (streaming reductions), 4 (softmax) or 16 (LayerNorm) rows;
 //  * lanes read the row with 16-byte loads, lane l taking vectors l, l+64, ...,
 //    so every load instruction of a wave covers 1 KiB of contiguous HBM;
 //  * rows that fit in registers are read from HBM exactly once; statistics are
@@ -104,7 +105,77 @@ hipError_t launch_reduce_any_rows_u8(const uint8_t* x, uint8_t* out, int64_t M, 
 }
 
 // ============================================================== reduce_sum / reduce_max
-// kind 0: out[m] = sum(x[m, :]) (f32 accumulation); kind 1: out[m] = max(x[m, :]) (NaN-propagating).
+// kind 0: out[m] = sum(x[m, :]) (f32 accumulation); kind 1: out[m] = max(x[m, :]) (NaN-propagating,
+// as np.max).  Replaces the reference's row reductions (_kernel_reduce_sum/max over the last
+// axis, backends/cuda/codegen/intentir_to_cuda.py:1553-1690).
+//
+// Vector form: W waves per row (one-wave workgroups for many rows, 16 waves when there are few
+// rows to spread over the CUs).  Lane l of wave w takes 16-byte vectors (w*64 + l) + i*64*W
+// with kUnroll non-temporal loads in flight, folded into kAcc f32x4 partials; the 4*kAcc
+// partials are combined pairwise, then across the wave (6 xor-shuffles) and the row's waves
+// (LDS).  Sums start from +0.0 as numpy's add.reduce does, so a row of -0.0 (and an empty
+// row) sums to +0.0 as there; out-of-range elements contribute the start value.
+template <int kKind>
+__device__ __forceinline__ float red_op(float a, float b) {
+  return kKind == 0 ? a + b : max_nan(a, b);
+}
+
+template <int kKind, int W, int kUnroll, int kAcc>
+__global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const f32x4* __restrict__ x, float* __restrict__ out,
+                                                              int64_t M, int64_t n4) {
+  static_assert(kUnroll % kAcc == 0 && (kAcc & (kAcc - 1)) == 0, "loads fold evenly into a power-of-two of partials");
+  const float id = kKind == 0 ? 0.0f : -__builtin_inff();
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  if (row >= M) return;
+  const f32x4* xr = x + row * n4;
+  f32x4 acc[kAcc];
+#pragma unroll
+  for (int u = 0; u < kAcc; ++u) acc[u] = f32x4{id, id, id, id};
+  for (int64_t base = wave * kWave + lane; base < n4; base += static_cast<int64_t>(kWave) * W * kUnroll) {
+    f32x4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + static_cast<int64_t>(u) * kWave * W;
+      v[u] = (i < n4) ? __builtin_nontemporal_load(xr + i) : f32x4{id, id, id, id};
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      f32x4& a = acc[u % kAcc];
+      a.x = red_op<kKind>(a.x, v[u].x);
+      a.y = red_op<kKind>(a.y, v[u].y);
+      a.z = red_op<kKind>(a.z, v[u].z);
+      a.w = red_op<kKind>(a.w, v[u].w);
+    }
+  }
+#pragma unroll
+  for (int h = kAcc / 2; h > 0; h /= 2)
+#pragma unroll
+    for (int u = 0; u < h; ++u) {
+      acc[u].x = red_op<kKind>(acc[u].x, acc[u + h].x);
+      acc[u].y = red_op<kKind>(acc[u].y, acc[u + h].y);
+      acc[u].z = red_op<kKind>(acc[u].z, acc[u + h].z);
+      acc[u].w = red_op<kKind>(acc[u].w, acc[u + h].w);
+    }
+  float r = red_op<kKind>(red_op<kKind>(acc[0].x, acc[0].y), red_op<kKind>(acc[0].z, acc[0].w));
+  r = kKind == 0 ? wave_sum(r) : wave_max_nan(r);
+  if (W > 1) {
+    __shared__ float part[W];
+    if (lane == 0) part[wave] = r;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float t = part[0];
+#pragma unroll
+      for (int i = 1; i < W; ++i) t = red_op<kKind>(t, part[i]);
+      out[row] = t;
+    }
+  } else if (lane == 0) {
+    out[row] = r;
+  }
+}
+
+// Scalar form for rows the vector form cannot take (N % 4 != 0 or a base not 16-byte aligned).
 template <int kKind>
 __global__ __launch_bounds__(256) void reduce_rows_f32(const float* __restrict__ x, float* __restrict__ out, int64_t M,
                                                        int64_t N) {
@@ -113,18 +184,37 @@ __global__ __launch_bounds__(256) void reduce_rows_f32(const float* __restrict__
   if (row >= M) return;
   const float* xr = x + row * N;
   float acc = kKind == 0 ? 0.0f : -__builtin_inff();
-  for (int64_t i = lane; i < N; i += kWave) acc = kKind == 0 ? acc + xr[i] : max_nan(acc, xr[i]);
+  for (int64_t i = lane; i < N; i += kWave) acc = red_op<kKind>(acc, xr[i]);
   acc = kKind == 0 ? wave_sum(acc) : wave_max_nan(acc);
   if (lane == 0) out[row] = acc;
 }
 
+// Loads in flight per lane in the one-wave form (8 measured level with 16 on [8192, 4096]).
+constexpr int kRedUnroll = 16;
+
+template <int kKind>
+static void launch_reduce_rows(const float* x, float* out, int64_t M, int64_t N, hipStream_t s) {
+  const bool vec = N % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  if (!vec) {
+    reduce_rows_f32<kKind><<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(x, out, M, N);
+    return;
+  }
+  const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+  const int64_t n4 = N / 4;
+  const dim3 grid(static_cast<unsigned>(M));
+  if (M >= 2048 || n4 <= 4 * kWave)  // enough rows for the CUs, or short rows: a wave per row
+    reduce_rows_f32_vec<kKind, 1, kRedUnroll, 4><<<grid, dim3(64), 0, s>>>(x4, out, M, n4);
+  else  // few long rows: 16 waves per row
+    reduce_rows_f32_vec<kKind, 16, 8, 4><<<grid, dim3(1024), 0, s>>>(x4, out, M, n4);
+}
+
 hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, hipStream_t s) {
   if (M == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row
   if (kind == 0)
-    reduce_rows_f32<0><<<grid, block, 0, s>>>(x, out, M, N);
+    launch_reduce_rows<0>(x, out, M, N, s);
   else
-    reduce_rows_f32<1><<<grid, block, 0, s>>>(x, out, M, N);
+    launch_reduce_rows<1>(x, out, M, N, s);
   return hipGetLastError();
 }
 

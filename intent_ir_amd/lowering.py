@@ -317,7 +317,12 @@ def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
     if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
         raise HipLoweringError("HIP row reductions take f32 input and output")
     M, N = c.rows(x)
-    return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32", c.io([x, oname]), _row_launch(M), [oname], dict(c.b),
+    if N % 4 == 0:  # vector form: a wave per row, or 16 waves per row for few long rows
+        few_long = M < 2048 and N // 4 > 256
+        launch = HipLaunch((max(1, M), 1, 1), (1024 if few_long else 64, 1, 1), 64 if few_long else 0)
+    else:
+        launch = _row_launch(M)
+    return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b),
                             (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N),
                              ("i32", 0 if kind == "rsum" else 1)))
 

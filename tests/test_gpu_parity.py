@@ -125,6 +125,64 @@ def test_reduce_any_full_config(hip):
     assert 0.2 < out["out"].mean() < 0.5  # ~33% of rows hold a Bernoulli(1e-4) hit
 
 
+# ------------------------------------------------------------------ row reduce_sum / reduce_max
+def _row_reduce_ir(op: str) -> dict:
+    return {"name": f"row_{op}", "tensors": {"x": {"dtype": "f32", "shape": ["M", "N"]},
+                                             "out": {"dtype": "f32", "shape": ["M"]}},
+            "ops": [{"op": op, "inputs": ["x"], "output": "out", "attrs": {"dims": [1]}}], "outputs": ["out"]}
+
+
+ROW_REDUCE_SHAPES = ([(m, n) for m in (1, 3, 17) for n in EDGE + [64, 255, 256, 1023, 1025, 4096, 4100, 65536]]
+                     + [(2048, 256), (2048, 4100), (4096, 1024), (1000, 2048)])
+
+
+@pytest.mark.parametrize("op", ["reduce_sum", "reduce_max"])
+@pytest.mark.parametrize("M,N", ROW_REDUCE_SHAPES)
+def test_row_reduce_edge_shapes(hip, op, M, N):
+    """reduce_sum / reduce_max over the last axis (interpreter.py:478-500): sums within rtol 1e-5
+    (a different f32 summation order than numpy's pairwise one), maxima bit-exact.  Covers the
+    wave-per-row and 16-waves-per-row vector forms and the scalar form (N % 4 != 0)."""
+    ir = _row_reduce_ir(op)
+    b = {"M": M, "N": N}
+    x = np.random.default_rng(M * 7 + N).standard_normal((M, N)).astype(np.float32)
+    out = run_case(ir, {"x": x}, b)["out"]
+    ref = oracle_outputs(ir, {"x": x}, b)["out"]
+    if op == "reduce_max":
+        np.testing.assert_array_equal(out, ref)
+    else:
+        check({"out": out}, {"out": ref}, ["out"], {"atol": 1e-4, "rtol": 1e-5}, f"{op} {b}")
+
+
+@pytest.mark.parametrize("N", [8, 4096, 4100])
+def test_row_reduce_special_values(hip, N):
+    """NaN propagates through both; inf and -inf as in numpy (inf + -inf = NaN); a row of -0.0
+    sums to +0.0 (numpy's add.reduce starts from +0.0) and has max -0.0; an empty row sums to
+    +0.0."""
+    M = 6
+    x = np.ones((M, N), np.float32)
+    x[0, N // 2] = np.nan
+    x[1, N - 1] = np.inf
+    x[2, 0] = -np.inf
+    x[3, 1], x[3, N - 2] = np.inf, -np.inf
+    x[4, :] = -0.0
+    x[5, :] = -3.0
+    for op in ("reduce_sum", "reduce_max"):
+        out = run_case(_row_reduce_ir(op), {"x": x}, {"M": M, "N": N})["out"]
+        ref = x.sum(axis=1) if op == "reduce_sum" else x.max(axis=1)
+        np.testing.assert_array_equal(out, ref.astype(np.float32))
+        assert np.signbit(out[4]) == np.signbit(ref[4]), f"{op} of a -0.0 row: sign of zero as numpy"
+    empty = run_case(_row_reduce_ir("reduce_sum"), {"x": np.zeros((3, 0), np.float32)}, {"M": 3, "N": 0})["out"]
+    assert empty.tolist() == [0.0, 0.0, 0.0] and not np.signbit(empty).any()
+
+
+def test_row_reduce_full_size(hip):
+    """[8192, 4096] f32, the reduce_any workload's shape: sums against the oracle."""
+    ir = _row_reduce_ir("reduce_sum")
+    b = {"M": 8192, "N": 4096}
+    x = np.random.default_rng(5).standard_normal((8192, 4096)).astype(np.float32)
+    check(run_case(ir, {"x": x}, b), oracle_outputs(ir, {"x": x}, b), ["out"], {"atol": 1e-4, "rtol": 1e-5}, "sum full")
+
+
 # ------------------------------------------------------------------ softmax
 @pytest.mark.parametrize("M", [1, 7, 33])
 @pytest.mark.parametrize("N", EDGE + [64, 256, 1000, 1024, 4096, 5000])
