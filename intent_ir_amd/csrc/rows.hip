@@ -60,7 +60,30 @@ __global__ __launch_bounds__(256) void reduce_any_rows_f32_scalar(const float* _
   if (lane == 0) out[row] = acc != 0u;
 }
 
-// bool/u8 input: out[m] = any(x[m, :] != 0).
+// bool/u8 input: out[m] = any(x[m, :] != 0).  Vector form (N % 16 == 0, 16-byte aligned
+// base): a wave per row ORs 16-byte words, 16 loads per lane in flight, as the f32 kernel.
+template <int kUnroll>
+__global__ __launch_bounds__(64) void reduce_any_rows_u8_vec(const u32x4* __restrict__ x, uint8_t* __restrict__ out,
+                                                             int64_t M, int64_t n16) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = blockIdx.x;
+  if (row >= M) return;
+  const u32x4* xr = x + row * n16;
+  uint32_t acc = 0;
+  for (int64_t base = lane; base < n16; base += kWave * kUnroll) {
+    u32x4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + static_cast<int64_t>(u) * kWave;
+      v[u] = i < n16 ? __builtin_nontemporal_load(xr + i) : u32x4(0u);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc |= v[u].x | v[u].y | v[u].z | v[u].w;
+  }
+  acc = wave_or(acc);
+  if (lane == 0) out[row] = acc != 0u;
+}
+
 __global__ __launch_bounds__(256) void reduce_any_rows_u8(const uint8_t* __restrict__ x, uint8_t* __restrict__ out,
                                                           int64_t M, int64_t N) {
   const int lane = threadIdx.x & 63;
@@ -100,7 +123,12 @@ hipError_t launch_reduce_any_rows_f32(const float* x, uint8_t* out, int64_t M, i
 
 hipError_t launch_reduce_any_rows_u8(const uint8_t* x, uint8_t* out, int64_t M, int64_t N, hipStream_t s) {
   if (M == 0) return hipSuccess;
-  reduce_any_rows_u8<<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(x, out, M, N);
+  if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row in the vector form
+  if (N % 16 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0)
+    reduce_any_rows_u8_vec<16><<<dim3(static_cast<unsigned>(M)), dim3(kStreamBlock), 0, s>>>(
+        reinterpret_cast<const u32x4*>(x), out, M, N / 16);
+  else
+    reduce_any_rows_u8<<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(x, out, M, N);
   return hipGetLastError();
 }
 
@@ -268,6 +296,55 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restr
   }
 }
 
+// Rows longer than one wave holds (N > 4096): kW waves share a row, one row per workgroup.
+// Wave v holds the vectors (v*64 + lane) + i*64*kW, i < kVpl, in registers, so the row is
+// read from HBM once; the row max and sum are exchanged through LDS and every wave combines
+// the kW partials in the same order.  Same arithmetic per element as the one-wave kernel.
+template <int kVpl, int kW>
+__global__ __launch_bounds__(64 * kW) void softmax_rows_f32_multi(const f32x4* __restrict__ x, f32x4* __restrict__ y,
+                                                                  int64_t M, int n4) {
+  __shared__ float part_m[kW], part_s[kW];
+  const int lane = threadIdx.x & 63, v = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  if (row >= M) return;  // uniform per workgroup
+  const f32x4* xr = x + row * n4 + v * kWave + lane;
+  f32x4* yr = y + row * n4 + v * kWave + lane;
+  const float ninf = -__builtin_inff();
+  f32x4 xv[kVpl];
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+    xv[i] = v * kWave + lane + i * kWave * kW < n4 ? __builtin_nontemporal_load(xr + i * kWave * kW)
+                                                   : f32x4{ninf, ninf, ninf, ninf};
+  float mx = ninf;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) mx = max_nan(max_nan(mx, xv[i].x), max_nan(max_nan(xv[i].y, xv[i].z), xv[i].w));
+  mx = wave_max_nan(mx);
+  if (lane == 0) part_m[v] = mx;
+  __syncthreads();
+  mx = part_m[0];
+#pragma unroll
+  for (int k = 1; k < kW; ++k) mx = max_nan(mx, part_m[k]);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    xv[i].x = exp_nonpos(xv[i].x - mx);
+    xv[i].y = exp_nonpos(xv[i].y - mx);
+    xv[i].z = exp_nonpos(xv[i].z - mx);
+    xv[i].w = exp_nonpos(xv[i].w - mx);
+    if (v * kWave + lane + i * kWave * kW < n4) sum += (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) part_s[v] = sum;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < kW; ++k) tot += part_s[k];
+  const float inv = 1.0f / tot;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+    if (v * kWave + lane + i * kWave * kW < n4) __builtin_nontemporal_store(xv[i] * inv, yr + i * kWave * kW);
+}
+
 // Any N: one workgroup per row, three passes (max, sum, write) over the row.
 __global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restrict__ x, float* __restrict__ y, int64_t N) {
   __shared__ float scratch[4];
@@ -310,6 +387,14 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
     launch_softmax_reg<8>(x4, y4, M, n4i, s);
   else if (vec && n4 <= 1024)
     launch_softmax_reg<16>(x4, y4, M, n4i, s);
+  else if (vec && n4 <= 2048)
+    softmax_rows_f32_multi<16, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x4, y4, M, n4i);
+  else if (vec && n4 <= 4096)
+    softmax_rows_f32_multi<16, 4><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x4, y4, M, n4i);
+  else if (vec && n4 <= 8192)
+    softmax_rows_f32_multi<16, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x4, y4, M, n4i);
+  else if (vec && n4 <= 16384)
+    softmax_rows_f32_multi<16, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x4, y4, M, n4i);
   else
     softmax_rows_f32_any<<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, N);
   return hipGetLastError();
@@ -413,6 +498,87 @@ __global__ __launch_bounds__(64 * kLnRows) void layernorm_rows_f16_wave(
   }
 }
 
+// Rows longer than one wave holds (N > 4096): kW waves share a row, kWaves / kW rows per
+// workgroup of kWaves waves.  Wave v of a row holds the 16-byte vectors (v*64 + lane) + i*64*kW,
+// i < kVpl, in registers (the row is read from HBM once, as in the one-wave kernel); the
+// wave sums are exchanged through LDS, and every wave adds the kW partials in the same order,
+// so all waves of a row hold the same mean and rstd.  w and b are read from global memory
+// (L2-resident, shared by all rows) rather than staged: a row of 64K halves would need 256 KiB.
+template <int kVpl, int kW, int kWaves>
+__global__ __launch_bounds__(64 * kWaves) void layernorm_rows_f16_multi(
+    const u32x4* __restrict__ x, const u32x4* __restrict__ w, const u32x4* __restrict__ b, u32x4* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t M, int n8, int N, float eps) {
+  constexpr int kRows = kWaves / kW;
+  static_assert(kRows * kW == kWaves, "whole rows per workgroup");
+  __shared__ float part_s[kRows][kW], part_q[kRows][kW];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6, r = wave / kW, v = wave % kW;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRows + r;
+  const bool live = row0 < M;  // waves past the last row read row M-1 and store nothing
+  const int64_t row = live ? row0 : M - 1;
+  const u32x4* xr = x + row * n8 + v * kWave + lane;
+  f16x8_t xv[kVpl];
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+    xv[i] = __builtin_bit_cast(f16x8_t, v * kWave + lane + i * kWave * kW < n8
+                                            ? __builtin_nontemporal_load(xr + i * kWave * kW)
+                                            : u32x4(0u));
+  float s = 0.f;
+  const f16x2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f16x2_t p = {xv[i][2 * j], xv[i][2 * j + 1]};
+      s = __builtin_amdgcn_fdot2(p, one, s, false);  // padding lanes hold +0
+    }
+  s = wave_sum(s);
+  if (lane == 0) part_s[r][v] = s;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < kW; ++k) tot += part_s[r][k];
+  const float mean = tot / static_cast<float>(N);
+  float unit;  // an opaque 1.0, as in the one-wave kernel: x*unit - mean is one v_fma_mix_f32
+  asm volatile("v_mov_b32 %0, 1.0" : "=v"(unit));
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float d = __builtin_fmaf(static_cast<float>(xv[i][j]), unit, -mean);
+      q = __builtin_fmaf(d, v * kWave + lane + i * kWave * kW < n8 ? d : 0.f, q);
+    }
+  q = wave_sum(q);
+  if (lane == 0) part_q[r][v] = q;
+  __syncthreads();
+  float qt = 0.f;
+#pragma unroll
+  for (int k = 0; k < kW; ++k) qt += part_q[r][k];
+  const float rstd = 1.0f / sqrtf(qt / static_cast<float>(N) + eps);
+  float unit2;
+  asm volatile("v_mov_b32 %0, 1.0" : "=v"(unit2));
+  u32x4* yr = y + row * n8;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const int idx = v * kWave + lane + i * kWave * kW;
+    const bool in = idx < n8;
+    const f16x8_t wv = __builtin_bit_cast(f16x8_t, in ? w[idx] : u32x4(0u));
+    const f16x8_t bv = __builtin_bit_cast(f16x8_t, in ? b[idx] : u32x4(0u));
+    f16x8_t o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float d = __builtin_fmaf(static_cast<float>(xv[i][j]), unit2, -mean);
+      o[j] = static_cast<_Float16>(__builtin_fmaf(d * rstd, static_cast<float>(wv[j]), static_cast<float>(bv[j])));
+    }
+    if (live && in) __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), yr + idx);
+  }
+  if (live && v == 0 && lane == 0) {
+    mean_out[row] = mean;
+    rstd_out[row] = rstd;
+  }
+}
+
 // Any N: one workgroup per row, three passes over the row.
 __global__ __launch_bounds__(256) void layernorm_rows_f16_any(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                               const uint16_t* __restrict__ b, uint16_t* __restrict__ y,
@@ -455,13 +621,21 @@ static void launch_layernorm_wave(const u32x4* x8, const u32x4* w8, const u32x4*
     layernorm_rows_f16_wave<kVpl, false><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, N, eps);
 }
 
+template <int kVpl, int kW, int kWaves>
+static void launch_layernorm_multi(const u32x4* x8, const u32x4* w8, const u32x4* b8, u32x4* y8, float* mean,
+                                   float* rstd, int64_t M, int n8, int N, float eps, hipStream_t s) {
+  constexpr int kRows = kWaves / kW;
+  const dim3 grid(static_cast<unsigned>((M + kRows - 1) / kRows)), block(64 * kWaves);
+  layernorm_rows_f16_multi<kVpl, kW, kWaves><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, N, eps);
+}
+
 hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y, float* mean,
                                      float* rstd, int64_t M, int64_t N, float eps, hipStream_t s) {
   if (M == 0) return hipSuccess;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // grid.x limit of the row-per-workgroup fallback
   const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                        reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(y);
-  const bool vec = N > 0 && (N % 8 == 0) && ((al & 15) == 0) && N <= 512 * 8;
+  const bool vec = N > 0 && (N % 8 == 0) && ((al & 15) == 0) && N <= 65536;
   if (!vec) {
     layernorm_rows_f16_any<<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, w, b, y, mean, rstd, N, eps);
     return hipGetLastError();
@@ -477,8 +651,20 @@ hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const
     launch_layernorm_wave<2>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
   else if (n8 <= 256)
     launch_layernorm_wave<4>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
-  else
+  else if (n8 <= 512)
     launch_layernorm_wave<8>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
+  // Multi-wave forms, by measured rate on 64 MiB (1 << 25 halves) of rows: up to 8K halves, 2 waves
+  // per row and 8 rows per 1024-thread workgroup (74-75% of peak); longer rows, one row per
+  // workgroup with 16 vectors per lane (16K: 73%, 32K and 64K: 70-71%).  Shapes with 8 vectors
+  // per lane and 4 or more waves per row reached 60-62%: fewer bytes in flight per SIMD.
+  else if (n8 <= 1024)
+    launch_layernorm_multi<8, 2, 16>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
+  else if (n8 <= 2048)
+    launch_layernorm_multi<16, 2, 2>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
+  else if (n8 <= 4096)
+    launch_layernorm_multi<16, 4, 4>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
+  else
+    launch_layernorm_multi<16, 8, 8>(x8, w8, b8, y8, mean, rstd, M, n8, static_cast<int>(N), eps, s);
   return hipGetLastError();
 }
 

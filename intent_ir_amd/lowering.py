@@ -189,7 +189,10 @@ def _match_reduce_any(c: _Ctx) -> Optional[HipLoweredKernel]:
         kid = "ihip_reduce_any_rows_u8"
     else:
         raise HipLoweringError(f"reduce_any input dtype {dt} is not lowered")
-    launch = _row_launch(M, 1) if kid == "ihip_reduce_any_rows_f32" else _row_launch(M)
+    if kid == "ihip_reduce_any_rows_f32" or N % 16 == 0:  # a wave per row (bool: 16-byte vector form)
+        launch = _row_launch(M, 1)
+    else:
+        launch = _row_launch(M)
     return HipLoweredKernel(c.fn.name, kid, c.io([x, oname]), launch, [oname], dict(c.b), args)
 
 
@@ -218,7 +221,13 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
     if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
         raise HipLoweringError("HIP softmax takes f32 input and output")
     M, N = c.rows(x)
-    launch = _row_launch(M) if (N % 4 == 0 and N <= 4096) else HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
+    if N % 4 == 0 and N <= 4096:  # a wave per row, 4 rows per workgroup
+        launch = _row_launch(M)
+    elif N % 4 == 0 and N <= 65536:  # kW waves per row, one row per workgroup, partials in LDS
+        kw = next(w for w in (2, 4, 8, 16) if N // 4 <= 1024 * w)
+        launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
+    else:
+        launch = HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
     return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b),
                             (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N)))
 
@@ -261,10 +270,14 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     args = (("tensor", x), ("tensor", w), ("tensor", b), ("tensor", y), stat("mean"), stat("rstd"), ("i64", M),
             ("i64", N), ("f32", float(env["eps"][1])))
     names = [x, w, b, y] + [inv[r] for r in ("mean", "rstd") if r in inv]
-    vec = N % 8 == 0 and 0 < N <= 4096
-    if vec:  # 16 rows per 1024-thread workgroup; w and b staged in LDS (kVpl 16-byte vectors per lane)
+    if N % 8 == 0 and 0 < N <= 4096:  # 16 rows per 1024-thread workgroup; w and b staged in LDS
         kvpl = next(v for v in (1, 2, 4, 8) if N // 8 <= 64 * v)
         launch = HipLaunch((max(1, _cdiv(M, 16)), 1, 1), (1024, 1, 1), 2 * kvpl * 64 * 16)
+    elif N % 8 == 0 and N <= 8192:  # 2 waves per row, 8 rows per 1024-thread workgroup, partials in LDS
+        launch = HipLaunch((max(1, _cdiv(M, 8)), 1, 1), (1024, 1, 1), 128)
+    elif N % 8 == 0 and N <= 65536:  # kW waves per row, one row per workgroup
+        kw = 2 if N <= 16384 else 4 if N <= 32768 else 8
+        launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
     else:
         launch = HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
     return HipLoweredKernel(c.fn.name, "ihip_layernorm_rows_f16", c.io(names), launch, list(c.fn.outputs),

@@ -99,6 +99,26 @@ def test_reduce_any_special_values(hip):
     assert out["out"].tolist() == [False, False, True, True, True, True, False, True]
 
 
+@pytest.mark.parametrize("M,N", [(1, 16), (3, 4096), (17, 4112), (33, 17), (5, 4100), (2, 65536), (300, 1024)])
+def test_reduce_any_bool_input(hip, M, N):
+    """reduce_any over an i1 tensor (interpreter.py:489-494): the 16-byte vector form for
+    N % 16 == 0, the byte-wise form otherwise; rows with a single true at either end."""
+    ir = {"name": "anyb", "tensors": {"x": {"dtype": "i1", "shape": ["M", "N"]}, "out": {"dtype": "i1", "shape": ["M"]}},
+          "ops": [{"op": "reduce_any", "inputs": ["x"], "output": "out", "attrs": {"dims": [1]}}], "outputs": ["out"]}
+    rng = np.random.default_rng(M * 31 + N)
+    x = rng.random((M, N)) < 2.0 / N
+    x[0, :] = False
+    if M > 1:
+        x[1, :] = False
+        x[1, N - 1] = True
+    if M > 2:
+        x[2, :] = False
+        x[2, 0] = True
+    out = run_case(ir, {"x": x}, {"M": M, "N": N})
+    np.testing.assert_array_equal(out["out"], oracle_outputs(ir, {"x": x}, {"M": M, "N": N})["out"])
+    np.testing.assert_array_equal(out["out"], x.any(axis=1))
+
+
 def test_reduce_any_ne_form_with_nonzero_constant(hip):
     """`const, ne, reduce_any` form (tests/backends/cuda/test_cuda_backend_smoke.py:249-267) with c != 0."""
     ir = {
@@ -185,8 +205,11 @@ def test_row_reduce_full_size(hip):
 
 # ------------------------------------------------------------------ softmax
 @pytest.mark.parametrize("M", [1, 7, 33])
-@pytest.mark.parametrize("N", EDGE + [64, 256, 1000, 1024, 4096, 5000])
+@pytest.mark.parametrize("N", EDGE + [64, 256, 1000, 1024, 4096, 4100, 5000, 8192, 8196, 16384, 32000, 32768, 65536,
+                                      65540])
 def test_softmax_edge_shapes(hip, M, N):
+    """One wave per row up to N = 4096, 2-16 waves per row up to 65536 (4100, 8196: the first
+    size past a form's capacity), the three-pass kernel beyond or for N % 4 != 0."""
     w = WORKLOADS["softmax"]
     b = {"M": M, "N": N}
     inp = w.gen(b, seed=M + N)
@@ -231,8 +254,10 @@ def _check_ln(out, ref, what):
 
 
 @pytest.mark.parametrize("M", [1, 3, 17])
-@pytest.mark.parametrize("N", EDGE + [64, 1000, 1024, 4096, 4104, 8192])
+@pytest.mark.parametrize("N", EDGE + [64, 1000, 1024, 4096, 4104, 8192, 8200, 16384, 20000, 65536, 65544])
 def test_layernorm_edge_shapes(hip, M, N):
+    """One wave per row up to N = 4096; 2-16 waves per row up to 65536 (rows per workgroup
+    16 / waves, so M = 17 leaves waves past the last row); the three-pass kernel beyond."""
     w = WORKLOADS["layernorm"]
     b = {"M": M, "N": N}
     inp = w.gen(b, seed=M * 7 + N)
