@@ -345,6 +345,55 @@ __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_multi(const f32x4* _
     if (v * kWave + lane + i * kWave * kW < n4) __builtin_nontemporal_store(xv[i] * inv, yr + i * kWave * kW);
 }
 
+// Rows whose length is not a multiple of 4 (or a base not 16-byte aligned), up to 65536: the
+// row is still held in registers and read once, with 4-byte loads.  Element (i*kW + v)*64 + lane
+// belongs to lane `lane` of wave v, so each load instruction of a wave covers 256 contiguous
+// bytes; kW waves per row, partials through LDS as in the vector multi-wave form.
+template <int kEpl, int kW>
+__global__ __launch_bounds__(64 * kW) void softmax_rows_f32_regs(const float* __restrict__ x, float* __restrict__ y,
+                                                                 int64_t M, int64_t N) {
+  __shared__ float part_m[kW], part_s[kW];
+  const int lane = threadIdx.x & 63, v = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  if (row >= M) return;  // uniform per workgroup
+  const float* xr = x + row * N + v * kWave + lane;
+  float* yr = y + row * N + v * kWave + lane;
+  const int64_t left = N - (v * kWave + lane);  // elements of this lane: index i*kW*64 < left
+  const float ninf = -__builtin_inff();
+  float e[kEpl];
+#pragma unroll
+  for (int i = 0; i < kEpl; ++i) e[i] = i * kW * kWave < left ? __builtin_nontemporal_load(xr + i * kW * kWave) : ninf;
+  float mx = ninf;
+#pragma unroll
+  for (int i = 0; i < kEpl; ++i) mx = max_nan(mx, e[i]);
+  mx = wave_max_nan(mx);
+  if (kW > 1) {
+    if (lane == 0) part_m[v] = mx;
+    __syncthreads();
+    mx = part_m[0];
+#pragma unroll
+    for (int k = 1; k < kW; ++k) mx = max_nan(mx, part_m[k]);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kEpl; ++i) {
+    e[i] = exp_nonpos(e[i] - mx);
+    if (i * kW * kWave < left) sum += e[i];
+  }
+  sum = wave_sum(sum);
+  if (kW > 1) {
+    if (lane == 0) part_s[v] = sum;
+    __syncthreads();
+    sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < kW; ++k) sum += part_s[k];
+  }
+  const float inv = 1.0f / sum;
+#pragma unroll
+  for (int i = 0; i < kEpl; ++i)
+    if (i * kW * kWave < left) __builtin_nontemporal_store(e[i] * inv, yr + i * kW * kWave);
+}
+
 // Any N: one workgroup per row, three passes (max, sum, write) over the row.
 __global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restrict__ x, float* __restrict__ y, int64_t N) {
   __shared__ float scratch[4];
@@ -395,6 +444,18 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
     softmax_rows_f32_multi<16, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x4, y4, M, n4i);
   else if (vec && n4 <= 16384)
     softmax_rows_f32_multi<16, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x4, y4, M, n4i);
+  else if (!vec && N <= 64 * 16)
+    softmax_rows_f32_regs<16, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N);
+  else if (!vec && N <= 64 * 64)
+    softmax_rows_f32_regs<64, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N);
+  else if (!vec && N <= 64 * 64 * 2)
+    softmax_rows_f32_regs<64, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x, y, M, N);
+  else if (!vec && N <= 64 * 64 * 4)
+    softmax_rows_f32_regs<64, 4><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, M, N);
+  else if (!vec && N <= 64 * 64 * 8)
+    softmax_rows_f32_regs<64, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x, y, M, N);
+  else if (!vec && N <= 64 * 64 * 16)
+    softmax_rows_f32_regs<64, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, M, N);
   else
     softmax_rows_f32_any<<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, N);
   return hipGetLastError();

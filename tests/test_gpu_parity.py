@@ -205,11 +205,12 @@ def test_row_reduce_full_size(hip):
 
 # ------------------------------------------------------------------ softmax
 @pytest.mark.parametrize("M", [1, 7, 33])
-@pytest.mark.parametrize("N", EDGE + [64, 256, 1000, 1024, 4096, 4100, 5000, 8192, 8196, 16384, 32000, 32768, 65536,
-                                      65540])
+@pytest.mark.parametrize("N", EDGE + [64, 256, 1000, 1001, 1024, 1025, 4096, 4097, 4100, 5000, 8191, 8192, 8196, 16384,
+                                      32000, 32768, 50257, 65535, 65536, 65537, 65540])
 def test_softmax_edge_shapes(hip, M, N):
-    """One wave per row up to N = 4096, 2-16 waves per row up to 65536 (4100, 8196: the first
-    size past a form's capacity), the three-pass kernel beyond or for N % 4 != 0."""
+    """N % 4 == 0: one wave per row up to N = 4096, 2-16 waves per row up to 65536 (4100, 8196:
+    the first size past a form's capacity).  N % 4 != 0: the row in registers through 4-byte
+    loads up to 65535 (1025, 4097: past a form's capacity).  The three-pass kernel beyond."""
     w = WORKLOADS["softmax"]
     b = {"M": M, "N": N}
     inp = w.gen(b, seed=M + N)
