@@ -393,14 +393,31 @@ def _match_elementwise(c: _Ctx) -> Optional[HipLoweredKernel]:
     for n, _ in prog.inputs:
         if n not in used:
             used.append(n)
-    d3 = shp[-1] if shp else 1
-    rows = 1
-    for d in shp[:-1]:
-        rows *= d
-    gx = max(1, min(1024, _cdiv(_cdiv(d3, 4), 256)))
-    launch = HipLaunch((gx, max(1, min(rows, 65535, _cdiv(4096, gx))), 1), (256, 1, 1), 0)
+    launch = _ew_launch(prog, c.dtype)
     return HipLoweredKernel(c.fn.name, "ihip_elementwise_program", c.io(used + outs), launch, outs, dict(c.b),
                             (("ew_program", prog),))
+
+
+def _ew_launch(prog, dtype_of) -> HipLaunch:
+    """The launch ihip_elementwise_program plans (ewjit.hip plan_jit) for dense 16-byte aligned
+    outputs: lanes own 8 elements when every operand is 16-bit or narrower, else 4.  Inputs read
+    across their unit-stride axis (axis 2 contiguous, axis 3 strided; up to 4) select the
+    LDS-tiled form: one workgroup per 64 x 64 tile, a 64 x 65 f32 tile each.  Otherwise a few
+    thousand 256-lane workgroups stride over rows and vectors."""
+    sh = [1] * (4 - len(prog.shape)) + [int(d) for d in prog.shape]
+    narrow = all(dtype_of(n) in ("f16", "bf16", "bool", "i1", "u8") for n in [i for i, _ in prog.inputs] + list(prog.outputs))
+    v = 8 if narrow else 4
+    tiled = 0
+    if sh[2] > 1 and sh[3] > 1:
+        for _, st in prog.inputs:
+            if tiled < 4 and st[2] == 1 and st[3] not in (0, 1):
+                tiled += 1
+    if tiled:
+        tx, ty = _cdiv(sh[3], 64), sh[0] * sh[1] * _cdiv(sh[2], 64)
+        return HipLaunch((max(1, min(tx, 65535)), max(1, min(ty, 65535)), 1), (256, 1, 1), tiled * 64 * 65 * 4)
+    rows = sh[0] * sh[1] * sh[2]
+    gx = max(1, min(1024, _cdiv(_cdiv(sh[3], v), 256)))
+    return HipLaunch((gx, max(1, min(rows, 65535, _cdiv(4096, gx))), 1), (256, 1, 1), 0)
 
 
 _MATCHERS = (_match_gemm, _match_reduce_any, _match_softmax, _match_layernorm, _match_gelu_axpy, _match_row_reduce,

@@ -277,3 +277,16 @@ def test_c_abi_accepts_empty_iteration_space_without_a_device():
     st, err = _prog_call(load_library(), [(OP["load"], 0, 0, 0, 0), (OP["exp"], 1, 0, 0, 0),
                                           (OP["store"], 0, 1, 0, 0)], shape=(0, 8))
     assert st == 0, err
+
+
+@pytest.mark.parametrize("name,bindings,launch", [
+    ("transpose_add", {"M": 8192, "N": 8192}, ((128, 128, 1), 16640)),          # LDS-tiled: 64 x 64 tiles
+    ("transpose_batched_3d", {"A": 4, "M": 256, "N": 520}, ((4, 36, 1), 16640)),
+    ("half_inputs_bf16_out", {"M": 8192, "N": 8192}, ((4, 1024, 1), 0)),       # 16-bit operands: 8 per lane
+    ("add_bias_relu", {"M": 8192, "N": 8192}, ((8, 512, 1), 0)),               # f32: 4 per lane
+])
+def test_launch_descriptor_follows_the_native_plan(name, bindings, launch):
+    """The lowering's launch plan is the one ihip_elementwise_program uses for dense aligned operands."""
+    ir = next(c[1] for c in CASES if c[0] == name)
+    k = lower_intent_to_hip_kernel(ir, shape_bindings=bindings)
+    assert (k.launch.grid, k.launch.lds_bytes) == launch
