@@ -1,0 +1,152 @@
+"""Randomised element-wise chains through the program compiler and kernels.
+
+Each seed builds an IR over x, y [M, N], a bias b [N] (aligned by its symbol), a
+column c [M, 1] and a scalar attribute, with 4-14 ops drawn from the
+interpreter's element-wise tables (verify/interpreter.py:16-48) and one or two
+outputs.  Ops are kept well conditioned so that f32 rounding differences stay
+small: exp only of non-positive values, division only by 1 + |t|, no
+comparison of computed values against each other.
+
+* CPU: the numpy model of the program kernel (tests/test_ewprogram.py) is
+  judged against the oracle; it performs the same f32 operations, so this
+  checks the compiler (hash-consed DAG, Sethi-Ullman order, register
+  assignment by last use, broadcast strides), not rounding.
+* GPU: the native and interpreted kernels, at sizes with tails, are judged
+  against the oracle within f32 tolerances.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from intent_ir_amd import HipLoweringError, lower_intent_to_hip_kernel
+from tests.test_ewprogram import oracle_outputs, run_model
+
+UNARY = ["relu", "abs", "negate", "expneg", "sq", "floor"]
+BINARY = ["add", "sub", "mul", "max", "min", "div1"]
+
+
+SHAPE = {"full": ["M", "N"], "row": ["N"], "col": ["M", 1]}
+
+
+def _join(a: str, b: str) -> str:
+    """Shape class of a binary op's result: [N] with [M, 1] broadcasts to [M, N]."""
+    return a if a == b else "full"
+
+
+def random_chain(seed: int) -> dict:
+    rng = np.random.default_rng(seed)
+    tensors = {"x": {"dtype": "f32", "shape": SHAPE["full"]}, "y": {"dtype": "f32", "shape": SHAPE["full"]},
+               "b": {"dtype": "f32", "shape": SHAPE["row"]}, "c": {"dtype": "f32", "shape": SHAPE["col"]}}
+    kind = {"x": "full", "y": "full", "b": "row", "c": "col"}
+    ops, vals = [], ["x", "y", "b", "c"]
+    n_ops = int(rng.integers(4, 15))
+    k = 0
+
+    def fresh(shape_kind):
+        nonlocal k
+        k += 1
+        name = f"t{k}"
+        tensors[name] = {"dtype": "f32", "shape": SHAPE[shape_kind]}
+        kind[name] = shape_kind
+        return name
+
+    def pick():
+        # favour recent values so chains get deep, but reuse old ones for shared subexpressions
+        i = len(vals) - 1 - int(min(len(vals) - 1, rng.geometric(0.35) - 1))
+        return vals[i]
+
+    for _ in range(n_ops):
+        if rng.random() < 0.4:
+            u, a = UNARY[int(rng.integers(len(UNARY)))], pick()
+            ka = kind[a]
+            if u == "expneg":  # exp(-|a|) in (0, 1]
+                t1, t2, out = fresh(ka), fresh(ka), fresh(ka)
+                ops += [{"op": "abs", "inputs": [a], "output": t1},
+                        {"op": "mul", "inputs": [t1], "output": t2, "attrs": {"mul_factor": -1.0}},
+                        {"op": "exp", "inputs": [t2], "output": out}]
+            elif u == "sq":
+                out = fresh(ka)
+                ops.append({"op": "mul", "inputs": [a, a], "output": out})
+            elif u == "negate":
+                out = fresh(ka)
+                ops.append({"op": "mul", "inputs": [a], "output": out, "attrs": {"mul_factor": -1.0}})
+            else:
+                out = fresh(ka)
+                ops.append({"op": u, "inputs": [a], "output": out})
+        else:
+            bop, a, b = BINARY[int(rng.integers(len(BINARY)))], pick(), pick()
+            kab = _join(kind[a], kind[b])
+            if bop == "div1":  # a / (1 + |b|)
+                t1, t2, out = fresh(kind[b]), fresh(kind[b]), fresh(kab)
+                ops += [{"op": "abs", "inputs": [b], "output": t1},
+                        {"op": "add", "inputs": [t1], "output": t2, "attrs": {"addend": 1.0}},
+                        {"op": "div", "inputs": [a, t2], "output": out}]
+            elif rng.random() < 0.2:  # scalar-attribute form
+                out = fresh(kind[a])
+                attr = {"add": ("addend", 0.5), "sub": ("subtract", 0.25), "mul": ("mul_factor", -1.5),
+                        "max": ("other", 0.1), "min": ("other", -0.1)}[bop]
+                ops.append({"op": bop, "inputs": [a], "output": out, "attrs": {attr[0]: attr[1]}})
+            else:
+                out = fresh(kab)
+                ops.append({"op": bop, "inputs": [a, b], "output": out})
+        vals.append(out)
+    if kind[vals[-1]] != "full":  # outputs span the whole [M, N] space
+        out = fresh("full")
+        ops.append({"op": "add", "inputs": [vals[-1], "x"], "output": out})
+        vals.append(out)
+    outs = [vals[-1]]
+    if len(vals) > 6 and rng.random() < 0.4 and vals[-3] not in ("x", "y", "b", "c") and kind[vals[-3]] == "full":
+        outs.append(vals[-3])
+    return {"name": f"fuzz{seed}", "tensors": tensors, "ops": ops, "outputs": outs}
+
+
+def inputs_for(seed: int, M: int, N: int) -> dict:
+    rng = np.random.default_rng(seed + 1)
+    return {"x": rng.standard_normal((M, N)).astype(np.float32), "y": rng.standard_normal((M, N)).astype(np.float32),
+            "b": rng.standard_normal(N).astype(np.float32), "c": rng.standard_normal((M, 1)).astype(np.float32)}
+
+
+def lower_or_skip(ir: dict, b: dict):
+    try:
+        k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    except HipLoweringError as e:
+        assert "live" in str(e) or "register" in str(e), str(e)  # only the 8-register limit may refuse a chain
+        pytest.skip(f"needs more than 8 live values: {e}")
+    assert k.kernel_id == "ihip_elementwise_program"
+    return k
+
+
+@pytest.mark.parametrize("seed", range(120))
+def test_random_chain_compiles_to_the_oracle(seed):
+    ir = random_chain(seed)
+    b = {"M": 5, "N": 12}
+    k = lower_or_skip(ir, b)
+    storage = inputs_for(seed, 5, 12)
+    got = run_model(k.call_args[0][1], storage, {n: "f32" for n in ir["tensors"]})
+    ref = oracle_outputs(ir, storage, b)
+    for o in ir["outputs"]:
+        np.testing.assert_allclose(got[o].reshape(ref[o].shape), ref[o], rtol=1e-6, atol=1e-6, err_msg=f"seed {seed} {o}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", [0, 1], ids=["native", "interp"])
+@pytest.mark.parametrize("seed", range(0, 120, 3))
+def test_random_chain_on_gpu(hip, seed, mode):
+    from intent_ir_amd import run_lowered
+
+    ir = random_chain(seed)
+    M, N = 67, 1029  # tails in both axes
+    b = {"M": M, "N": N}
+    k = lower_or_skip(ir, b)
+    storage = inputs_for(seed, M, N)
+    prev = hip.ihip_elementwise_mode(mode)
+    try:
+        print(f"[case] fuzz seed={seed} mode={mode} M={M} N={N}", flush=True)
+        got = run_lowered(k, storage)
+    finally:
+        hip.ihip_elementwise_mode(prev)
+    ref = oracle_outputs(ir, storage, b)
+    for o in ir["outputs"]:
+        np.testing.assert_allclose(got[o].reshape(ref[o].shape), ref[o], rtol=2e-6, atol=2e-6, err_msg=f"seed {seed} {o}")
