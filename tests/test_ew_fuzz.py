@@ -12,7 +12,10 @@ comparison of computed values against each other.
   checks the compiler (hash-consed DAG, Sethi-Ullman order, register
   assignment by last use, broadcast strides), not rounding.
 * GPU: the native and interpreted kernels, at sizes with tails, are judged
-  against the oracle within f32 tolerances.
+  against the oracle within f32 tolerances (bf16 outputs: one RNE rounding).
+
+Variants: f32 or bf16 x, y and outputs (16-bit operands run 8 elements per lane),
+with or without an input read through transpose (the LDS-tiled form).
 """
 
 from __future__ import annotations
@@ -21,6 +24,7 @@ import numpy as np
 import pytest
 
 from intent_ir_amd import HipLoweringError, lower_intent_to_hip_kernel
+from intent_ir_amd.dtypes import bf16_bits_to_f32, f32_to_bf16_bits
 from tests.test_ewprogram import oracle_outputs, run_model
 
 UNARY = ["relu", "abs", "negate", "expneg", "sq", "floor"]
@@ -35,12 +39,20 @@ def _join(a: str, b: str) -> str:
     return a if a == b else "full"
 
 
-def random_chain(seed: int) -> dict:
+def random_chain(seed: int, dt: str = "f32", transpose: bool = False) -> dict:
+    """dt: dtype of x, y and the outputs (b, c stay f32).  transpose: a further input z [N, M]
+    enters the chain as transpose(z), which the kernels stage through LDS tiles."""
     rng = np.random.default_rng(seed)
-    tensors = {"x": {"dtype": "f32", "shape": SHAPE["full"]}, "y": {"dtype": "f32", "shape": SHAPE["full"]},
+    tensors = {"x": {"dtype": dt, "shape": SHAPE["full"]}, "y": {"dtype": dt, "shape": SHAPE["full"]},
                "b": {"dtype": "f32", "shape": SHAPE["row"]}, "c": {"dtype": "f32", "shape": SHAPE["col"]}}
     kind = {"x": "full", "y": "full", "b": "row", "c": "col"}
     ops, vals = [], ["x", "y", "b", "c"]
+    if transpose:
+        tensors["z"] = {"dtype": "f32", "shape": ["N", "M"]}
+        tensors["zt"] = {"dtype": "f32", "shape": SHAPE["full"]}
+        kind["zt"] = "full"
+        ops.append({"op": "transpose", "inputs": ["z"], "output": "zt", "attrs": {"perm": [1, 0]}})
+        vals.append("zt")
     n_ops = int(rng.integers(4, 15))
     k = 0
 
@@ -97,15 +109,22 @@ def random_chain(seed: int) -> dict:
         ops.append({"op": "add", "inputs": [vals[-1], "x"], "output": out})
         vals.append(out)
     outs = [vals[-1]]
-    if len(vals) > 6 and rng.random() < 0.4 and vals[-3] not in ("x", "y", "b", "c") and kind[vals[-3]] == "full":
+    if len(vals) > 6 and rng.random() < 0.4 and vals[-3] not in ("x", "y", "b", "c", "zt") and kind[vals[-3]] == "full":
         outs.append(vals[-3])
+    for o in outs:
+        tensors[o]["dtype"] = dt
     return {"name": f"fuzz{seed}", "tensors": tensors, "ops": ops, "outputs": outs}
 
 
-def inputs_for(seed: int, M: int, N: int) -> dict:
+def inputs_for(seed: int, M: int, N: int, dt: str = "f32", transpose: bool = False) -> dict:
     rng = np.random.default_rng(seed + 1)
-    return {"x": rng.standard_normal((M, N)).astype(np.float32), "y": rng.standard_normal((M, N)).astype(np.float32),
-            "b": rng.standard_normal(N).astype(np.float32), "c": rng.standard_normal((M, 1)).astype(np.float32)}
+    full = lambda: rng.standard_normal((M, N)).astype(np.float32)  # noqa: E731
+    x, y = (full(), full()) if dt == "f32" else (f32_to_bf16_bits(full()), f32_to_bf16_bits(full()))
+    d = {"x": x, "y": y, "b": rng.standard_normal(N).astype(np.float32),
+         "c": rng.standard_normal((M, 1)).astype(np.float32)}
+    if transpose:
+        d["z"] = rng.standard_normal((N, M)).astype(np.float32)
+    return d
 
 
 def lower_or_skip(ir: dict, b: dict):
@@ -118,35 +137,45 @@ def lower_or_skip(ir: dict, b: dict):
     return k
 
 
+VARIANTS = [("f32", False), ("f32", True), ("bf16", False), ("bf16", True)]
+TOLS = {"f32": (1e-6, 2e-6), "bf16": (1e-3, 1e-2)}  # (atol, rtol); bf16: one RNE rounding of the output
+
+
+def _check(got, ref, ir, dt, what):
+    atol, rtol = TOLS[dt]
+    for o in ir["outputs"]:
+        g = np.asarray(got[o])
+        g = bf16_bits_to_f32(g) if g.dtype == np.uint16 else g.astype(np.float32)
+        np.testing.assert_allclose(g.reshape(ref[o].shape), ref[o], rtol=rtol, atol=atol, err_msg=f"{what} {o}")
+
+
+@pytest.mark.parametrize("dt,transpose", VARIANTS, ids=[f"{d}{'-T' if t else ''}" for d, t in VARIANTS])
 @pytest.mark.parametrize("seed", range(120))
-def test_random_chain_compiles_to_the_oracle(seed):
-    ir = random_chain(seed)
+def test_random_chain_compiles_to_the_oracle(seed, dt, transpose):
+    ir = random_chain(seed, dt, transpose)
     b = {"M": 5, "N": 12}
     k = lower_or_skip(ir, b)
-    storage = inputs_for(seed, 5, 12)
-    got = run_model(k.call_args[0][1], storage, {n: "f32" for n in ir["tensors"]})
-    ref = oracle_outputs(ir, storage, b)
-    for o in ir["outputs"]:
-        np.testing.assert_allclose(got[o].reshape(ref[o].shape), ref[o], rtol=1e-6, atol=1e-6, err_msg=f"seed {seed} {o}")
+    storage = inputs_for(seed, 5, 12, dt, transpose)
+    got = run_model(k.call_args[0][1], storage, {n: t["dtype"] for n, t in ir["tensors"].items()})
+    _check(got, oracle_outputs(ir, storage, b), ir, dt, f"seed {seed}")
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("mode", [0, 1], ids=["native", "interp"])
-@pytest.mark.parametrize("seed", range(0, 120, 3))
-def test_random_chain_on_gpu(hip, seed, mode):
+@pytest.mark.parametrize("dt,transpose", VARIANTS, ids=[f"{d}{'-T' if t else ''}" for d, t in VARIANTS])
+@pytest.mark.parametrize("seed", range(0, 120, 4))
+def test_random_chain_on_gpu(hip, seed, dt, transpose, mode):
     from intent_ir_amd import run_lowered
 
-    ir = random_chain(seed)
-    M, N = 67, 1029  # tails in both axes
+    ir = random_chain(seed, dt, transpose)
+    M, N = 67, 1032 if dt == "bf16" else 1029  # tails in both axes (bf16: 8-wide vectors)
     b = {"M": M, "N": N}
     k = lower_or_skip(ir, b)
-    storage = inputs_for(seed, M, N)
+    storage = inputs_for(seed, M, N, dt, transpose)
     prev = hip.ihip_elementwise_mode(mode)
     try:
-        print(f"[case] fuzz seed={seed} mode={mode} M={M} N={N}", flush=True)
+        print(f"[case] fuzz seed={seed} dt={dt} transpose={transpose} mode={mode} M={M} N={N}", flush=True)
         got = run_lowered(k, storage)
     finally:
         hip.ihip_elementwise_mode(prev)
-    ref = oracle_outputs(ir, storage, b)
-    for o in ir["outputs"]:
-        np.testing.assert_allclose(got[o].reshape(ref[o].shape), ref[o], rtol=2e-6, atol=2e-6, err_msg=f"seed {seed} {o}")
+    _check(got, oracle_outputs(ir, storage, b), ir, dt, f"seed {seed}")
