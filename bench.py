@@ -239,7 +239,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every path here runs on one "
-              "MI355X; sharding is described in DESIGN.md)", file=sys.stderr)
+              "MI355X: the row workloads would shard by rows with no exchange, the GEMM by C tiles)", file=sys.stderr)
         sys.exit(2)
     import torch
 

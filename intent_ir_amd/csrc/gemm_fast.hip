@@ -11,6 +11,10 @@
 //  * one 256x256 C tile per workgroup of 256 threads = 4 waves in a 2x2 grid; wave (wm, wn)
 //    owns rows wm*128 + [0,128) and the four 32-column blocks wn*32 + 64*ni, ni = 0..3
 //    (4x4 MFMA blocks, 256 f32 accumulators per lane, held in AGPRs);
+//  * grids of at most 128 such tiles (half the CUs) use 128x128 tiles instead, with the same
+//    wave grid over 2x2 MFMA blocks per wave: twice the LDS reads per MFMA, but up to four
+//    times the busy CUs; every C element accumulates the same MFMAs in the same k order in
+//    either form, so the results are identical;
 //  * tiles are remapped so each of the 8 XCDs (private L2) works on one contiguous range,
 //    rastered in groups of 8 tile-rows, so concurrently running tiles share A rows and
 //    B columns in L2.
@@ -55,7 +59,6 @@ typedef __attribute__((address_space(3))) char lds_wchar_t;
 typedef __attribute__((address_space(3))) u32x2 lds_u32x2_t;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4_t;
 
-constexpr int kTile = 256;   // M and N extent of a workgroup tile
 constexpr int kGroupRows = 8;  // tile-rows per raster group
 
 typedef __bf16 bf16x2_pk_t __attribute__((ext_vector_type(2)));
@@ -68,13 +71,20 @@ typedef __bf16 bf16x2_pk_t __attribute__((ext_vector_type(2)));
 // identical results.
 // EDGE: the tile reaches past M or N; its copies go through range-checked buffer descriptors
 // (interior tiles use global_load_lds, which measured ~14% faster on full 8192^3 GEMMs).
-template <int DK, int STAGES, bool AKM = false, bool BKM = true, bool EDGE = false>
+// TILE: M and N extent of the workgroup tile (256, or 128 for grids that would leave CUs idle);
+// the four waves form a 2x2 grid either way, each owning TILE/64 x TILE/64 MFMA blocks.
+template <int DK, int STAGES, bool AKM = false, bool BKM = true, bool EDGE = false, int TILE = 256>
 struct FastGemm {
+  static_assert(TILE == 256 || TILE == 128, "tile extents");
+  static constexpr int kBlk = TILE / 64;           // 32-row A blocks and 32-column B blocks per wave
   static constexpr int kRowA = DK * 2;             // bytes per K-contiguous tile row
   static constexpr int kChunksA = DK / 8;          // 16-byte chunks per row
   static constexpr int kRowsPerWindow = 256 / kRowA;
-  static constexpr int kStageA = kTile * kRowA;    // bytes per operand tile (either layout)
-  static constexpr int kStageB = DK * kTile * 2;
+  static constexpr int kRowKM = TILE * 2;          // bytes per K-major tile row
+  static constexpr int kChunksKM = TILE / 8;       // 16-byte chunks per K-major row
+  static constexpr int kRowsPerInstrKM = 1024 / kRowKM;
+  static constexpr int kStageA = TILE * kRowA;     // bytes per operand tile (either layout)
+  static constexpr int kStageB = DK * TILE * 2;
   static constexpr int kStage = kStageA + kStageB;
   static constexpr int kInstrA = kStageA / 1024 / 4;  // direct-to-LDS instructions per wave per stage
   static constexpr int kInstrB = kStageB / 1024 / 4;
@@ -106,9 +116,11 @@ struct FastGemm {
       const int r0 = wave * kRowsPerInstrA + lane / kChunksA;
       return 2u * static_cast<uint32_t>((lane / kChunksA) * K + a_slot(lane % kChunksA, r0) * 8);
     }
-    // instruction j holds k-rows 2j, 2j+1; k & 3 == (2*wave + lane/32) & 3 for every i
-    const int kb = 2 * wave + (lane >> 5);
-    return 2u * static_cast<uint32_t>((lane >> 5) * ld + b_logical(lane & 31, kb) * 8);
+    // instruction j = 4i + wave holds k-rows j*RPK + lane / CK (RPK = 1024 / row bytes, CK
+    // chunks per row), chunk lane % CK; k & 3 == (wave*RPK + lane/CK) & 3 for every i
+    const int row = lane / kChunksKM;
+    const int kb = wave * kRowsPerInstrKM + row;
+    return 2u * static_cast<uint32_t>(row * ld + b_logical(lane % kChunksKM, kb) * 8);
   }
 
   // First k within the slice of the chunk a lane copies (K-contiguous operand; the swizzle
@@ -129,7 +141,7 @@ struct FastGemm {
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
         const int x = base + blk * step + (g & 1) * 16 + 4 * (i & 3);
-        o[blk] = region + k * 512 + b_slot(x >> 3, k) * 16 + (x & 7) * 2;
+        o[blk] = region + k * kRowKM + b_slot(x >> 3, k) * 16 + (x & 7) * 2;
       }
     }
   }
@@ -141,7 +153,7 @@ struct FastGemm {
     L.b = copy_off(BKM, N, K, wave, lane);
     L.ka = copy_k(AKM, wave, lane);
     L.kb = copy_k(BKM, wave, lane);
-    frag_off(AKM, 0, wm * 128, 32, lane, L.fa);
+    frag_off(AKM, 0, wm * (TILE / 2), 32, lane, L.fa);
     frag_off(BKM, kStageA, wn * 32, 64, lane, L.fb);
     return L;
   }
@@ -189,10 +201,10 @@ struct FastGemm {
   }
 
   // Byte offset of copy instruction j from its operand's slice base: tile rows j*RPI.. of a
-  // K-contiguous operand (leading dim K), k-rows 2j, 2j+1 of a K-major one (leading dim ld).
+  // K-contiguous operand (leading dim K), k-rows j*RPK.. of a K-major one (leading dim ld).
   template <bool kKMajor>
   static __device__ __forceinline__ uint32_t instr_off(int j, int64_t ld, int64_t K) {
-    return static_cast<uint32_t>(kKMajor ? 2 * j * ld * 2 : j * kRowsPerInstrA * K * 2);
+    return static_cast<uint32_t>(kKMajor ? j * kRowsPerInstrKM * ld * 2 : j * kRowsPerInstrA * K * 2);
   }
 
   // Slice base of an operand: tile rows x0.. at k0 (K-contiguous) or k-row k0 at column x0
@@ -241,19 +253,20 @@ struct FastGemm {
   }
 
   struct Frag {
-    bf16x8_t a[4], b[4];
+    bf16x8_t a[kBlk], b[kBlk];
   };
 
   template <bool kKMajor>
   static __device__ __forceinline__ void read_operand(const lds_char_t* st, int kk, const int (&o)[4], int blk_stride,
-                                                      bf16x8_t (&f)[4]) {
+                                                      bf16x8_t (&f)[kBlk]) {
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
+    for (int blk = 0; blk < kBlk; ++blk) {
       if (!kKMajor) {
         f[blk] = *(const lds_bf16x8_t*)(st + o[kk] + blk * blk_stride);
       } else {
-        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + kk * 16 * 512));
-        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + (kk * 16 + 4) * 512));
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + kk * 16 * kRowKM));
+        const i16x4_t hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + (kk * 16 + 4) * kRowKM));
         const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         f[blk] = __builtin_bit_cast(bf16x8_t, both);
       }
@@ -268,17 +281,18 @@ struct FastGemm {
   // The fragment reads of one k16 step as a flat list of LDS instructions ("slots"): A's
   // first, then B's; a K-contiguous operand takes one ds_read_b128 per block, a K-major one
   // two ds_read_b64_tr_b16 (low and high four k) per block.
-  static constexpr int kSlotsA = AKM ? 8 : 4;
-  static constexpr int kSlots = kSlotsA + (BKM ? 8 : 4);
+  static constexpr int kSlotsA = AKM ? 2 * kBlk : kBlk;
+  static constexpr int kSlots = kSlotsA + (BKM ? 2 * kBlk : kBlk);
 
   template <bool kKMajor>
   static __device__ __forceinline__ void read_operand_slot(const lds_char_t* st, int kk, const int (&o)[4],
-                                                           int blk_stride, bf16x8_t (&f)[4], int slot) {
+                                                           int blk_stride, bf16x8_t (&f)[kBlk], int slot) {
     if (!kKMajor) {
       f[slot] = *(const lds_bf16x8_t*)(st + o[kk] + slot * blk_stride);
     } else {
       const int blk = slot >> 1, half = slot & 1;
-      const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + (kk * 16 + half * 4) * 512));
+      const i16x4_t v =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + (kk * 16 + half * 4) * kRowKM));
       i16x8_t w = __builtin_bit_cast(i16x8_t, f[blk]);
       if (half == 0) {
         w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
@@ -297,9 +311,10 @@ struct FastGemm {
   }
 
   // The MFMAs of B block ni against A blocks lo .. hi-1.
-  static __device__ __forceinline__ void mfma_range(const Frag& f, f32x16_t (&acc)[4][4], int ni, int lo, int hi) {
+  static __device__ __forceinline__ void mfma_range(const Frag& f, f32x16_t (&acc)[kBlk][kBlk], int ni, int lo,
+                                                   int hi) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < kBlk; ++mi)
       if (mi >= lo && mi < hi)
         acc[ni][mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[ni], f.a[mi], acc[ni][mi], 0, 0, 0);
   }
@@ -327,22 +342,28 @@ struct FastGemm {
 
 };
 
-constexpr int kCPitch = kTile * 2 + 16;  // bytes per staged C row (16 bytes of padding)
-
-// LDS bytes of the stage ring, which after the main loop holds the bf16 C tile.
-template <int DK, int STAGES>
-constexpr int fast_lds_bytes() {
-  return STAGES * FastGemm<DK, STAGES>::kStage > kTile * kCPitch ? STAGES * FastGemm<DK, STAGES>::kStage
-                                                                  : kTile * kCPitch;
+// Bytes per staged C row (16 bytes of padding).
+template <int TILE>
+constexpr int c_pitch() {
+  return TILE * 2 + 16;
 }
 
-// One 256x256 C tile at (m0, n0); lds_raw / bias_lds are the kernel's LDS.
-template <int DK, int STAGES, bool AKM, bool BKM, bool EDGE>
+// LDS bytes of the stage ring, which after the main loop holds the bf16 C tile.
+template <int DK, int STAGES, int TILE>
+constexpr int fast_lds_bytes() {
+  constexpr int ring = STAGES * FastGemm<DK, STAGES, false, true, false, TILE>::kStage;
+  return ring > TILE * c_pitch<TILE>() ? ring : TILE * c_pitch<TILE>();
+}
+
+// One TILE x TILE C tile at (m0, n0); lds_raw / bias_lds are the kernel's LDS.
+template <int DK, int STAGES, bool AKM, bool BKM, bool EDGE, int TILE>
 __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                const float* __restrict__ bias, uint16_t* __restrict__ C, int64_t M,
                                                int64_t N, int64_t K, int relu, int64_t m0, int64_t n0, char* lds_raw,
                                                float* bias_lds) {
-  using G = FastGemm<DK, STAGES, AKM, BKM, EDGE>;
+  using G = FastGemm<DK, STAGES, AKM, BKM, EDGE, TILE>;
+  constexpr int kBlk = G::kBlk;
+  constexpr int kCPitch = c_pitch<TILE>();
   static_assert(STAGES >= 3, "the pipeline keeps two slices ahead");
   const lds_char_t* lds = (const lds_char_t*)lds_raw;
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
@@ -350,15 +371,16 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave & 1, wn = wave >> 1;
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[kBlk][kBlk];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kBlk; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < kBlk; ++j) acc[i][j] = f32x16_t{};
 
-  // The tile's 256 bias values are staged in LDS now, so the epilogue does not wait on global
+  // The tile's TILE bias values are staged in LDS now, so the epilogue does not wait on global
   // loads (their latency hides behind the prologue copies; the prologue barrier publishes them).
-  bias_lds[threadIdx.x] = bias != nullptr && (!EDGE || n0 + threadIdx.x < N) ? bias[n0 + threadIdx.x] : 0.0f;
+  if (threadIdx.x < TILE)
+    bias_lds[threadIdx.x] = bias != nullptr && (!EDGE || n0 + threadIdx.x < N) ? bias[n0 + threadIdx.x] : 0.0f;
 
   const typename G::Lane L = G::lane_plan(M, N, K, wave, wm, wn, lane);
   const int KT = static_cast<int>((K + DK - 1) / DK);  // a ragged last slice only in edge instances
@@ -371,8 +393,8 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
   G::wait_copies((KT < kLead ? KT : kLead) - 1);
   __syncthreads();
 
-  // Main loop, software-pipelined per k16 step.  A step is four quarters of four MFMAs (one
-  // B block against the four A blocks); the next step's fragment reads are slotted between a
+  // Main loop, software-pipelined per k16 step.  A step is kBlk quarters of kBlk MFMAs (one
+  // B block against the wave's A blocks); the next step's fragment reads are slotted between a
   // quarter's MFMAs (sched_group_barrier), so no MFMA waits on LDS, and one copy instruction of
   // slice kt+kLead follows each of the first kPerStep quarters, so a wave never issues its
   // copies in a burst (a burst of copies stalls the issuing wave and skews the waves against
@@ -385,9 +407,9 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
   // next slice.
   constexpr int NK = DK / 16;
   constexpr int kPerStep = G::kInstr / NK;
-  static_assert(G::kInstr % NK == 0 && kPerStep <= 4, "at most one copy per quarter");
-  constexpr int kPerQ = G::kSlots / 4;
-  static_assert(G::kSlots % 4 == 0, "reads split evenly over quarters");
+  static_assert(G::kInstr % NK == 0 && kPerStep <= kBlk, "at most one copy per quarter");
+  constexpr int kPerQ = G::kSlots / kBlk;
+  static_assert(G::kSlots % kBlk == 0 && kPerQ <= 4, "reads split evenly over quarters");
   static_assert(NK % 2 == 0, "fragment double buffer alternates within a slice");
   constexpr int kPre = 1;
   // copies in flight when slice kt+1 must have landed: slices kt+2 .. kt+kLead-1 and the part
@@ -410,7 +432,7 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
       const lds_char_t* rs = boundary ? lds + ((kt + 1) % STAGES) * G::kStage : st;
       const int rk = boundary ? 0 : kk + 1;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < kBlk; ++q) {
         // every quarter starts after all instructions of the previous one
         __builtin_amdgcn_sched_barrier(0);
         const bool pre = boundary && q == 0 && more;
@@ -428,11 +450,11 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
 #pragma unroll
           for (int r = 0; r < kPerQ; ++r) G::read_slot(rs, rk, L, nxt, q * kPerQ + r);
         }
-        G::mfma_range(cur, acc, q, from, 4);
+        G::mfma_range(cur, acc, q, from, kBlk);
         if (more) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            if (j < 4 - from) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            if (j < kBlk - from) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
             if (j < kPerQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // one LDS read
           }
         }
@@ -462,14 +484,14 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
   lds_wchar_t* ct = (lds_wchar_t*)lds_raw;
   const float floor_v = relu ? 0.0f : -__builtin_inff();
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) {
+  for (int ni = 0; ni < kBlk; ++ni) {
     f32x4_t bv[4];
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4)
       bv[g4] = *reinterpret_cast<const f32x4_t*>(&bias_lds[wn * 32 + ni * 64 + g4 * 8 + (lane >> 5) * 4]);
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      const int ml = wm * 128 + mi * 32 + (lane & 31);
+    for (int mi = 0; mi < kBlk; ++mi) {
+      const int ml = wm * (TILE / 2) + mi * 32 + (lane & 31);
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         const int nl = wn * 32 + ni * 64 + g4 * 8 + (lane >> 5) * 4;
@@ -485,26 +507,30 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
     }
   }
   __syncthreads();
-  // 256 rows of 512 bytes; one store instruction covers two rows (32 lanes x 16 bytes each).
-  // An edge tile stores only rows < M and 16-byte chunks of columns < N (N % 8 == 0).
-  const bool col_ok = n0 + (lane & 31) * 8 < N;
+  // TILE rows of TILE*2 bytes; one store instruction covers 64 / (TILE/8) rows (TILE/8 lanes of
+  // 16 bytes per row).  An edge tile stores only rows < M and 16-byte chunks of columns < N
+  // (N % 8 == 0).
+  constexpr int kLanesPerRow = TILE / 8;
+  constexpr int kRowsPerStore = 64 / kLanesPerRow;
+  const int chunk = lane % kLanesPerRow;
+  const bool col_ok = n0 + chunk * 8 < N;
 #pragma unroll 4
-  for (int i = 0; i < kTile / 8; ++i) {
-    const int row = (i * 4 + wave) * 2 + (lane >> 5);
-    const u32x4 v = *(const lds_u32x4_t*)(ct + row * kCPitch + (lane & 31) * 16);
-    if (!EDGE || (col_ok && m0 + row < M)) *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + (lane & 31) * 8) = v;
+  for (int i = 0; i < TILE / (4 * kRowsPerStore); ++i) {
+    const int row = (i * 4 + wave) * kRowsPerStore + lane / kLanesPerRow;
+    const u32x4 v = *(const lds_u32x4_t*)(ct + row * kCPitch + chunk * 16);
+    if (!EDGE || (col_ok && m0 + row < M)) *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + chunk * 8) = v;
   }
 }
 
-template <int DK, int STAGES, bool AKM = false, bool BKM = true>
+template <int DK, int STAGES, bool AKM, bool BKM, int TILE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const float* __restrict__ bias,
                            uint16_t* __restrict__ C, int64_t M, int64_t N, int64_t K, int relu, int tiles_m,
                            int tiles_n) {
-  constexpr int kLdsBytes = fast_lds_bytes<DK, STAGES>();
-  static_assert(kLdsBytes + kTile * 4 <= 160 * 1024, "LDS");
+  constexpr int kLdsBytes = fast_lds_bytes<DK, STAGES, TILE>();
+  static_assert(kLdsBytes + TILE * 4 <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) char lds_raw[kLdsBytes];
-  __shared__ float bias_lds[kTile];
+  __shared__ float bias_lds[TILE];
 
   int bid = blockIdx.x;
   const int T = gridDim.x;
@@ -513,19 +539,24 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
   const int grp = bid / per_group, first_m = grp * kGroupRows;
   const int gsz = (tiles_m - first_m) < kGroupRows ? (tiles_m - first_m) : kGroupRows;
   const int tm = first_m + (bid % per_group) % gsz, tn = (bid % per_group) / gsz;
-  const int64_t m0 = static_cast<int64_t>(tm) * kTile, n0 = static_cast<int64_t>(tn) * kTile;
+  const int64_t m0 = static_cast<int64_t>(tm) * TILE, n0 = static_cast<int64_t>(tn) * TILE;
 
   // Uniform per workgroup: edge tiles (and every tile when K is not a whole number of K steps)
   // run the range-checked instance of the tile code.
-  if (m0 + kTile <= M && n0 + kTile <= N && K % DK == 0)
-    gemm_fast_tile<DK, STAGES, AKM, BKM, false>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
+  if (m0 + TILE <= M && n0 + TILE <= N && K % DK == 0)
+    gemm_fast_tile<DK, STAGES, AKM, BKM, false, TILE>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
   else
-    gemm_fast_tile<DK, STAGES, AKM, BKM, true>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
+    gemm_fast_tile<DK, STAGES, AKM, BKM, true, TILE>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
 }
 
 // K step and ring depth of the fast path.
 constexpr int kFastDK = 32;
 constexpr int kFastStages = 4;
+// At most this many 256x256 tiles (half of the 256 CUs busy) the launch uses 128x128 tiles:
+// measured 0.74-0.99 PF/s on such grids against 0.4-0.8 with 256x256 tiles; from 144 tiles up
+// the 256x256 kernel is faster (fewer busy CUs also run at a higher clock on this power-limited
+// chip).
+constexpr int64_t kSmallGridTiles = 128;
 
 // Any M, N and K (edge tiles are copied through the descriptor's range check and stored under
 // masks) as long as every row of A, B and C starts 16 bytes aligned: N % 8 == 0, K % 8 == 0,
@@ -542,20 +573,38 @@ bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, const voi
          sizes && ragged_k_ok;
 }
 
-// transpose_a: A is given as [K, M]; transpose_b: B is given as [N, K].
-hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
-                            int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s) {
-  const int64_t tm = (M + kTile - 1) / kTile, tn = (N + kTile - 1) / kTile;
+int gemm_fast_tile_extent(int64_t M, int64_t N) {
+  const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
+  return tiles256 <= kSmallGridTiles ? 128 : 256;
+}
+
+template <int TILE>
+static void launch_tiles(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
+                         int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s) {
+  const int64_t tm = (M + TILE - 1) / TILE, tn = (N + TILE - 1) / TILE;
   const dim3 grid(static_cast<unsigned>(tm * tn)), block(256);
   const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);
   if (!transpose_a && !transpose_b)
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, false, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, false, true, TILE><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu,
+                                                                                         itm, itn);
   else if (!transpose_a)
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, false, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, false, false, TILE><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu,
+                                                                                          itm, itn);
   else if (!transpose_b)
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, true, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, true, true, TILE><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu,
+                                                                                        itm, itn);
   else
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, true, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    gemm_bf16_fast_kernel<kFastDK, kFastStages, true, false, TILE><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu,
+                                                                                         itm, itn);
+}
+
+// transpose_a: A is given as [K, M]; transpose_b: B is given as [N, K].
+hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
+                            int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s) {
+  if (gemm_fast_tile_extent(M, N) == 128)
+    launch_tiles<128>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
+  else
+    launch_tiles<256>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
   return hipGetLastError();
 }
 

@@ -154,8 +154,14 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     ragged_k_ok = K % 32 == 0 or (M * K * 2 < (1 << 31) and K * N * 2 < (1 << 31))
     full = (M > 0 and N > 0 and K > 0 and N % 8 == 0 and K % 8 == 0 and (not ta or M % 8 == 0)
             and K * 512 < lim and N * 128 < lim and M * 128 < lim and ragged_k_ok)
-    # fast path LDS: max(4-stage ring 131072, bf16 C tile 256 x 528) + 256 f32 bias values
-    launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 136192 if full else 147456)
+    # fast path: 256x256 tiles, or 128x128 tiles when at most 128 tiles of 256x256 (half the
+    # CUs) would be busy (gemm_fast_tile_extent); LDS max(4-stage ring, bf16 C tile) + bias:
+    # 256: max(131072, 256 x 528) + 1024, 128: max(65536, 128 x 272) + 512
+    if full:
+        t = 128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256
+        launch = HipLaunch((_cdiv(M, t) * _cdiv(N, t), 1, 1), (256, 1, 1), 136192 if t == 256 else 66048)
+    else:
+        launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 147456)
     kid = "ihip_gemm_bf16_bias_relu_t" if (ta or tb) else "ihip_gemm_bf16_bias_relu"
     return HipLoweredKernel(c.fn.name, kid, c.io(names), launch, [oname], dict(c.b), tuple(args))
 

@@ -170,16 +170,21 @@ def test_gemm_forms_and_errors():
     assert lower_intent_to_hip_kernel(ir, shape_bindings=b).call_args[-1] == ("i32", 1)
 
 
-@pytest.mark.parametrize("M,N,K,tiled", [(256, 256, 64, True), (300, 264, 1000, True), (8, 8, 8, True),
-                                         (256, 250, 64, False), (256, 256, 60, False), (65536, 16384, 40960, True),
-                                         (65536, 16384, 40968, False)])
-def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tiled):
-    """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N (its LDS:
-    max(4-stage ring, staged C tile) + 256 bias floats); otherwise the guarded kernel.  A ragged
-    K needs operands below 2 GiB."""
+@pytest.mark.parametrize("M,N,K,tile", [(256, 256, 64, 128), (300, 264, 1000, 128), (8, 8, 8, 128),
+                                        (4096, 4096, 64, 256), (4096, 2048, 64, 128), (4096, 2304, 64, 256),
+                                        (4100, 4104, 72, 256),
+                                        (256, 250, 64, 0), (256, 256, 60, 0), (65536, 16384, 40960, 256),
+                                        (65536, 16384, 40968, 0)])
+def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tile):
+    """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N: 256x256
+    tiles (LDS max(4-stage ring, staged C tile) + 256 bias floats), or 128x128 tiles when at
+    most 128 tiles of 256x256 (half the CUs) would be busy; otherwise (tile 0 here) the guarded
+    kernel.
+    A ragged K needs operands below 2 GiB."""
     k = lower_intent_to_hip_kernel(matmul_bias_relu2d_ir(), shape_bindings={"M": M, "N": N, "K": K})
-    assert k.launch.grid == (-(-M // 256) * -(-N // 256), 1, 1)
-    assert k.launch.lds_bytes == (136192 if tiled else 147456)
+    t = tile or 256
+    assert k.launch.grid == (-(-M // t) * -(-N // t), 1, 1)
+    assert k.launch.lds_bytes == {256: 136192, 128: 66048, 0: 147456}[tile]
 
 
 def test_unsupported_ops_raise():
