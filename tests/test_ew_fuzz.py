@@ -14,7 +14,7 @@ comparison of computed values against each other.
 * GPU: the native and interpreted kernels, at sizes with tails, are judged
   against the oracle within f32 tolerances (bf16 outputs: one RNE rounding).
 
-Variants: f32 or bf16 x, y and outputs (16-bit operands run 8 elements per lane),
+Variants: f32, bf16 or f16 x, y and outputs (16-bit operands run 8 elements per lane),
 with or without an input read through transpose (the LDS-tiled form).
 """
 
@@ -119,7 +119,8 @@ def random_chain(seed: int, dt: str = "f32", transpose: bool = False) -> dict:
 def inputs_for(seed: int, M: int, N: int, dt: str = "f32", transpose: bool = False) -> dict:
     rng = np.random.default_rng(seed + 1)
     full = lambda: rng.standard_normal((M, N)).astype(np.float32)  # noqa: E731
-    x, y = (full(), full()) if dt == "f32" else (f32_to_bf16_bits(full()), f32_to_bf16_bits(full()))
+    cast = {"f32": lambda a: a, "bf16": f32_to_bf16_bits, "f16": lambda a: a.astype(np.float16)}[dt]
+    x, y = cast(full()), cast(full())
     d = {"x": x, "y": y, "b": rng.standard_normal(N).astype(np.float32),
          "c": rng.standard_normal((M, 1)).astype(np.float32)}
     if transpose:
@@ -137,8 +138,9 @@ def lower_or_skip(ir: dict, b: dict):
     return k
 
 
-VARIANTS = [("f32", False), ("f32", True), ("bf16", False), ("bf16", True)]
-TOLS = {"f32": (1e-6, 2e-6), "bf16": (1e-3, 1e-2)}  # (atol, rtol); bf16: one RNE rounding of the output
+VARIANTS = [("f32", False), ("f32", True), ("bf16", False), ("bf16", True), ("f16", False), ("f16", True)]
+# (atol, rtol); 16-bit outputs: one RNE rounding (bf16 2^-9, f16 2^-11 relative)
+TOLS = {"f32": (1e-6, 2e-6), "bf16": (1e-3, 1e-2), "f16": (1e-3, 1e-3)}
 
 
 def _check(got, ref, ir, dt, what):
@@ -168,7 +170,7 @@ def test_random_chain_on_gpu(hip, seed, dt, transpose, mode):
     from intent_ir_amd import run_lowered
 
     ir = random_chain(seed, dt, transpose)
-    M, N = 67, 1032 if dt == "bf16" else 1029  # tails in both axes (bf16: 8-wide vectors)
+    M, N = 67, 1029 if dt == "f32" else 1032  # tails in both axes (16-bit: 8-wide vectors)
     b = {"M": M, "N": N}
     k = lower_or_skip(ir, b)
     storage = inputs_for(seed, M, N, dt, transpose)
