@@ -65,11 +65,12 @@ struct EwJitArgs {
 // twice); non-finite inputs and results take the IEEE value.
 __device__ __forceinline__ float ew_exp(float x) {
   // 2^(x*log2 e): the product carried as head t + tail, v_exp_f32 on the head, first-order
-  // correction e*(1 + tail*ln 2) for the tail.
+  // correction e*(1 + tail*ln 2) for the tail.  No correction where the head overflowed
+  // (e = +inf: a negative tail would make inf - inf = NaN) or the input is not finite.
   const float t = x * 1.44269502f;
   const float tail = __builtin_fmaf(x, 1.92596303e-08f, __builtin_fmaf(x, 1.44269502f, -t));
   const float e = __builtin_amdgcn_exp2f(t);
-  return __builtin_isfinite(tail) ? __builtin_fmaf(e, tail * 0.693147182f, e) : e;
+  return __builtin_isfinite(tail) && __builtin_isfinite(e) ? __builtin_fmaf(e, tail * 0.693147182f, e) : e;
 }
 // x / y as v_rcp_f32 and one Newton step on the quotient.  `bad` is set where that form
 // does not hold (zero, infinite or NaN reciprocal or quotient); those elements take ew_div,

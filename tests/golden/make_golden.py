@@ -3,7 +3,7 @@
 
 Run in the build container only (the reference tree is not on the GPU box):
 
-    python tests/golden/make_golden.py /root/reference
+    python tests/golden/make_golden.py /root/reference [case ...]
 
 For each case it stores the IntentIR document (after this backend's macro
 expansion, which only emits ops the reference interpreter knows), the inputs
@@ -11,7 +11,8 @@ and the reference outputs in ``tests/golden/<case>.npz``, plus the numpy
 version that produced them.  The cases cover what no closed form pins:
 end-to-end ``execute_intent`` on the five workload IRs at tiny bindings, and the
 interpreter's helpers for 1-D/2-D alignment by symbol name, reduce-dims
-fallback, string-valued consts, 1-input scalar-attr ops and reduce scale.
+fallback, string-valued consts, 1-input scalar-attr ops and reduce scale, and
+every element-wise table entry, where, cast and iota on special values.
 """
 
 from __future__ import annotations
@@ -88,14 +89,54 @@ def _cases():
                 {"op": "reduce_sum", "inputs": ["y6"], "output": "s", "attrs": {"dims": [1], "scale": "1/N"}}],
         "outputs": ["cn", "ce", "y6", "s"]}, {"X": np.linspace(-2, 2, 15, dtype=np.float32).reshape(3, 5)}, \
         {"M": 3, "N": 5}
+    # Every element-wise table entry (interpreter.py:14-47), where, cast, iota, transpose and
+    # reshape (:253-302) on special values: NaN, +-inf, +-0, denormals, ties, overflow.
+    X = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.5, -1.5, 2.0, -2.5, 0.5, 3.75, -7.25, 100.0, -100.0, 1e-3,
+                  -1e-3, 2.0, 3.0, -3.0, 0.0, 5.5, -0.5, 88.0, -88.0, 1e-40, -1e-40, 7.0, 0.25, -0.25, 65504.0, 1e30,
+                  -1e30], np.float32).reshape(4, 8)
+    Y = np.array([1.0, np.inf, 2.0, -0.0, 0.0, 1.5, 1.5, np.nan, -2.5, 0.25, -3.75, 7.25, 100.0, 50.0, -1e-3, 1e-3,
+                  2.0, -3.0, -3.0, 1.0, -5.5, 0.5, 1.0, -1.0, 1e-40, 0.0, -7.0, 4.0, 0.25, 2.0, -1e30, 1e30],
+                 np.float32).reshape(4, 8)
+    Z = np.array([-2.5, -1.5, -0.5, 0.5, 1.5, 2.5, -0.0, 0.0, 1.0 / 3, -2.0 / 3, 2049.0, 2051.0, 65519.0, -65521.0,
+                  6e-8, -6e-8, 1e-5, 7.9999, -7.9999, 123.456, 1e4, -1e4, 0.099975586, 1.0009766, 2.999, -2.999,
+                  0.25, -0.75, 1023.5, -1023.5, 3e-5, 5.96e-8], np.float32).reshape(4, 8)
+    full = ["M", "N"]
+    tens = {"X": t("f32", full), "Y": t("f32", full), "Z": t("f32", full), "tr": t("f32", ["N", "M"]),
+            "rs": t("f32", ["N", "M"]), "io": t("i32", full), "k_i32": t("i32", full), "k_f16": t("f16", full),
+            "k_bool": t("bool", full), "w": t("f32", full)}
+    ops = []
+    for o in ("add", "sub", "mul", "div", "max", "min"):
+        tens[f"b_{o}"] = t("f32", full)
+        ops.append({"op": o, "inputs": ["X", "Y"], "output": f"b_{o}"})
+    for o in ("relu", "exp", "rsqrt", "abs", "floor", "identity"):
+        tens[f"u_{o}"] = t("f32", full)
+        ops.append({"op": o, "inputs": ["X"], "output": f"u_{o}"})
+    for o in ("ne", "lt", "le", "gt", "ge"):
+        tens[f"c_{o}"] = t("bool", full)
+        ops.append({"op": o, "inputs": ["X", "Y"], "output": f"c_{o}"})
+    for name, o, ins in (("l_and", "and", ["c_lt", "c_ne"]), ("l_or", "or", ["c_le", "c_ge"]), ("l_not", "not", ["c_ne"])):
+        tens[name] = t("bool", full)
+        ops.append({"op": o, "inputs": ins, "output": name})
+    ops += [{"op": "where", "inputs": ["c_lt", "X", "Y"], "output": "w"},
+            {"op": "cast", "inputs": ["Z"], "output": "k_i32", "attrs": {"to": "i32"}},
+            {"op": "cast", "inputs": ["Z"], "output": "k_f16", "attrs": {"to": "f16"}},
+            {"op": "cast", "inputs": ["X"], "output": "k_bool", "attrs": {"to": "bool"}},
+            {"op": "iota", "inputs": [], "output": "io", "attrs": {"shape": full, "axis": 1, "dtype": "i32"}},
+            {"op": "transpose", "inputs": ["X"], "output": "tr", "attrs": {"perm": [1, 0]}},
+            {"op": "reshape", "inputs": ["Z"], "output": "rs", "attrs": {"shape": ["N", "M"]}}]
+    outs = [o["output"] for o in ops]
+    yield "elementwise_tables", {"name": "ew_tables", "tensors": tens, "ops": ops, "outputs": outs}, \
+        {"X": X, "Y": Y, "Z": Z}, {"M": 4, "N": 8}
 
 
-def main(ref_root: str) -> None:
+def main(ref_root: str, only: set | None = None) -> None:
     sys.path.insert(0, ref_root)
     from intent_ir.ir import IntentFunction  # reference
     from verify.interpreter import execute_intent  # reference
 
     for name, ir, inputs, bindings in _cases():
+        if only and name not in only:
+            continue
         fn = IntentFunction.from_json_dict(ir)
         out = execute_intent(fn, {k: np.asarray(v) for k, v in inputs.items()}, dict(bindings))
         blob = {f"in__{k}": np.asarray(v) for k, v in inputs.items()}
@@ -107,4 +148,5 @@ def main(ref_root: str) -> None:
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    # usage: make_golden.py [reference_root] [case ...]   (no case names: every case)
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference", set(sys.argv[2:]) or None)

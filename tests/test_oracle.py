@@ -86,7 +86,9 @@ def _golden_catches() -> bool:
             got = execute_intent(meta["ir"], ins, meta["bindings"], numpy_semantics="native")
             for k, ref in outs.items():
                 g = np.asarray(got[k], dtype=np.float64)
-                if g.shape != ref.shape or not np.allclose(g, ref.astype(np.float64), rtol=1e-5, atol=1e-6):
+                if g.shape != ref.shape or not np.allclose(g, ref.astype(np.float64), rtol=1e-5, atol=1e-6,
+                                                           equal_nan=True) or not np.array_equal(np.signbit(g),
+                                                                                                 np.signbit(ref)):
                     return True
         except Exception:
             return True
@@ -102,6 +104,42 @@ def test_unplanted_oracle_passes_all_goldens():
 def test_planted_arithmetic_mistake_is_caught(monkeypatch, op, wrong):
     monkeypatch.setitem(oi.NUM_BIN_OPS, op, wrong)
     assert _golden_catches(), f"a wrong '{op}' went unnoticed by every golden vector"
+
+
+@pytest.mark.parametrize("table,op,wrong", [
+    ("NUM_BIN_OPS", "max", np.fmax), ("NUM_BIN_OPS", "min", np.fmin), ("NUM_BIN_OPS", "div", np.floor_divide),
+    ("NUM_UNARY_OPS", "floor", np.ceil), ("NUM_UNARY_OPS", "floor", np.trunc),
+    ("NUM_UNARY_OPS", "relu", lambda x: np.fmax(x, 0)), ("NUM_UNARY_OPS", "relu", lambda x: np.maximum(0, x)),
+    ("NUM_UNARY_OPS", "rsqrt", lambda x: np.sqrt(1.0 / x)), ("NUM_UNARY_OPS", "exp", np.exp2),
+    ("CMP_BIN_OPS", "lt", np.less_equal), ("CMP_BIN_OPS", "ge", np.greater), ("CMP_BIN_OPS", "ne", np.equal),
+    ("BOOL_BIN_OPS", "and", np.logical_xor), ("BOOL_BIN_OPS", "or", np.logical_xor)])
+def test_planted_elementwise_table_mistake_is_caught(monkeypatch, table, op, wrong):
+    """The elementwise_tables fixture (reference interpreter on NaN, +-inf, +-0, denormals)
+    catches plausible table mistakes: NaN-dropping fmax/fmin, ceil or trunc for floor, a
+    relu that returns +0 for -0 or drops NaN, reordered rsqrt, comparisons off by equality."""
+    import warnings
+
+    monkeypatch.setitem(getattr(oi, table), op, wrong)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        assert _golden_catches(), f"a wrong '{op}' went unnoticed by every golden vector"
+
+
+def test_planted_wrong_cast_is_caught(monkeypatch):
+    """cast to i32 truncates toward zero (astype); rounding instead must be caught."""
+    import warnings
+
+    orig = oi._Exec.op
+
+    def op(self, o, env):
+        if o.op == "cast" and o.attrs.get("to") == "i32":
+            return np.rint(np.asarray(env[o.inputs[0]])).astype(np.int32)
+        return orig(self, o, env)
+
+    monkeypatch.setattr(oi._Exec, "op", op)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        assert _golden_catches()
 
 
 def test_planted_wrong_reduce_axis_is_caught(monkeypatch):
