@@ -94,7 +94,8 @@ int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* 
 /* The same with matmul's transpose flags (verify/interpreter.py:507-520): when transpose_a,
  * A is given as [K, M] and the product uses its transpose; when transpose_b, B is given as
  * [N, K].  Every layout runs the same MFMA schedule and accumulates in the same order, so a
- * transposed operand gives bit-identical C. */
+ * transposed operand gives bit-identical C.  With B given as [N, K] the tiled kernel takes
+ * any N (K % 8 == 0): C rows that are not 16-byte aligned are written with 2-byte stores. */
 int ihip_gemm_bf16_bias_relu_t(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                                int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, void* stream);
 

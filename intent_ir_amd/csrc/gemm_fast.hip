@@ -1,8 +1,9 @@
 // Tiled bf16 GEMM for gfx950: C = act(A @ B + bias), A [M,K], B [K,N] row-major bf16,
 // f32 accumulation on v_mfma_f32_32x32x16_bf16, C bf16 (RNE).  Any M, N and K as long as
-// every row of A, B and C starts 16-byte aligned (N % 8 == 0, K % 8 == 0, and M % 8 == 0
-// when A is given as [K,M]) and the bases are 16-byte aligned; other shapes take the
-// guarded kernel in gemm.hip.  Edge tiles (past M or N, or all tiles when K is not a
+// every row of A and B starts 16-byte aligned (K % 8 == 0, M % 8 == 0 when A is given as
+// [K,M], N % 8 == 0 when B is given as [K,N]) and the bases are 16-byte aligned; C rows that
+// are not (N % 8 != 0 with B given as [N,K]) are written with 2-byte stores.  Other shapes
+// take the guarded kernel in gemm.hip.  Edge tiles (past M or N, or all tiles when K is not a
 // multiple of DK) copy through range-checked buffer descriptors: reads past the end of a
 // tensor and k-chunks past K load zeros, and what an edge tile reads outside [M) x [N) only
 // reaches C rows >= M or columns >= N, which are never stored.
@@ -355,8 +356,10 @@ constexpr int fast_lds_bytes() {
   return ring > TILE * c_pitch<TILE>() ? ring : TILE * c_pitch<TILE>();
 }
 
-// One TILE x TILE C tile at (m0, n0); lds_raw / bias_lds are the kernel's LDS.
-template <int DK, int STAGES, bool AKM, bool BKM, bool EDGE, int TILE>
+// One TILE x TILE C tile at (m0, n0); lds_raw / bias_lds are the kernel's LDS.  CU: C rows
+// are not 16-byte aligned (N % 8 != 0, only with B given as [N, K]); C is then written with
+// 2-byte stores.
+template <int DK, int STAGES, bool AKM, bool BKM, bool EDGE, int TILE, bool CU>
 __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                const float* __restrict__ bias, uint16_t* __restrict__ C, int64_t M,
                                                int64_t N, int64_t K, int relu, int64_t m0, int64_t n0, char* lds_raw,
@@ -508,21 +511,31 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
   }
   __syncthreads();
   // TILE rows of TILE*2 bytes; one store instruction covers 64 / (TILE/8) rows (TILE/8 lanes of
-  // 16 bytes per row).  An edge tile stores only rows < M and 16-byte chunks of columns < N
-  // (N % 8 == 0).
+  // 16 bytes per row).  An edge tile stores only rows < M and columns < N (whole 16-byte
+  // chunks when N % 8 == 0, single elements otherwise).
   constexpr int kLanesPerRow = TILE / 8;
   constexpr int kRowsPerStore = 64 / kLanesPerRow;
   const int chunk = lane % kLanesPerRow;
   const bool col_ok = n0 + chunk * 8 < N;
+  const int64_t col_left = N - (n0 + chunk * 8);  // columns of this chunk inside C (CU)
 #pragma unroll 4
   for (int i = 0; i < TILE / (4 * kRowsPerStore); ++i) {
     const int row = (i * 4 + wave) * kRowsPerStore + lane / kLanesPerRow;
     const u32x4 v = *(const lds_u32x4_t*)(ct + row * kCPitch + chunk * 16);
-    if (!EDGE || (col_ok && m0 + row < M)) *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + chunk * 8) = v;
+    if constexpr (CU) {
+      if (!EDGE || (col_ok && m0 + row < M)) {
+        uint16_t* dst = C + (m0 + row) * N + n0 + chunk * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (!EDGE || e < col_left) dst[e] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
+      }
+    } else {
+      if (!EDGE || (col_ok && m0 + row < M)) *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + chunk * 8) = v;
+    }
   }
 }
 
-template <int DK, int STAGES, bool AKM, bool BKM, int TILE>
+template <int DK, int STAGES, bool AKM, bool BKM, int TILE, bool CU>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const float* __restrict__ bias,
                            uint16_t* __restrict__ C, int64_t M, int64_t N, int64_t K, int relu, int tiles_m,
@@ -544,9 +557,9 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
   // Uniform per workgroup: edge tiles (and every tile when K is not a whole number of K steps)
   // run the range-checked instance of the tile code.
   if (m0 + TILE <= M && n0 + TILE <= N && K % DK == 0)
-    gemm_fast_tile<DK, STAGES, AKM, BKM, false, TILE>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
+    gemm_fast_tile<DK, STAGES, AKM, BKM, false, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
   else
-    gemm_fast_tile<DK, STAGES, AKM, BKM, true, TILE>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
+    gemm_fast_tile<DK, STAGES, AKM, BKM, true, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
 }
 
 // K step and ring depth of the fast path.
@@ -559,18 +572,21 @@ constexpr int kFastStages = 4;
 constexpr int64_t kSmallGridTiles = 128;
 
 // Any M, N and K (edge tiles are copied through the descriptor's range check and stored under
-// masks) as long as every row of A, B and C starts 16 bytes aligned: N % 8 == 0, K % 8 == 0,
-// and M % 8 == 0 when A is given as [K, M].  When K is not a whole number of K steps, A and B
+// masks) as long as every row of A and B starts 16 bytes aligned: K % 8 == 0, M % 8 == 0 when
+// A is given as [K, M], and N % 8 == 0 when B is given as [K, N].  With B given as [N, K]
+// (the layout of a linear layer's weight) N may be anything: C rows that are not 16-byte
+// aligned are written with 2-byte stores.  When K is not a whole number of K steps, A and B
 // must be below 2 GiB each (the ragged k-chunks are pointed past every record).
-bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, const void* A, const void* B, const void* C) {
+bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, bool transpose_b, const void* A, const void* B,
+                    const void* C) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
   // per-lane copy offsets from a slice base are 32-bit: up to 256 rows of K elements, or
   // 64 k-rows of M or N elements
   const int64_t lim = int64_t(1) << 32;
   const bool sizes = K * 512 < lim && N * 128 < lim && M * 128 < lim;
   const bool ragged_k_ok = K % kFastDK == 0 || (M * K * 2 < (int64_t(1) << 31) && K * N * 2 < (int64_t(1) << 31));
-  return M > 0 && N > 0 && K > 0 && N % 8 == 0 && K % 8 == 0 && (!transpose_a || M % 8 == 0) && (al & 15) == 0 &&
-         sizes && ragged_k_ok;
+  return M > 0 && N > 0 && K > 0 && (N % 8 == 0 || transpose_b) && K % 8 == 0 && (!transpose_a || M % 8 == 0) &&
+         (al & 15) == 0 && sizes && ragged_k_ok;
 }
 
 int gemm_fast_tile_extent(int64_t M, int64_t N) {
@@ -578,33 +594,42 @@ int gemm_fast_tile_extent(int64_t M, int64_t N) {
   return tiles256 <= kSmallGridTiles ? 128 : 256;
 }
 
-template <int TILE>
+template <int TILE, bool CU>
 static void launch_tiles(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
                          int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s) {
   const int64_t tm = (M + TILE - 1) / TILE, tn = (N + TILE - 1) / TILE;
   const dim3 grid(static_cast<unsigned>(tm * tn)), block(256);
   const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);
-  if (!transpose_a && !transpose_b)
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, false, true, TILE><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu,
-                                                                                         itm, itn);
-  else if (!transpose_a)
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, false, false, TILE><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu,
-                                                                                          itm, itn);
-  else if (!transpose_b)
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, true, true, TILE><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu,
-                                                                                        itm, itn);
-  else
-    gemm_bf16_fast_kernel<kFastDK, kFastStages, true, false, TILE><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu,
-                                                                                         itm, itn);
+  constexpr int DK = kFastDK, ST = kFastStages;
+  if constexpr (CU) {  // only B given as [N, K] reaches here
+    if (!transpose_a)
+      gemm_bf16_fast_kernel<DK, ST, false, false, TILE, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    else
+      gemm_bf16_fast_kernel<DK, ST, true, false, TILE, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+  } else {
+    if (!transpose_a && !transpose_b)
+      gemm_bf16_fast_kernel<DK, ST, false, true, TILE, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    else if (!transpose_a)
+      gemm_bf16_fast_kernel<DK, ST, false, false, TILE, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    else if (!transpose_b)
+      gemm_bf16_fast_kernel<DK, ST, true, true, TILE, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+    else
+      gemm_bf16_fast_kernel<DK, ST, true, false, TILE, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, relu, itm, itn);
+  }
 }
 
 // transpose_a: A is given as [K, M]; transpose_b: B is given as [N, K].
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
                             int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s) {
-  if (gemm_fast_tile_extent(M, N) == 128)
-    launch_tiles<128>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
+  const bool small = gemm_fast_tile_extent(M, N) == 128, cu = N % 8 != 0;
+  if (small && cu)
+    launch_tiles<128, true>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
+  else if (small)
+    launch_tiles<128, false>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
+  else if (cu)
+    launch_tiles<256, true>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
   else
-    launch_tiles<256>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
+    launch_tiles<256, false>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
   return hipGetLastError();
 }
 

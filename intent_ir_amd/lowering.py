@@ -152,7 +152,7 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     # decides for 16-byte aligned tensors
     lim = 1 << 32
     ragged_k_ok = K % 32 == 0 or (M * K * 2 < (1 << 31) and K * N * 2 < (1 << 31))
-    full = (M > 0 and N > 0 and K > 0 and N % 8 == 0 and K % 8 == 0 and (not ta or M % 8 == 0)
+    full = (M > 0 and N > 0 and K > 0 and (N % 8 == 0 or tb) and K % 8 == 0 and (not ta or M % 8 == 0)
             and K * 512 < lim and N * 128 < lim and M * 128 < lim and ragged_k_ok)
     # fast path: 256x256 tiles, or 128x128 tiles when at most 128 tiles of 256x256 (half the
     # CUs) would be busy (gemm_fast_tile_extent); LDS max(4-stage ring, bf16 C tile) + bias:

@@ -187,6 +187,20 @@ def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tile):
     assert k.launch.lds_bytes == {256: 136192, 128: 66048, 0: 147456}[tile]
 
 
+@pytest.mark.parametrize("N,tb,lds", [(50257, True, 136192), (263, True, 66048), (263, False, 147456),
+                                      (50257, False, 147456)])
+def test_gemm_odd_n_takes_the_tiled_kernel_with_b_as_nk(N, tb, lds):
+    """With B given as [N, K] (transpose_b) the rows of A and B stay 16-byte aligned at any N,
+    so the tiled kernel runs (C written with 2-byte stores); B as [K, N] with N % 8 != 0 takes
+    the guarded kernel."""
+    ir = matmul_bias_relu2d_ir()
+    if tb:
+        ir["tensors"]["B"]["shape"] = ["N", "K"]
+        ir["ops"][0]["attrs"] = {"transpose_b": True}
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 300, "N": N, "K": 64})
+    assert k.launch.lds_bytes == lds
+
+
 def test_unsupported_ops_raise():
     ir = {"name": "g", "tensors": {"x": {"dtype": "f32", "shape": ["N"]}, "i": {"dtype": "i32", "shape": ["N"]},
                                    "y": {"dtype": "f32", "shape": ["N"]}},
