@@ -22,8 +22,6 @@ import pytest
 
 from intent_ir_amd import HipLoweringError, lower_intent_to_hip_kernel
 
-pytestmark = pytest.mark.gpu
-
 FIXTURE = Path(__file__).resolve().parent / "golden" / "elementwise_tables.npz"
 ROUNDED = {"b_div": (1e-6, 2e-6), "u_exp": (1e-6, 2e-6), "u_rsqrt": (1e-6, 2e-6)}  # (atol, rtol)
 
@@ -59,6 +57,7 @@ def test_reshape_across_axes_is_rejected():
         lower_intent_to_hip_kernel(sub_ir(META["ir"], "rs"), shape_bindings=META["bindings"])
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("mode", [0, 1], ids=["native", "interp"])
 @pytest.mark.parametrize("out", NAMES)
 def test_program_matches_reference_interpreter(hip, out, mode):
