@@ -394,6 +394,70 @@ __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_regs(const float* __
     if (i * kW * kWave < left) __builtin_nontemporal_store(e[i] * inv, yr + i * kW * kWave);
 }
 
+// Rows whose starts are not all 16-byte aligned (N % 4 != 0), 1024 < N <= 4096*kW, with x and
+// y sharing their alignment modulo 16 bytes: each row is split into a head of h < 4 elements
+// (up to the first 16-byte boundary), a 16-byte aligned body of nb vectors held in registers
+// exactly as in the multi-wave vector form, and a tail of t < 4 elements.  Thread j < h holds
+// head element j, thread j < t tail element j.  Every access is bounded by the row: body
+// vector k < nb covers elements h + 4k .. h + 4k + 3 < h + 4nb <= N.
+template <int kVpl, int kW>
+__global__ __launch_bounds__(64 * kW) void softmax_rows_f32_skew(const float* __restrict__ x, float* __restrict__ y,
+                                                                 int64_t M, int64_t N) {
+  __shared__ float part_m[kW], part_s[kW];
+  const int lane = threadIdx.x & 63, v = threadIdx.x >> 6, tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  if (row >= M) return;  // uniform per workgroup
+  const float* xr = x + row * N;
+  float* yr = y + row * N;
+  const int64_t to_edge = (4 - ((reinterpret_cast<uintptr_t>(xr) >> 2) & 3)) & 3;
+  const int64_t head = to_edge < N ? to_edge : N;
+  const int64_t nb = (N - head) >> 2;
+  const int64_t tail = N - head - 4 * nb;
+  const int64_t first = v * kWave + lane;  // this lane's first body vector
+  const f32x4* xb = reinterpret_cast<const f32x4*>(xr + head) + first;
+  f32x4* yb = reinterpret_cast<f32x4*>(yr + head) + first;
+  const float ninf = -__builtin_inff();
+  f32x4 xv[kVpl];
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+    xv[i] = first + i * kWave * kW < nb ? __builtin_nontemporal_load(xb + i * kWave * kW)
+                                        : f32x4{ninf, ninf, ninf, ninf};
+  float hv = tid < head ? xr[tid] : ninf;
+  float tv = tid < tail ? xr[head + 4 * nb + tid] : ninf;
+  float mx = max_nan(hv, tv);
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) mx = max_nan(max_nan(mx, xv[i].x), max_nan(max_nan(xv[i].y, xv[i].z), xv[i].w));
+  mx = wave_max_nan(mx);
+  if (lane == 0) part_m[v] = mx;
+  __syncthreads();
+  mx = part_m[0];
+#pragma unroll
+  for (int k = 1; k < kW; ++k) mx = max_nan(mx, part_m[k]);
+  hv = exp_nonpos(hv - mx);
+  tv = exp_nonpos(tv - mx);
+  float sum = (tid < head ? hv : 0.f) + (tid < tail ? tv : 0.f);
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    xv[i].x = exp_nonpos(xv[i].x - mx);
+    xv[i].y = exp_nonpos(xv[i].y - mx);
+    xv[i].z = exp_nonpos(xv[i].z - mx);
+    xv[i].w = exp_nonpos(xv[i].w - mx);
+    if (first + i * kWave * kW < nb) sum += (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) part_s[v] = sum;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < kW; ++k) tot += part_s[k];
+  const float inv = 1.0f / tot;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+    if (first + i * kWave * kW < nb) __builtin_nontemporal_store(xv[i] * inv, yb + i * kWave * kW);
+  if (tid < head) yr[tid] = hv * inv;
+  if (tid < tail) yr[head + 4 * nb + tid] = tv * inv;
+}
+
 // Any N: one workgroup per row, three passes (max, sum, write) over the row.
 __global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restrict__ x, float* __restrict__ y, int64_t N) {
   __shared__ float scratch[4];
@@ -422,6 +486,9 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
   if (M == 0 || N == 0) return hipSuccess;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // grid.x limit of the row-per-workgroup fallback
   const bool vec = (N % 4 == 0) && (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0);
+  // rows of a non-vector shape split at the same 16-byte boundaries in x and y
+  const bool skew = !vec && (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 3) == 0) &&
+                    (((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(y)) & 15) == 0);
   const int64_t n4 = N / 4;
   const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
   f32x4* y4 = reinterpret_cast<f32x4*>(y);
@@ -446,6 +513,16 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
     softmax_rows_f32_multi<16, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x4, y4, M, n4i);
   else if (!vec && N <= 64 * 16)
     softmax_rows_f32_regs<16, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N);
+  else if (skew && N <= 4096)
+    softmax_rows_f32_skew<16, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N);
+  else if (skew && N <= 4096 * 2)
+    softmax_rows_f32_skew<16, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x, y, M, N);
+  else if (skew && N <= 4096 * 4)
+    softmax_rows_f32_skew<16, 4><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, M, N);
+  else if (skew && N <= 4096 * 8)
+    softmax_rows_f32_skew<16, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x, y, M, N);
+  else if (skew && N <= 4096 * 16)
+    softmax_rows_f32_skew<16, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, M, N);
   else if (!vec && N <= 64 * 64)
     softmax_rows_f32_regs<64, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N);
   else if (!vec && N <= 64 * 64 * 2)

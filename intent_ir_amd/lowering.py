@@ -232,9 +232,10 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
     elif N % 4 == 0 and N <= 65536:  # kW waves per row, one row per workgroup, partials in LDS
         kw = next(w for w in (2, 4, 8, 16) if N // 4 <= 1024 * w)
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
-    elif N <= 65536:  # N % 4 != 0: the row in registers through 4-byte loads, kW waves per row
+    elif N <= 65536:  # N % 4 != 0: the row in registers, kW waves per row; above 1024 a 4-byte
+        # head and tail around a 16-byte aligned body (partials in LDS even for one wave)
         kw = next(w for w in (1, 2, 4, 8, 16) if N <= 4096 * w)
-        launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw if kw > 1 else 0)
+        launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw if (kw > 1 or N > 1024) else 0)
     else:
         launch = HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
     return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b),

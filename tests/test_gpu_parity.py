@@ -366,6 +366,36 @@ def test_gelu_full_config(hip):
     np.testing.assert_allclose(out, yref, rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("N", [1029, 4099, 8195, 50257, 65533])
+@pytest.mark.parametrize("ox,oy", [(0, 0), (1, 1), (2, 2), (3, 3), (1, 2), (0, 3)])
+def test_softmax_odd_rows_at_every_alignment(hip, N, ox, oy):
+    """N % 4 != 0 through the C-ABI with x and y placed ox, oy floats past 256-byte aligned
+    allocations: equal offsets take the head / aligned body / tail kernel (every row starts at
+    another alignment), unequal ones the 4-byte-load kernel.  Judged against the oracle."""
+    import ctypes
+
+    import torch
+
+    w = WORKLOADS["softmax"]
+    out = w.ir()["outputs"][0]
+    M = 7
+    b = {"M": M, "N": N}
+    inp = w.gen(b, seed=N + 10 * ox + oy)
+    xt = torch.empty(M * N + ox, dtype=torch.float32, device="cuda")
+    xt[ox:] = torch.from_numpy(inp["input_ptr"].reshape(-1)).cuda()
+    yt = torch.full((M * N + oy + 4,), 7.0, dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    print(f"[case] softmax odd rows N={N} ox={ox} oy={oy}", flush=True)
+    st = hip.ihip_softmax_rows_f32(ctypes.c_void_p(xt.data_ptr() + 4 * ox), ctypes.c_void_p(yt.data_ptr() + 4 * oy),
+                                   M, N, ctypes.c_void_p(s))
+    assert st == 0, hip.ihip_last_error().decode()
+    torch.cuda.synchronize()
+    yh = yt.cpu().numpy()
+    assert (yh[:oy] == 7.0).all() and (yh[oy + M * N:] == 7.0).all(), "write outside y"
+    ref = oracle_outputs(w.ir(), inp, b)
+    check({out: yh[oy:oy + M * N].reshape(M, N)}, ref, [out], TOL["softmax"], f"softmax N={N} {ox},{oy}")
+
+
 # ------------------------------------------------------------------ GEMM
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (3, 5, 7), (17, 33, 31), (32, 48, 16), (256, 256, 64), (255, 257, 65),
                                    (512, 256, 128), (300, 600, 1000)])
