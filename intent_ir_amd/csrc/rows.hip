@@ -149,15 +149,23 @@ __device__ __forceinline__ float red_op(float a, float b) {
 }
 
 template <int kKind, int W, int kUnroll, int kAcc>
-__global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const f32x4* __restrict__ x, float* __restrict__ out,
-                                                              int64_t M, int64_t n4) {
+__global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const float* __restrict__ x, float* __restrict__ out,
+                                                              int64_t M, int64_t N) {
   static_assert(kUnroll % kAcc == 0 && (kAcc & (kAcc - 1)) == 0, "loads fold evenly into a power-of-two of partials");
   const float id = kKind == 0 ? 0.0f : -__builtin_inff();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t row = blockIdx.x;
   if (row >= M) return;
-  const f32x4* xr = x + row * n4;
+  // The row splits into a head of up to 3 elements (to its first 16-byte boundary), n4
+  // aligned vectors and a tail of up to 3 elements; rows that start aligned with N % 4 == 0
+  // have neither head nor tail.
+  const float* rowp = x + row * N;
+  const int64_t to_edge = (4 - ((reinterpret_cast<uintptr_t>(rowp) >> 2) & 3)) & 3;
+  const int64_t head = to_edge < N ? to_edge : N;
+  const int64_t n4 = (N - head) >> 2;
+  const int64_t tail = N - head - 4 * n4;
+  const f32x4* xr = reinterpret_cast<const f32x4*>(rowp + head);
   f32x4 acc[kAcc];
 #pragma unroll
   for (int u = 0; u < kAcc; ++u) acc[u] = f32x4{id, id, id, id};
@@ -187,6 +195,10 @@ __global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const f32x4* __res
       acc[u].w = red_op<kKind>(acc[u].w, acc[u + h].w);
     }
   float r = red_op<kKind>(red_op<kKind>(acc[0].x, acc[0].y), red_op<kKind>(acc[0].z, acc[0].w));
+  if (wave == 0) {  // head and tail elements (at most 3 each) join lanes 0..2 of the first wave
+    if (lane < head) r = red_op<kKind>(r, rowp[lane]);
+    if (lane < tail) r = red_op<kKind>(r, rowp[head + 4 * n4 + lane]);
+  }
   r = kKind == 0 ? wave_sum(r) : wave_max_nan(r);
   if (W > 1) {
     __shared__ float part[W];
@@ -222,18 +234,17 @@ constexpr int kRedUnroll = 16;
 
 template <int kKind>
 static void launch_reduce_rows(const float* x, float* out, int64_t M, int64_t N, hipStream_t s) {
-  const bool vec = N % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-  if (!vec) {
+  // 16-byte loads over each row's aligned body whenever x is 4-byte aligned (any N)
+  if ((reinterpret_cast<uintptr_t>(x) & 3) != 0 || N == 0) {
     reduce_rows_f32<kKind><<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(x, out, M, N);
     return;
   }
-  const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
   const int64_t n4 = N / 4;
   const dim3 grid(static_cast<unsigned>(M));
   if (M >= 2048 || n4 <= 4 * kWave)  // enough rows for the CUs, or short rows: a wave per row
-    reduce_rows_f32_vec<kKind, 1, kRedUnroll, 4><<<grid, dim3(64), 0, s>>>(x4, out, M, n4);
+    reduce_rows_f32_vec<kKind, 1, kRedUnroll, 4><<<grid, dim3(64), 0, s>>>(x, out, M, N);
   else  // few long rows: 16 waves per row
-    reduce_rows_f32_vec<kKind, 16, 8, 4><<<grid, dim3(1024), 0, s>>>(x4, out, M, n4);
+    reduce_rows_f32_vec<kKind, 16, 8, 4><<<grid, dim3(1024), 0, s>>>(x, out, M, N);
 }
 
 hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, hipStream_t s) {

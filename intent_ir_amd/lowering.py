@@ -340,7 +340,8 @@ def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
     if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
         raise HipLoweringError("HIP row reductions take f32 input and output")
     M, N = c.rows(x)
-    if N % 4 == 0:  # vector form: a wave per row, or 16 waves per row for few long rows
+    if N > 0:  # 16-byte body loads (a head and tail of < 4 elements around them when rows are
+        # not 16-byte aligned): a wave per row, or 16 waves per row for few long rows
         few_long = M < 2048 and N // 4 > 256
         launch = HipLaunch((max(1, M), 1, 1), (1024 if few_long else 64, 1, 1), 64 if few_long else 0)
     else:

@@ -153,7 +153,7 @@ def _row_reduce_ir(op: str) -> dict:
 
 
 ROW_REDUCE_SHAPES = ([(m, n) for m in (1, 3, 17) for n in EDGE + [64, 255, 256, 1023, 1025, 4096, 4100, 65536]]
-                     + [(2048, 256), (2048, 4100), (4096, 1024), (1000, 2048)])
+                     + [(2048, 256), (2048, 4100), (4096, 1024), (1000, 2048), (2048, 4099), (64, 65537)])
 
 
 @pytest.mark.parametrize("op", ["reduce_sum", "reduce_max"])
@@ -161,7 +161,8 @@ ROW_REDUCE_SHAPES = ([(m, n) for m in (1, 3, 17) for n in EDGE + [64, 255, 256, 
 def test_row_reduce_edge_shapes(hip, op, M, N):
     """reduce_sum / reduce_max over the last axis (interpreter.py:478-500): sums within rtol 1e-5
     (a different f32 summation order than numpy's pairwise one), maxima bit-exact.  Covers the
-    wave-per-row and 16-waves-per-row vector forms and the scalar form (N % 4 != 0)."""
+    wave-per-row and 16-waves-per-row forms, with rows that start at every alignment (N % 4 != 0:
+    a head and tail of < 4 elements around the 16-byte body)."""
     ir = _row_reduce_ir(op)
     b = {"M": M, "N": N}
     x = np.random.default_rng(M * 7 + N).standard_normal((M, N)).astype(np.float32)
@@ -173,7 +174,7 @@ def test_row_reduce_edge_shapes(hip, op, M, N):
         check({"out": out}, {"out": ref}, ["out"], {"atol": 1e-4, "rtol": 1e-5}, f"{op} {b}")
 
 
-@pytest.mark.parametrize("N", [8, 4096, 4100])
+@pytest.mark.parametrize("N", [7, 8, 4096, 4099, 4100])
 def test_row_reduce_special_values(hip, N):
     """NaN propagates through both; inf and -inf as in numpy (inf + -inf = NaN); a row of -0.0
     sums to +0.0 (numpy's add.reduce starts from +0.0) and has max -0.0; an empty row sums to
