@@ -19,13 +19,25 @@ namespace ihip {
 // out[m] = any(x[m, :] != c)   (numpy semantics: NaN != c is true, -0.0 != 0 is false)
 // For c == 0 the test is on the bits: |x| has a non-zero bit pattern.
 template <bool kZero, int kUnroll>
-__global__ __launch_bounds__(256) void reduce_any_rows_f32_vec(const f32x4* __restrict__ x, uint8_t* __restrict__ out,
-                                                               int64_t M, int64_t n4, float c) {
+__global__ __launch_bounds__(256) void reduce_any_rows_f32_vec(const float* __restrict__ x, uint8_t* __restrict__ out,
+                                                               int64_t M, int64_t N, float c) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
-  const f32x4* xr = x + row * n4;
+  // head of up to 3 elements to the row's first 16-byte boundary, n4 aligned vectors, tail of
+  // up to 3 elements (neither when rows start aligned)
+  const float* rowp = x + row * N;
+  const int64_t to_edge = (4 - ((reinterpret_cast<uintptr_t>(rowp) >> 2) & 3)) & 3;
+  const int64_t head = to_edge < N ? to_edge : N;
+  const int64_t n4 = (N - head) >> 2;
+  const int64_t tail = N - head - 4 * n4;
+  const f32x4* xr = reinterpret_cast<const f32x4*>(rowp + head);
   uint32_t acc = 0;
+  if (lane < head) acc |= kZero ? (__float_as_uint(rowp[lane]) & 0x7fffffffu) : static_cast<uint32_t>(rowp[lane] != c);
+  if (lane < tail) {
+    const float t = rowp[head + 4 * n4 + lane];
+    acc |= kZero ? (__float_as_uint(t) & 0x7fffffffu) : static_cast<uint32_t>(t != c);
+  }
   for (int64_t base = lane; base < n4; base += kWave * kUnroll) {
     f32x4 v[kUnroll];
 #pragma unroll
@@ -104,19 +116,20 @@ hipError_t launch_reduce_any_rows_f32(const float* x, uint8_t* out, int64_t M, i
   if (M == 0) return hipSuccess;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row
   const dim3 grid(static_cast<unsigned>(M)), block(kStreamBlock);
-  const bool vec = (N % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+  // 16-byte loads over each row's aligned body whenever x is 4-byte aligned (any N)
+  const bool vec = (reinterpret_cast<uintptr_t>(x) & 3) == 0;
   if (!vec) {
     reduce_any_rows_f32_scalar<<<grid, block, 0, s>>>(x, out, M, N, c);
   } else if (c == 0.0f) {
     if (N / 4 >= kWave * 16)
-      reduce_any_rows_f32_vec<true, 16><<<grid, block, 0, s>>>(reinterpret_cast<const f32x4*>(x), out, M, N / 4, c);
+      reduce_any_rows_f32_vec<true, 16><<<grid, block, 0, s>>>(x, out, M, N, c);
     else
-      reduce_any_rows_f32_vec<true, 4><<<grid, block, 0, s>>>(reinterpret_cast<const f32x4*>(x), out, M, N / 4, c);
+      reduce_any_rows_f32_vec<true, 4><<<grid, block, 0, s>>>(x, out, M, N, c);
   } else {
     if (N / 4 >= kWave * 16)
-      reduce_any_rows_f32_vec<false, 16><<<grid, block, 0, s>>>(reinterpret_cast<const f32x4*>(x), out, M, N / 4, c);
+      reduce_any_rows_f32_vec<false, 16><<<grid, block, 0, s>>>(x, out, M, N, c);
     else
-      reduce_any_rows_f32_vec<false, 4><<<grid, block, 0, s>>>(reinterpret_cast<const f32x4*>(x), out, M, N / 4, c);
+      reduce_any_rows_f32_vec<false, 4><<<grid, block, 0, s>>>(x, out, M, N, c);
   }
   return hipGetLastError();
 }

@@ -68,7 +68,7 @@ def check(pred, ref, names, tol, what=""):
 
 # ------------------------------------------------------------------ reduce_any
 @pytest.mark.parametrize("M", [1, 3, 17, 33])
-@pytest.mark.parametrize("N", EDGE + [64, 255, 256, 1023, 4096, 4100])
+@pytest.mark.parametrize("N", EDGE + [64, 255, 256, 1023, 4096, 4099, 4100, 65537])
 def test_reduce_any_edge_shapes(hip, M, N):
     w = WORKLOADS["any"]
     b = {"M": M, "N": N}
