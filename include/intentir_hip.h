@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define IHIP_ABI_VERSION 1
+#define IHIP_ABI_VERSION 2
 
 #define IHIP_OK 0
 #define IHIP_ERR_INVALID_ARG (-1)
@@ -61,13 +61,37 @@ int ihip_reduce_any_rows_u8(const uint8_t* x, uint8_t* out, int64_t M, int64_t N
  * backends/cuda/codegen/intentir_to_cuda.py:1553-1690. */
 int ihip_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, void* stream);
 
+/* Bytes of workspace ihip_reduce_rows_f32_ws uses for an [M, N] reduction: M * S floats when
+ * rows are too few to fill the GPU (M < 256) and long enough to split into S <= 64 segments
+ * of at least 64 KiB each, else 0 (the rows are not split).  Depends on M and N only. */
+int64_t ihip_reduce_rows_f32_workspace_size(int64_t M, int64_t N);
+
+/* ihip_reduce_rows_f32 with a caller-owned device workspace (the library still allocates
+ * nothing): when ihip_reduce_rows_f32_workspace_size(M, N) > 0, each row is split over S
+ * workgroups whose partial results go to the workspace and a second kernel folds them in a
+ * fixed order (results are reproducible; a sum's rounding order differs from the unsplit
+ * form).  workspace may be NULL (no split, exactly ihip_reduce_rows_f32); otherwise it must
+ * hold at least workspace_size bytes, 4-byte aligned, and stay untouched until the work on
+ * `stream` completes.  Same semantics as ihip_reduce_rows_f32 (verify/interpreter.py:478-500). */
+int ihip_reduce_rows_f32_ws(const float* x, float* out, int64_t M, int64_t N, int kind, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* y = softmax(x) over the last axis, x and y f32 [M, N] (y may not alias x).
  * Replaces _kernel_softmax_2d_last_f32 (backends/cuda/codegen/intentir_to_cuda.py:1103-1247)
  * and its device templates (backends/cuda/runtime/kernels/softmax.cuh:92-663). */
 int ihip_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, void* stream);
 
+/* The same with a launch-shape knob, the role of the reference's SOFTMAX_THREADS binding
+ * (backends/cuda/codegen/intentir_to_cuda.py:1175-1200): rows_per_wg = 0 chooses
+ * automatically; 1, 2 or 4 sets how many rows (one wave each) share a workgroup.  Only the
+ * one-wave-per-row form (N % 4 == 0, N <= 4096, 16-byte aligned x and y) has that choice;
+ * for other shapes rows_per_wg must be 0 or 1 (IHIP_ERR_INVALID_ARG otherwise).  Results do
+ * not depend on rows_per_wg. */
+int ihip_softmax_rows_f32_ex(const float* x, float* y, int64_t M, int64_t N, int rows_per_wg, void* stream);
+
 /* LayerNorm forward over the last axis: x, y f16 [M, N]; w, b f16 [N];
- * mean, rstd f32 [M]; f32 statistics, rstd = 1/sqrt(var + eps).  Replaces
+ * mean, rstd f32 [M] (either may be NULL: that statistic is then not written);
+ * f32 statistics, rstd = 1/sqrt(var + eps).  Replaces
  * _kernel_layernorm_2d_f32 (backends/cuda/codegen/intentir_to_cuda.py:1250-1338,
  * backends/cuda/runtime/kernels/layernorm.cuh:11-98), extended to f16 I/O. */
 int ihip_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y, float* mean,
@@ -98,6 +122,16 @@ int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* 
  * any N (K % 8 == 0): C rows that are not 16-byte aligned are written with 2-byte stores. */
 int ihip_gemm_bf16_bias_relu_t(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                                int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, void* stream);
+
+/* The same with a tile knob, the role of the reference's WMMA_* tile bindings and schedule
+ * tile_m / tile_n (backends/cuda/codegen/intentir_to_cuda.py:659-664, 2074-2097): tile = 0
+ * chooses automatically (256x256 C tiles, 128x128 when at most 128 tiles of 256x256 would
+ * run); 128 or 256 fixes the tiled kernel's tile extent.  128 needs a shape and alignment the
+ * tiled kernel takes (listed above); the guarded kernel has 256x256 tiles only.  Every
+ * tile extent accumulates in the same order, so C does not depend on tile. */
+int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                                int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
+                                void* stream);
 
 /* ---------------------------------------------------------------------------
  * Generic element-wise program: any chain of element-wise ops over inputs that

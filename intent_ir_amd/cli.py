@@ -26,20 +26,8 @@ import json
 import sys
 from typing import Any, Dict, List, Optional
 
-from .ewprogram import EwProgram
 from .ir import IntentIRValidationError
-from .lowering import HipLoweredKernel, HipLoweringError, lower_intent_to_hip_kernel
-
-
-def _call_arg_json(kind: str, v: Any) -> Dict[str, Any]:
-    if kind == "tensor":
-        return {"kind": kind, "name": v}
-    if kind == "ew_program":
-        assert isinstance(v, EwProgram)
-        return {"kind": kind, "code": [list(c) for c in v.code],
-                "inputs": [{"name": n, "stride": list(st)} for n, st in v.inputs],
-                "outputs": list(v.outputs), "shape": list(v.shape), "listing": v.listing()}
-    return {"kind": kind, "value": v}
+from .lowering import HipLoweredKernel, HipLoweringError, call_args_to_json, lower_intent_to_hip_kernel
 
 
 def lowered_to_json(k: HipLoweredKernel) -> Dict[str, Any]:
@@ -50,7 +38,7 @@ def lowered_to_json(k: HipLoweredKernel) -> Dict[str, Any]:
         "launch": {"grid": list(k.launch.grid), "block": list(k.launch.block), "lds_bytes": k.launch.lds_bytes},
         "output_names": list(k.output_names),
         "bindings": k.bindings,
-        "call_args": [_call_arg_json(kind, v) for kind, v in k.call_args],
+        "call_args": call_args_to_json(k.call_args),
     }
 
 

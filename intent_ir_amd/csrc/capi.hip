@@ -20,14 +20,17 @@
 namespace ihip {
 hipError_t launch_reduce_any_rows_f32(const float*, uint8_t*, int64_t, int64_t, float, hipStream_t);
 hipError_t launch_reduce_any_rows_u8(const uint8_t*, uint8_t*, int64_t, int64_t, hipStream_t);
-hipError_t launch_reduce_rows_f32(const float*, float*, int64_t, int64_t, int, hipStream_t);
-hipError_t launch_softmax_rows_f32(const float*, float*, int64_t, int64_t, hipStream_t);
+hipError_t launch_reduce_rows_f32(const float*, float*, int64_t, int64_t, int, float*, hipStream_t);
+int reduce_rows_segments(int64_t, int64_t);
+hipError_t launch_softmax_rows_f32(const float*, float*, int64_t, int64_t, int, hipStream_t);
+bool softmax_rows_per_wg_form(const float*, const float*, int64_t);
 hipError_t launch_layernorm_rows_f16(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, float*,
                                      int64_t, int64_t, float, hipStream_t);
 hipError_t launch_bias_gelu_axpy_bf16(const uint16_t*, const uint16_t*, uint16_t*, int64_t, int64_t, float,
                                       hipStream_t);
 hipError_t launch_gemm_bf16_bias_relu(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t,
-                                      int64_t, bool, bool, int, hipStream_t);
+                                      int64_t, bool, bool, int, int, hipStream_t);
+bool gemm_fast_fits(int64_t, int64_t, int64_t, bool, bool, const void*, const void*, const void*);
 hipError_t launch_elementwise_program(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*,
                                       int, const int64_t (&)[4], hipStream_t);
 hipError_t launch_elementwise_jit(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*, int,
@@ -164,29 +167,62 @@ int ihip_reduce_any_rows_u8(const uint8_t* x, uint8_t* out, int64_t M, int64_t N
   return finish(ihip::launch_reduce_any_rows_u8(x, out, M, N, static_cast<hipStream_t>(stream)), "reduce_any_rows_u8");
 }
 
-int ihip_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, void* stream) {
-  const int64_t n = numel2(M, N);
-  IHIP_REQUIRE(n >= 0, "reduce_rows_f32: invalid shape [%lld, %lld]", (long long)M, (long long)N);
-  IHIP_REQUIRE(kind == IHIP_REDUCE_SUM || kind == IHIP_REDUCE_MAX, "reduce_rows_f32: unknown kind %d", kind);
-  IHIP_REQUIRE(!(kind == IHIP_REDUCE_MAX && N == 0 && M > 0),
-               "reduce_rows_f32: max over an empty axis has no identity");
-  IHIP_REQUIRE(M == 0 || out != nullptr, "reduce_rows_f32: out is null");
-  IHIP_REQUIRE(n == 0 || x != nullptr, "reduce_rows_f32: x is null");
-  return finish(ihip::launch_reduce_rows_f32(x, out, M, N, kind, static_cast<hipStream_t>(stream)), "reduce_rows_f32");
+int64_t ihip_reduce_rows_f32_workspace_size(int64_t M, int64_t N) {
+  const int S = ihip::reduce_rows_segments(M, N);
+  return S > 1 ? M * S * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
-int ihip_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, void* stream) {
+// Argument checks shared by the row-reduction entry points; 0 or a failure code.
+static int check_reduce_rows(const char* who, const float* x, float* out, int64_t M, int64_t N, int kind) {
+  const int64_t n = numel2(M, N);
+  IHIP_REQUIRE(n >= 0, "%s: invalid shape [%lld, %lld]", who, (long long)M, (long long)N);
+  IHIP_REQUIRE(kind == IHIP_REDUCE_SUM || kind == IHIP_REDUCE_MAX, "%s: unknown kind %d", who, kind);
+  IHIP_REQUIRE(!(kind == IHIP_REDUCE_MAX && N == 0 && M > 0), "%s: max over an empty axis has no identity", who);
+  IHIP_REQUIRE(M == 0 || out != nullptr, "%s: out is null", who);
+  IHIP_REQUIRE(n == 0 || x != nullptr, "%s: x is null", who);
+  return 0;
+}
+
+int ihip_reduce_rows_f32_ws(const float* x, float* out, int64_t M, int64_t N, int kind, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  const int bad = check_reduce_rows("reduce_rows_f32", x, out, M, N, kind);
+  if (bad) return bad;
+  const int64_t need = ihip_reduce_rows_f32_workspace_size(M, N);
+  IHIP_REQUIRE(workspace == nullptr || workspace_bytes >= need,
+               "reduce_rows_f32: workspace of %lld bytes, [%lld, %lld] needs %lld", (long long)workspace_bytes,
+               (long long)M, (long long)N, (long long)need);
+  IHIP_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 3) == 0, "reduce_rows_f32: workspace not 4-byte aligned");
+  float* part = need > 0 ? static_cast<float*>(workspace) : nullptr;
+  return finish(ihip::launch_reduce_rows_f32(x, out, M, N, kind, part, static_cast<hipStream_t>(stream)),
+                "reduce_rows_f32");
+}
+
+int ihip_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, void* stream) {
+  return ihip_reduce_rows_f32_ws(x, out, M, N, kind, nullptr, 0, stream);
+}
+
+int ihip_softmax_rows_f32_ex(const float* x, float* y, int64_t M, int64_t N, int rows_per_wg, void* stream) {
   const int64_t n = numel2(M, N);
   IHIP_REQUIRE(n >= 0, "softmax_rows_f32: invalid shape [%lld, %lld]", (long long)M, (long long)N);
   IHIP_REQUIRE(n == 0 || (x != nullptr && y != nullptr), "softmax_rows_f32: null pointer");
-  return finish(ihip::launch_softmax_rows_f32(x, y, M, N, static_cast<hipStream_t>(stream)), "softmax_rows_f32");
+  IHIP_REQUIRE(rows_per_wg == 0 || rows_per_wg == 1 || rows_per_wg == 2 || rows_per_wg == 4,
+               "softmax_rows_f32: rows_per_wg %d is not 0 (automatic), 1, 2 or 4", rows_per_wg);
+  IHIP_REQUIRE(rows_per_wg <= 1 || n == 0 || ihip::softmax_rows_per_wg_form(x, y, N),
+               "softmax_rows_f32: rows_per_wg %d needs the one-wave-per-row form (N %% 4 == 0, N <= 4096, "
+               "16-byte aligned x and y); N = %lld runs one row per workgroup",
+               rows_per_wg, (long long)N);
+  return finish(ihip::launch_softmax_rows_f32(x, y, M, N, rows_per_wg, static_cast<hipStream_t>(stream)),
+                "softmax_rows_f32");
+}
+
+int ihip_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, void* stream) {
+  return ihip_softmax_rows_f32_ex(x, y, M, N, 0, stream);
 }
 
 int ihip_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y, float* mean,
                             float* rstd, int64_t M, int64_t N, float eps, void* stream) {
   const int64_t n = numel2(M, N);
   IHIP_REQUIRE(n >= 0, "layernorm_rows_f16: invalid shape [%lld, %lld]", (long long)M, (long long)N);
-  IHIP_REQUIRE(M == 0 || (mean != nullptr && rstd != nullptr), "layernorm_rows_f16: null statistics pointer");
   IHIP_REQUIRE(n == 0 || (x != nullptr && y != nullptr && w != nullptr && b != nullptr),
                "layernorm_rows_f16: null pointer");
   return finish(ihip::launch_layernorm_rows_f16(x, w, b, y, mean, rstd, M, N, eps, static_cast<hipStream_t>(stream)),
@@ -202,15 +238,28 @@ int ihip_bias_gelu_tanh_axpy_bf16(const uint16_t* x, const uint16_t* bias, uint1
                 "bias_gelu_tanh_axpy_bf16");
 }
 
-int ihip_gemm_bf16_bias_relu_t(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
-                               int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, void* stream) {
+int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                                int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
+                                void* stream) {
   IHIP_REQUIRE(numel2(M, K) >= 0 && numel2(K, N) >= 0 && numel2(M, N) >= 0,
                "gemm_bf16_bias_relu: invalid shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
   IHIP_REQUIRE(M == 0 || N == 0 || C != nullptr, "gemm_bf16_bias_relu: C is null");
   IHIP_REQUIRE(M == 0 || N == 0 || K == 0 || (A != nullptr && B != nullptr), "gemm_bf16_bias_relu: A or B is null");
+  IHIP_REQUIRE(tile == 0 || tile == 128 || tile == 256, "gemm_bf16_bias_relu: tile %d is not 0 (automatic), 128 or 256",
+               tile);
+  IHIP_REQUIRE(tile != 128 || M == 0 || N == 0 ||
+                   ihip::gemm_fast_fits(M, N, K, transpose_a != 0, transpose_b != 0, A, B, C),
+               "gemm_bf16_bias_relu: tile 128 needs the tiled kernel (rows of A, B and C 16-byte aligned); "
+               "M=%lld N=%lld K=%lld runs the guarded kernel's 256x256 tiles",
+               (long long)M, (long long)N, (long long)K);
   return finish(ihip::launch_gemm_bf16_bias_relu(A, B, bias, C, M, N, K, transpose_a != 0, transpose_b != 0, relu,
-                                                 static_cast<hipStream_t>(stream)),
+                                                 tile, static_cast<hipStream_t>(stream)),
                 "gemm_bf16_bias_relu");
+}
+
+int ihip_gemm_bf16_bias_relu_t(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                               int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, void* stream) {
+  return ihip_gemm_bf16_bias_relu_ex(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, 0, stream);
 }
 
 int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,

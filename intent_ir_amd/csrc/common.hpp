@@ -35,6 +35,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Two float32 -> one word of two bf16 (lo in bits 0-15), round to nearest even, with
+// gfx950's v_cvt_pk_bf16_f32 (NaN stays NaN).
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
@@ -49,11 +57,15 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
 // a head RN(d*L) and a tail (its exact rounding error plus d*(log2 e - L)); the
 // head goes through the hardware 2^x and the tail through a first-order
 // correction, |tail| <= 2^-24 |t|.  Relative error about 2 ulp for d >= -87;
-// below that the result is under 1e-38.
+// below that the result is under 1e-38.  d is first clamped to -160 (e^-160 is 0 in
+// f32): without the clamp d = -inf (a masked logit) gives t = -inf and a NaN tail
+// (-inf + inf), and 0 * NaN would make the result NaN instead of 0.  The clamp is
+// NaN-propagating, so NaN still maps to NaN.
 __device__ __forceinline__ float exp_nonpos(float d) {
   constexpr float kL = 1.44269502f;        // RN(log2 e)
   constexpr float kLlo = 1.92596303e-08f;  // log2 e - kL
   constexpr float kLn2 = 0.693147182f;
+  d = __builtin_elementwise_maximum(d, -160.0f);
   const float t = d * kL;
   const float tail = __builtin_fmaf(d, kLlo, __builtin_fmaf(d, kL, -t));
   const float e = __builtin_amdgcn_exp2f(t);

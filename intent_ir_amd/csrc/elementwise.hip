@@ -6,41 +6,67 @@
 // together; a wave covers 1 KiB of contiguous row per load instruction.
 //
 // Arithmetic: gelu_tanh(z) = z / (1 + exp(-2*sqrt(2/pi)*(z + 0.044715*z^3))).  The
-// kernel evaluates the same expression with the exponential as 2^(u * k*log2(e))
-// on the hardware exp2, and the quotient as z * rcp(1 + e).  Both are within a few
-// float32 ulps of the op-by-op reference, three orders of magnitude below the bf16
-// output rounding.
+// kernel evaluates the same expression with the exponential as 2^t on the hardware exp2,
+// t = z * (k + k*0.044715 * z^2) with k = -2*sqrt(2/pi)*log2(e), and folds alpha into the
+// reciprocal: alpha * z / (1 + e) = z * rcp(e/alpha + 1/alpha), one FMA before the rcp and
+// one after it (y = z * r + x).  Outputs are packed two at a time by the hardware
+// round-to-nearest-even conversion (v_cvt_pk_bf16_f32).  That is ~7.5 VALU instructions
+// per element plus the two transcendentals, against ~16 for the op-by-op form with a
+// software bf16 rounding; at 8 TB/s the op-by-op form would be VALU-bound.  Error: a few
+// float32 ulps of the op-by-op reference, three orders of magnitude below the bf16 output
+// rounding.  alpha = 0 or 1/alpha not finite (no reciprocal to fold) takes the unfolded
+// form z * rcp(1 + e) * alpha + x.
 #include "common.hpp"
 
 namespace ihip {
 
-constexpr float kGeluCubic = 0.044715f;
-// -2*sqrt(2/pi) * log2(e): the exponent of the logistic form in base 2.
+// -2*sqrt(2/pi) * log2(e): the exponent of the logistic form in base 2, and its cubic term.
 constexpr float kGeluExp2Scale = -2.3022082f;
+constexpr float kGeluExp2Cubic = -2.3022082f * 0.044715f;
+constexpr float kGeluCubic = 0.044715f;
 
+// t = z * (k + c z^2): the base-2 exponent of the logistic form.
+__device__ __forceinline__ float gelu_exp2_arg(float z) {
+  return z * __builtin_fmaf(kGeluExp2Cubic, z * z, kGeluExp2Scale);
+}
+
+// alpha * gelu_tanh(x + b) + x with ia = 1 / alpha folded into the reciprocal.
+__device__ __forceinline__ float gelu_axpy_folded(float xv, float bv, float ia) {
+  const float z = xv + bv;
+  const float e = __builtin_amdgcn_exp2f(gelu_exp2_arg(z));
+  return __builtin_fmaf(z, __builtin_amdgcn_rcpf(__builtin_fmaf(e, ia, ia)), xv);
+}
+
+// The unfolded form, for any alpha (0, or one whose reciprocal overflows).
 __device__ __forceinline__ float gelu_axpy(float xv, float bv, float alpha) {
   const float z = xv + bv;
-  const float z2 = z * z;
-  const float p = __builtin_fmaf(kGeluCubic, z2, 1.0f);
-  const float u = z * p;
-  const float e = __builtin_amdgcn_exp2f(u * kGeluExp2Scale);
+  const float p = __builtin_fmaf(kGeluCubic, z * z, 1.0f);
+  const float e = __builtin_amdgcn_exp2f((z * p) * kGeluExp2Scale);
   const float g = z * __builtin_amdgcn_rcpf(1.0f + e);
   return __builtin_fmaf(g, alpha, xv);
 }
 
-__device__ __forceinline__ uint32_t bf16x2_apply(uint32_t xw, uint32_t bw, float alpha) {
+template <bool kFolded>
+__device__ __forceinline__ uint32_t bf16x2_apply(uint32_t xw, float b0, float b1, float a) {
   const float x0 = __uint_as_float(xw << 16), x1 = __uint_as_float(xw & 0xffff0000u);
-  const float b0 = __uint_as_float(bw << 16), b1 = __uint_as_float(bw & 0xffff0000u);
-  const float y0 = gelu_axpy(x0, b0, alpha), y1 = gelu_axpy(x1, b1, alpha);
-  return static_cast<uint32_t>(f32_to_bf16_rne(y0)) | (static_cast<uint32_t>(f32_to_bf16_rne(y1)) << 16);
+  const float y0 = kFolded ? gelu_axpy_folded(x0, b0, a) : gelu_axpy(x0, b0, a);
+  const float y1 = kFolded ? gelu_axpy_folded(x1, b1, a) : gelu_axpy(x1, b1, a);
+  return pack_bf16x2_rne(y0, y1);
 }
 
-template <int kRows>
+// a: 1/alpha when kFolded, else alpha.
+template <int kRows, bool kFolded>
 __global__ __launch_bounds__(256) void bias_gelu_axpy_bf16_vec(const u32x4* __restrict__ x, const u32x4* __restrict__ bias,
-                                                               u32x4* __restrict__ y, int64_t M, int64_t n8, float alpha) {
+                                                               u32x4* __restrict__ y, int64_t M, int64_t n8, float a) {
   const int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (col >= n8) return;
-  const u32x4 bv = bias[col];
+  const u32x4 bw = bias[col];
+  float bf[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bf[2 * j] = __uint_as_float(bw[j] << 16);
+    bf[2 * j + 1] = __uint_as_float(bw[j] & 0xffff0000u);
+  }
   for (int64_t row0 = static_cast<int64_t>(blockIdx.y) * kRows; row0 < M;
        row0 += static_cast<int64_t>(gridDim.y) * kRows) {
     u32x4 v[kRows];
@@ -54,10 +80,8 @@ __global__ __launch_bounds__(256) void bias_gelu_axpy_bf16_vec(const u32x4* __re
       const int64_t row = row0 + r;
       if (row < M) {
         u32x4 o;
-        o.x = bf16x2_apply(v[r].x, bv.x, alpha);
-        o.y = bf16x2_apply(v[r].y, bv.y, alpha);
-        o.z = bf16x2_apply(v[r].z, bv.z, alpha);
-        o.w = bf16x2_apply(v[r].w, bv.w, alpha);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = bf16x2_apply<kFolded>(v[r][j], bf[2 * j], bf[2 * j + 1], a);
         __builtin_nontemporal_store(o, y + row * n8 + col);
       }
     }
@@ -85,9 +109,14 @@ hipError_t launch_bias_gelu_axpy_bf16(const uint16_t* x, const uint16_t* bias, u
     int64_t row_blocks = (M + kRows - 1) / kRows;
     if (row_blocks > 65535) row_blocks = 65535;  // grid.y limit; the kernel strides over the rest
     const dim3 grid(static_cast<unsigned>((n8 + 255) / 256), static_cast<unsigned>(row_blocks));
-    bias_gelu_axpy_bf16_vec<kRows><<<grid, dim3(256), 0, s>>>(reinterpret_cast<const u32x4*>(x),
-                                                              reinterpret_cast<const u32x4*>(bias),
-                                                              reinterpret_cast<u32x4*>(y), M, n8, alpha);
+    const u32x4* x8 = reinterpret_cast<const u32x4*>(x);
+    const u32x4* b8 = reinterpret_cast<const u32x4*>(bias);
+    u32x4* y8 = reinterpret_cast<u32x4*>(y);
+    const float ia = 1.0f / alpha;
+    if (alpha != 0.0f && __builtin_isfinite(ia) && __builtin_isfinite(alpha))
+      bias_gelu_axpy_bf16_vec<kRows, true><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, ia);
+    else
+      bias_gelu_axpy_bf16_vec<kRows, false><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, alpha);
   } else {
     const int64_t total = M * N;
     int64_t blocks = (total + 255) / 256;

@@ -221,7 +221,7 @@ void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* 
 bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, bool transpose_b, const void* A, const void* B,
                     const void* C);
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
-                            int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s);
+                            int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s);
 
 template <bool kTA, bool kTB>
 static void launch_guarded(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
@@ -230,11 +230,14 @@ static void launch_guarded(const uint16_t* A, const uint16_t* B, const float* bi
       A, B, bias, C, M, N, K, relu, tm, tn);
 }
 
+// tile: 0 = automatic, else the tiled kernel's tile extent (128 or 256; the caller has checked
+// that the tiled kernel runs this shape when it is 128).
 hipError_t launch_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
-                                      int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu,
+                                      int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu, int tile,
                                       hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (gemm_fast_fits(M, N, K, transpose_a, transpose_b, A, B, C)) return launch_gemm_fast(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
+  if (gemm_fast_fits(M, N, K, transpose_a, transpose_b, A, B, C))
+    return launch_gemm_fast(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, s);
   const int64_t tm = (M + kBM - 1) / kBM, tn = (N + kBN - 1) / kBN;
   if (tm * tn > 0x7fffffffLL) return hipErrorInvalidValue;
   const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);

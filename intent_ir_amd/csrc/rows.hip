@@ -161,14 +161,20 @@ __device__ __forceinline__ float red_op(float a, float b) {
   return kKind == 0 ? a + b : max_nan(a, b);
 }
 
-template <int kKind, int W, int kUnroll, int kAcc>
+// kSplit: the row is split over S workgroups (segments); workgroup blockIdx.x takes segment
+// blockIdx.x % S of row blockIdx.x / S, i.e. aligned vectors [seg*per, (seg+1)*per) of the
+// row's body (segment 0 also the head, segment S-1 the tail), and writes its partial to
+// part[row * S + seg] instead of out[row]; reduce_rows_combine then folds the S partials.
+template <int kKind, int W, int kUnroll, int kAcc, bool kSplit = false>
 __global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const float* __restrict__ x, float* __restrict__ out,
-                                                              int64_t M, int64_t N) {
+                                                              int64_t M, int64_t N, int S = 1,
+                                                              float* __restrict__ part = nullptr) {
   static_assert(kUnroll % kAcc == 0 && (kAcc & (kAcc - 1)) == 0, "loads fold evenly into a power-of-two of partials");
   const float id = kKind == 0 ? 0.0f : -__builtin_inff();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t row = blockIdx.x;
+  const int64_t row = kSplit ? blockIdx.x / S : blockIdx.x;
+  const int seg = kSplit ? static_cast<int>(blockIdx.x % S) : 0;
   if (row >= M) return;
   // The row splits into a head of up to 3 elements (to its first 16-byte boundary), n4
   // aligned vectors and a tail of up to 3 elements; rows that start aligned with N % 4 == 0
@@ -179,15 +185,19 @@ __global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const float* __res
   const int64_t n4 = (N - head) >> 2;
   const int64_t tail = N - head - 4 * n4;
   const f32x4* xr = reinterpret_cast<const f32x4*>(rowp + head);
+  // vectors [v0, v1) of the body: all of it, or this segment's share
+  const int64_t per = kSplit ? (n4 + S - 1) / S : n4;
+  const int64_t v0 = kSplit ? (seg * per < n4 ? seg * per : n4) : 0;
+  const int64_t v1 = kSplit ? (v0 + per < n4 ? v0 + per : n4) : n4;
   f32x4 acc[kAcc];
 #pragma unroll
   for (int u = 0; u < kAcc; ++u) acc[u] = f32x4{id, id, id, id};
-  for (int64_t base = wave * kWave + lane; base < n4; base += static_cast<int64_t>(kWave) * W * kUnroll) {
+  for (int64_t base = v0 + wave * kWave + lane; base < v1; base += static_cast<int64_t>(kWave) * W * kUnroll) {
     f32x4 v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t i = base + static_cast<int64_t>(u) * kWave * W;
-      v[u] = (i < n4) ? __builtin_nontemporal_load(xr + i) : f32x4{id, id, id, id};
+      v[u] = (i < v1) ? __builtin_nontemporal_load(xr + i) : f32x4{id, id, id, id};
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -209,23 +219,37 @@ __global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const float* __res
     }
   float r = red_op<kKind>(red_op<kKind>(acc[0].x, acc[0].y), red_op<kKind>(acc[0].z, acc[0].w));
   if (wave == 0) {  // head and tail elements (at most 3 each) join lanes 0..2 of the first wave
-    if (lane < head) r = red_op<kKind>(r, rowp[lane]);
-    if (lane < tail) r = red_op<kKind>(r, rowp[head + 4 * n4 + lane]);
+    if (lane < head && seg == 0) r = red_op<kKind>(r, rowp[lane]);
+    if (lane < tail && seg == S - 1) r = red_op<kKind>(r, rowp[head + 4 * n4 + lane]);
   }
   r = kKind == 0 ? wave_sum(r) : wave_max_nan(r);
+  float* dst = kSplit ? part + row * S + seg : out + row;
   if (W > 1) {
-    __shared__ float part[W];
-    if (lane == 0) part[wave] = r;
+    __shared__ float wpart[W];
+    if (lane == 0) wpart[wave] = r;
     __syncthreads();
     if (threadIdx.x == 0) {
-      float t = part[0];
+      float t = wpart[0];
 #pragma unroll
-      for (int i = 1; i < W; ++i) t = red_op<kKind>(t, part[i]);
-      out[row] = t;
+      for (int i = 1; i < W; ++i) t = red_op<kKind>(t, wpart[i]);
+      *dst = t;
     }
   } else if (lane == 0) {
-    out[row] = r;
+    *dst = r;
   }
+}
+
+// out[row] = fold of the row's S <= 64 segment partials part[row*S ..], one wave per row, lane
+// l holding partial l; the xor-shuffle tree fixes the order, so results are reproducible.
+template <int kKind>
+__global__ __launch_bounds__(256) void reduce_rows_combine(const float* __restrict__ part, float* __restrict__ out,
+                                                           int64_t M, int S) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= M) return;
+  float r = lane < S ? part[row * S + lane] : (kKind == 0 ? 0.0f : -__builtin_inff());
+  r = kKind == 0 ? wave_sum(r) : wave_max_nan(r);
+  if (lane == 0) out[row] = r;
 }
 
 // Scalar form for rows the vector form cannot take (N % 4 != 0 or a base not 16-byte aligned).
@@ -245,8 +269,24 @@ __global__ __launch_bounds__(256) void reduce_rows_f32(const float* __restrict__
 // Loads in flight per lane in the one-wave form (8 measured level with 16 on [8192, 4096]).
 constexpr int kRedUnroll = 16;
 
+// Row split for rows too few to fill the GPU: S segments per row (1 = no split), so that
+// M * S workgroups of 16 waves give every CU about two, each segment at least
+// kRedSegMinVec 16-byte vectors (64 KiB).  Depends on the shape only.
+constexpr int kRedMaxSegments = 64;
+constexpr int64_t kRedSplitRows = 256;      // rows below this may split (fewer rows than CUs)
+constexpr int64_t kRedSplitTarget = 512;    // workgroups to aim for
+constexpr int64_t kRedSegMinVec = 4096;
+int reduce_rows_segments(int64_t M, int64_t N) {
+  if (M <= 0 || M >= kRedSplitRows || N <= 0) return 1;
+  const int64_t n4 = N / 4;
+  int64_t S = (kRedSplitTarget + M - 1) / M;
+  if (S > kRedMaxSegments) S = kRedMaxSegments;
+  while (S > 1 && n4 / S < kRedSegMinVec) --S;
+  return static_cast<int>(S);
+}
+
 template <int kKind>
-static void launch_reduce_rows(const float* x, float* out, int64_t M, int64_t N, hipStream_t s) {
+static void launch_reduce_rows(const float* x, float* out, int64_t M, int64_t N, float* part, int S, hipStream_t s) {
   // 16-byte loads over each row's aligned body whenever x is 4-byte aligned (any N)
   if ((reinterpret_cast<uintptr_t>(x) & 3) != 0 || N == 0) {
     reduce_rows_f32<kKind><<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(x, out, M, N);
@@ -254,19 +294,27 @@ static void launch_reduce_rows(const float* x, float* out, int64_t M, int64_t N,
   }
   const int64_t n4 = N / 4;
   const dim3 grid(static_cast<unsigned>(M));
-  if (M >= 2048 || n4 <= 4 * kWave)  // enough rows for the CUs, or short rows: a wave per row
+  if (S > 1 && part != nullptr) {  // few long rows split over S workgroups each, then combined
+    reduce_rows_f32_vec<kKind, 16, 8, 4, true><<<dim3(static_cast<unsigned>(M * S)), dim3(1024), 0, s>>>(
+        x, out, M, N, S, part);
+    reduce_rows_combine<kKind><<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(part, out, M, S);
+  } else if (M >= 2048 || n4 <= 4 * kWave) {  // enough rows for the CUs, or short rows: a wave per row
     reduce_rows_f32_vec<kKind, 1, kRedUnroll, 4><<<grid, dim3(64), 0, s>>>(x, out, M, N);
-  else  // few long rows: 16 waves per row
+  } else {  // few long rows: 16 waves per row
     reduce_rows_f32_vec<kKind, 16, 8, 4><<<grid, dim3(1024), 0, s>>>(x, out, M, N);
+  }
 }
 
-hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, hipStream_t s) {
+// part: workspace of M * reduce_rows_segments(M, N) floats, or null (no row split).
+hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, float* part,
+                                  hipStream_t s) {
   if (M == 0) return hipSuccess;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row
+  const int S = part != nullptr ? reduce_rows_segments(M, N) : 1;
   if (kind == 0)
-    launch_reduce_rows<0>(x, out, M, N, s);
+    launch_reduce_rows<0>(x, out, M, N, part, S, s);
   else
-    launch_reduce_rows<1>(x, out, M, N, s);
+    launch_reduce_rows<1>(x, out, M, N, part, S, s);
   return hipGetLastError();
 }
 
@@ -497,17 +545,27 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restr
   for (int64_t i = threadIdx.x; i < N; i += blockDim.x) yr[i] = expf(xr[i] - mx) / s;
 }
 
+// rows: rows (one wave each) per workgroup, 1, 2 or 4 (the kernel reads it from blockDim).
 template <int kVpl>
-static void launch_softmax_reg(const f32x4* x4, f32x4* y4, int64_t M, int n4, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+static void launch_softmax_reg(const f32x4* x4, f32x4* y4, int64_t M, int n4, int rows, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((M + rows - 1) / rows)), block(64 * rows);
   if (n4 == kVpl * kWave)
     softmax_rows_f32_reg<kVpl, true><<<grid, block, 0, s>>>(x4, y4, M, n4);
   else
     softmax_rows_f32_reg<kVpl, false><<<grid, block, 0, s>>>(x4, y4, M, n4);
 }
 
-hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, hipStream_t s) {
+// True when launch_softmax_rows_f32 runs the one-wave-per-row form, the only form with a
+// choice of rows per workgroup (every other form is one row per workgroup).
+bool softmax_rows_per_wg_form(const float* x, const float* y, int64_t N) {
+  const bool vec = (N % 4 == 0) && (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0);
+  return vec && N / 4 <= 1024;
+}
+
+// rows_per_wg: 0 = automatic (4), else 1, 2 or 4 for the one-wave-per-row form.
+hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, int rows_per_wg, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
+  const int rows = rows_per_wg > 0 ? rows_per_wg : 4;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // grid.x limit of the row-per-workgroup fallback
   const bool vec = (N % 4 == 0) && (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0);
   // rows of a non-vector shape split at the same 16-byte boundaries in x and y
@@ -518,15 +576,15 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
   f32x4* y4 = reinterpret_cast<f32x4*>(y);
   const int n4i = static_cast<int>(n4 < 0x7fffffff ? n4 : 0x7fffffff);
   if (vec && n4 <= 64)
-    launch_softmax_reg<1>(x4, y4, M, n4i, s);
+    launch_softmax_reg<1>(x4, y4, M, n4i, rows, s);
   else if (vec && n4 <= 128)
-    launch_softmax_reg<2>(x4, y4, M, n4i, s);
+    launch_softmax_reg<2>(x4, y4, M, n4i, rows, s);
   else if (vec && n4 <= 256)
-    launch_softmax_reg<4>(x4, y4, M, n4i, s);
+    launch_softmax_reg<4>(x4, y4, M, n4i, rows, s);
   else if (vec && n4 <= 512)
-    launch_softmax_reg<8>(x4, y4, M, n4i, s);
+    launch_softmax_reg<8>(x4, y4, M, n4i, rows, s);
   else if (vec && n4 <= 1024)
-    launch_softmax_reg<16>(x4, y4, M, n4i, s);
+    launch_softmax_reg<16>(x4, y4, M, n4i, rows, s);
   else if (vec && n4 <= 2048)
     softmax_rows_f32_multi<16, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x4, y4, M, n4i);
   else if (vec && n4 <= 4096)
@@ -654,9 +712,9 @@ __global__ __launch_bounds__(64 * kLnRows) void layernorm_rows_f16_wave(
     }
     if (kExact || (live && idx < n8)) __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), yr + idx);
   }
-  if ((kExact || live) && lane == 0) {
-    mean_out[row] = mean;
-    rstd_out[row] = rstd;
+  if ((kExact || live) && lane == 0) {  // null statistics pointers: not wanted, not written
+    if (mean_out != nullptr) mean_out[row] = mean;
+    if (rstd_out != nullptr) rstd_out[row] = rstd;
   }
 }
 
@@ -736,8 +794,8 @@ __global__ __launch_bounds__(64 * kWaves) void layernorm_rows_f16_multi(
     if (live && in) __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), yr + idx);
   }
   if (live && v == 0 && lane == 0) {
-    mean_out[row] = mean;
-    rstd_out[row] = rstd;
+    if (mean_out != nullptr) mean_out[row] = mean;
+    if (rstd_out != nullptr) rstd_out[row] = rstd;
   }
 }
 
@@ -768,8 +826,8 @@ __global__ __launch_bounds__(256) void layernorm_rows_f16_any(const uint16_t* __
     yr[i] = f32_to_f16_rne(scaled + f16_to_f32(b[i]));
   }
   if (threadIdx.x == 0) {
-    mean_out[row] = mean;
-    rstd_out[row] = rstd;
+    if (mean_out != nullptr) mean_out[row] = mean;
+    if (rstd_out != nullptr) rstd_out[row] = rstd;
   }
 }
 

@@ -9,6 +9,16 @@ handling (:2074-2097) and an error type raised for unsupported IR (:23-24,
 C-ABI entry point of ``libintentir_hip.so`` (``kernel_id``) and the argument
 list to call it with (``call_args``).
 
+Schedule knobs (the reference's ``CUDA_RESPECT_SCHEDULE`` and knobs-in-bindings
+convention, intentir_to_cuda.py:1012,1175-1200,2074-2097): a schedule is authoritative
+when ``schedule_override`` is given or the bindings set ``HIP_RESPECT_SCHEDULE=1``, and
+is otherwise a hint the backend ignores.  The precompiled kernels offer a few
+variants: ``HIP_GEMM_TILE`` / schedule ``tile_m``, ``tile_n`` (128 or 256) for the GEMM
+and ``HIP_ROWS_PER_WG`` / schedule ``tile_m`` (1, 2 or 4 rows per workgroup) for the
+one-wave-per-row softmax.  A knob or authoritative schedule field that the selected
+kernel cannot honour raises ``HipLoweringError`` instead of being ignored, and so does
+an unknown ``HIP_*`` binding.
+
 Kernel families are recognised structurally (``patterns.py``), in this order:
 GEMM (+bias, +ReLU, incl. ``matmul{epilogue}``), reduce_any (incl.
 ``const, ne, reduce_any``), softmax (op or expanded chain), LayerNorm
@@ -50,8 +60,9 @@ class HipLoweredKernel:
     output_names: List[str]
     bindings: Dict[str, Any]
     # Arguments of the C call in order: ("tensor", name) | ("i64", v) | ("i32", v) | ("f32", v)
-    # | ("null", None) | ("scratch_f32", n): a device temporary of n floats the runtime provides
-    # | ("ew_program", EwProgram): the program, operand table and shape of ihip_elementwise_program.
+    # | ("null", None) | ("workspace", nbytes): a device workspace the caller provides, passed as
+    # pointer + byte count | ("ew_program", EwProgram): the program, operand table and shape of
+    # ihip_elementwise_program.  io_spec["hip_call"] holds the same plan as JSON.
     call_args: Tuple[Tuple[str, Any], ...] = field(default_factory=tuple)
 
 
@@ -77,10 +88,98 @@ def _normalize_bindings(shape_bindings: Mapping[str, Any]) -> Dict[str, Any]:
     return out
 
 
+# Knobs carried in the bindings and the values each accepts (None: any 0/1 flag).
+KNOBS: Dict[str, Optional[Tuple[int, ...]]] = {
+    "HIP_RESPECT_SCHEDULE": None,
+    "HIP_GEMM_TILE": (128, 256),
+    "HIP_ROWS_PER_WG": (1, 2, 4),
+}
+_SCHED_FIELDS = ("tile_m", "tile_n", "tile_k", "vec_width", "pipeline_depth")
+
+
+class _Knobs:
+    """Launch-variant requests: binding knobs, and the schedule when it is authoritative.
+
+    Matchers take what their kernel can honour (``gemm_tile``, ``rows_per_wg``);
+    ``check_used`` then rejects whatever is left, so nothing is silently ignored."""
+
+    def __init__(self, fn: IntentFunction, b: Mapping[str, Any]):
+        for k in b:
+            if k.startswith("HIP_") and k not in KNOBS:
+                raise HipLoweringError(f"unknown HIP knob {k} (known: {sorted(KNOBS)})")
+        self.values: Dict[str, int] = {}
+        for k, allowed in KNOBS.items():
+            if k not in b:
+                continue
+            v = b[k]
+            if not isinstance(v, int) or (allowed is not None and v not in allowed) or (allowed is None and v not in (0, 1)):
+                raise HipLoweringError(f"{k}={v!r} is not one of {allowed or (0, 1)}")
+            self.values[k] = v
+        self.respect = bool(self.values.get("HIP_RESPECT_SCHEDULE", 0))
+        self.sched: Dict[str, int] = {}
+        if self.respect and fn.schedule is not None:
+            for f in _SCHED_FIELDS:
+                v = getattr(fn.schedule, f)
+                if v is None:
+                    continue
+                if isinstance(v, str):
+                    if v not in b or not isinstance(b[v], int):
+                        raise HipLoweringError(f"schedule.{f}={v!r} names no integer binding")
+                    v = b[v]
+                self.sched[f] = int(v)
+        self.used: set = {"HIP_RESPECT_SCHEDULE"}
+
+    def _fields(self, allowed: Mapping[str, Tuple[Optional[int], ...]], what: str) -> None:
+        for f, v in self.sched.items():
+            if f in allowed and v not in allowed[f]:
+                raise HipLoweringError(f"schedule.{f}={v} is not available for {what} "
+                                       f"(choices: {[a for a in allowed[f] if a is not None]})")
+        self.used |= set(allowed)
+
+    def gemm_tile(self) -> int:
+        """C tile extent the GEMM must use: 0 = the kernel's own choice, else 128 or 256."""
+        self.used.add("HIP_GEMM_TILE")
+        knob = self.values.get("HIP_GEMM_TILE")
+        allowed: Dict[str, Tuple[Optional[int], ...]] = {"tile_k": (32,), "pipeline_depth": (4,), "vec_width": (8,)}
+        if knob is None:
+            allowed.update(tile_m=(128, 256), tile_n=(128, 256))
+        else:  # the binding knob overrides the schedule's tile (as SOFTMAX_THREADS does in the reference)
+            self.used |= {"tile_m", "tile_n"}
+        self._fields(allowed, "the GEMM (K slices of 32 in a 4-stage ring, 16-byte copies)")
+        if knob is not None:
+            return knob
+        tm, tn = self.sched.get("tile_m"), self.sched.get("tile_n")
+        if tm is not None and tn is not None and tm != tn:
+            raise HipLoweringError(f"GEMM tiles are square: schedule tile_m={tm}, tile_n={tn}")
+        return tm or tn or 0
+
+    def rows_per_wg(self) -> int:
+        """Rows per workgroup the one-wave-per-row softmax must use: 0 = its own choice."""
+        self.used.add("HIP_ROWS_PER_WG")
+        knob = self.values.get("HIP_ROWS_PER_WG")
+        allowed: Dict[str, Tuple[Optional[int], ...]] = {"vec_width": (4,)}
+        if knob is None:
+            allowed["tile_m"] = (1, 2, 4)
+        else:
+            self.used.add("tile_m")
+        self._fields(allowed, "softmax (rows per workgroup; 16-byte vectors)")
+        return knob if knob is not None else self.sched.get("tile_m", 0)
+
+    def check_used(self, kernel_id: str) -> None:
+        for k in self.values:
+            if k not in self.used:
+                raise HipLoweringError(f"{k} does not apply to {kernel_id}")
+        left = sorted(f for f in self.sched if f not in self.used)
+        if left:
+            raise HipLoweringError(f"authoritative schedule fields {left} are not available for {kernel_id}: "
+                                   "it has a single launch schedule")
+
+
 class _Ctx:
     def __init__(self, fn: IntentFunction, bindings: Dict[str, Any]):
         self.fn = fn
         self.b = bindings
+        self.knobs = _Knobs(fn, bindings)
         self.eb = ExprBuilder(fn, bindings)
         self.outs = {o: self.eb.get(o) for o in fn.outputs}
 
@@ -144,10 +243,11 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
         bn = env["bias"][1]
         if c.dtype(bn) != "f32" or c.shape(bn) != (N,):
             raise HipLoweringError(f"GEMM bias must be f32 [{N}]")
+    tile = c.knobs.gemm_tile()
     args = [("tensor", a), ("tensor", b), ("tensor", env["bias"][1]) if has_bias else ("null", None),
             ("tensor", oname), ("i64", M), ("i64", N), ("i64", K)]
-    args += [("i32", int(ta)), ("i32", int(tb))] if (ta or tb) else []
-    args += [("i32", int(relu))]
+    args += [("i32", int(ta)), ("i32", int(tb))] if (ta or tb or tile) else []
+    args += [("i32", int(relu))] + ([("i32", tile)] if tile else [])
     # tiled fast path (any M and N; rows 16-byte aligned) vs guarded kernel, as gemm_fast_fits
     # decides for 16-byte aligned tensors
     lim = 1 << 32
@@ -158,11 +258,15 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     # CUs) would be busy (gemm_fast_tile_extent); LDS max(4-stage ring, bf16 C tile) + bias:
     # 256: max(131072, 256 x 528) + 1024, 128: max(65536, 128 x 272) + 512
     if full:
-        t = 128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256
+        t = tile or (128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256)
         launch = HipLaunch((_cdiv(M, t) * _cdiv(N, t), 1, 1), (256, 1, 1), 136192 if t == 256 else 66048)
     else:
+        if tile == 128:
+            raise HipLoweringError(f"GEMM tile 128 needs the tiled kernel; M={M} N={N} K={K} (transpose_a={ta}, "
+                                   f"transpose_b={tb}) runs the guarded kernel, whose tiles are 256x256")
         launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 147456)
-    kid = "ihip_gemm_bf16_bias_relu_t" if (ta or tb) else "ihip_gemm_bf16_bias_relu"
+    kid = ("ihip_gemm_bf16_bias_relu_ex" if tile else "ihip_gemm_bf16_bias_relu_t" if (ta or tb)
+           else "ihip_gemm_bf16_bias_relu")
     return HipLoweredKernel(c.fn.name, kid, c.io(names), launch, [oname], dict(c.b), tuple(args))
 
 
@@ -227,8 +331,12 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
     if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
         raise HipLoweringError("HIP softmax takes f32 input and output")
     M, N = c.rows(x)
-    if N % 4 == 0 and N <= 4096:  # a wave per row, 4 rows per workgroup
-        launch = _row_launch(M)
+    rows = c.knobs.rows_per_wg()
+    if rows > 1 and not (N % 4 == 0 and N <= 4096):
+        raise HipLoweringError(f"{rows} rows per workgroup needs the one-wave-per-row softmax (N % 4 == 0, "
+                               f"N <= 4096); N = {N} runs one row per workgroup")
+    if N % 4 == 0 and N <= 4096:  # a wave per row, 4 rows per workgroup unless a knob says otherwise
+        launch = _row_launch(M, rows or 4)
     elif N % 4 == 0 and N <= 65536:  # kW waves per row, one row per workgroup, partials in LDS
         kw = next(w for w in (2, 4, 8, 16) if N // 4 <= 1024 * w)
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
@@ -238,8 +346,11 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw if (kw > 1 or N > 1024) else 0)
     else:
         launch = HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
-    return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b),
-                            (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N)))
+    args = (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N))
+    if rows:
+        return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32_ex", c.io([x, oname]), launch, [oname], dict(c.b),
+                                args + (("i32", rows),))
+    return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b), args)
 
 
 def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
@@ -273,10 +384,14 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     for n in (x, w, b, y):
         if c.dtype(n) != "f16":
             raise HipLoweringError(f"HIP LayerNorm takes f16 x, w, b, y; {n} is {c.dtype(n)}")
+    for n in (w, b):  # the kernel reads N elements of each; a [1] weight would broadcast in numpy
+        if c.shape(n) != (N,):
+            raise HipLoweringError(f"HIP LayerNorm takes w and b of shape [{N}]; {n} is {list(c.shape(n))}")
     for role in ("mean", "rstd"):
         if role in inv and c.dtype(inv[role]) != "f32":
             raise HipLoweringError(f"LayerNorm {role} output must be f32")
-    stat = lambda r: ("tensor", inv[r]) if r in inv else ("scratch_f32", M)  # noqa: E731
+    # statistics that are not outputs are not written (null pointers): no scratch memory
+    stat = lambda r: ("tensor", inv[r]) if r in inv else ("null", None)  # noqa: E731
     args = (("tensor", x), ("tensor", w), ("tensor", b), ("tensor", y), stat("mean"), stat("rstd"), ("i64", M),
             ("i64", N), ("f32", float(env["eps"][1])))
     names = [x, w, b, y] + [inv[r] for r in ("mean", "rstd") if r in inv]
@@ -340,15 +455,32 @@ def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
     if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
         raise HipLoweringError("HIP row reductions take f32 input and output")
     M, N = c.rows(x)
+    args = (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N), ("i32", 0 if kind == "rsum" else 1))
+    segs = reduce_rows_segments(M, N)
+    if segs > 1:  # rows too few for the CUs: S workgroups of 16 waves per row, partials in a workspace
+        launch = HipLaunch((M * segs, 1, 1), (1024, 1, 1), 64)
+        return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32_ws", c.io([x, oname]), launch, [oname], dict(c.b),
+                                args + (("workspace", 4 * M * segs),))
     if N > 0:  # 16-byte body loads (a head and tail of < 4 elements around them when rows are
         # not 16-byte aligned): a wave per row, or 16 waves per row for few long rows
         few_long = M < 2048 and N // 4 > 256
         launch = HipLaunch((max(1, M), 1, 1), (1024 if few_long else 64, 1, 1), 64 if few_long else 0)
     else:
         launch = _row_launch(M)
-    return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b),
-                            (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N),
-                             ("i32", 0 if kind == "rsum" else 1)))
+    return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b), args)
+
+
+def reduce_rows_segments(M: int, N: int) -> int:
+    """Segments per row of the split row reduction (rows.hip reduce_rows_segments): rows below
+    256 are split so that about 512 workgroups run, at most 64 per row, each segment at least
+    4096 16-byte vectors; 1 = no split."""
+    if M <= 0 or M >= 256 or N <= 0:
+        return 1
+    n4 = N // 4
+    s = min(64, _cdiv(512, M))
+    while s > 1 and n4 // s < 4096:
+        s -= 1
+    return s
 
 
 _EW_KINDS = frozenset({"in", "const", "bcast", "transpose", "iota", "cast", "where"}) | frozenset(EW_BINARY) | frozenset(
@@ -428,6 +560,42 @@ def _ew_launch(prog, dtype_of) -> HipLaunch:
     return HipLaunch((gx, max(1, min(rows, 65535, _cdiv(4096, gx))), 1), (256, 1, 1), 0)
 
 
+def call_args_to_json(call_args) -> List[Dict[str, Any]]:
+    """The C argument plan as JSON (element-wise programs spelled out as tables)."""
+    from .ewprogram import EwProgram  # noqa: PLC0415
+
+    out = []
+    for kind, v in call_args:
+        if kind == "tensor":
+            out.append({"kind": kind, "name": v})
+        elif kind == "ew_program":
+            assert isinstance(v, EwProgram)
+            out.append({"kind": kind, "code": [list(ins) for ins in v.code],
+                        "inputs": [{"name": n, "stride": list(st)} for n, st in v.inputs],
+                        "outputs": list(v.outputs), "shape": list(v.shape), "listing": v.listing()})
+        else:
+            out.append({"kind": kind, "value": v})
+    return out
+
+
+def call_args_from_json(plan) -> Tuple[Tuple[str, Any], ...]:
+    """Inverse of ``call_args_to_json``."""
+    from .ewprogram import EwProgram  # noqa: PLC0415
+
+    out: List[Tuple[str, Any]] = []
+    for a in plan:
+        kind = a["kind"]
+        if kind == "tensor":
+            out.append((kind, a["name"]))
+        elif kind == "ew_program":
+            code = tuple((int(op), int(d), int(x), int(y), int(z), float(imm)) for op, d, x, y, z, imm in a["code"])
+            ins = tuple((i["name"], tuple(int(t) for t in i["stride"])) for i in a["inputs"])
+            out.append((kind, EwProgram(code, ins, tuple(a["outputs"]), tuple(int(d) for d in a["shape"]))))
+        else:
+            out.append((kind, a["value"]))
+    return tuple(out)
+
+
 _MATCHERS = (_match_gemm, _match_reduce_any, _match_softmax, _match_layernorm, _match_gelu_axpy, _match_row_reduce,
              _match_elementwise)
 
@@ -456,8 +624,13 @@ def lower_intent_to_hip_kernel(intent, *, shape_bindings: Mapping[str, Any],
     for m in _MATCHERS:
         k = m(ctx)
         if k is not None:
+            ctx.knobs.check_used(k.kernel_id)
+            # the argument plan also travels in io_spec (as the reference's io_spec carries its
+            # host_launch), so run_hip_kernel needs only the reference's arguments
+            k.io_spec["hip_call"] = call_args_to_json(k.call_args)
             return k
     raise HipLoweringError(f"HIP lowering unsupported for intent: name={fn.name} ops={sorted({o.op for o in fn.ops})}")
 
 
-__all__ = ["HipLoweringError", "HipLaunch", "HipLoweredKernel", "lower_intent_to_hip_kernel"]
+__all__ = ["HipLoweringError", "HipLaunch", "HipLoweredKernel", "KNOBS", "call_args_from_json", "call_args_to_json",
+           "lower_intent_to_hip_kernel", "reduce_rows_segments"]

@@ -41,11 +41,15 @@ SIGNATURES: Dict[str, Tuple[Any, Tuple[Any, ...]]] = {
     "ihip_reduce_any_rows_f32": (_I32, (_P, _P, _I64, _I64, _F32, _P)),
     "ihip_reduce_any_rows_u8": (_I32, (_P, _P, _I64, _I64, _P)),
     "ihip_reduce_rows_f32": (_I32, (_P, _P, _I64, _I64, _I32, _P)),
+    "ihip_reduce_rows_f32_workspace_size": (_I64, (_I64, _I64)),
+    "ihip_reduce_rows_f32_ws": (_I32, (_P, _P, _I64, _I64, _I32, _P, _I64, _P)),
     "ihip_softmax_rows_f32": (_I32, (_P, _P, _I64, _I64, _P)),
+    "ihip_softmax_rows_f32_ex": (_I32, (_P, _P, _I64, _I64, _I32, _P)),
     "ihip_layernorm_rows_f16": (_I32, (_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _P)),
     "ihip_bias_gelu_tanh_axpy_bf16": (_I32, (_P, _P, _P, _I64, _I64, _F32, _P)),
     "ihip_gemm_bf16_bias_relu": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _P)),
     "ihip_gemm_bf16_bias_relu_t": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _P)),
+    "ihip_gemm_bf16_bias_relu_ex": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P)),
     "ihip_elementwise_program": (_I32, (_P, _I32, _P, _I32, _P, _I32, _P, _I32, _P)),
     "ihip_elementwise_mode": (_I32, (_I32,)),
     "ihip_elementwise_prepare": (_I32, (_P, _I32, _P, _I32, _P, _I32)),
@@ -85,7 +89,9 @@ def ew_program_args(prog, ptrs: Mapping[str, int], dtypes: Mapping[str, str]) ->
     return [ctypes.cast(code, _P), _I32(len(prog.code)), ctypes.cast(ins, _P), _I32(len(prog.inputs)),
             ctypes.cast(outs, _P), _I32(len(prog.outputs)), ctypes.cast(shape, _P), _I32(len(prog.shape)),
             (code, ins, outs, shape)]
-ABI_VERSION = 1
+
+
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -173,14 +179,16 @@ def _check_buffer(name: str, t, dtype: str, shape: Sequence[int]) -> None:
         raise HipRuntimeError(f"{name}: tensor must be contiguous")
 
 
-def _ctype_args(call_args: Iterable[Tuple[str, Any]], buffers: Mapping[str, Any], scratch: list,
-                dtypes: Optional[Mapping[str, str]] = None):
-    torch = _torch()
+def _ctype_args(call_args: Iterable[Tuple[str, Any]], buffers: Mapping[str, Any], keep: list,
+                dtypes: Optional[Mapping[str, str]] = None, stream=None):
+    """ctypes arguments of a lowered call.  A workspace is a fresh torch allocation marked as used
+    by ``stream`` (record_stream), so the caching allocator does not hand it out again before the
+    kernels reading it have run: no host synchronisation is needed."""
     out = []
     for kind, v in call_args:
         if kind == "ew_program":
             args = ew_program_args(v, {n: buffers[n].data_ptr() for n in buffers}, dtypes or {})
-            scratch.append(args.pop())  # keep the ctypes arrays alive through the call
+            keep.append(args.pop())  # keep the ctypes arrays alive through the call
             out.extend(args)
         elif kind == "tensor":
             out.append(_P(buffers[v].data_ptr()))
@@ -192,10 +200,13 @@ def _ctype_args(call_args: Iterable[Tuple[str, Any]], buffers: Mapping[str, Any]
             out.append(_F32(float(v)))
         elif kind == "null":
             out.append(_P(None))
-        elif kind == "scratch_f32":
-            t = torch.empty(max(1, int(v)), dtype=torch.float32, device="cuda")
-            scratch.append(t)
-            out.append(_P(t.data_ptr()))
+        elif kind == "workspace":
+            torch = _torch()
+            t = torch.empty(max(1, int(v)), dtype=torch.uint8, device="cuda")
+            if stream is not None:
+                t.record_stream(stream)
+            keep.append(t)
+            out.extend([_P(t.data_ptr()), _I64(int(v))])
         else:
             raise HipRuntimeError(f"unknown call argument kind {kind}")
     return out
@@ -218,19 +229,27 @@ def launch_lowered(lowered, buffers: Mapping[str, Any], stream=None) -> None:
             raise HipRuntimeError(f"missing buffer for {n}")
         _check_buffer(n, buffers[n], spec["dtype"], shapes[n])
     s = stream if stream is not None else torch.cuda.current_stream()
-    scratch: list = []
+    keep: list = []  # host-side ctypes arrays of an element-wise program (copied at launch)
     dtypes = {n: spec["dtype"] for n, spec in lowered.io_spec["tensors"].items()}
-    args = _ctype_args(lowered.call_args, buffers, scratch, dtypes)
+    args = _ctype_args(lowered.call_args, buffers, keep, dtypes, s)
     call(lowered.kernel_id, *args, _P(s.cuda_stream))
-    if any(isinstance(t, torch.Tensor) for t in scratch):
-        s.synchronize()  # device temporaries must outlive the kernel (host arrays are copied at launch)
 
 
 def run_hip_kernel(*, kernel_name: str, kernel_id: str, io_spec: Mapping[str, Any], launch: Any,
                    bindings: Mapping[str, Any], inputs_np: Mapping[str, np.ndarray], output_names: Iterable[str],
-                   call_args: Sequence[Tuple[str, Any]]) -> Dict[str, np.ndarray]:
-    """Allocate, copy inputs, launch, synchronise, and return inputs + outputs as numpy."""
+                   call_args: Optional[Sequence[Tuple[str, Any]]] = None) -> Dict[str, np.ndarray]:
+    """Allocate, copy inputs, launch, synchronise, and return inputs + outputs as numpy.
+
+    Called like the reference's ``run_cuda_kernel`` (its ``cuda_src`` replaced by
+    ``kernel_id``).  The argument plan comes from ``io_spec["hip_call"]``, which the
+    lowering writes; ``call_args`` (``HipLoweredKernel.call_args``) overrides it."""
     torch = _torch()
+    if call_args is None:
+        if "hip_call" not in io_spec:
+            raise HipRuntimeError(f"io_spec of {kernel_name} carries no hip_call plan and no call_args were given")
+        from .lowering import call_args_from_json  # noqa: PLC0415
+
+        call_args = call_args_from_json(io_spec["hip_call"])
     shapes = tensor_shapes(io_spec, bindings)
     outs = list(output_names)
     buffers: Dict[str, Any] = {}

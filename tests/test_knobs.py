@@ -1,0 +1,138 @@
+"""Schedule knobs and the reference-shaped runtime call — CPU only (lowering, no launches).
+
+The reference steers launch shapes with ``CUDA_RESPECT_SCHEDULE`` (a schedule override
+is authoritative, a recovered schedule only a hint) and with knobs carried in the
+bindings (backends/cuda/codegen/intentir_to_cuda.py:1012,1175-1200,2074-2097).  Here
+each knob either selects one of the precompiled variants or raises HipLoweringError.
+"""
+
+from __future__ import annotations
+
+import inspect
+import json
+
+import pytest
+
+from intent_ir_amd import HipLoweringError, lower_intent_to_hip_kernel
+from intent_ir_amd.configs import WORKLOADS
+from intent_ir_amd.lowering import call_args_from_json
+from intent_ir_amd.runtime import run_hip_kernel
+from tests.ew_cases import CASES as EW_CASES
+
+GEMM_B = {"M": 1024, "N": 1024, "K": 512}  # 16 tiles of 256x256: the automatic choice is 128x128
+
+
+def test_gemm_tile_binding_knob():
+    ir = WORKLOADS["matmul"].ir()
+    auto = lower_intent_to_hip_kernel(ir, shape_bindings=GEMM_B)
+    assert auto.kernel_id == "ihip_gemm_bf16_bias_relu" and auto.launch.grid[0] == 64
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 256})
+    assert k.kernel_id == "ihip_gemm_bf16_bias_relu_ex"
+    assert k.call_args[-3:] == (("i32", 0), ("i32", 1), ("i32", 256))  # transpose_b, relu, tile
+    assert k.launch.grid[0] == 16 and k.launch.lds_bytes == 136192
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 128})
+    assert k.call_args[-1] == ("i32", 128) and k.launch.grid[0] == 64 and k.launch.lds_bytes == 66048
+    with pytest.raises(HipLoweringError, match="is not one of"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 64})
+
+
+def test_gemm_tile_from_an_authoritative_schedule():
+    ir = WORKLOADS["matmul"].ir()
+    k = lower_intent_to_hip_kernel(ir, shape_bindings=GEMM_B,
+                                   schedule_override={"tile_m": 256, "tile_n": 256, "tile_k": 32, "pipeline_depth": 4})
+    assert k.call_args[-1] == ("i32", 256) and k.bindings["HIP_RESPECT_SCHEDULE"] == 1
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "T": 128}, schedule_override={"tile_m": "T"})
+    assert k.call_args[-1] == ("i32", 128)
+    # the binding knob overrides the schedule's tile, as the reference's tuning knobs do
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 128},
+                                   schedule_override={"tile_m": 256, "tile_n": 256})
+    assert k.call_args[-1] == ("i32", 128)
+    for sched, msg in (({"tile_m": 64}, "not available"), ({"tile_m": 128, "tile_n": 256}, "square"),
+                       ({"tile_k": 64}, "not available"), ({"pipeline_depth": 2}, "not available"),
+                       ({"tile_m": "NOPE"}, "names no integer binding")):
+        with pytest.raises(HipLoweringError, match=msg):
+            lower_intent_to_hip_kernel(ir, shape_bindings=GEMM_B, schedule_override=sched)
+
+
+def test_recovered_schedule_is_a_hint_unless_respected():
+    """The IR's own schedule (tile_m=32, ...) is ignored by default, authoritative on request."""
+    ir = WORKLOADS["matmul"].ir()
+    assert ir["schedule"]["tile_m"] == 32
+    assert lower_intent_to_hip_kernel(ir, shape_bindings=GEMM_B).kernel_id == "ihip_gemm_bf16_bias_relu"
+    with pytest.raises(HipLoweringError, match="not available"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_RESPECT_SCHEDULE": 1})
+
+
+def test_gemm_tile_128_needs_the_tiled_kernel():
+    ir = WORKLOADS["matmul"].ir()
+    b = {"M": 64, "N": 263, "K": 64}  # N % 8 != 0 with B as [K, N]: the guarded kernel
+    assert lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 256}).launch.lds_bytes == 147456
+    with pytest.raises(HipLoweringError, match="guarded"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 128})
+
+
+@pytest.mark.parametrize("rows", [1, 2, 4])
+def test_softmax_rows_per_workgroup_knob(rows):
+    ir = WORKLOADS["softmax"].ir()
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 1000, "N": 1024, "HIP_ROWS_PER_WG": rows})
+    assert k.kernel_id == "ihip_softmax_rows_f32_ex" and k.call_args[-1] == ("i32", rows)
+    assert k.launch.block[0] == 64 * rows and k.launch.grid[0] == -(-1000 // rows)
+    k2 = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 1000, "N": 1024}, schedule_override={"tile_m": rows})
+    assert k2.call_args == k.call_args and k2.launch == k.launch
+
+
+def test_softmax_rows_knob_outside_the_one_wave_form():
+    ir = WORKLOADS["softmax"].ir()
+    with pytest.raises(HipLoweringError, match="one-wave-per-row"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={"M": 8, "N": 8192, "HIP_ROWS_PER_WG": 2})
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 8, "N": 8192, "HIP_ROWS_PER_WG": 1})
+    assert k.call_args[-1] == ("i32", 1)
+    with pytest.raises(HipLoweringError, match="not available"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={"M": 8, "N": 1024}, schedule_override={"tile_m": 16})
+
+
+@pytest.mark.parametrize("key,bindings,msg", [
+    ("softmax", {"HIP_GEMM_TILE": 256}, "does not apply"),
+    ("any", {"HIP_ROWS_PER_WG": 1}, "does not apply"),
+    ("layernorm", {"HIP_GEMM_TILE": 128}, "does not apply"),
+    ("gelu", {"HIP_FOO": 1}, "unknown HIP knob"),
+    ("any", {"HIP_RESPECT_SCHEDULE": 2}, "is not one of"),
+])
+def test_knobs_that_do_not_apply_are_rejected(key, bindings, msg):
+    w = WORKLOADS[key]
+    b = {k: min(v, 64) for k, v in w.bindings.items()}
+    with pytest.raises(HipLoweringError, match=msg):
+        lower_intent_to_hip_kernel(w.ir(), shape_bindings={**b, **bindings})
+
+
+@pytest.mark.parametrize("key", ["any", "layernorm", "gelu"])
+def test_single_schedule_kernels_reject_authoritative_schedules(key):
+    w = WORKLOADS[key]
+    b = {k: min(v, 64) for k, v in w.bindings.items()}
+    with pytest.raises(HipLoweringError, match="single launch schedule"):
+        lower_intent_to_hip_kernel(w.ir(), shape_bindings=b, schedule_override={"tile_m": 16})
+    # an override that sets no field asks for nothing
+    lower_intent_to_hip_kernel(w.ir(), shape_bindings=b, schedule_override={})
+
+
+def _all_lowerings():
+    for key, w in WORKLOADS.items():
+        yield key, lower_intent_to_hip_kernel(w.ir(), shape_bindings={k: min(v, 64) for k, v in w.bindings.items()})
+    for name, ir, bindings, _ in EW_CASES[:6]:
+        yield name, lower_intent_to_hip_kernel(ir, shape_bindings=bindings)
+
+
+def test_call_plan_travels_in_io_spec_as_json():
+    for name, k in _all_lowerings():
+        spec = json.loads(json.dumps(k.io_spec))  # JSON-serialisable as is
+        assert call_args_from_json(spec["hip_call"]) == k.call_args, name
+
+
+def test_run_hip_kernel_takes_the_reference_arguments():
+    """run_cuda_kernel(*, kernel_name, cuda_src, io_spec, launch, bindings, inputs_np, output_names,
+    extra_cuda_cflags=None) (backends/cuda/runtime.py:22-45): the same keywords, cuda_src replaced
+    by kernel_id, and nothing else required."""
+    sig = inspect.signature(run_hip_kernel)
+    required = {n for n, p in sig.parameters.items() if p.default is inspect.Parameter.empty}
+    assert required == {"kernel_name", "kernel_id", "io_spec", "launch", "bindings", "inputs_np", "output_names"}
+    assert all(p.kind is inspect.Parameter.KEYWORD_ONLY for p in sig.parameters.values())

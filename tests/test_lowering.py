@@ -131,11 +131,47 @@ def test_layernorm_chain_with_wrong_divisor_is_rejected():
         lower_intent_to_hip_kernel(ir, shape_bindings={"M": 8, "N": 64})
 
 
-def test_layernorm_without_stat_outputs_uses_scratch():
+def test_layernorm_without_stat_outputs_passes_null_statistics():
+    """Statistics that are not outputs are not written: null pointers, no scratch buffers."""
     ir = WORKLOADS["layernorm"].ir()
     ir["outputs"] = ["out_ptr"]
     k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 8, "N": 64})
-    assert [a for a in k.call_args if a[0] == "scratch_f32"] == [("scratch_f32", 8), ("scratch_f32", 8)]
+    assert k.call_args[4] == ("null", None) and k.call_args[5] == ("null", None)
+    assert set(k.io_spec["tensors"]) == {"in_ptr", "weight_ptr", "bias_ptr", "out_ptr"}
+    ir["outputs"] = ["out_ptr", "out_rstd_ptr"]
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 8, "N": 64})
+    assert k.call_args[4] == ("null", None) and k.call_args[5] == ("tensor", "out_rstd_ptr")
+
+
+def _layernorm_with_scalar_affine():
+    """LN whose weight and bias are [1] tensors broadcast by numpy directly (no broadcast_in_dim)."""
+    ir = WORKLOADS["layernorm"].ir()
+    ir["tensors"]["weight_ptr"]["shape"] = [1]
+    ir["tensors"]["bias_ptr"]["shape"] = [1]
+    ops = [o for o in ir["ops"] if o["op"] != "broadcast_in_dim"]
+    for o in ops:
+        o["inputs"] = ["weight_ptr" if i == "w_b" else "bias_ptr" if i == "b_b" else i for i in o["inputs"]]
+    ir["ops"] = ops
+    for t in ("w_b", "b_b"):
+        del ir["tensors"][t]
+    return ir
+
+
+def test_layernorm_with_scalar_weight_and_bias_is_not_the_row_kernel():
+    """The kernel reads N elements of w and b; [1]-shaped ones would be read out of bounds."""
+    import numpy as np
+
+    from oracle.interpreter import execute_intent
+
+    ir = _layernorm_with_scalar_affine()
+    b = {"M": 4, "N": 64}
+    rng = np.random.default_rng(0)
+    inp = {"in_ptr": rng.standard_normal((4, 64)).astype(np.float32),
+           "weight_ptr": np.array([1.5], np.float32), "bias_ptr": np.array([0.25], np.float32)}
+    out = execute_intent(ir, inp, b)  # the IR is valid: numpy broadcasts the [1] operands
+    assert out["out_ptr"].shape == (4, 64)
+    with pytest.raises(HipLoweringError, match="w and b of shape"):
+        lower_intent_to_hip_kernel(ir, shape_bindings=b)
 
 
 def test_gelu_with_wrong_constant_is_not_gelu():
@@ -212,7 +248,7 @@ def test_unsupported_ops_raise():
 # ---------------------------------------------------------------- C-ABI library
 def _header_symbols():
     text = (ROOT / "include" / "intentir_hip.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(ihip_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(ihip_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_every_runtime_signature():
@@ -226,7 +262,7 @@ def test_library_exports_every_declared_symbol():
     for sym in _header_symbols():
         assert hasattr(lib, sym), sym
     lib.ihip_abi_version.restype = ctypes.c_int
-    assert lib.ihip_abi_version() == 1
+    assert lib.ihip_abi_version() == 2
     lib.ihip_last_error.restype = ctypes.c_char_p
     assert lib.ihip_last_error() == b""
 
@@ -244,3 +280,7 @@ def test_library_rejects_bad_arguments_without_a_device():
     assert st == -1 and b"null" in lib.ihip_last_error()
     st = lib.ihip_reduce_any_rows_f32(None, None, 1 << 62, 1 << 62, 0.0, None)
     assert st == -1  # element count overflows int64
+    st = lib.ihip_softmax_rows_f32_ex(None, None, 0, 8, 3, None)
+    assert st == -1 and b"rows_per_wg 3" in lib.ihip_last_error()
+    st = lib.ihip_gemm_bf16_bias_relu_ex(None, None, None, None, 0, 0, 0, 0, 0, 1, 64, None)
+    assert st == -1 and b"tile 64" in lib.ihip_last_error()
