@@ -76,6 +76,16 @@ int64_t ihip_reduce_rows_f32_workspace_size(int64_t M, int64_t N);
 int ihip_reduce_rows_f32_ws(const float* x, float* out, int64_t M, int64_t N, int kind, void* workspace,
                             int64_t workspace_bytes, void* stream);
 
+/* ihip_reduce_rows_f32_ws without a workspace argument and without any allocation: no
+ * counterpart in the reference; it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The row-split partials go
+ * to a fixed 64 KiB scratch array in device memory that each GPU holds until the process
+ * ends; every call on one GPU shares it, so calls that overlap on one GPU (concurrent
+ * streams, threads) race and must be serialised by the caller.  Shapes whose split needs
+ * more than 64 KiB are rejected (IHIP_ERR_INVALID_ARG); the split rule keeps every shape
+ * within it.  Results are identical to ihip_reduce_rows_f32_ws. */
+int ihip_reduce_rows_f32_noalloc(const float* x, float* out, int64_t M, int64_t N, int kind, void* stream);
+
 /* y = softmax(x) over the last axis, x and y f32 [M, N] (y may not alias x).
  * Replaces _kernel_softmax_2d_last_f32 (backends/cuda/codegen/intentir_to_cuda.py:1103-1247)
  * and its device templates (backends/cuda/runtime/kernels/softmax.cuh:92-663). */

@@ -12,6 +12,7 @@
 #include <stdio.h>
 
 #include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/intentir_hip.h"
@@ -40,7 +41,36 @@ bool prepare_elementwise_jit_operands(const ihip_ew_instr*, int, const ihip_ew_o
                                       int, const int64_t (&)[4], std::string*);
 }  // namespace ihip
 
+// Scratch of ihip_reduce_rows_f32_noalloc: the row-split partials (M * S floats; the split
+// rule gives M < 256 and S <= 64, so at most 255 * 64).  Each GPU the library runs on holds
+// its own copy until the process ends.  In host code `scratch` is only a symbol handle: its
+// device address comes from hipGetSymbolAddress, per device, and only that address is ever
+// passed to kernels.
+static constexpr int64_t kScratchFloats = 256 * 64;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch, resolved on the first call on that device.
+hipError_t scratch_address(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
 
 thread_local char g_last_error[512] = "";
 std::atomic<int> g_ew_mode{IHIP_EW_MODE_AUTO};
@@ -199,6 +229,23 @@ int ihip_reduce_rows_f32_ws(const float* x, float* out, int64_t M, int64_t N, in
 
 int ihip_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, void* stream) {
   return ihip_reduce_rows_f32_ws(x, out, M, N, kind, nullptr, 0, stream);
+}
+
+int ihip_reduce_rows_f32_noalloc(const float* x, float* out, int64_t M, int64_t N, int kind, void* stream) {
+  const int bad = check_reduce_rows("reduce_rows_f32_noalloc", x, out, M, N, kind);
+  if (bad) return bad;
+  const int64_t need = ihip_reduce_rows_f32_workspace_size(M, N);
+  IHIP_REQUIRE(need <= kScratchFloats * static_cast<int64_t>(sizeof(float)),
+               "reduce_rows_f32_noalloc: [%lld, %lld] needs %lld bytes of scratch, the maximum is %lld",
+               (long long)M, (long long)N, (long long)need, (long long)(kScratchFloats * sizeof(float)));
+  float* part = nullptr;
+  if (need > 0) {  // every partial is written before it is read: nothing to clear
+    const hipError_t e = scratch_address(&part);
+    if (e != hipSuccess) return fail(static_cast<int>(e), "reduce_rows_f32_noalloc: scratch address: %s",
+                                     hipGetErrorString(e));
+  }
+  return finish(ihip::launch_reduce_rows_f32(x, out, M, N, kind, part, static_cast<hipStream_t>(stream)),
+                "reduce_rows_f32_noalloc");
 }
 
 int ihip_softmax_rows_f32_ex(const float* x, float* y, int64_t M, int64_t N, int rows_per_wg, void* stream) {
