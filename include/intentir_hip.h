@@ -224,6 +224,16 @@ int ihip_elementwise_program(const ihip_ew_instr* code, int32_t n_code, const ih
                              int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs,
                              const int64_t* shape, int32_t rank, void* stream);
 
+/* The HIP C++ source that ihip_elementwise_program compiles for exactly this launch (same
+ * arguments, without the stream): the role of the reference lowering's cuda_src
+ * (backends/cuda/codegen/intentir_to_cuda.py:27-35).  Needs no device: pointers are only
+ * inspected for their alignment.  *src_len (when not NULL) receives the source length in
+ * bytes; when buf_len > 0 the source is copied to buf, truncated to buf_len - 1 bytes and
+ * NUL-terminated.  Returns IHIP_OK or an argument error as ihip_elementwise_program. */
+int ihip_elementwise_source(const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,
+                            int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs, const int64_t* shape,
+                            int32_t rank, char* buf, int64_t buf_len, int64_t* src_len);
+
 /* How ihip_elementwise_program executes a program (process-wide):
  *  AUTO   - native code specialised for the program and its operand types, compiled with
  *           hiprtc on first use and cached (per device) for the life of the process; the

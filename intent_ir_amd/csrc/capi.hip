@@ -10,6 +10,7 @@
 //    the message of the calling thread's last failure.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
 
 #include <atomic>
 #include <mutex>
@@ -39,6 +40,8 @@ hipError_t launch_elementwise_jit(const ihip_ew_instr*, int, const ihip_ew_opera
 bool prepare_elementwise_jit(const ihip_ew_instr*, int, int, const int*, int, const int*, std::string*);
 bool prepare_elementwise_jit_operands(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*,
                                       int, const int64_t (&)[4], std::string*);
+std::string source_elementwise_jit_operands(const ihip_ew_instr*, int, const ihip_ew_operand*, int,
+                                            const ihip_ew_operand*, int, const int64_t (&)[4]);
 }  // namespace ihip
 
 // Scratch of ihip_reduce_rows_f32_noalloc: the row-split partials (M * S floats; the split
@@ -405,6 +408,28 @@ int ihip_elementwise_prepare_operands(const ihip_ew_instr* code, int32_t n_code,
   if (total != 0 &&
       !ihip::prepare_elementwise_jit_operands(code, n_code, inputs, n_inputs, outputs, n_outputs, sh, &why))
     return fail(static_cast<int>(hipErrorNotSupported), "elementwise_prepare_operands: %s", why.c_str());
+  g_last_error[0] = '\0';
+  return IHIP_OK;
+}
+
+int ihip_elementwise_source(const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,
+                            int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs, const int64_t* shape,
+                            int32_t rank, char* buf, int64_t buf_len, int64_t* src_len) {
+  int64_t sh[4], total = 0;
+  const int bad = check_ew_launch("elementwise_source", code, n_code, inputs, n_inputs, outputs, n_outputs, shape,
+                                  rank, sh, &total);
+  if (bad) return bad;
+  IHIP_REQUIRE(buf_len >= 0 && (buf_len == 0 || buf != nullptr), "elementwise_source: buffer of %lld bytes is null",
+               (long long)buf_len);
+  const std::string src =
+      total == 0 ? std::string() : ihip::source_elementwise_jit_operands(code, n_code, inputs, n_inputs, outputs,
+                                                                         n_outputs, sh);
+  if (src_len != nullptr) *src_len = static_cast<int64_t>(src.size());
+  if (buf_len > 0) {
+    const size_t n = src.size() < static_cast<size_t>(buf_len - 1) ? src.size() : static_cast<size_t>(buf_len - 1);
+    memcpy(buf, src.data(), n);
+    buf[n] = '\0';
+  }
   g_last_error[0] = '\0';
   return IHIP_OK;
 }

@@ -86,6 +86,22 @@ __device__ __forceinline__ float ew_div(float x, float y) {
   const float q = ew_div_fast(x, y, bad);
   return bad ? x / y : q;
 }
+// x / (exp(u) + 1), the logistic shape of GELU-tanh and sigmoid, in one pass: the same head +
+// tail exp, the same reciprocal and Newton step as ew_exp and ew_div_fast, so the value is
+// bit-identical to the unfused chain wherever this form is taken; but for u <= 80 the exp
+// cannot overflow and the reciprocal of e + 1 (in [1.8e-35, 1]) is finite and non-zero, so
+// only the quotient needs checking.  `bad` (u > 80, u NaN or -inf, a non-finite quotient)
+// sends the vector to the unfused chain.
+__device__ __forceinline__ float ew_logistic_div_fast(float x, float u, bool& bad) {
+  const float t = u * 1.44269502f;
+  const float tail = __builtin_fmaf(u, 1.92596303e-08f, __builtin_fmaf(u, 1.44269502f, -t));
+  const float e = __builtin_amdgcn_exp2f(t);
+  const float d = __builtin_fmaf(e, tail * 0.693147182f, e) + 1.0f;
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float q = x * r;
+  bad |= !(u <= 80.0f) || !__builtin_isfinite(q);
+  return __builtin_fmaf(__builtin_fmaf(-d, q, x), r, q);
+}
 // 1/sqrt(x) as v_rsq_f32 and one Newton step r + r/2 (1 - x r^2); `bad` as for division.
 __device__ __forceinline__ float ew_rsqrt_fast(float x, bool& bad) {
   const float r = __builtin_amdgcn_rsqf(x);
@@ -280,6 +296,75 @@ int ew_jit_width(int n_inputs, const int* in_dt, int n_outputs, const int* out_d
 
 static bool is_tiled(char kind) { return kind == 'v' || kind == 't'; }
 
+// Registers an instruction reads (up to 3) and the one it writes (-1 for a store).
+static int ew_reads(const ihip_ew_instr& in, int (&r)[3]) {
+  switch (in.op) {
+    case IHIP_EW_LOAD: case IHIP_EW_IMM: case IHIP_EW_IOTA: return 0;
+    case IHIP_EW_STORE: r[0] = in.a; return 1;
+    case IHIP_EW_WHERE: r[0] = in.a; r[1] = in.b; r[2] = in.c; return 3;
+    default:
+      r[0] = in.a;
+      if (in.op >= IHIP_EW_ADD && in.op <= IHIP_EW_OR) {
+        r[1] = in.b;
+        return 2;
+      }
+      return 1;
+  }
+}
+static int ew_writes(const ihip_ew_instr& in) { return in.op == IHIP_EW_STORE ? -1 : in.dst; }
+
+// Index of the instruction that last wrote register reg before pc, or -1.
+static int ew_last_writer(const ihip_ew_instr* code, int pc, int reg) {
+  for (int k = pc - 1; k >= 0; --k)
+    if (ew_writes(code[k]) == reg) return k;
+  return -1;
+}
+
+// True when the value instruction w writes is read by instruction `only` and no other, before
+// the register is written again.
+static bool ew_single_use(const ihip_ew_instr* code, int n_code, int w, int only) {
+  const int reg = ew_writes(code[w]);
+  for (int k = w + 1; k < n_code; ++k) {
+    int r[3];
+    const int nr = ew_reads(code[k], r);
+    for (int i = 0; i < nr; ++i)
+      if (r[i] == reg && k != only) return false;
+    if (ew_writes(code[k]) == reg) return true;
+  }
+  return true;
+}
+
+// Logistic fusion plan: DIV(x, ADD(EXP(u), IMM 1.0)) with the exp and the add feeding only
+// the division and u unchanged until it becomes x / (exp(u) + 1) in one step.  fuse_u[pc] = u's
+// register at the division (-1 elsewhere); skip[pc] marks the exp and add it absorbs.
+static void ew_plan_logistic(const ihip_ew_instr* code, int n_code, int* fuse_u, bool* skip) {
+  for (int pc = 0; pc < n_code; ++pc) fuse_u[pc] = -1, skip[pc] = false;
+  for (int pd = 0; pd < n_code; ++pd) {
+    const ihip_ew_instr& dv = code[pd];
+    if (dv.op != IHIP_EW_DIV || dv.a == dv.b) continue;
+    const int pa = ew_last_writer(code, pd, dv.b);
+    if (pa < 0 || code[pa].op != IHIP_EW_ADD || skip[pa] || !ew_single_use(code, n_code, pa, pd)) continue;
+    for (int order = 0; order < 2; ++order) {
+      const int re = order ? code[pa].b : code[pa].a, ro = order ? code[pa].a : code[pa].b;
+      if (re == ro) continue;
+      const int pe = ew_last_writer(code, pa, re), po = ew_last_writer(code, pa, ro);
+      if (pe < 0 || po < 0 || code[pe].op != IHIP_EW_EXP || skip[pe]) continue;
+      if (code[po].op != IHIP_EW_IMM || __builtin_bit_cast(uint32_t, code[po].imm) != 0x3f800000u) continue;
+      if (!ew_single_use(code, n_code, pe, pa)) continue;
+      // u still holds its value at the division: the skipped exp and add write nothing (their
+      // values have no other reader), so only the instructions in between may not write u
+      const int u = code[pe].a;
+      bool kept = true;
+      for (int k = pe + 1; k < pd && kept; ++k)
+        if (k != pa) kept = ew_writes(code[k]) != u;
+      if (!kept || dv.a == re) continue;
+      fuse_u[pd] = u;
+      skip[pe] = skip[pa] = true;
+      break;
+    }
+  }
+}
+
 // Program body: the instruction list as straight-line code over r[8][EW_V].  Inputs and
 // outputs are accessed in their form (in_kind / out_kind, see ldk); in the tiled form
 // (`tiled`) staged inputs ('v', 't') are read from their LDS tile (slot = their rank among
@@ -287,8 +372,20 @@ static bool is_tiled(char kind) { return kind == 'v' || kind == 't'; }
 static std::string ew_jit_body(const ihip_ew_instr* code, int n_code, const int* in_dt, const int* out_dt,
                                const char* in_kind, const char* out_kind, bool tiled, const char* ind) {
   std::string s;
+  int fuse_u[IHIP_EW_MAX_CODE];
+  bool skip[IHIP_EW_MAX_CODE];
+  ew_plan_logistic(code, n_code, fuse_u, skip);
   for (int pc = 0; pc < n_code; ++pc) {
     const ihip_ew_instr& in = code[pc];
+    if (skip[pc]) continue;
+    if (fuse_u[pc] >= 0) {  // x / (exp(u) + 1): one fast pass, the unfused chain where it does not hold
+      const std::string xs = fmt(" const float x = r[%d][j]; const float u = r[%d][j];", in.a, fuse_u[pc]);
+      s += fmt("%s{ float t[EW_V]; bool bad = false; for (int j = 0; j < EW_V; ++j) {%s t[j] = "
+               "ew_logistic_div_fast(x, u, bad); } if (bad) for (int j = 0; j < EW_V; ++j) {%s t[j] = "
+               "ew_div(x, ew_exp(u) + 1.0f); } for (int j = 0; j < EW_V; ++j) r[%d][j] = t[j]; }\n",
+               ind, xs.c_str(), xs.c_str(), in.dst);
+      continue;
+    }
     switch (in.op) {
       case IHIP_EW_LOAD:
         if (tiled && is_tiled(in_kind[in.a])) {
@@ -628,6 +725,15 @@ bool prepare_elementwise_jit_operands(const ihip_ew_instr* code, int n_code, con
   JitPlan pl;
   if (!plan_jit(code, n_code, inputs, n_inputs, outputs, n_outputs, shape, pl)) return true;
   return compile_checked(pl.src, why);
+}
+
+// The source that launch_elementwise_jit would compile for these operands and shape ("" when
+// the launch is empty); no device is needed.
+std::string source_elementwise_jit_operands(const ihip_ew_instr* code, int n_code, const ihip_ew_operand* inputs,
+                                            int n_inputs, const ihip_ew_operand* outputs, int n_outputs,
+                                            const int64_t (&shape)[4]) {
+  JitPlan pl;
+  return plan_jit(code, n_code, inputs, n_inputs, outputs, n_outputs, shape, pl) ? pl.src : std::string();
 }
 
 // Launch the specialised kernel of a validated program; compiles on first use.  Returns

@@ -799,6 +799,145 @@ __global__ __launch_bounds__(64 * kWaves) void layernorm_rows_f16_multi(
   }
 }
 
+// Halves h .. h+7 (h < 8) of the 16 halves in (lo, hi), branch-free: dword q + i of the eight
+// (q = h / 2) is selected in two stages (offset by 2 dwords when q & 2, then by 1 when q & 1;
+// h is uniform per row, so the selects are too), and adjacent dwords are joined with
+// v_alignbit by 16 bits when h is odd (by 0 bits, i.e. unchanged, when it is even).
+// (Named scalars, not an array: with an array the compiler indexed it in scratch memory.)
+__device__ __forceinline__ u32x4 halves_from(const u32x4& lo, const u32x4& hi, int h) {
+  const bool by2 = (h & 4) != 0, by1 = (h & 2) != 0;
+  const uint32_t e0 = by2 ? lo.z : lo.x, e1 = by2 ? lo.w : lo.y, e2 = by2 ? hi.x : lo.z;
+  const uint32_t e3 = by2 ? hi.y : lo.w, e4 = by2 ? hi.z : hi.x, e5 = by2 ? hi.w : hi.y;
+  const uint32_t f0 = by1 ? e1 : e0, f1 = by1 ? e2 : e1, f2 = by1 ? e3 : e2, f3 = by1 ? e4 : e3, f4 = by1 ? e5 : e4;
+  const uint32_t r = (h & 1) ? 16u : 0u;
+  return u32x4{__builtin_amdgcn_alignbit(f1, f0, r), __builtin_amdgcn_alignbit(f2, f1, r),
+               __builtin_amdgcn_alignbit(f3, f2, r), __builtin_amdgcn_alignbit(f4, f3, r)};
+}
+
+// Elements e0 .. e0+7 of a 16-byte aligned f16 vector v of n elements, e0 = 8k + h (h < 8), read
+// as the aligned 16-byte vectors k and k+1 (the second only when h > 0; element-wise past n).
+__device__ __forceinline__ f16x8_t f16x8_at(const uint16_t* __restrict__ v, int64_t n, int64_t k, int h) {
+  const u32x4* v8 = reinterpret_cast<const u32x4*>(v);
+  const u32x4 lo = v8[k];
+  if (h == 0) return __builtin_bit_cast(f16x8_t, lo);
+  u32x4 hi;
+  if (8 * k + 16 <= n) {
+    hi = v8[k + 1];
+  } else {
+    uint16_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = 8 * k + 8 + j < n ? v[8 * k + 8 + j] : uint16_t(0);
+    hi = u32x4{e[0] | (uint32_t(e[1]) << 16), e[2] | (uint32_t(e[3]) << 16), e[4] | (uint32_t(e[5]) << 16),
+               e[6] | (uint32_t(e[7]) << 16)};
+  }
+  return __builtin_bit_cast(f16x8_t, halves_from(lo, hi, h));
+}
+
+// Rows that do not all start 16-byte aligned (N % 8 != 0), N <= 4096 * kW, with x and y
+// sharing their alignment modulo 16 bytes: one row per workgroup of kW waves.  Each row splits
+// into a head of h < 8 halves (up to its first 16-byte boundary), nb 16-byte aligned vectors
+// held in registers (vector k on wave k / 64 % kW, as in the multi-wave form) and a tail of
+// t < 8 halves; thread j < h holds head element j, thread j < t tail element j, so the row is
+// read from HBM once.  w and b stay in L2, shared by every row: kAlignedWB (w and b 16-byte aligned) reads them as aligned 16-byte vectors
+// realigned to the row's head (f16x8_at), otherwise element by element.  Same op order and
+// precision as the vector forms: f32 statistics, two-pass centred variance,
+// y = (d * rstd) * w + b as one FMA, rounded to f16.  Every access is bounded by the row: body
+// vector k < nb covers elements h + 8k .. h + 8k + 7 < h + 8nb <= N.
+template <int kVpl, int kW, bool kAlignedWB>
+__global__ __launch_bounds__(64 * kW) void layernorm_rows_f16_skew(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b,
+    uint16_t* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t M, int64_t N,
+    float eps) {
+  __shared__ float part_s[kW], part_q[kW];
+  const int lane = threadIdx.x & 63, v = threadIdx.x >> 6, tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  if (row >= M) return;  // uniform per workgroup
+  const uint16_t* xr = x + row * N;
+  uint16_t* yr = y + row * N;
+  const int64_t to_edge = (8 - ((reinterpret_cast<uintptr_t>(xr) >> 1) & 7)) & 7;
+  const int64_t head = to_edge < N ? to_edge : N;
+  const int64_t nb = (N - head) >> 3;
+  const int64_t tail = N - head - 8 * nb;
+  const int64_t first = v * kWave + lane;  // this lane's first body vector
+  const u32x4* xb = reinterpret_cast<const u32x4*>(xr + head) + first;
+  u32x4* yb = reinterpret_cast<u32x4*>(yr + head) + first;
+  f16x8_t xv[kVpl];
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+    xv[i] = __builtin_bit_cast(f16x8_t, first + i * kWave * kW < nb ? __builtin_nontemporal_load(xb + i * kWave * kW)
+                                                                    : u32x4(0u));
+  const float hx = tid < head ? f16_to_f32(xr[tid]) : 0.0f;
+  const float tx = tid < tail ? f16_to_f32(xr[head + 8 * nb + tid]) : 0.0f;
+  float s = hx + tx;  // padding is +0
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += static_cast<float>(xv[i][j]);
+  s = wave_sum(s);
+  if (kW > 1) {
+    if (lane == 0) part_s[v] = s;
+    __syncthreads();
+    s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kW; ++k) s += part_s[k];
+  }
+  const float mean = s / static_cast<float>(N);
+  float q = 0.f;
+  if (tid < head) q = (hx - mean) * (hx - mean);
+  if (tid < tail) q = __builtin_fmaf(tx - mean, tx - mean, q);
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const bool in = first + i * kWave * kW < nb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float d = static_cast<float>(xv[i][j]) - mean;
+      q = __builtin_fmaf(d, in ? d : 0.f, q);
+    }
+  }
+  q = wave_sum(q);
+  if (kW > 1) {
+    if (lane == 0) part_q[v] = q;
+    __syncthreads();
+    q = 0.f;
+#pragma unroll
+    for (int k = 0; k < kW; ++k) q += part_q[k];
+  }
+  const float rstd = 1.0f / sqrtf(q / static_cast<float>(N) + eps);
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const int64_t k = first + i * kWave * kW;
+    if (k < nb) {
+      f16x8_t wv, bv;
+      if (kAlignedWB) {
+        wv = f16x8_at(w, N, k, static_cast<int>(head));
+        bv = f16x8_at(b, N, k, static_cast<int>(head));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          wv[j] = __builtin_bit_cast(_Float16, w[head + 8 * k + j]);
+          bv[j] = __builtin_bit_cast(_Float16, b[head + 8 * k + j]);
+        }
+      }
+      f16x8_t o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float d = static_cast<float>(xv[i][j]) - mean;
+        o[j] = static_cast<_Float16>(__builtin_fmaf(d * rstd, static_cast<float>(wv[j]), static_cast<float>(bv[j])));
+      }
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), yb + i * kWave * kW);
+    }
+  }
+  if (tid < head) yr[tid] = f32_to_f16_rne(__builtin_fmaf((hx - mean) * rstd, f16_to_f32(w[tid]), f16_to_f32(b[tid])));
+  if (tid < tail) {
+    const int64_t e = head + 8 * nb + tid;
+    yr[e] = f32_to_f16_rne(__builtin_fmaf((tx - mean) * rstd, f16_to_f32(w[e]), f16_to_f32(b[e])));
+  }
+  if (tid == 0) {
+    if (mean_out != nullptr) mean_out[row] = mean;
+    if (rstd_out != nullptr) rstd_out[row] = rstd;
+  }
+}
+
 // Any N: one workgroup per row, three passes over the row.
 __global__ __launch_bounds__(256) void layernorm_rows_f16_any(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                               const uint16_t* __restrict__ b, uint16_t* __restrict__ y,
@@ -849,6 +988,24 @@ static void launch_layernorm_multi(const u32x4* x8, const u32x4* w8, const u32x4
   layernorm_rows_f16_multi<kVpl, kW, kWaves><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, N, eps);
 }
 
+// kW waves per row for rows of at most 4096 * kW + 7 halves: a body of nb <= 512 * kW vectors
+// (8 per lane) plus a head and tail of < 8 each.
+template <bool kAlignedWB>
+static void launch_layernorm_skew(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y, float* mean,
+                                  float* rstd, int64_t M, int64_t N, float eps, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(M));
+  if (N <= 4096 + 7)
+    layernorm_rows_f16_skew<8, 1, kAlignedWB><<<grid, dim3(64), 0, s>>>(x, w, b, y, mean, rstd, M, N, eps);
+  else if (N <= 8192 + 7)
+    layernorm_rows_f16_skew<8, 2, kAlignedWB><<<grid, dim3(128), 0, s>>>(x, w, b, y, mean, rstd, M, N, eps);
+  else if (N <= 16384 + 7)
+    layernorm_rows_f16_skew<8, 4, kAlignedWB><<<grid, dim3(256), 0, s>>>(x, w, b, y, mean, rstd, M, N, eps);
+  else if (N <= 32768 + 7)
+    layernorm_rows_f16_skew<8, 8, kAlignedWB><<<grid, dim3(512), 0, s>>>(x, w, b, y, mean, rstd, M, N, eps);
+  else
+    layernorm_rows_f16_skew<8, 16, kAlignedWB><<<grid, dim3(1024), 0, s>>>(x, w, b, y, mean, rstd, M, N, eps);
+}
+
 hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y, float* mean,
                                      float* rstd, int64_t M, int64_t N, float eps, hipStream_t s) {
   if (M == 0) return hipSuccess;
@@ -856,6 +1013,18 @@ hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const
   const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                        reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(y);
   const bool vec = N > 0 && (N % 8 == 0) && ((al & 15) == 0) && N <= 65536;
+  // rows split at the same 16-byte boundaries in x and y (torch allocations are 16-byte aligned,
+  // so any N qualifies); w and b are read per element
+  const bool skew = !vec && N > 0 && N <= 65536 + 7 && (al & 1) == 0 &&
+                    ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+  if (skew) {
+    const bool wb16 = ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
+    if (wb16)
+      launch_layernorm_skew<true>(x, w, b, y, mean, rstd, M, N, eps, s);
+    else
+      launch_layernorm_skew<false>(x, w, b, y, mean, rstd, M, N, eps, s);
+    return hipGetLastError();
+  }
   if (!vec) {
     layernorm_rows_f16_any<<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, w, b, y, mean, rstd, N, eps);
     return hipGetLastError();

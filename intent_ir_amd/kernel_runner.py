@@ -2,6 +2,12 @@
 
     python -m intent_ir_amd.kernel_runner --config softmax --launches 20 [--copy-mib 512]
     python -m intent_ir_amd.kernel_runner --config matmul --bindings M=4096,N=50257,K=4096 --transpose-b
+    python -m intent_ir_amd.kernel_runner --ew-chain all --launches 20
+
+``--ew-chain`` runs generic element-wise programs (ihip_elementwise_program, native code)
+on 8192 x 8192 operands and prints each chain's rate: per launch, every input's bytes
+read once and every output's written once, over the median of 5 timed rounds of
+``--launches`` launches (HIP events, after a compile-and-warm-up launch).
 
 Inputs are generated on the GPU; launches rotate over enough buffer sets that
 reads come from HBM rather than the Infinity Cache (as in bench.py).  With
@@ -20,18 +26,124 @@ import sys
 ROTATE_MIN_BYTES = 640 << 20
 
 
+def _t(dtype, *shape):
+    return {"dtype": dtype, "shape": list(shape)}
+
+
+def _op(name, inputs, output, **attrs):
+    d = {"op": name, "inputs": list(inputs), "output": output}
+    if attrs:
+        d["attrs"] = attrs
+    return d
+
+
+def _gelu_ir(dt):
+    from .configs import bias_gelu_axpy_ir  # noqa: PLC0415
+
+    return bias_gelu_axpy_ir(dt)
+
+
+# Element-wise chains timed by --ew-chain: (IR, bindings, extra bindings).  8192 x 8192 unless
+# stated; 16-bit inputs where the chain says so.
+EW_CHAINS = {
+    "leaky_where_f32": lambda: ({"name": "leaky", "tensors": {
+        "x": _t("f32", "M", "N"), "z": _t("f32"), "p": _t("i1", "M", "N"), "s": _t("f32", "M", "N"),
+        "y": _t("f32", "M", "N")},
+        "ops": [_op("const", [], "z", value=0.0, dtype="f32"), _op("gt", ["x", "z"], "p"),
+                _op("mul", ["x"], "s", mul_factor=0.1), _op("where", ["p", "x", "s"], "y")], "outputs": ["y"]},
+        {"M": 8192, "N": 8192}),
+    "bias_relu_f32": lambda: ({"name": "bias_relu", "tensors": {
+        "x": _t("f32", "M", "N"), "b": _t("f32", "N"), "t": _t("f32", "M", "N"), "y": _t("f32", "M", "N")},
+        "ops": [_op("add", ["x", "b"], "t"), _op("relu", ["t"], "y")], "outputs": ["y"]}, {"M": 8192, "N": 8192}),
+    "gelu_f32": lambda: (_gelu_ir("f32"), {"M": 8192, "N": 8192}),
+    "scale_f16_bf16": lambda: ({"name": "scale", "tensors": {
+        "x": _t("f16", "M", "N"), "w": _t("bf16", "N"), "t": _t("f32", "M", "N"), "y": _t("bf16", "M", "N")},
+        "ops": [_op("mul", ["x", "w"], "t"), _op("add", ["t"], "y", addend=0.25)], "outputs": ["y"]},
+        {"M": 8192, "N": 8192}),
+    "transpose_bias_f32": lambda: ({"name": "tb", "tensors": {
+        "x": _t("f32", "N", "M"), "b": _t("f32", "N"), "xt": _t("f32", "M", "N"), "y": _t("f32", "M", "N")},
+        "ops": [_op("transpose", ["x"], "xt", perm=[1, 0]), _op("add", ["xt", "b"], "y")], "outputs": ["y"]},
+        {"M": 8192, "N": 8192}),
+    "sigmoid_bf16": lambda: ({"name": "sigmoid", "tensors": {
+        "x": _t("bf16", "M", "N"), "u": _t("f32", "M", "N"), "e": _t("f32", "M", "N"), "one": _t("f32"),
+        "d": _t("f32", "M", "N"), "y": _t("bf16", "M", "N")},
+        "ops": [_op("mul", ["x"], "u", mul_factor=-1.0), _op("exp", ["u"], "e"),
+                _op("const", [], "one", value=1.0, dtype="f32"), _op("add", ["e", "one"], "d"),
+                _op("div", ["one", "d"], "y")], "outputs": ["y"]}, {"M": 8192, "N": 8192}),
+    # the GELU workload (bf16 [32768, 8192]) through the generic program instead of its kernel
+    "gelu_bf16_workload": lambda: (_gelu_ir("bf16"), {"M": 32768, "N": 8192, "HIP_ELEMENTWISE_PROGRAM": 1}),
+}
+
+
+def _ew_inputs(k, torch, g):
+    from .runtime import tensor_shapes, torch_dtype  # noqa: PLC0415
+
+    shapes = tensor_shapes(k.io_spec, k.bindings)
+    bufs, nbytes = {}, 0
+    for n, spec in k.io_spec["tensors"].items():
+        dt = torch_dtype(spec["dtype"])
+        if n in k.output_names:
+            bufs[n] = torch.empty(shapes[n], dtype=dt, device="cuda")
+        elif dt == torch.bool:
+            bufs[n] = torch.rand(shapes[n], generator=g, device="cuda") < 0.5
+        else:
+            bufs[n] = torch.randn(shapes[n], generator=g, device="cuda").to(dt)
+        nbytes += bufs[n].numel() * bufs[n].element_size()
+    return bufs, nbytes
+
+
+def run_ew_chains(names, launches, torch) -> int:
+    import statistics  # noqa: PLC0415
+
+    from . import lower_intent_to_hip_kernel  # noqa: PLC0415
+    from .runtime import launch_lowered  # noqa: PLC0415
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4321)
+    for name in names:
+        ir, b = EW_CHAINS[name]()
+        k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+        assert k.kernel_id == "ihip_elementwise_program", k.kernel_id
+        bufs, nbytes = _ew_inputs(k, torch, g)
+        launch_lowered(k, bufs)  # compiles the native code, warms up
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        times = []
+        for _ in range(5):
+            t0.record()
+            for _ in range(launches):
+                launch_lowered(k, bufs)
+            t1.record()
+            torch.cuda.synchronize()
+            times.append(t0.elapsed_time(t1) / launches)
+        ms = statistics.median(times)
+        prog = k.call_args[0][1]
+        print(f"[runner] ew {name}: {len(prog.code)} instructions, {nbytes / 2**20:.0f} MiB/launch, "
+              f"{ms * 1e3:.1f} us/launch, {nbytes / (ms * 1e-3) / 1e12:.2f} TB/s", flush=True)
+        del bufs
+        torch.cuda.empty_cache()
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", required=True, choices=["any", "softmax", "layernorm", "gelu", "matmul"])
+    ap.add_argument("--config", choices=["any", "softmax", "layernorm", "gelu", "matmul"])
+    ap.add_argument("--ew-chain", choices=sorted(EW_CHAINS) + ["all"],
+                    help="time a generic element-wise program chain (or all of them)")
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--copy-mib", type=int, default=0)
     ap.add_argument("--bindings", default="", help="comma-separated SYMBOL=VALUE overrides, e.g. M=1000,N=4096")
     ap.add_argument("--transpose-b", action="store_true", help="matmul: B given as [N, K] (matmul{transpose_b})")
     args = ap.parse_args(argv)
+    if (args.config is None) == (args.ew_chain is None):
+        ap.error("give exactly one of --config and --ew-chain")
     if args.transpose_b and args.config != "matmul":
         ap.error("--transpose-b applies to --config matmul only")
 
     import torch
+
+    if args.ew_chain:
+        return run_ew_chains(sorted(EW_CHAINS) if args.ew_chain == "all" else [args.ew_chain], args.launches, torch)
 
     from . import lower_intent_to_hip_kernel
     from .configs import WORKLOADS, algorithmic_bytes, gen_device

@@ -93,6 +93,10 @@ KNOBS: Dict[str, Optional[Tuple[int, ...]]] = {
     "HIP_RESPECT_SCHEDULE": None,
     "HIP_GEMM_TILE": (128, 256),
     "HIP_ROWS_PER_WG": (1, 2, 4),
+    # 1: an element-wise chain that has a specialised kernel (bias + GELU + axpy) runs as a
+    # generic element-wise program instead (the role of INTENTIR_CUDA_CODEGEN's choice of
+    # code generator in the reference, intentir_to_cuda.py:2099-2104)
+    "HIP_ELEMENTWISE_PROGRAM": None,
 }
 _SCHED_FIELDS = ("tile_m", "tile_n", "tile_k", "vec_width", "pipeline_depth")
 
@@ -403,6 +407,9 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     elif N % 8 == 0 and N <= 65536:  # kW waves per row, one row per workgroup
         kw = 2 if N <= 16384 else 4 if N <= 32768 else 8
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
+    elif 0 < N <= 65536 + 7:  # N % 8 != 0: head / 16-byte body / tail, kW waves per row, one row per workgroup
+        kw = next(k for k in (1, 2, 4, 8, 16) if N <= 4096 * k + 7)
+        launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
     else:
         launch = HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
     return HipLoweredKernel(c.fn.name, "ihip_layernorm_rows_f16", c.io(names), launch, list(c.fn.outputs),
@@ -410,7 +417,8 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
 
 
 def _match_gelu_axpy(c: _Ctx) -> Optional[HipLoweredKernel]:
-    if len(c.outs) != 1:
+    c.knobs.used.add("HIP_ELEMENTWISE_PROGRAM")
+    if len(c.outs) != 1 or c.knobs.values.get("HIP_ELEMENTWISE_PROGRAM"):
         return None
     (oname, ov), = c.outs.items()
     X = ("?in", "x")
@@ -424,12 +432,12 @@ def _match_gelu_axpy(c: _Ctx) -> Optional[HipLoweredKernel]:
             and env["one"][1] == 1.0):
         return None
     x, bias = env["x"][1], env["bias"][1]
-    for n in (x, bias, oname):
-        if c.dtype(n) != "bf16":
-            raise HipLoweringError(f"HIP bias+GELU+axpy takes bf16 x, bias, y; {n} is {c.dtype(n)}")
+    # other dtypes and shapes run as a generic element-wise program (_match_elementwise)
+    if any(c.dtype(n) != "bf16" for n in (x, bias, oname)):
+        return None
     M, N = c.rows(x)
     if c.fn.tensors[x].rank != 2 or c.shape(bias) != (N,):
-        raise HipLoweringError("bias+GELU+axpy expects x [M,N] and bias [N]")
+        return None
     if N % 8 == 0:
         launch = HipLaunch((max(1, _cdiv(N // 8, 256)), max(1, min(65535, _cdiv(M, 8))), 1), (256, 1, 1), 0)
     else:
@@ -511,6 +519,7 @@ def _leaves(tree: Any, out: List[str]) -> None:
 def _match_elementwise(c: _Ctx) -> Optional[HipLoweredKernel]:
     """Any remaining chain of element-wise ops: one register program on ihip_elementwise_program
     (the reference's fused element-wise lowering, intentir_to_cuda.py:229-534, dispatched at :2170-2199)."""
+    c.knobs.used.add("HIP_ELEMENTWISE_PROGRAM")
     outs = list(c.fn.outputs)
     if not all(_is_elementwise(c.outs[o].tree) for o in outs):
         return None

@@ -55,6 +55,7 @@ SIGNATURES: Dict[str, Tuple[Any, Tuple[Any, ...]]] = {
     "ihip_elementwise_mode": (_I32, (_I32,)),
     "ihip_elementwise_prepare": (_I32, (_P, _I32, _P, _I32, _P, _I32)),
     "ihip_elementwise_prepare_operands": (_I32, (_P, _I32, _P, _I32, _P, _I32, _P, _I32)),
+    "ihip_elementwise_source": (_I32, (_P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I64, _P)),
 }
 EW_MODE_AUTO, EW_MODE_INTERP, EW_MODE_NATIVE = 0, 1, 2
 
@@ -69,6 +70,24 @@ class EwOperand(ctypes.Structure):
     """ihip_ew_operand (include/intentir_hip.h)."""
     _fields_ = [("ptr", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
                 ("stride", ctypes.c_int64 * 4)]
+
+
+def elementwise_source(prog, ptrs: Mapping[str, int], dtypes: Mapping[str, str]) -> str:
+    """The HIP source ihip_elementwise_program compiles for an EwProgram with operands at ``ptrs``
+    (only their alignment matters; no device needed)."""
+    lib = load_library()
+    args = ew_program_args(prog, ptrs, dtypes)
+    keep = args.pop()
+    n = ctypes.c_int64(0)
+    st = lib.ihip_elementwise_source(*args, None, 0, ctypes.byref(n))
+    if st != 0:
+        raise HipRuntimeError(f"ihip_elementwise_source failed (status {st}): {lib.ihip_last_error().decode()}")
+    buf = ctypes.create_string_buffer(n.value + 1)
+    st = lib.ihip_elementwise_source(*args, buf, n.value + 1, None)
+    del keep
+    if st != 0:
+        raise HipRuntimeError(f"ihip_elementwise_source failed (status {st}): {lib.ihip_last_error().decode()}")
+    return buf.value.decode()
 
 
 def ew_program_args(prog, ptrs: Mapping[str, int], dtypes: Mapping[str, str]) -> list:
@@ -307,5 +326,5 @@ def run_lowered(lowered, inputs_np: Mapping[str, np.ndarray]) -> Dict[str, np.nd
                           output_names=lowered.output_names, call_args=lowered.call_args)
 
 
-__all__ = ["HipRuntimeError", "SIGNATURES", "EwInstr", "EwOperand", "ew_program_args", "make_hip_ref_fn", "LIB_PATH", "load_library", "call", "launch_lowered", "run_hip_kernel",
+__all__ = ["HipRuntimeError", "SIGNATURES", "EwInstr", "EwOperand", "elementwise_source", "ew_program_args", "make_hip_ref_fn", "LIB_PATH", "load_library", "call", "launch_lowered", "run_hip_kernel",
            "run_lowered", "to_device", "to_host", "torch_dtype", "tensor_shapes"]

@@ -188,6 +188,22 @@ case("gelu_f32_chain", {
     "ops": [op("add", ["x", "b"], "z"), op("gelu_tanh", ["z"], "g"), op("add", ["g", "x"], "y")], "outputs": ["y"]},
     {"M": 8, "N": 128}, lambda r, b: {"x": _f(r, b["M"], b["N"]), "b": _f(r, b["N"], scale=0.1)})
 
+# the logistic shape x / (exp(u) + 1), which native code evaluates in one fused step: values
+# past exp's range (u > 80 and u = +-inf from x = -+inf), NaN, -0.0 and large |x| take the
+# unfused fallback, the rest the fused form
+def _logistic_special(r, b):
+    x = (r.standard_normal(b["N"]) * 30.0).astype(np.float32)
+    x[:12] = [np.inf, -np.inf, np.nan, -0.0, 0.0, -60.0, 60.0, -47.0, -48.0, 3.0e38, -3.0e38, 1e-30]
+    return {"x": x}
+
+
+case("logistic_special", {
+    "tensors": {"x": T("f32", "N"), "u": T("f32", "N"), "e": T("f32", "N"), "one": T("f32"),
+                "d": T("f32", "N"), "y": T("f32", "N")},
+    "ops": [op("mul", ["x"], "u", mul_factor=-1.7), op("exp", ["u"], "e"), op("const", [], "one", value=1.0, dtype="f32"),
+            op("add", ["e", "one"], "d"), op("div", ["x", "d"], "y")], "outputs": ["y"]},
+    {"N": 1000}, _logistic_special)
+
 # copy of a bool tensor
 case("identity_bool", {
     "tensors": {"x": T("i1", "M", "N"), "y": T("i1", "M", "N")},

@@ -266,6 +266,52 @@ def test_layernorm_edge_shapes(hip, M, N):
     _check_ln(run_case(w.ir(), inp, b), oracle_outputs(w.ir(), inp, b), f"LN {b}")
 
 
+@pytest.mark.parametrize("M", [3, 64])
+@pytest.mark.parametrize("N", [4097, 4099, 4103, 5000 + 3, 8191, 12345, 32767, 50257, 65535])
+def test_layernorm_rows_not_16_byte_aligned(hip, M, N):
+    """N % 8 != 0: each row splits into a head of < 8 halves, a 16-byte aligned body held in
+    registers and a tail of < 8 halves (1-16 waves per row), at every row alignment."""
+    w = WORKLOADS["layernorm"]
+    b = {"M": M, "N": N}
+    inp = w.gen(b, seed=M + N)
+    _check_ln(run_case(w.ir(), inp, b), oracle_outputs(w.ir(), inp, b), f"LN {b}")
+
+
+@pytest.mark.parametrize("N", [1000, 4099, 8200])
+@pytest.mark.parametrize("ox,oy,ow", [(1, 1, 0), (3, 3, 0), (7, 7, 0), (1, 2, 0), (0, 5, 0), (3, 3, 1), (0, 0, 3)])
+def test_layernorm_at_every_alignment(hip, N, ox, oy, ow):
+    """Through the C-ABI with x and y offset by ox, oy halves from a 16-byte boundary: equal
+    offsets take the head/body/tail form, unequal ones the three-pass kernel; w and b offset by
+    ow halves are read element by element instead of as realigned 16-byte vectors.  All against
+    the oracle."""
+    import ctypes
+
+    import torch
+
+    w = WORKLOADS["layernorm"]
+    M = 5
+    inp = w.gen({"M": M, "N": N}, seed=N + ox)
+    xs = torch.zeros(M * N + 16, dtype=torch.float16, device="cuda")
+    ys = torch.zeros(M * N + 16, dtype=torch.float16, device="cuda")
+    xs[ox:ox + M * N] = torch.from_numpy(inp["in_ptr"].reshape(-1)).cuda()
+    wt = torch.zeros(N + 8, dtype=torch.float16, device="cuda")
+    bt = torch.zeros(N + 8, dtype=torch.float16, device="cuda")
+    wt[ow:ow + N] = torch.from_numpy(inp["weight_ptr"]).cuda()
+    bt[ow:ow + N] = torch.from_numpy(inp["bias_ptr"]).cuda()
+    mean = torch.empty(M, device="cuda")
+    rstd = torch.empty(M, device="cuda")
+    st = hip.ihip_layernorm_rows_f16(ctypes.c_void_p(xs.data_ptr() + 2 * ox), ctypes.c_void_p(wt.data_ptr() + 2 * ow),
+                                     ctypes.c_void_p(bt.data_ptr() + 2 * ow), ctypes.c_void_p(ys.data_ptr() + 2 * oy),
+                                     ctypes.c_void_p(mean.data_ptr()), ctypes.c_void_p(rstd.data_ptr()), M, N,
+                                     ctypes.c_float(1e-5), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0, hip.ihip_last_error()
+    torch.cuda.synchronize()
+    out = {"out_ptr": ys[oy:oy + M * N].cpu().numpy().reshape(M, N).astype(np.float32),
+           "out_mean_ptr": mean.cpu().numpy(), "out_rstd_ptr": rstd.cpu().numpy()}
+    _check_ln(out, oracle_outputs(w.ir(), inp, {"M": M, "N": N}), f"LN N={N} offsets {ox},{oy}")
+    assert (ys[:oy] == 0).all() and (ys[oy + M * N:] == 0).all(), "writes outside y"
+
+
 @pytest.mark.parametrize("N", [512, 1024, 2048, 4096])
 def test_layernorm_exact_and_tail_paths_agree(hip, N):
     """Rows per workgroup: M % 16 == 0 with full-width rows takes the unmasked kernel, M = 31 the

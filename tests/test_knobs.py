@@ -136,3 +136,22 @@ def test_run_hip_kernel_takes_the_reference_arguments():
     required = {n for n, p in sig.parameters.items() if p.default is inspect.Parameter.empty}
     assert required == {"kernel_name", "kernel_id", "io_spec", "launch", "bindings", "inputs_np", "output_names"}
     assert all(p.kind is inspect.Parameter.KEYWORD_ONLY for p in sig.parameters.values())
+
+
+def test_gelu_chain_in_other_dtypes_runs_as_a_program():
+    """The bias + GELU + axpy kernel is bf16-only; the same chain in f32 or f16 is a generic program."""
+    from intent_ir_amd.configs import bias_gelu_axpy_ir
+
+    for dt in ("f32", "f16"):
+        k = lower_intent_to_hip_kernel(bias_gelu_axpy_ir(dt), shape_bindings={"M": 8, "N": 64})
+        assert k.kernel_id == "ihip_elementwise_program", dt
+
+
+def test_elementwise_program_knob():
+    w = WORKLOADS["gelu"]
+    b = {"M": 8, "N": 64}
+    assert lower_intent_to_hip_kernel(w.ir(), shape_bindings=b).kernel_id == "ihip_bias_gelu_tanh_axpy_bf16"
+    k = lower_intent_to_hip_kernel(w.ir(), shape_bindings={**b, "HIP_ELEMENTWISE_PROGRAM": 1})
+    assert k.kernel_id == "ihip_elementwise_program"
+    with pytest.raises(HipLoweringError, match="does not apply"):
+        lower_intent_to_hip_kernel(WORKLOADS["softmax"].ir(), shape_bindings={**b, "HIP_ELEMENTWISE_PROGRAM": 1})
