@@ -136,8 +136,7 @@ int ihip_gemm_bf16_bias_relu_t(const uint16_t* A, const uint16_t* B, const float
 /* The same with a tile knob, the role of the reference's WMMA_* tile bindings and schedule
  * tile_m / tile_n (backends/cuda/codegen/intentir_to_cuda.py:659-664, 2074-2097): tile = 0
  * chooses automatically (256x256 C tiles, 128x128 when at most 128 tiles of 256x256 would
- * run); 128 or 256 fixes the tiled kernel's tile extent.  128 needs a shape and alignment the
- * tiled kernel takes (listed above); the guarded kernel has 256x256 tiles only.  Every
+ * run); 128 or 256 fixes the tile extent, of the tiled and of the guarded kernel alike.  Every
  * tile extent accumulates in the same order, so C does not depend on tile. */
 int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                                 int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,

@@ -32,7 +32,6 @@ hipError_t launch_bias_gelu_axpy_bf16(const uint16_t*, const uint16_t*, uint16_t
                                       hipStream_t);
 hipError_t launch_gemm_bf16_bias_relu(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t,
                                       int64_t, bool, bool, int, int, hipStream_t);
-bool gemm_fast_fits(int64_t, int64_t, int64_t, bool, bool, const void*, const void*, const void*);
 hipError_t launch_elementwise_program(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*,
                                       int, const int64_t (&)[4], hipStream_t);
 hipError_t launch_elementwise_jit(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*, int,
@@ -297,11 +296,6 @@ int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const floa
   IHIP_REQUIRE(M == 0 || N == 0 || K == 0 || (A != nullptr && B != nullptr), "gemm_bf16_bias_relu: A or B is null");
   IHIP_REQUIRE(tile == 0 || tile == 128 || tile == 256, "gemm_bf16_bias_relu: tile %d is not 0 (automatic), 128 or 256",
                tile);
-  IHIP_REQUIRE(tile != 128 || M == 0 || N == 0 ||
-                   ihip::gemm_fast_fits(M, N, K, transpose_a != 0, transpose_b != 0, A, B, C),
-               "gemm_bf16_bias_relu: tile 128 needs the tiled kernel (rows of A, B and C 16-byte aligned); "
-               "M=%lld N=%lld K=%lld runs the guarded kernel's 256x256 tiles",
-               (long long)M, (long long)N, (long long)K);
   return finish(ihip::launch_gemm_bf16_bias_relu(A, B, bias, C, M, N, K, transpose_a != 0, transpose_b != 0, relu,
                                                  tile, static_cast<hipStream_t>(stream)),
                 "gemm_bf16_bias_relu");

@@ -6,8 +6,10 @@
 // K % 8 == 0, M % 8 == 0 for a transposed A) with 16-byte aligned operands go to
 // gemm_fast.hip, for any M, N and K; every other shape runs the guarded kernel below, which
 // stages operands through registers:
-//  * workgroup tile 256(M) x 256(N), K step 64; 256 threads = 4 waves in a 2x2 grid,
-//    each wave owning a 128x128 sub-tile = 4x4 blocks of v_mfma_f32_32x32x16_bf16;
+//  * workgroup tile TB(M) x TB(N), TB = 256, or 128 for grids of at most 128 tiles of 256x256
+//    (half the CUs; as in gemm_fast.hip), K step 64; 256 threads = 4 waves in a 2x2 grid,
+//    each wave owning a TB/2 x TB/2 sub-tile = (TB/64)^2 blocks of v_mfma_f32_32x32x16_bf16;
+//    both tile extents accumulate every C element in the same k order (identical results);
 //  * LDS double buffer: A tile as [m][k] and B tile transposed to [n][k] (rows padded
 //    to 144 B) so both MFMA operands are 16-byte reads of 8 consecutive k;
 //  * B is transposed on the way into LDS: each thread loads an 8(k) x 8(n) block and
@@ -23,11 +25,12 @@ namespace ihip {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBK = 64;
 constexpr int kLdsRow = 72;                      // halves per LDS row (64 + 8 pad)
-constexpr int kTileHalves = 256 * kLdsRow;       // one operand tile
-constexpr int kLdsHalves = 2 * 2 * kTileHalves;  // {A, Bt} x double buffer = 147456 B
 constexpr int kGroupM = 8;                       // tile-rows per raster group
+// One operand tile of TB rows, and the LDS of {A, Bt} x double buffer (147456 B for TB = 256).
+template <int TB> constexpr int tile_halves() { return TB * kLdsRow; }
+template <int TB> constexpr int lds_halves() { return 2 * 2 * tile_halves<TB>(); }
 
 __device__ __forceinline__ uint32_t dw(const uint4& v, int q) {
   return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
@@ -35,11 +38,12 @@ __device__ __forceinline__ uint32_t dw(const uint4& v, int q) {
 __device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xffff0000u); }
 
-template <bool kGuard>
+// TB rows x 64 k as 16-byte chunks, TB/32 per thread.
+template <bool kGuard, int TB>
 __device__ __forceinline__ void load_a(const uint16_t* __restrict__ A, int64_t M, int64_t K, int64_t m0, int64_t k0,
                                        int tid, uint4 (&ra)[8]) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < TB / 32; ++i) {
     const int c = tid + 256 * i;
     const int64_t gm = m0 + (c >> 3), gk = k0 + (c & 7) * 8;
     if (!kGuard) {
@@ -54,15 +58,17 @@ __device__ __forceinline__ void load_a(const uint16_t* __restrict__ A, int64_t M
   }
 }
 
+template <int TB>
 __device__ __forceinline__ void store_a(uint16_t* lds_a, int tid, const uint4 (&ra)[8]) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < TB / 32; ++i) {
     const int c = tid + 256 * i;
     *reinterpret_cast<uint4*>(lds_a + (c >> 3) * kLdsRow + (c & 7) * 8) = ra[i];
   }
 }
 
-// Thread t owns the 8(k) x 8(n) block (kb = t & 7, nb = t >> 3) of the 64 x 256 B tile.
+// Thread t < TB owns the 8(k) x 8(n) block (kb = t & 7, nb = t >> 3) of the 64 x TB B tile
+// (with TB = 128 the last two waves own none: the callers skip them, a uniform branch).
 template <bool kGuard>
 __device__ __forceinline__ void load_b(const uint16_t* __restrict__ B, int64_t K, int64_t N, int64_t k0, int64_t n0,
                                        int tid, uint4 (&rb)[8]) {
@@ -106,31 +112,42 @@ __device__ __forceinline__ void store_bt(uint16_t* lds_b, int tid, const uint4 (
 __device__ __forceinline__ float relu_np(float v) { return v < 0.0f ? 0.0f : v; }  // keeps -0.0 and NaN
 
 // One K slice of both operands into registers, then into the [m][k] / [n][k] LDS tiles.
-template <bool kGuard, bool kTA, bool kTB>
+template <bool kGuard, bool kTA, bool kTB, int TB>
 __device__ __forceinline__ void load_slice(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, int64_t M,
                                            int64_t N, int64_t K, int64_t m0, int64_t n0, int64_t k0, int tid,
                                            uint4 (&ra)[8], uint4 (&rb)[8]) {
-  if (!kTA) load_a<kGuard>(A, M, K, m0, k0, tid, ra);
-  else load_b<kGuard>(A, K, M, k0, m0, tid, ra);
-  if (!kTB) load_b<kGuard>(B, K, N, k0, n0, tid, rb);
-  else load_a<kGuard>(B, N, K, n0, k0, tid, rb);
+  const bool blk = tid < TB;  // owns an 8x8 block of a K-major operand
+  if (!kTA) load_a<kGuard, TB>(A, M, K, m0, k0, tid, ra);
+  else if (blk) load_b<kGuard>(A, K, M, k0, m0, tid, ra);
+  if (!kTB) {
+    if (blk) load_b<kGuard>(B, K, N, k0, n0, tid, rb);
+  } else {
+    load_a<kGuard, TB>(B, N, K, n0, k0, tid, rb);
+  }
 }
 
-template <bool kTA, bool kTB>
+template <bool kTA, bool kTB, int TB>
 __device__ __forceinline__ void store_slice(uint16_t* lds_a, uint16_t* lds_b, int tid, const uint4 (&ra)[8],
                                             const uint4 (&rb)[8]) {
-  if (!kTA) store_a(lds_a, tid, ra);
-  else store_bt(lds_a, tid, ra);
-  if (!kTB) store_bt(lds_b, tid, rb);
-  else store_a(lds_b, tid, rb);
+  const bool blk = tid < TB;
+  if (!kTA) store_a<TB>(lds_a, tid, ra);
+  else if (blk) store_bt(lds_a, tid, ra);
+  if (!kTB) {
+    if (blk) store_bt(lds_b, tid, rb);
+  } else {
+    store_a<TB>(lds_b, tid, rb);
+  }
 }
 
-template <bool kGuard, bool kTA, bool kTB>
+template <bool kGuard, bool kTA, bool kTB, int TB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                 const float* __restrict__ bias, uint16_t* __restrict__ C, int64_t M, int64_t N,
                                 int64_t K, int relu, int tiles_m, int tiles_n) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[kLdsHalves];
+  static_assert(TB == 256 || TB == 128, "tile extents");
+  constexpr int kBlk = TB / 64;  // 32x32 blocks per wave and dimension
+  constexpr int kTileHalves = tile_halves<TB>();
+  __shared__ __attribute__((aligned(16))) uint16_t lds[lds_halves<TB>()];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
 
@@ -142,60 +159,61 @@ void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* 
   const int g = bid / per_group, first_m = g * kGroupM;
   const int gsz = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
   const int tm = first_m + (bid % per_group) % gsz, tn = (bid % per_group) / gsz;
-  const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
+  const int64_t m0 = static_cast<int64_t>(tm) * TB, n0 = static_cast<int64_t>(tn) * TB;
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[kBlk][kBlk];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kBlk; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < kBlk; ++j) acc[i][j] = f32x16_t{};
 
   const int KT = static_cast<int>((K + kBK - 1) / kBK);
   uint4 ra[8], rb[8];
   if (KT > 0) {
-    load_slice<kGuard, kTA, kTB>(A, B, M, N, K, m0, n0, 0, tid, ra, rb);
-    store_slice<kTA, kTB>(lds, lds + kTileHalves, tid, ra, rb);
+    load_slice<kGuard, kTA, kTB, TB>(A, B, M, N, K, m0, n0, 0, tid, ra, rb);
+    store_slice<kTA, kTB, TB>(lds, lds + kTileHalves, tid, ra, rb);
   }
   __syncthreads();
 
-  const int a_off = (wm * 128 + (lane & 31)) * kLdsRow + (lane >> 5) * 8;
-  const int b_off = (wn * 128 + (lane & 31)) * kLdsRow + (lane >> 5) * 8;
+  const int a_off = (wm * (TB / 2) + (lane & 31)) * kLdsRow + (lane >> 5) * 8;
+  const int b_off = (wn * (TB / 2) + (lane & 31)) * kLdsRow + (lane >> 5) * 8;
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < KT;
-    if (more) load_slice<kGuard, kTA, kTB>(A, B, M, N, K, m0, n0, static_cast<int64_t>(kt + 1) * kBK, tid, ra, rb);
+    if (more)
+      load_slice<kGuard, kTA, kTB, TB>(A, B, M, N, K, m0, n0, static_cast<int64_t>(kt + 1) * kBK, tid, ra, rb);
     const uint16_t* la = lds + cur * 2 * kTileHalves + a_off;
     const uint16_t* lb = lds + cur * 2 * kTileHalves + kTileHalves + b_off;
 #pragma unroll
     for (int kk = 0; kk < kBK / 16; ++kk) {
-      bf16x8_t af[4], bf[4];
+      bf16x8_t af[kBlk], bf[kBlk];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kBlk; ++i) {
         af[i] = *reinterpret_cast<const bf16x8_t*>(la + i * 32 * kLdsRow + kk * 16);
         bf[i] = *reinterpret_cast<const bf16x8_t*>(lb + i * 32 * kLdsRow + kk * 16);
       }
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni)
+      for (int ni = 0; ni < kBlk; ++ni)
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
+        for (int mi = 0; mi < kBlk; ++mi)
           acc[ni][mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[ni], af[mi], acc[ni][mi], 0, 0, 0);
     }
     if (more) {
       uint16_t* nxt = lds + (cur ^ 1) * 2 * kTileHalves;
-      store_slice<kTA, kTB>(nxt, nxt + kTileHalves, tid, ra, rb);
+      store_slice<kTA, kTB, TB>(nxt, nxt + kTileHalves, tid, ra, rb);
     }
     __syncthreads();
   }
 
   // ---- epilogue: lane holds C[m][n..n+3] for m = lane&31 (+block), n = 8*g + 4*(lane>>5) (+block)
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) {
+  for (int ni = 0; ni < kBlk; ++ni) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      const int64_t m = m0 + wm * 128 + mi * 32 + (lane & 31);
+    for (int mi = 0; mi < kBlk; ++mi) {
+      const int64_t m = m0 + wm * (TB / 2) + mi * 32 + (lane & 31);
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        const int64_t n = n0 + wn * 128 + ni * 32 + g4 * 8 + (lane >> 5) * 4;
+        const int64_t n = n0 + wn * (TB / 2) + ni * 32 + g4 * 8 + (lane >> 5) * 4;
         float v[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -223,29 +241,38 @@ bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, bool tran
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
                             int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s);
 
-template <bool kTA, bool kTB>
-static void launch_guarded(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
-                           int64_t K, int relu, int tm, int tn, hipStream_t s) {
-  gemm_bf16_bias_relu_kernel<true, kTA, kTB><<<dim3(static_cast<unsigned>(tm) * tn), dim3(256), 0, s>>>(
-      A, B, bias, C, M, N, K, relu, tm, tn);
+template <bool kTA, bool kTB, int TB>
+static hipError_t launch_guarded(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                                 int64_t N, int64_t K, int relu, hipStream_t s) {
+  const int64_t tm = (M + TB - 1) / TB, tn = (N + TB - 1) / TB;
+  if (tm * tn > 0x7fffffffLL) return hipErrorInvalidValue;
+  gemm_bf16_bias_relu_kernel<true, kTA, kTB, TB><<<dim3(static_cast<unsigned>(tm * tn)), dim3(256), 0, s>>>(
+      A, B, bias, C, M, N, K, relu, static_cast<int>(tm), static_cast<int>(tn));
+  return hipGetLastError();
 }
 
-// tile: 0 = automatic, else the tiled kernel's tile extent (128 or 256; the caller has checked
-// that the tiled kernel runs this shape when it is 128).
+template <int TB>
+static hipError_t launch_guarded_tb(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                                    int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu, hipStream_t s) {
+  if (!transpose_a && !transpose_b) return launch_guarded<false, false, TB>(A, B, bias, C, M, N, K, relu, s);
+  if (!transpose_a) return launch_guarded<false, true, TB>(A, B, bias, C, M, N, K, relu, s);
+  if (!transpose_b) return launch_guarded<true, false, TB>(A, B, bias, C, M, N, K, relu, s);
+  return launch_guarded<true, true, TB>(A, B, bias, C, M, N, K, relu, s);
+}
+
+int gemm_fast_tile_extent(int64_t M, int64_t N);
+
+// tile: 0 = automatic (256x256 tiles, 128x128 for grids of at most 128 256x256 tiles), else
+// 128 or 256; the same rule and choice for the tiled and the guarded kernel.
 hipError_t launch_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                                       int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu, int tile,
                                       hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
   if (gemm_fast_fits(M, N, K, transpose_a, transpose_b, A, B, C))
     return launch_gemm_fast(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, s);
-  const int64_t tm = (M + kBM - 1) / kBM, tn = (N + kBN - 1) / kBN;
-  if (tm * tn > 0x7fffffffLL) return hipErrorInvalidValue;
-  const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);
-  if (!transpose_a && !transpose_b) launch_guarded<false, false>(A, B, bias, C, M, N, K, relu, itm, itn, s);
-  else if (!transpose_a) launch_guarded<false, true>(A, B, bias, C, M, N, K, relu, itm, itn, s);
-  else if (!transpose_b) launch_guarded<true, false>(A, B, bias, C, M, N, K, relu, itm, itn, s);
-  else launch_guarded<true, true>(A, B, bias, C, M, N, K, relu, itm, itn, s);
-  return hipGetLastError();
+  const int tb = tile != 0 ? tile : gemm_fast_tile_extent(M, N);
+  return tb == 128 ? launch_guarded_tb<128>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s)
+                   : launch_guarded_tb<256>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
 }
 
 }  // namespace ihip

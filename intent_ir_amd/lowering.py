@@ -261,14 +261,11 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     # fast path: 256x256 tiles, or 128x128 tiles when at most 128 tiles of 256x256 (half the
     # CUs) would be busy (gemm_fast_tile_extent); LDS max(4-stage ring, bf16 C tile) + bias:
     # 256: max(131072, 256 x 528) + 1024, 128: max(65536, 128 x 272) + 512
+    t = tile or (128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256)
     if full:
-        t = tile or (128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256)
         launch = HipLaunch((_cdiv(M, t) * _cdiv(N, t), 1, 1), (256, 1, 1), 136192 if t == 256 else 66048)
-    else:
-        if tile == 128:
-            raise HipLoweringError(f"GEMM tile 128 needs the tiled kernel; M={M} N={N} K={K} (transpose_a={ta}, "
-                                   f"transpose_b={tb}) runs the guarded kernel, whose tiles are 256x256")
-        launch = HipLaunch((max(1, _cdiv(M, 256) * _cdiv(N, 256)), 1, 1), (256, 1, 1), 147456)
+    else:  # guarded kernel: the same tile choice, a double-buffered {A, Bt} tile pair of 64-k slices
+        launch = HipLaunch((max(1, _cdiv(M, t) * _cdiv(N, t)), 1, 1), (256, 1, 1), 147456 if t == 256 else 73728)
     kid = ("ihip_gemm_bf16_bias_relu_ex" if tile else "ihip_gemm_bf16_bias_relu_t" if (ta or tb)
            else "ihip_gemm_bf16_bias_relu")
     return HipLoweredKernel(c.fn.name, kid, c.io(names), launch, [oname], dict(c.b), tuple(args))

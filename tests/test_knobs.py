@@ -63,12 +63,15 @@ def test_recovered_schedule_is_a_hint_unless_respected():
         lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_RESPECT_SCHEDULE": 1})
 
 
-def test_gemm_tile_128_needs_the_tiled_kernel():
+def test_gemm_tile_knob_on_the_guarded_kernel():
     ir = WORKLOADS["matmul"].ir()
     b = {"M": 64, "N": 263, "K": 64}  # N % 8 != 0 with B as [K, N]: the guarded kernel
-    assert lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 256}).launch.lds_bytes == 147456
-    with pytest.raises(HipLoweringError, match="guarded"):
-        lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 128})
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 256})
+    assert k.launch.lds_bytes == 147456 and k.launch.grid[0] == 2
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 128})
+    assert k.launch.lds_bytes == 73728 and k.launch.grid[0] == 3
+    auto = lower_intent_to_hip_kernel(ir, shape_bindings=b)  # 2 tiles of 256x256: 128x128 tiles
+    assert auto.launch == k.launch
 
 
 @pytest.mark.parametrize("rows", [1, 2, 4])

@@ -206,24 +206,24 @@ def test_gemm_forms_and_errors():
     assert lower_intent_to_hip_kernel(ir, shape_bindings=b).call_args[-1] == ("i32", 1)
 
 
-@pytest.mark.parametrize("M,N,K,tile", [(256, 256, 64, 128), (300, 264, 1000, 128), (8, 8, 8, 128),
-                                        (4096, 4096, 64, 256), (4096, 2048, 64, 128), (4096, 2304, 64, 256),
-                                        (4100, 4104, 72, 256),
-                                        (256, 250, 64, 0), (256, 256, 60, 0), (65536, 16384, 40960, 256),
-                                        (65536, 16384, 40968, 0)])
-def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tile):
-    """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N: 256x256
-    tiles (LDS max(4-stage ring, staged C tile) + 256 bias floats), or 128x128 tiles when at
-    most 128 tiles of 256x256 (half the CUs) would be busy; otherwise (tile 0 here) the guarded
-    kernel.
-    A ragged K needs operands below 2 GiB."""
+@pytest.mark.parametrize("M,N,K,tile,guarded", [
+    (256, 256, 64, 128, False), (300, 264, 1000, 128, False), (8, 8, 8, 128, False), (4096, 4096, 64, 256, False),
+    (4096, 2048, 64, 128, False), (4096, 2304, 64, 256, False), (4100, 4104, 72, 256, False),
+    (256, 250, 64, 128, True), (256, 256, 60, 128, True), (65536, 16384, 40960, 256, False),
+    (65536, 16384, 40968, 256, True), (5000, 3001, 64, 256, True)])
+def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tile, guarded):
+    """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N (LDS
+    max(4-stage ring, staged C tile) + 256 bias floats), other shapes the guarded kernel (a
+    double-buffered pair of 64-k operand tiles).  Both use 256x256 tiles, or 128x128 tiles when
+    at most 128 tiles of 256x256 (half the CUs) would be busy.  A ragged K needs operands below
+    2 GiB for the tiled kernel."""
     k = lower_intent_to_hip_kernel(matmul_bias_relu2d_ir(), shape_bindings={"M": M, "N": N, "K": K})
-    t = tile or 256
-    assert k.launch.grid == (-(-M // t) * -(-N // t), 1, 1)
-    assert k.launch.lds_bytes == {256: 136192, 128: 66048, 0: 147456}[tile]
+    assert k.launch.grid == (-(-M // tile) * -(-N // tile), 1, 1)
+    assert k.launch.lds_bytes == {(256, False): 136192, (128, False): 66048, (256, True): 147456,
+                                  (128, True): 73728}[(tile, guarded)]
 
 
-@pytest.mark.parametrize("N,tb,lds", [(50257, True, 136192), (263, True, 66048), (263, False, 147456),
+@pytest.mark.parametrize("N,tb,lds", [(50257, True, 136192), (263, True, 66048), (263, False, 73728),
                                       (50257, False, 147456)])
 def test_gemm_odd_n_takes_the_tiled_kernel_with_b_as_nk(N, tb, lds):
     """With B given as [N, K] (transpose_b) the rows of A and B stay 16-byte aligned at any N,
