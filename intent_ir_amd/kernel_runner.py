@@ -3,11 +3,15 @@
     python -m intent_ir_amd.kernel_runner --config softmax --launches 20 [--copy-mib 512]
     python -m intent_ir_amd.kernel_runner --config matmul --bindings M=4096,N=50257,K=4096 --transpose-b
     python -m intent_ir_amd.kernel_runner --ew-chain all --launches 20
+    python -m intent_ir_amd.kernel_runner --row-reduce sum --bindings M=64,N=1048576 --launches 20
 
 ``--ew-chain`` runs generic element-wise programs (ihip_elementwise_program, native code)
 on 8192 x 8192 operands and prints each chain's rate: per launch, every input's bytes
 read once and every output's written once, over the median of 5 timed rounds of
-``--launches`` launches (HIP events, after a compile-and-warm-up launch).
+``--launches`` launches (HIP events, after a compile-and-warm-up launch).  ``--row-reduce``
+times reduce_sum / reduce_max over the last axis of an f32 [M, N] tensor the same way
+(rotating buffer sets over > 640 MiB), default [64, 1048576]: few long rows, which the
+library splits over several workgroups per row with partial results in a workspace.
 
 Inputs are generated on the GPU; launches rotate over enough buffer sets that
 reads come from HBM rather than the Infinity Cache (as in bench.py).  With
@@ -125,18 +129,54 @@ def run_ew_chains(names, launches, torch) -> int:
     return 0
 
 
+def run_row_reduce(kind, bindings, launches, torch) -> int:
+    import statistics  # noqa: PLC0415
+
+    from . import lower_intent_to_hip_kernel  # noqa: PLC0415
+    from .runtime import launch_lowered  # noqa: PLC0415
+
+    op = {"sum": "reduce_sum", "max": "reduce_max"}[kind]
+    ir = {"name": f"row_{op}", "tensors": {"x": _t("f32", "M", "N"), "out": _t("f32", "M")},
+          "ops": [_op(op, ["x"], "out", dims=[1])], "outputs": ["out"]}
+    b = {"M": 64, "N": 1 << 20, **bindings}
+    k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    per = 4 * b["M"] * b["N"] + 4 * b["M"]
+    nsets = max(2, math.ceil(ROTATE_MIN_BYTES / per))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(99)
+    sets = [{"x": torch.randn((b["M"], b["N"]), generator=g, device="cuda"),
+             "out": torch.empty(b["M"], device="cuda")} for _ in range(nsets)]
+    for i in range(nsets):
+        launch_lowered(k, sets[i])
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(5):
+        t0.record()
+        for i in range(launches):
+            launch_lowered(k, sets[i % nsets])
+        t1.record()
+        torch.cuda.synchronize()
+        times.append(t0.elapsed_time(t1) / launches)
+    ms = statistics.median(times)
+    print(f"[runner] row {op} {b}: {k.kernel_id}, {ms * 1e3:.1f} us/launch, {per / (ms * 1e-3) / 1e12:.2f} TB/s",
+          flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", choices=["any", "softmax", "layernorm", "gelu", "matmul"])
     ap.add_argument("--ew-chain", choices=sorted(EW_CHAINS) + ["all"],
                     help="time a generic element-wise program chain (or all of them)")
+    ap.add_argument("--row-reduce", choices=["sum", "max"], help="time a row reduction (f32 [M, N], --bindings)")
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--copy-mib", type=int, default=0)
     ap.add_argument("--bindings", default="", help="comma-separated SYMBOL=VALUE overrides, e.g. M=1000,N=4096")
     ap.add_argument("--transpose-b", action="store_true", help="matmul: B given as [N, K] (matmul{transpose_b})")
     args = ap.parse_args(argv)
-    if (args.config is None) == (args.ew_chain is None):
-        ap.error("give exactly one of --config and --ew-chain")
+    if sum(x is not None for x in (args.config, args.ew_chain, args.row_reduce)) != 1:
+        ap.error("give exactly one of --config, --ew-chain and --row-reduce")
     if args.transpose_b and args.config != "matmul":
         ap.error("--transpose-b applies to --config matmul only")
 
@@ -144,6 +184,9 @@ def main(argv=None) -> int:
 
     if args.ew_chain:
         return run_ew_chains(sorted(EW_CHAINS) if args.ew_chain == "all" else [args.ew_chain], args.launches, torch)
+    if args.row_reduce:
+        rb = {n: int(v) for n, _, v in (item.partition("=") for item in filter(None, args.bindings.split(",")))}
+        return run_row_reduce(args.row_reduce, rb, args.launches, torch)
 
     from . import lower_intent_to_hip_kernel
     from .configs import WORKLOADS, algorithmic_bytes, gen_device

@@ -193,7 +193,10 @@ case("gelu_f32_chain", {
 # unfused fallback, the rest the fused form
 def _logistic_special(r, b):
     x = (r.standard_normal(b["N"]) * 30.0).astype(np.float32)
-    x[:12] = [np.inf, -np.inf, np.nan, -0.0, 0.0, -60.0, 60.0, -47.0, -48.0, 3.0e38, -3.0e38, 1e-30]
+    special = np.array([np.inf, -np.inf, np.nan, -0.0, 0.0, -60.0, 60.0, -47.0, -48.0, 3.0e38, -3.0e38, 1e-30],
+                       np.float32)
+    n = min(len(special), b["N"])
+    x[:n] = special[:n]
     return {"x": x}
 
 
