@@ -21,17 +21,21 @@
 //    B columns in L2.
 //
 // Operand staging
-//  * a ring of STAGES LDS stages, each holding a 256 x DK slice of A and a DK x 256 slice
-//    of B; the copy of K-slice kt+STAGES-1 is issued while slice kt is multiplied, so a
-//    copy has STAGES-1 slices of MFMA time to land;
+//  * a ring of STAGES LDS stages of B (DK x 256 slices); the copy of K-slice kt+STAGES-1 is
+//    issued while slice kt is multiplied, so a copy has STAGES-1 slices of MFMA time to land;
+//  * A given as [M, K] sits in a ring of three regions, each holding 256 rows of 2*DK k (a
+//    pair of slices, 128-byte rows), so every copy reads whole 128-byte cache lines: the two
+//    row halves of pair P are copied while slices 2P-4 and 2P-3 are multiplied.  A given as
+//    [K, M] uses STAGES stages of DK k-rows like B;
 //  * copies use gfx950's direct-to-LDS loads (global_load_lds_dwordx4 in interior tiles,
 //    buffer_load_dwordx4 ... lds in edge tiles): lane l of a wave writes 16 bytes at LDS
 //    m0 + 16*l; no VGPR holds tile data;
 //  * because the LDS position is fixed by the lane, bank conflicts are avoided by choosing
 //    which global 16-byte chunk each lane fetches (XOR swizzles, 64-bank LDS):
-//      A row r (DK*2 bytes) stores logical k-chunk c in slot c ^ ((r / RPW) % CA), where
-//        CA = DK/8 chunks per row and RPW = 256 / (DK*2) rows per 256-byte bank window:
-//        the 16 rows one ds_read_b128 cycle serves cover all 16 bank positions;
+//      a K-contiguous row r (R bytes: 128 for a paired A, DK*2 for B given as [N, K]) stores
+//        logical k-chunk c in slot c ^ ((r / RPW) % CA), where CA = R/16 chunks per row and
+//        RPW = 256 / R rows per 256-byte bank window: the 16 rows one ds_read_b128 cycle
+//        serves cover all 16 bank positions;
 //      B row k (512 bytes) stores logical n-chunk c in slot c ^ 2*(k & 3) ^ 8*((c >> 1) & 1):
 //        the 4 rows x 2 column groups one 32-lane ds_read_b64_tr_b16 cycle serves land on
 //        8 distinct 32-byte windows;
@@ -86,15 +90,39 @@ struct FastGemm {
   static constexpr int kRowsPerInstrKM = 1024 / kRowKM;
   static constexpr int kStageA = TILE * kRowA;     // bytes per operand tile (either layout)
   static constexpr int kStageB = DK * TILE * 2;
-  static constexpr int kStage = kStageA + kStageB;
   static constexpr int kInstrA = kStageA / 1024 / 4;  // direct-to-LDS instructions per wave per stage
   static constexpr int kInstrB = kStageB / 1024 / 4;
   static constexpr int kInstr = kInstrA + kInstrB;
   static constexpr int kRowsPerInstrA = 1024 / kRowA;
-  static_assert(kStage * STAGES <= 160 * 1024, "stages exceed the 160 KiB LDS");
   static_assert(kInstr * (STAGES - 2) <= 63, "vmcnt field");
 
+  // A given as [M, K] (K-contiguous) is staged in pairs of K slices: a region holds the tile's
+  // TILE rows of 2*DK k, 128-byte rows, so that every copy reads whole 128-byte cache lines
+  // (64-byte row pieces, one slice each, took ~3% of the GEMM's rate).  Pair P (slices 2P and
+  // 2P+1) lives in region P % 3; its upper-row and lower-row halves are copied during slices
+  // 2P-4 and 2P-3, when the pair that used the region before (P-3, slices 2P-6 and 2P-5) has
+  // been read.  Slice kt reads its pair's k-half kt & 1.  Three regions of 2*DK k and a B ring
+  // of STAGES slices fill the 160 KiB LDS.
+  static constexpr bool kPairA = !AKM;
+  static constexpr int kRowP = 4 * DK;             // bytes per paired A row
+  static constexpr int kChunksP = kRowP / 16;
+  static constexpr int kRowsPerWindowP = 256 / kRowP;
+  static constexpr int kRowsPerInstrP = 1024 / kRowP;
+  static constexpr int kRegionA = kPairA ? TILE * kRowP : kStageA;
+  static constexpr int kRegionsA = kPairA ? 3 : STAGES;
+  static constexpr int kRingA = kRegionsA * kRegionA;
+  static constexpr int kLdsRing = kRingA + STAGES * kStageB;
+  static_assert(!kPairA || (DK == 32 && STAGES == 4), "paired A: 128-byte rows and a lead of three slices");
+  static_assert(kLdsRing <= 160 * 1024, "stages exceed the 160 KiB LDS");
+
+  // LDS byte offsets of slice kt's A stage (unpaired A) and B stage.  A paired A's region is
+  // carried through the loops; its k-half is selected by XOR-ing bit 6 into the fragment
+  // offsets (the upper half's chunks sit at slots c ^ 4 of the lower half's).
+  static __device__ __forceinline__ int a_region(int kt) { return (kt % STAGES) * kStageA; }
+  static __device__ __forceinline__ int b_stage(int kt) { return kRingA + (kt % STAGES) * kStageB; }
+
   static __device__ __forceinline__ int a_slot(int c, int r) { return c ^ ((r / kRowsPerWindow) % kChunksA); }
+  static __device__ __forceinline__ int p_slot(int c, int r) { return c ^ ((r / kRowsPerWindowP) % kChunksP); }
   static __device__ __forceinline__ int b_slot(int c, int k) { return c ^ ((k & 3) << 1) ^ (((c >> 1) & 1) << 3); }
   static __device__ __forceinline__ int b_logical(int p, int k) {
     const int x = p ^ ((k & 3) << 1);
@@ -147,15 +175,36 @@ struct FastGemm {
     }
   }
 
+  // Paired A.  Copy instruction j = 4i + wave of a half holds region rows
+  // h*TILE/2 + j*RPI + lane / CP (RPI = 8 rows of CP = 8 chunks), slot lane % CP; the swizzle
+  // term (r / 2) % 8 = (4j + lane / 16) % 8 depends on j only through j & 1 = wave & 1.
+  static __device__ __forceinline__ int pair_row(int wave, int lane) {
+    return (wave & 1) * kRowsPerInstrP + lane / kChunksP;
+  }
+  static __device__ __forceinline__ uint32_t pair_copy_off(int64_t K, int wave, int lane) {
+    return 2u * static_cast<uint32_t>((lane / kChunksP) * K + p_slot(lane % kChunksP, pair_row(wave, lane)) * 8);
+  }
+  static __device__ __forceinline__ void pair_frag_off(int base, int lane, int (&o)[4]) {
+    const int r = base + (lane & 31);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) o[kk] = kk < DK / 16 ? r * kRowP + p_slot(2 * kk + (lane >> 5), r) * 16 : 0;
+  }
+
   static __device__ __forceinline__ Lane lane_plan(int64_t M, int64_t N, int64_t K, int wave, int wm, int wn,
                                                    int lane) {
     Lane L;
-    L.a = copy_off(AKM, M, K, wave, lane);
+    if constexpr (kPairA) {
+      L.a = pair_copy_off(K, wave, lane);
+      L.ka = p_slot(lane % kChunksP, pair_row(wave, lane)) * 8;
+      pair_frag_off(wm * (TILE / 2), lane, L.fa);
+    } else {
+      L.a = copy_off(AKM, M, K, wave, lane);
+      L.ka = copy_k(AKM, wave, lane);
+      frag_off(AKM, 0, wm * (TILE / 2), 32, lane, L.fa);
+    }
     L.b = copy_off(BKM, N, K, wave, lane);
-    L.ka = copy_k(AKM, wave, lane);
     L.kb = copy_k(BKM, wave, lane);
-    frag_off(AKM, 0, wm * (TILE / 2), 32, lane, L.fa);
-    frag_off(BKM, kStageA, wn * 32, 64, lane, L.fb);
+    frag_off(BKM, 0, wn * 32, 64, lane, L.fb);
     return L;
   }
 
@@ -229,11 +278,63 @@ struct FastGemm {
     }
   }
 
-  static __device__ __forceinline__ void copy_slice(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-                                                    int64_t M, int64_t N, int64_t K, int64_t m0, int64_t n0,
-                                                    int64_t k0, uint32_t stage, int wave, const Lane& L) {
-    copy_operand<AKM, kInstrA>(A, A + M * K, M, K, m0, k0, stage, wave, L.a, L.ka);
-    copy_operand<BKM, kInstrB>(B, B + K * N, N, K, n0, k0, stage + kStageA, wave, L.b, L.kb);
+  // With an odd number of K slices (more than one) the last A pair holds a single slice.
+  static __device__ __forceinline__ bool single_last(int KT) { return (KT & 1) && KT > 1; }
+
+  // Where half h of A pair P comes from and goes to.  A single-slice last pair is copied from
+  // one slice lower (k0 - DK), so that no lane of an interior tile reads past K, and its slice
+  // is read from the upper k-half.  Pairs past the last are placeholders that keep every
+  // slice's copy count fixed (the waits count instructions): they re-read the last pair into a
+  // region that no slice reads again.
+  struct PairSrc {
+    const uint16_t* base;  // the half's first row at the pair's first k
+    int64_t k_left;        // k from there to K
+    uint32_t dst;          // LDS address of the half
+  };
+  // First k copied for pair P (last: index of the last pair; single: the last pair's index if it
+  // holds one slice, else -1).
+  static __device__ __forceinline__ int64_t pair_k0(int P, int last, int single) {
+    const int pr = P < last ? P : last;
+    return static_cast<int64_t>(pr) * 2 * DK - (pr == single ? DK : 0);
+  }
+  // rows: A + (m0 + h*TILE/2)*K; k0: pair_k0 of the pair; region: where the pair goes.
+  static __device__ __forceinline__ PairSrc pair_src(const uint16_t* rows, int64_t K, int64_t k0, int region, int h,
+                                                     uint32_t lds_addr) {
+    return {rows + k0, K - k0, lds_addr + static_cast<uint32_t>(region * kRegionA + h * (TILE / 2) * kRowP)};
+  }
+
+  // Copy instruction j of a pair half (end: one past A's last element).
+  static __device__ __forceinline__ void copy_pair(const PairSrc& ps, const uint16_t* end, int64_t K, int j,
+                                                   const Lane& L) {
+    const uint32_t ioff = static_cast<uint32_t>(j * kRowsPerInstrP * K * 2);
+    if constexpr (EDGE)
+      dma16(rsrc_of(ps.base, end), L.ka < ps.k_left ? L.a + ioff : kNoRecord, ps.dst + j * 1024);
+    else
+      dma16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(ps.base) + ioff), L.a, ps.dst + j * 1024);
+  }
+
+  // All of this wave's instructions of A pair P (both halves) into region P (prologue: P < 3).
+  static __device__ __forceinline__ void copy_pair_all(const uint16_t* rows0, const uint16_t* rows1,
+                                                       const uint16_t* end, int64_t K, int P, int last, int single,
+                                                       int wave, const Lane& L, uint32_t lds_addr) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const PairSrc ps = pair_src(h ? rows1 : rows0, K, pair_k0(P, last, single), P, h, lds_addr);
+#pragma unroll
+      for (int i = 0; i < kInstrA; ++i) copy_pair(ps, end, K, 4 * i + wave, L);
+    }
+  }
+
+  // This wave's share of K slice s of B (and of an unpaired A).
+  static __device__ __forceinline__ void copy_b(const uint16_t* __restrict__ B, int64_t N, int64_t K, int64_t n0, int s,
+                                                int wave, const Lane& L, uint32_t lds_addr) {
+    copy_operand<BKM, kInstrB>(B, B + K * N, N, K, n0, static_cast<int64_t>(s) * DK, lds_addr + b_stage(s), wave, L.b,
+                               L.kb);
+  }
+  static __device__ __forceinline__ void copy_a(const uint16_t* __restrict__ A, int64_t M, int64_t K, int64_t m0, int s,
+                                                int wave, const Lane& L, uint32_t lds_addr) {
+    copy_operand<AKM, kInstrA>(A, A + M * K, M, K, m0, static_cast<int64_t>(s) * DK, lds_addr + a_region(s), wave, L.a,
+                               L.ka);
   }
 
   // Wait until at most `pending` slices of this wave's copies are still in flight
@@ -257,13 +358,14 @@ struct FastGemm {
     bf16x8_t a[kBlk], b[kBlk];
   };
 
+  // Fragment reads of one k16 step from slice bases `st` (hx: the k-half XOR of a paired A).
   template <bool kKMajor>
-  static __device__ __forceinline__ void read_operand(const lds_char_t* st, int kk, const int (&o)[4], int blk_stride,
-                                                      bf16x8_t (&f)[kBlk]) {
+  static __device__ __forceinline__ void read_operand(const lds_char_t* st, int hx, int kk, const int (&o)[4],
+                                                      int blk_stride, bf16x8_t (&f)[kBlk]) {
 #pragma unroll
     for (int blk = 0; blk < kBlk; ++blk) {
       if (!kKMajor) {
-        f[blk] = *(const lds_bf16x8_t*)(st + o[kk] + blk * blk_stride);
+        f[blk] = *(const lds_bf16x8_t*)(st + (o[kk] ^ hx) + blk * blk_stride);
       } else {
         const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(st + o[blk] + kk * 16 * kRowKM));
         const i16x4_t hi =
@@ -274,9 +376,13 @@ struct FastGemm {
     }
   }
 
-  static __device__ __forceinline__ void read(const lds_char_t* st, int kk, const Lane& L, Frag& f) {
-    read_operand<AKM>(st, kk, L.fa, 32 * kRowA, f.a);
-    read_operand<BKM>(st, kk, L.fb, 64 * kRowA, f.b);
+  // Bytes between the 32-row A blocks of a wave (paired or unpaired rows).
+  static constexpr int kBlkStrideA = 32 * (kPairA ? kRowP : kRowA);
+
+  static __device__ __forceinline__ void read(const lds_char_t* sa, int hx, const lds_char_t* sb, int kk,
+                                              const Lane& L, Frag& f) {
+    read_operand<AKM>(sa, hx, kk, L.fa, kBlkStrideA, f.a);
+    read_operand<BKM>(sb, 0, kk, L.fb, 64 * kRowA, f.b);
   }
 
   // The fragment reads of one k16 step as a flat list of LDS instructions ("slots"): A's
@@ -286,10 +392,10 @@ struct FastGemm {
   static constexpr int kSlots = kSlotsA + (BKM ? 2 * kBlk : kBlk);
 
   template <bool kKMajor>
-  static __device__ __forceinline__ void read_operand_slot(const lds_char_t* st, int kk, const int (&o)[4],
+  static __device__ __forceinline__ void read_operand_slot(const lds_char_t* st, int hx, int kk, const int (&o)[4],
                                                            int blk_stride, bf16x8_t (&f)[kBlk], int slot) {
     if (!kKMajor) {
-      f[slot] = *(const lds_bf16x8_t*)(st + o[kk] + slot * blk_stride);
+      f[slot] = *(const lds_bf16x8_t*)(st + (o[kk] ^ hx) + slot * blk_stride);
     } else {
       const int blk = slot >> 1, half = slot & 1;
       const i16x4_t v =
@@ -304,11 +410,12 @@ struct FastGemm {
     }
   }
 
-  static __device__ __forceinline__ void read_slot(const lds_char_t* st, int kk, const Lane& L, Frag& f, int slot) {
+  static __device__ __forceinline__ void read_slot(const lds_char_t* sa, int hx, const lds_char_t* sb, int kk,
+                                                   const Lane& L, Frag& f, int slot) {
     if (slot < kSlotsA)
-      read_operand_slot<AKM>(st, kk, L.fa, 32 * kRowA, f.a, slot);
+      read_operand_slot<AKM>(sa, hx, kk, L.fa, kBlkStrideA, f.a, slot);
     else
-      read_operand_slot<BKM>(st, kk, L.fb, 64 * kRowA, f.b, slot - kSlotsA);
+      read_operand_slot<BKM>(sb, 0, kk, L.fb, 64 * kRowA, f.b, slot - kSlotsA);
   }
 
   // The MFMAs of B block ni against A blocks lo .. hi-1.
@@ -320,17 +427,26 @@ struct FastGemm {
         acc[ni][mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[ni], f.a[mi], acc[ni][mi], 0, 0, 0);
   }
 
-  // Copy instruction i (0 .. kInstr-1) of a K slice: A's instructions first, then B's.
+  // Copy instruction i (0 .. kInstr-1) issued during slice kt: A's instructions first (ps: half
+  // kt & 1 of pair kt/2 + 2, or slice kt + STAGES - 1 of an unpaired A), then B's (slice
+  // kt + STAGES - 1).
   static __device__ __forceinline__ void copy_instr(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-                                                    int64_t M, int64_t N, int64_t K, int64_t m0, int64_t n0,
-                                                    int64_t k0, uint32_t stage, int wave, const Lane& L, int i) {
+                                                    int64_t M, int64_t N, int64_t K, int64_t m0, int64_t n0, int kt,
+                                                    const PairSrc& ps, uint32_t lds_addr, int wave, const Lane& L,
+                                                    int i) {
+    const int nt = kt + STAGES - 1;
+    const int64_t k0 = static_cast<int64_t>(nt) * DK;
     if (i < kInstrA) {
       const int j = 4 * i + wave;
-      copy_one<AKM>(slice_base<AKM>(A, M, K, m0, k0), A + M * K, M, K, j, L.a, K - k0, L.ka, stage + j * 1024);
+      if constexpr (kPairA)
+        copy_pair(ps, A + M * K, K, j, L);
+      else
+        copy_one<AKM>(slice_base<AKM>(A, M, K, m0, k0), A + M * K, M, K, j, L.a, K - k0, L.ka,
+                      lds_addr + a_region(nt) + j * 1024);
     } else {
       const int j = 4 * (i - kInstrA) + wave;
       copy_one<BKM>(slice_base<BKM>(B, N, K, n0, k0), B + K * N, N, K, j, L.b, K - k0, L.kb,
-                    stage + kStageA + j * 1024);
+                    lds_addr + b_stage(nt) + j * 1024);
     }
   }
 
@@ -349,21 +465,22 @@ constexpr int c_pitch() {
   return TILE * 2 + 16;
 }
 
-// LDS bytes of the stage ring, which after the main loop holds the bf16 C tile.
-template <int DK, int STAGES, int TILE>
+// LDS bytes of the operand rings, which after the main loop hold the bf16 C tile and the
+// tile's bias values.
+template <int DK, int STAGES, bool AKM, bool BKM, int TILE>
 constexpr int fast_lds_bytes() {
-  constexpr int ring = STAGES * FastGemm<DK, STAGES, false, true, false, TILE>::kStage;
-  return ring > TILE * c_pitch<TILE>() ? ring : TILE * c_pitch<TILE>();
+  constexpr int ring = FastGemm<DK, STAGES, AKM, BKM, false, TILE>::kLdsRing;
+  constexpr int tail = TILE * c_pitch<TILE>() + TILE * 4;
+  return ring > tail ? ring : tail;
 }
 
-// One TILE x TILE C tile at (m0, n0); lds_raw / bias_lds are the kernel's LDS.  CU: C rows
-// are not 16-byte aligned (N % 8 != 0, only with B given as [N, K]); C is then written with
-// 2-byte stores.
+// One TILE x TILE C tile at (m0, n0); lds_raw is the kernel's LDS.  CU: C rows are not 16-byte
+// aligned (N % 8 != 0, only with B given as [N, K]); C is then written with 2-byte stores.
 template <int DK, int STAGES, bool AKM, bool BKM, bool EDGE, int TILE, bool CU>
 __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                const float* __restrict__ bias, uint16_t* __restrict__ C, int64_t M,
-                                               int64_t N, int64_t K, int relu, int64_t m0, int64_t n0, char* lds_raw,
-                                               float* bias_lds) {
+                                               int64_t N, int64_t K, int relu, int64_t m0, int64_t n0,
+                                               char* lds_raw) {
   using G = FastGemm<DK, STAGES, AKM, BKM, EDGE, TILE>;
   constexpr int kBlk = G::kBlk;
   constexpr int kCPitch = c_pitch<TILE>();
@@ -380,20 +497,49 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) acc[i][j] = f32x16_t{};
 
-  // The tile's TILE bias values are staged in LDS now, so the epilogue does not wait on global
-  // loads (their latency hides behind the prologue copies; the prologue barrier publishes them).
-  if (threadIdx.x < TILE)
-    bias_lds[threadIdx.x] = bias != nullptr && (!EDGE || n0 + threadIdx.x < N) ? bias[n0 + threadIdx.x] : 0.0f;
+  // The tile's TILE bias values are loaded now, one per thread, so the epilogue does not wait
+  // on global loads; they are staged in LDS after the main loop, whose rings fill the LDS.
+  const float bias_v =
+      threadIdx.x < TILE && bias != nullptr && (!EDGE || n0 + threadIdx.x < N) ? bias[n0 + threadIdx.x] : 0.0f;
 
   const typename G::Lane L = G::lane_plan(M, N, K, wave, wm, wn, lane);
   const int KT = static_cast<int>((K + DK - 1) / DK);  // a ragged last slice only in edge instances
   // Slice kt's copies fill the stage slice kt-1 used, so a copy is issued kLead slices ahead.
   constexpr int kLead = STAGES - 1;
-  // Prologue: slices 0 .. kLead-1 in flight, then slice 0 must land.
+  // Paired A: row bases of the two halves of the tile, the last pair, and the last pair (or
+  // slice) again when it holds a single slice (else -1).
+  const uint16_t* const a_rows0 = A + m0 * K;
+  const uint16_t* const a_rows1 = A + (m0 + TILE / 2) * K;
+  const int last_pair = (KT - 1) >> 1;
+  const int single_pair = G::single_last(KT) ? last_pair : -1;
+  const int single_slice = G::single_last(KT) ? KT - 1 : -1;
+  if constexpr (G::kPairA) {
+    // Prologue: A pairs 0 and 1 (slices 0-3) and B slices 0-2 in flight, in the order
+    // [pair 0, B 0] [B 1] [pair 1, B 2], then the first group must land.  With the steady
+    // loop's kInstr copies per slice, the waits below stay exact: when slice kt+1 must land,
+    // every copy issued up to slice kt-2 (B slice kt+1, pair (kt+1)/2) is complete.
+    G::copy_pair_all(a_rows0, a_rows1, A + M * K, K, 0, last_pair, single_pair, wave, L, lds_addr);
+    G::copy_b(B, N, K, n0, 0, wave, L, lds_addr);
+    if (KT > 1) G::copy_b(B, N, K, n0, 1, wave, L, lds_addr);
+    if (KT > 2) {
+      G::copy_pair_all(a_rows0, a_rows1, A + M * K, K, 1, last_pair, single_pair, wave, L, lds_addr);
+      G::copy_b(B, N, K, n0, 2, wave, L, lds_addr);
+      G::template wait_vm<2 * G::kInstr>();
+    } else if (KT > 1) {
+      G::template wait_vm<G::kInstrB>();
+    } else {
+      G::template wait_vm<0>();
+    }
+  } else {
+    // Prologue: slices 0 .. kLead-1 in flight, then slice 0 must land.
 #pragma unroll
-  for (int s = 0; s < kLead; ++s)
-    if (s < KT) G::copy_slice(A, B, M, N, K, m0, n0, static_cast<int64_t>(s) * DK, lds_addr + s * G::kStage, wave, L);
-  G::wait_copies((KT < kLead ? KT : kLead) - 1);
+    for (int s = 0; s < kLead; ++s)
+      if (s < KT) {
+        G::copy_a(A, M, K, m0, s, wave, L, lds_addr);
+        G::copy_b(B, N, K, n0, s, wave, L, lds_addr);
+      }
+    G::wait_copies((KT < kLead ? KT : kLead) - 1);
+  }
   __syncthreads();
 
   // Main loop, software-pipelined per k16 step.  A step is kBlk quarters of kBlk MFMAs (one
@@ -419,20 +565,37 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
   // of slice kt+kLead issued before the last step
   constexpr int kSteadyPending = (kLead - 2) * G::kInstr + (NK - 1) * kPerStep;
   typename G::Frag f[2];
-  G::read(lds, 0, L, f[0]);
-  auto slice = [&](int kt, auto copy_tag, int pending) {
+  G::read(lds + (G::kPairA ? 0 : G::a_region(0)), 0, lds + G::b_stage(0), 0, L, f[0]);
+  // Slice kt.  pa: region of its A pair (paired A); a_k0: pair_k0 of the pair it copies
+  // (kt/2 + 2); par_tag: kt & 1 when known at compile time (-1: read kt).  Steady slices
+  // (copy_tag true) never hold the single-slice last pair, so their k-halves follow kt & 1.
+  auto slice = [&](int kt, int pa, int64_t a_k0, auto copy_tag, auto par_tag, int pending) {
     constexpr bool kCopy = decltype(copy_tag)::value;
-    const lds_char_t* st = lds + (kt % STAGES) * G::kStage;
-    const int nt = kt + kLead;
-    const uint32_t cdst = lds_addr + (nt % STAGES) * G::kStage;
-    const int64_t ck0 = static_cast<int64_t>(nt) * DK;
+    constexpr int kPar = decltype(par_tag)::value;
+    const int odd = kPar >= 0 ? kPar : (kt & 1);
+    const int pa1 = odd ? (pa == 2 ? 0 : pa + 1) : pa;
+    const lds_char_t* sa = lds + (G::kPairA ? pa * G::kRegionA : G::a_region(kt));
+    const lds_char_t* sa1 = lds + (G::kPairA ? pa1 * G::kRegionA : G::a_region(kt + 1));
+    int hx = odd << 6, hx1 = (odd ^ 1) << 6;
+    if (!kCopy) {
+      hx = kt == single_slice ? 64 : hx;
+      hx1 = kt + 1 == single_slice ? 64 : hx1;
+    }
+    if (!G::kPairA) hx = hx1 = 0;
+    const lds_char_t* sb = lds + G::b_stage(kt);
+    // A copies of this slice: half kt & 1 of pair kt/2 + 2, into the region pair kt/2 - 1 used
+    typename G::PairSrc ps{};
+    if constexpr (kCopy && G::kPairA)
+      ps = G::pair_src(odd ? a_rows1 : a_rows0, K, a_k0, pa == 0 ? 2 : pa - 1, odd, lds_addr);
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       typename G::Frag& cur = f[kk & 1];
       typename G::Frag& nxt = f[(kk & 1) ^ 1];
       const bool boundary = kk + 1 == NK;
       const bool more = !boundary || pending >= 0;  // a next step exists
-      const lds_char_t* rs = boundary ? lds + ((kt + 1) % STAGES) * G::kStage : st;
+      const lds_char_t* ra = boundary ? sa1 : sa;
+      const lds_char_t* rb = boundary ? lds + G::b_stage(kt + 1) : sb;
+      const int rhx = boundary ? hx1 : hx;
       const int rk = boundary ? 0 : kk + 1;
 #pragma unroll
       for (int q = 0; q < kBlk; ++q) {
@@ -451,7 +614,7 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
         const int from = pre ? kPre : 0;
         if (more) {
 #pragma unroll
-          for (int r = 0; r < kPerQ; ++r) G::read_slot(rs, rk, L, nxt, q * kPerQ + r);
+          for (int r = 0; r < kPerQ; ++r) G::read_slot(ra, rhx, rb, rk, L, nxt, q * kPerQ + r);
         }
         G::mfma_range(cur, acc, q, from, kBlk);
         if (more) {
@@ -464,17 +627,33 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
         if constexpr (kCopy) {
           if (q < kPerStep) {
             __builtin_amdgcn_sched_barrier(0);
-            G::copy_instr(A, B, M, N, K, m0, n0, ck0, cdst, wave, L, kk * kPerStep + q);
+            G::copy_instr(A, B, M, N, K, m0, n0, kt, ps, lds_addr, wave, L, kk * kPerStep + q);
           }
         }
       }
     }
   };
-  int kt = 0;
-  // steady state: every slice copies, and waits for a fixed number of copies
-  for (; kt + kLead < KT; ++kt) slice(kt, std::true_type{}, 0);
+  using Even = std::integral_constant<int, 0>;
+  using Odd = std::integral_constant<int, 1>;
+  using AnyPar = std::integral_constant<int, -1>;
+  int kt = 0, pa = 0;
+  // steady state: every slice copies, and waits for a fixed number of copies; two slices (one
+  // A pair) per iteration, then at most one more
+  for (; kt + 1 + kLead < KT; kt += 2) {
+    const int64_t a_k0 = G::pair_k0((kt >> 1) + 2, last_pair, single_pair);
+    slice(kt, pa, a_k0, std::true_type{}, Even{}, 0);
+    slice(kt + 1, pa, a_k0, std::true_type{}, Odd{}, 0);
+    pa = pa == 2 ? 0 : pa + 1;
+  }
+  if (kt + kLead < KT) {
+    slice(kt, pa, G::pair_k0((kt >> 1) + 2, last_pair, single_pair), std::true_type{}, Even{}, 0);
+    ++kt;
+  }
   // tail: everything is issued; slice kt+1 must land, later ones may stay in flight
-  for (; kt < KT; ++kt) slice(kt, std::false_type{}, kt + 1 < KT ? KT - 2 - kt : -1);
+  for (; kt < KT; ++kt) {
+    slice(kt, pa, 0, std::false_type{}, AnyPar{}, kt + 1 < KT ? KT - 2 - kt : -1);
+    if (kt & 1) pa = pa == 2 ? 0 : pa + 1;
+  }
 
   // Epilogue.  The tile is staged in LDS as bf16 rows and then written out in full 512-byte
   // rows: stored straight from the MFMA layout, every store instruction would write 16 bytes
@@ -483,7 +662,10 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
   // stays NaN) and no ReLU is maximum(t, -inf); v_cvt_pk_bf16_f32 rounds two values to
   // nearest even in one instruction.  One 32x32 block at a time (the empty asm keeps the
   // compiler from pulling all 256 accumulators into VGPRs at once).
-  __syncthreads();  // every wave's last fragment reads are done before the ring is overwritten
+  __syncthreads();  // every wave's last fragment reads are done before the rings are overwritten
+  float* bias_lds = reinterpret_cast<float*>(lds_raw + TILE * kCPitch);
+  if (threadIdx.x < TILE) bias_lds[threadIdx.x] = bias_v;
+  __syncthreads();
   lds_wchar_t* ct = (lds_wchar_t*)lds_raw;
   const float floor_v = relu ? 0.0f : -__builtin_inff();
 #pragma unroll
@@ -540,10 +722,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, const float* __restrict__ bias,
                            uint16_t* __restrict__ C, int64_t M, int64_t N, int64_t K, int relu, int tiles_m,
                            int tiles_n) {
-  constexpr int kLdsBytes = fast_lds_bytes<DK, STAGES, TILE>();
-  static_assert(kLdsBytes + TILE * 4 <= 160 * 1024, "LDS");
+  constexpr int kLdsBytes = fast_lds_bytes<DK, STAGES, AKM, BKM, TILE>();
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) char lds_raw[kLdsBytes];
-  __shared__ float bias_lds[TILE];
 
   int bid = blockIdx.x;
   const int T = gridDim.x;
@@ -554,12 +735,13 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
   const int tm = first_m + (bid % per_group) % gsz, tn = (bid % per_group) / gsz;
   const int64_t m0 = static_cast<int64_t>(tm) * TILE, n0 = static_cast<int64_t>(tn) * TILE;
 
-  // Uniform per workgroup: edge tiles (and every tile when K is not a whole number of K steps)
-  // run the range-checked instance of the tile code.
-  if (m0 + TILE <= M && n0 + TILE <= N && K % DK == 0)
-    gemm_fast_tile<DK, STAGES, AKM, BKM, false, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
+  // Uniform per workgroup: edge tiles (and every tile when K is not a whole number of K steps,
+  // or, with a paired A, a single K step, whose pair would reach past K) run the range-checked
+  // instance of the tile code.
+  if (m0 + TILE <= M && n0 + TILE <= N && K % DK == 0 && (AKM || K > DK))
+    gemm_fast_tile<DK, STAGES, AKM, BKM, false, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw);
   else
-    gemm_fast_tile<DK, STAGES, AKM, BKM, true, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, bias_lds);
+    gemm_fast_tile<DK, STAGES, AKM, BKM, true, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw);
 }
 
 // K step and ring depth of the fast path.
