@@ -133,6 +133,7 @@ struct FastGemm {
   // offsets.  K-contiguous operand: off[kk], blocks at a fixed stride; K-major: off[block].
   struct Lane {
     uint32_t a, b;
+    uint32_t ai[4], bi[4];  // copy offsets per instruction i of a slice (a or b + that instruction's rows)
     int ka, kb;  // first k (within a slice) of the lane's 16-byte chunk; 0 for a K-major operand
     int fa[4], fb[4];
   };
@@ -205,6 +206,15 @@ struct FastGemm {
     L.b = copy_off(BKM, N, K, wave, lane);
     L.kb = copy_k(BKM, wave, lane);
     frag_off(BKM, 0, wn * 32, 64, lane, L.fb);
+    // Instruction j = 4i + wave of a slice starts j*RPI rows (or k-rows) past the slice base;
+    // with that offset in the lane's VGPR the slice base is the only scalar address per slice.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * i + wave;
+      L.ai[i] = i < kInstrA ? L.a + (kPairA ? static_cast<uint32_t>(j * kRowsPerInstrP * K * 2) : instr_off<AKM>(j, M, K))
+                            : 0u;
+      L.bi[i] = i < kInstrB ? L.b + instr_off<BKM>(j, N, K) : 0u;
+    }
     return L;
   }
 
@@ -235,19 +245,18 @@ struct FastGemm {
   // Lane offset that no descriptor covers (operands of a ragged-K launch are < 2 GiB).
   static constexpr uint32_t kNoRecord = 0x80000000u;
 
-  // Copy instruction j of an operand slice starting at `base` (`end`: one past the tensor's
-  // last element; lane offset `off`).  In an edge tile, the lanes of a K-contiguous operand
-  // whose chunk starts at or past K (k_left = K - k0 elements remain from the slice start,
-  // chunk_k = the chunk's first k) take an offset past every record and load zeros; a
-  // K-major operand's k-rows past K lie past the tensor's end.
+  // One copy instruction of an operand slice starting at `base` (`end`: one past the tensor's
+  // last element; voff: the lane's offset for this instruction).  In an edge tile, the lanes
+  // of a K-contiguous operand whose chunk starts at or past K (k_left = K - k0 elements remain
+  // from the slice start, chunk_k = the chunk's first k) take an offset past every record and
+  // load zeros; a K-major operand's k-rows past K lie past the tensor's end.
   template <bool kKMajor>
-  static __device__ __forceinline__ void copy_one(const uint16_t* base, const uint16_t* end, int64_t ld, int64_t K,
-                                                  int j, uint32_t off, int64_t k_left, int chunk_k, uint32_t dst) {
+  static __device__ __forceinline__ void copy_one(const uint16_t* base, const uint16_t* end, uint32_t voff,
+                                                  int64_t k_left, int chunk_k, uint32_t dst) {
     if constexpr (EDGE)
-      dma16(rsrc_of(base, end), kKMajor || chunk_k < k_left ? off + instr_off<kKMajor>(j, ld, K) : kNoRecord, dst);
+      dma16(rsrc_of(base, end), kKMajor || chunk_k < k_left ? voff : kNoRecord, dst);
     else
-      dma16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(base) + instr_off<kKMajor>(j, ld, K)), off,
-            dst);
+      dma16(base, voff, dst);
   }
 
   // Byte offset of copy instruction j from its operand's slice base: tile rows j*RPI.. of a
@@ -269,13 +278,10 @@ struct FastGemm {
   template <bool kKMajor, int kInstrOp>
   static __device__ __forceinline__ void copy_operand(const uint16_t* __restrict__ X, const uint16_t* end, int64_t ld,
                                                       int64_t K, int64_t x0, int64_t k0, uint32_t dst, int wave,
-                                                      uint32_t off, int chunk_k) {
+                                                      const uint32_t (&voff)[4], int chunk_k) {
     const uint16_t* base = slice_base<kKMajor>(X, ld, K, x0, k0);
 #pragma unroll
-    for (int i = 0; i < kInstrOp; ++i) {
-      const int j = 4 * i + wave;
-      copy_one<kKMajor>(base, end, ld, K, j, off, K - k0, chunk_k, dst + j * 1024);
-    }
+    for (int i = 0; i < kInstrOp; ++i) copy_one<kKMajor>(base, end, voff[i], K - k0, chunk_k, dst + (4 * i + wave) * 1024);
   }
 
   // With an odd number of K slices (more than one) the last A pair holds a single slice.
@@ -303,14 +309,15 @@ struct FastGemm {
     return {rows + k0, K - k0, lds_addr + static_cast<uint32_t>(region * kRegionA + h * (TILE / 2) * kRowP)};
   }
 
-  // Copy instruction j of a pair half (end: one past A's last element).
-  static __device__ __forceinline__ void copy_pair(const PairSrc& ps, const uint16_t* end, int64_t K, int j,
+  // Copy instruction i (rows of instruction j = 4i + wave) of a pair half (end: one past A's
+  // last element).
+  static __device__ __forceinline__ void copy_pair(const PairSrc& ps, const uint16_t* end, int i, int wave,
                                                    const Lane& L) {
-    const uint32_t ioff = static_cast<uint32_t>(j * kRowsPerInstrP * K * 2);
+    const uint32_t dst = ps.dst + (4 * i + wave) * 1024;
     if constexpr (EDGE)
-      dma16(rsrc_of(ps.base, end), L.ka < ps.k_left ? L.a + ioff : kNoRecord, ps.dst + j * 1024);
+      dma16(rsrc_of(ps.base, end), L.ka < ps.k_left ? L.ai[i] : kNoRecord, dst);
     else
-      dma16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(ps.base) + ioff), L.a, ps.dst + j * 1024);
+      dma16(ps.base, L.ai[i], dst);
   }
 
   // All of this wave's instructions of A pair P (both halves) into region P (prologue: P < 3).
@@ -321,19 +328,19 @@ struct FastGemm {
     for (int h = 0; h < 2; ++h) {
       const PairSrc ps = pair_src(h ? rows1 : rows0, K, pair_k0(P, last, single), P, h, lds_addr);
 #pragma unroll
-      for (int i = 0; i < kInstrA; ++i) copy_pair(ps, end, K, 4 * i + wave, L);
+      for (int i = 0; i < kInstrA; ++i) copy_pair(ps, end, i, wave, L);
     }
   }
 
   // This wave's share of K slice s of B (and of an unpaired A).
   static __device__ __forceinline__ void copy_b(const uint16_t* __restrict__ B, int64_t N, int64_t K, int64_t n0, int s,
                                                 int wave, const Lane& L, uint32_t lds_addr) {
-    copy_operand<BKM, kInstrB>(B, B + K * N, N, K, n0, static_cast<int64_t>(s) * DK, lds_addr + b_stage(s), wave, L.b,
+    copy_operand<BKM, kInstrB>(B, B + K * N, N, K, n0, static_cast<int64_t>(s) * DK, lds_addr + b_stage(s), wave, L.bi,
                                L.kb);
   }
   static __device__ __forceinline__ void copy_a(const uint16_t* __restrict__ A, int64_t M, int64_t K, int64_t m0, int s,
                                                 int wave, const Lane& L, uint32_t lds_addr) {
-    copy_operand<AKM, kInstrA>(A, A + M * K, M, K, m0, static_cast<int64_t>(s) * DK, lds_addr + a_region(s), wave, L.a,
+    copy_operand<AKM, kInstrA>(A, A + M * K, M, K, m0, static_cast<int64_t>(s) * DK, lds_addr + a_region(s), wave, L.ai,
                                L.ka);
   }
 
@@ -437,16 +444,15 @@ struct FastGemm {
     const int nt = kt + STAGES - 1;
     const int64_t k0 = static_cast<int64_t>(nt) * DK;
     if (i < kInstrA) {
-      const int j = 4 * i + wave;
       if constexpr (kPairA)
-        copy_pair(ps, A + M * K, K, j, L);
+        copy_pair(ps, A + M * K, i, wave, L);
       else
-        copy_one<AKM>(slice_base<AKM>(A, M, K, m0, k0), A + M * K, M, K, j, L.a, K - k0, L.ka,
-                      lds_addr + a_region(nt) + j * 1024);
+        copy_one<AKM>(slice_base<AKM>(A, M, K, m0, k0), A + M * K, L.ai[i], K - k0, L.ka,
+                      lds_addr + a_region(nt) + (4 * i + wave) * 1024);
     } else {
-      const int j = 4 * (i - kInstrA) + wave;
-      copy_one<BKM>(slice_base<BKM>(B, N, K, n0, k0), B + K * N, N, K, j, L.b, K - k0, L.kb,
-                    lds_addr + b_stage(nt) + j * 1024);
+      const int ib = i - kInstrA;
+      copy_one<BKM>(slice_base<BKM>(B, N, K, n0, k0), B + K * N, L.bi[ib], K - k0, L.kb,
+                    lds_addr + b_stage(nt) + (4 * ib + wave) * 1024);
     }
   }
 
