@@ -336,8 +336,11 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
     if rows > 1 and not (N % 4 == 0 and N <= 4096):
         raise HipLoweringError(f"{rows} rows per workgroup needs the one-wave-per-row softmax (N % 4 == 0, "
                                f"N <= 4096); N = {N} runs one row per workgroup")
-    if N % 4 == 0 and N <= 4096:  # a wave per row, 4 rows per workgroup unless a knob says otherwise
+    if N % 4 == 0 and N <= 4096:  # 4 rows per workgroup unless a knob says otherwise: a wave per
+        # row, or for N <= 1024 and 4 rows two waves of two rows each
         launch = _row_launch(M, rows or 4)
+        if N <= 1024 and (rows or 4) == 4:
+            launch = HipLaunch(launch.grid, (128, 1, 1), 0)
     elif N % 4 == 0 and N <= 65536:  # kW waves per row, one row per workgroup, partials in LDS
         kw = next(w for w in (2, 4, 8, 16) if N // 4 <= 1024 * w)
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)

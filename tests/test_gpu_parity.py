@@ -485,13 +485,16 @@ def _gemm_abi(hip, A, B, bias, M, N, K, ta=False, tb=False, offset=0):
 @pytest.mark.parametrize("M,N,K", [(300, 264, 64), (8, 8, 32), (257, 8, 32), (513, 520, 96), (1000, 1000, 256),
                                    (2000, 136, 4096), (300, 264, 1000), (257, 136, 40), (64, 64, 8), (512, 512, 264),
                                    (4100, 4104, 72), (4100, 4104, 64), (3968, 4104, 1000),
+                                   (4096, 4352, 32), (4096, 4352, 96), (4352, 4096, 160),
                                    (300, 263, 64), (1000, 1001, 256), (257, 50257, 64), (4100, 4099, 64)])
 def test_gemm_edge_tiles_fast_path(hip, M, N, K, ta, tb):
     """Shapes that are not multiples of the tile or of the 32-deep K step, with 16-byte aligned
     rows (K % 8 == 0; M % 8 != 0 sends a transposed A to the guarded kernel), run
     the tiled fast kernel with range-checked copies, k-chunks past K loaded as zeros and
     masked edge stores: 128x128 tiles up to 128 tiles of 256x256, 256x256 tiles above (4100 x
-    4104 and the like).  N % 8 != 0 (the last four shapes) runs the tiled kernel with 2-byte C
+    4104 and the like).  4096 x 4352 with K = 32, 96, 160 (1, 3 and 5 K slices) runs full 256x256
+    tiles with a single K slice (range-checked, a paired A would reach past K) and with a last A
+    pair that holds one slice.  N % 8 != 0 (the last four shapes) runs the tiled kernel with 2-byte C
     stores when B is given as [N, K], the guarded kernel otherwise.  Judged against the oracle,
     and bit for bit against the guarded kernel (same MFMA over the same k order) run on 2-byte
     aligned copies."""

@@ -79,7 +79,8 @@ def test_softmax_rows_per_workgroup_knob(rows):
     ir = WORKLOADS["softmax"].ir()
     k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 1000, "N": 1024, "HIP_ROWS_PER_WG": rows})
     assert k.kernel_id == "ihip_softmax_rows_f32_ex" and k.call_args[-1] == ("i32", rows)
-    assert k.launch.block[0] == 64 * rows and k.launch.grid[0] == -(-1000 // rows)
+    # four rows of 1024 floats run as two waves of two rows each
+    assert k.launch.block[0] == (128 if rows == 4 else 64 * rows) and k.launch.grid[0] == -(-1000 // rows)
     k2 = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 1000, "N": 1024}, schedule_override={"tile_m": rows})
     assert k2.call_args == k.call_args and k2.launch == k.launch
 
