@@ -142,6 +142,25 @@ int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const floa
                                 int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
                                 void* stream);
 
+/* Workspace bytes ihip_gemm_bf16_bias_relu_ws needs for this shape: 0 when every operand's
+ * rows can start 16-byte aligned (K % 8 == 0, N % 8 == 0 with B given as [K, N], M % 8 == 0
+ * with A given as [K, M]); else room for K-contiguous copies of the operands that cannot,
+ * K rounded up to 8, 256-byte aligned.  Same shapes and layouts as the entries above (the
+ * reference allocates nothing for matmul: its kernels take any shape in place,
+ * intentir_to_cuda.py:537-985). */
+int64_t ihip_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int transpose_a, int transpose_b);
+
+/* ihip_gemm_bf16_bias_relu_ex with a caller workspace (256-byte aligned, workspace_bytes
+ * long; NULL / 0 allowed): operands the tiled kernel cannot read in place are copied into
+ * it as K-contiguous rows of K rounded up to 8 elements (zeros past K) and the tiled kernel
+ * runs on the copies; C rows that are not 16-byte aligned are written with 2-byte stores.
+ * Results are bit-identical to the guarded kernel's (the same zeros in the same k slots,
+ * the same MFMA order), which runs when the workspace is too small.  The workspace must
+ * stay untouched until the launch completes on the stream. */
+int ihip_gemm_bf16_bias_relu_ws(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                                int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
+                                void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Generic element-wise program: any chain of element-wise ops over inputs that
  * broadcast, transpose or repeat along the axes of one iteration space (rank <= 4).

@@ -32,6 +32,9 @@ hipError_t launch_bias_gelu_axpy_bf16(const uint16_t*, const uint16_t*, uint16_t
                                       hipStream_t);
 hipError_t launch_gemm_bf16_bias_relu(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t,
                                       int64_t, bool, bool, int, int, hipStream_t);
+hipError_t launch_gemm_bf16_bias_relu_ws(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t,
+                                         int64_t, bool, bool, int, int, void*, int64_t, hipStream_t);
+int64_t gemm_workspace_bytes(int64_t, int64_t, int64_t, bool, bool);
 hipError_t launch_elementwise_program(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*,
                                       int, const int64_t (&)[4], hipStream_t);
 hipError_t launch_elementwise_jit(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*, int,
@@ -298,6 +301,28 @@ int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const floa
                tile);
   return finish(ihip::launch_gemm_bf16_bias_relu(A, B, bias, C, M, N, K, transpose_a != 0, transpose_b != 0, relu,
                                                  tile, static_cast<hipStream_t>(stream)),
+                "gemm_bf16_bias_relu");
+}
+
+int64_t ihip_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int transpose_a, int transpose_b) {
+  if (numel2(M, K) < 0 || numel2(K, N) < 0 || numel2(M, N) < 0) return 0;
+  return ihip::gemm_workspace_bytes(M, N, K, transpose_a != 0, transpose_b != 0);
+}
+
+int ihip_gemm_bf16_bias_relu_ws(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                                int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
+  IHIP_REQUIRE(numel2(M, K) >= 0 && numel2(K, N) >= 0 && numel2(M, N) >= 0,
+               "gemm_bf16_bias_relu: invalid shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  IHIP_REQUIRE(M == 0 || N == 0 || C != nullptr, "gemm_bf16_bias_relu: C is null");
+  IHIP_REQUIRE(M == 0 || N == 0 || K == 0 || (A != nullptr && B != nullptr), "gemm_bf16_bias_relu: A or B is null");
+  IHIP_REQUIRE(tile == 0 || tile == 128 || tile == 256, "gemm_bf16_bias_relu: tile %d is not 0 (automatic), 128 or 256",
+               tile);
+  IHIP_REQUIRE(workspace_bytes >= 0 && (workspace_bytes == 0 || workspace != nullptr),
+               "gemm_bf16_bias_relu: workspace of %lld bytes at a null pointer", (long long)workspace_bytes);
+  return finish(ihip::launch_gemm_bf16_bias_relu_ws(A, B, bias, C, M, N, K, transpose_a != 0, transpose_b != 0, relu,
+                                                    tile, workspace, workspace_bytes,
+                                                    static_cast<hipStream_t>(stream)),
                 "gemm_bf16_bias_relu");
 }
 

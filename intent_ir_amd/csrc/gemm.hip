@@ -239,7 +239,11 @@ void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* 
 bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, bool transpose_b, const void* A, const void* B,
                     const void* C);
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
-                            int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s);
+                            int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s,
+                            bool c_unaligned);
+hipError_t launch_gemm_packed(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                              int64_t N, int64_t K, bool ta, bool tb, int relu, int tile, void* ws, int64_t ws_bytes,
+                              hipStream_t s);
 
 template <bool kTA, bool kTB, int TB>
 static hipError_t launch_guarded(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
@@ -269,10 +273,25 @@ hipError_t launch_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, cons
                                       hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
   if (gemm_fast_fits(M, N, K, transpose_a, transpose_b, A, B, C))
-    return launch_gemm_fast(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, s);
+    return launch_gemm_fast(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, s, false);
   const int tb = tile != 0 ? tile : gemm_fast_tile_extent(M, N);
   return tb == 128 ? launch_guarded_tb<128>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s)
                    : launch_guarded_tb<256>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
+}
+
+// The same with a workspace (ws, ws_bytes; may be null / 0): operands the tiled kernel cannot
+// read in place are packed into it and the tiled kernel runs on the copies (gemm_pack.hip);
+// without a large enough workspace the guarded kernel runs, as above.
+hipError_t launch_gemm_bf16_bias_relu_ws(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C,
+                                         int64_t M, int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu,
+                                         int tile, void* ws, int64_t ws_bytes, hipStream_t s) {
+  if (M == 0 || N == 0) return hipSuccess;
+  if (!gemm_fast_fits(M, N, K, transpose_a, transpose_b, A, B, C)) {
+    const hipError_t e =
+        launch_gemm_packed(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, ws, ws_bytes, s);
+    if (e != hipErrorNotSupported) return e;
+  }
+  return launch_gemm_bf16_bias_relu(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, s);
 }
 
 }  // namespace ihip

@@ -807,10 +807,12 @@ static void launch_tiles(const uint16_t* A, const uint16_t* B, const float* bias
 }
 
 // transpose_a: A is given as [K, M]; transpose_b: B is given as [N, K].  tile: 0 = by grid
-// size (gemm_fast_tile_extent), else 128 or 256.
+// size (gemm_fast_tile_extent), else 128 or 256.  c_unaligned: C's base is not 16-byte aligned
+// (only with transpose_b): C is written with 2-byte stores, as for N % 8 != 0.
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
-                            int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s) {
-  const bool small = (tile == 0 ? gemm_fast_tile_extent(M, N) : tile) == 128, cu = N % 8 != 0;
+                            int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s,
+                            bool c_unaligned) {
+  const bool small = (tile == 0 ? gemm_fast_tile_extent(M, N) : tile) == 128, cu = N % 8 != 0 || c_unaligned;
   if (small && cu)
     launch_tiles<128, true>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
   else if (small)

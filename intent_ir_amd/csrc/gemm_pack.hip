@@ -1,0 +1,127 @@
+// Packed GEMM path: operands the tiled kernel cannot read in place (rows that do not start
+// 16 bytes aligned: K % 8 != 0, N % 8 != 0 with B given as [K, N], M % 8 != 0 with A given as
+// [K, M], or 2-byte aligned bases) are first copied into a caller workspace as K-contiguous
+// rows of K8 = K rounded up to 8 elements, zero past K, and the tiled kernel then runs on the
+// copies (A as [M, K8], B as [N, K8]; C rows that are not 16-byte aligned are written with
+// 2-byte stores).  The zeros past K add exact zeros in the k slots the guarded kernel also
+// fills with zeros, and both kernels issue the same MFMAs in the same k order, so the result
+// is bit-identical to the guarded kernel's.
+//
+// Packing is one HBM pass per packed operand (read R x K, write R x K8 elements):
+//  * a K-contiguous source (A [M, K], B [N, K]) is re-pitched row by row: each thread writes
+//    8 consecutive elements (one 16-byte store) from 2-byte loads, since the source rows
+//    start at any even address;
+//  * a K-major source (A [K, M], B [K, N]) is transposed through LDS in 64 x 64 tiles, read
+//    and written along rows of 128 bytes.
+#include "common.hpp"
+
+namespace ihip {
+
+bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, bool transpose_b, const void* A, const void* B,
+                    const void* C);
+hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
+                            int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s,
+                            bool c_unaligned);
+
+namespace {
+
+constexpr int64_t kWsAlign = 256;
+
+int64_t round8(int64_t k) { return (k + 7) / 8 * 8; }
+int64_t align_up(int64_t b) { return (b + kWsAlign - 1) / kWsAlign * kWsAlign; }
+
+// Which operands the shape alone sends through a packed copy (pointer alignment aside).
+bool shape_packs_a(int64_t M, int64_t K, bool ta) { return K % 8 != 0 || (ta && M % 8 != 0); }
+bool shape_packs_b(int64_t N, int64_t K, bool tb) { return K % 8 != 0 || (!tb && N % 8 != 0); }
+
+// dst [R, K8] from a K-contiguous src [R, K] (leading dimension K).
+__global__ __launch_bounds__(256) void pack_rows_kc(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                    int64_t R, int64_t K, int64_t K8) {
+  const int64_t chunks = K8 / 8;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= R * chunks) return;
+  const int64_t r = t / chunks, k0 = (t % chunks) * 8;
+  const uint16_t* s = src + r * K;
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t k = k0 + 2 * e;
+    const uint32_t lo = k < K ? s[k] : 0u, hi = k + 1 < K ? s[k + 1] : 0u;
+    w[e] = lo | (hi << 16);
+  }
+  *reinterpret_cast<u32x4*>(dst + r * K8 + k0) = u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// dst [R, K8] from a K-major src [K, R] (leading dimension R): 64 x 64 tiles through LDS.
+constexpr int kT = 64;
+__global__ __launch_bounds__(256) void pack_rows_km(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                    int64_t R, int64_t K, int64_t K8) {
+  __shared__ uint16_t tile[kT][kT + 2];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kT, k0 = static_cast<int64_t>(blockIdx.y) * kT;
+  const int c = threadIdx.x & (kT - 1), q = threadIdx.x >> 6;  // 4 row groups of 64 lanes
+  // read: src row k0 + i holds r0 .. r0+63 contiguously
+  for (int i = q; i < kT; i += 4) {
+    const int64_t k = k0 + i, r = r0 + c;
+    tile[i][c] = (k < K && r < R) ? src[k * R + r] : 0;
+  }
+  __syncthreads();
+  // write: dst row r0 + i gets k0 .. k0+63 (zeros past K; K8 may end inside the tile)
+  for (int i = q; i < kT; i += 4) {
+    const int64_t r = r0 + i, k = k0 + c;
+    if (r < R && k < K8) dst[r * K8 + k] = tile[c][i];
+  }
+}
+
+hipError_t pack(const uint16_t* src, uint16_t* dst, int64_t R, int64_t K, bool kmajor, hipStream_t s) {
+  const int64_t K8 = round8(K);
+  if (!kmajor) {
+    const int64_t threads = R * (K8 / 8);
+    pack_rows_kc<<<dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s>>>(src, dst, R, K, K8);
+  } else {
+    const dim3 grid(static_cast<unsigned>((R + kT - 1) / kT), static_cast<unsigned>((K8 + kT - 1) / kT));
+    pack_rows_km<<<grid, dim3(256), 0, s>>>(src, dst, R, K, K8);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Workspace bytes the packed path needs for this shape (0: the shape needs no packed copy;
+// operands whose only problem is a 2-byte aligned base are packed too when the workspace
+// passed at launch is large enough for them).
+int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool ta, bool tb) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const int64_t K8 = round8(K);
+  return (shape_packs_a(M, K, ta) ? align_up(M * K8 * 2) : 0) + (shape_packs_b(N, K, tb) ? align_up(N * K8 * 2) : 0);
+}
+
+// The packed path, or hipErrorNotSupported when it does not apply (then the caller runs the
+// guarded kernel): the tiled kernel's size limits on the packed shape, and a workspace that
+// holds every operand that must be packed.
+hipError_t launch_gemm_packed(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                              int64_t N, int64_t K, bool ta, bool tb, int relu, int tile, void* ws, int64_t ws_bytes,
+                              hipStream_t s) {
+  if (ws == nullptr || K <= 0 || (reinterpret_cast<uintptr_t>(ws) & (kWsAlign - 1)) != 0) return hipErrorNotSupported;
+  const int64_t K8 = round8(K);
+  const bool c_unaligned = N % 8 != 0 || (reinterpret_cast<uintptr_t>(C) & 15) != 0;
+  const bool pa = shape_packs_a(M, K, ta) || (reinterpret_cast<uintptr_t>(A) & 15) != 0;
+  // C written with 2-byte stores needs B as [N, K]: pack B then too
+  const bool pb = shape_packs_b(N, K, tb) || (reinterpret_cast<uintptr_t>(B) & 15) != 0 || (c_unaligned && !tb);
+  const int64_t a_bytes = pa ? align_up(M * K8 * 2) : 0, b_bytes = pb ? align_up(N * K8 * 2) : 0;
+  if (a_bytes + b_bytes > ws_bytes) return hipErrorNotSupported;
+  uint16_t* a_ws = static_cast<uint16_t*>(ws);
+  uint16_t* b_ws = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + a_bytes);
+  const uint16_t* A2 = pa ? a_ws : A;
+  const uint16_t* B2 = pb ? b_ws : B;
+  const bool ta2 = pa ? false : ta, tb2 = pb ? true : tb;
+  // the tiled kernel's conditions on the packed operands (C's alignment is handled by the
+  // 2-byte store path; a 16-byte aligned stand-in is passed for it)
+  if (!gemm_fast_fits(M, N, K8, ta2, tb2, A2, B2, ws)) return hipErrorNotSupported;
+  hipError_t e = hipSuccess;
+  if (pa) e = pack(A, a_ws, M, K, ta, s);
+  if (e == hipSuccess && pb) e = pack(B, b_ws, N, K, !tb, s);
+  if (e != hipSuccess) return e;
+  return launch_gemm_fast(A2, B2, bias, C, M, N, K8, ta2, tb2, relu, tile, s, c_unaligned);
+}
+
+}  // namespace ihip

@@ -252,23 +252,69 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
             ("tensor", oname), ("i64", M), ("i64", N), ("i64", K)]
     args += [("i32", int(ta)), ("i32", int(tb))] if (ta or tb or tile) else []
     args += [("i32", int(relu))] + ([("i32", tile)] if tile else [])
-    # tiled fast path (any M and N; rows 16-byte aligned) vs guarded kernel, as gemm_fast_fits
-    # decides for 16-byte aligned tensors
-    lim = 1 << 32
-    ragged_k_ok = K % 32 == 0 or (M * K * 2 < (1 << 31) and K * N * 2 < (1 << 31))
-    full = (M > 0 and N > 0 and K > 0 and (N % 8 == 0 or tb) and K % 8 == 0 and (not ta or M % 8 == 0)
-            and K * 512 < lim and N * 128 < lim and M * 128 < lim and ragged_k_ok)
-    # fast path: 256x256 tiles, or 128x128 tiles when at most 128 tiles of 256x256 (half the
-    # CUs) would be busy (gemm_fast_tile_extent); LDS max(4-stage ring, bf16 C tile) + bias:
-    # 256: max(131072, 256 x 528) + 1024, 128: max(65536, 128 x 272) + 512
+    # tiled fast path (any M and N; rows 16-byte aligned), packed copies then the tiled path
+    # (rows that cannot start 16-byte aligned), or the guarded kernel, as gemm_fast_fits and
+    # launch_gemm_packed decide for 16-byte aligned tensors
+    full = _gemm_fast_fits(M, N, K, ta, tb)
+    ws = 0 if full else gemm_workspace_bytes(M, N, K, ta, tb)
+    K8 = _cdiv(K, 8) * 8
+    ta2 = ta and not _gemm_packs_a(M, K, ta)
+    tb2 = tb or _gemm_packs_b(N, K, tb)
+    packed = ws > 0 and _gemm_fast_fits(M, N, K8, ta2, tb2, packed=True)
+    # 256x256 tiles, or 128x128 tiles when at most 128 tiles of 256x256 (half the CUs) would
+    # be busy (gemm_fast_tile_extent)
     t = tile or (128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256)
-    if full:
-        launch = HipLaunch((_cdiv(M, t) * _cdiv(N, t), 1, 1), (256, 1, 1), 136192 if t == 256 else 66048)
+    grid = (max(1, _cdiv(M, t) * _cdiv(N, t)), 1, 1)
+    if full or packed:
+        launch = HipLaunch(grid, (256, 1, 1), _gemm_fast_lds(t, ta2 if packed else ta))
     else:  # guarded kernel: the same tile choice, a double-buffered {A, Bt} tile pair of 64-k slices
-        launch = HipLaunch((max(1, _cdiv(M, t) * _cdiv(N, t)), 1, 1), (256, 1, 1), 147456 if t == 256 else 73728)
+        launch = HipLaunch(grid, (256, 1, 1), 147456 if t == 256 else 73728)
+    if packed:
+        args = [("tensor", a), ("tensor", b), ("tensor", env["bias"][1]) if has_bias else ("null", None),
+                ("tensor", oname), ("i64", M), ("i64", N), ("i64", K), ("i32", int(ta)), ("i32", int(tb)),
+                ("i32", int(relu)), ("i32", tile), ("workspace", ws)]
+        return HipLoweredKernel(c.fn.name, "ihip_gemm_bf16_bias_relu_ws", c.io(names), launch, [oname], dict(c.b),
+                                tuple(args))
     kid = ("ihip_gemm_bf16_bias_relu_ex" if tile else "ihip_gemm_bf16_bias_relu_t" if (ta or tb)
            else "ihip_gemm_bf16_bias_relu")
     return HipLoweredKernel(c.fn.name, kid, c.io(names), launch, [oname], dict(c.b), tuple(args))
+
+
+def _gemm_fast_fits(M: int, N: int, K: int, ta: bool, tb: bool, packed: bool = False) -> bool:
+    """gemm_fast.hip gemm_fast_fits for 16-byte aligned tensors.  packed: the operands are the
+    workspace copies (A as [M, K], B as [N, K] where packed), of the same sizes."""
+    lim = 1 << 32
+    ragged_k_ok = K % 32 == 0 or (M * K * 2 < (1 << 31) and K * N * 2 < (1 << 31))
+    return (M > 0 and N > 0 and K > 0 and (N % 8 == 0 or tb) and K % 8 == 0 and (not ta or M % 8 == 0)
+            and K * 512 < lim and N * 128 < lim and M * 128 < lim and ragged_k_ok)
+
+
+def _gemm_fast_lds(tile: int, ta: bool) -> int:
+    """LDS bytes of the tiled kernel (gemm_fast.hip fast_lds_bytes): the operand rings (A as
+    [M, K]: three paired-slice regions of tile x 128 bytes; A as [K, M]: four stages of
+    tile x 64 bytes; B: four stages of tile x 64 bytes), at least the bf16 C tile (pitch
+    2 * tile + 16) and the bias."""
+    ring = (3 * tile * 128 if not ta else 4 * tile * 64) + 4 * tile * 64
+    return max(ring, tile * (2 * tile + 16) + 4 * tile)
+
+
+def _gemm_packs_a(M: int, K: int, ta: bool) -> bool:
+    return K % 8 != 0 or (ta and M % 8 != 0)
+
+
+def _gemm_packs_b(N: int, K: int, tb: bool) -> bool:
+    return K % 8 != 0 or (not tb and N % 8 != 0)
+
+
+def gemm_workspace_bytes(M: int, N: int, K: int, ta: bool, tb: bool) -> int:
+    """Workspace bytes of ihip_gemm_bf16_bias_relu_ws (gemm_pack.hip gemm_workspace_bytes): a
+    K-contiguous copy, K rounded up to 8 and 256-byte aligned, of each operand whose rows cannot
+    start 16-byte aligned; 0 when none is needed."""
+    if M <= 0 or N <= 0 or K <= 0:
+        return 0
+    k8 = _cdiv(K, 8) * 8
+    al = lambda n: _cdiv(n, 256) * 256  # noqa: E731
+    return (al(M * k8 * 2) if _gemm_packs_a(M, K, ta) else 0) + (al(N * k8 * 2) if _gemm_packs_b(N, K, tb) else 0)
 
 
 def _match_reduce_any(c: _Ctx) -> Optional[HipLoweredKernel]:

@@ -88,6 +88,13 @@ static void row_kernels() {
              IHIP_ERR_INVALID_ARG, "gemm tile 64");
   EXPECT(ihip_gemm_bf16_bias_relu_t(nullptr, nullptr, nullptr, nullptr, 1LL << 40, 1LL << 40, 1LL << 40, 0, 0, 0,
                                     nullptr) == IHIP_ERR_INVALID_ARG, "gemm overflow");
+  EXPECT(ihip_gemm_bf16_bias_relu_ws(nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0, 1, 0, nullptr, 64, nullptr) ==
+             IHIP_ERR_INVALID_ARG, "gemm workspace bytes at null");
+  EXPECT(ihip_gemm_bf16_bias_relu_ws(nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0, 1, 0, nullptr, -1, nullptr) ==
+             IHIP_ERR_INVALID_ARG, "gemm negative workspace");
+  EXPECT(ihip_gemm_workspace_size(1LL << 40, 1LL << 40, 1LL << 40, 0, 0) == 0, "gemm workspace size overflow");
+  EXPECT(ihip_gemm_workspace_size(7, 9, 3, 0, 0) == 256 + 256, "gemm workspace size 7x9x3");
+  EXPECT(ihip_gemm_workspace_size(64, 263, 64, 0, 1) == 0, "gemm workspace size with B as [N, K]");
 }
 
 static void program_checker() {

@@ -28,6 +28,7 @@ import pytest
 
 from intent_ir_amd import lower_intent_to_hip_kernel, run_lowered
 from intent_ir_amd.configs import WORKLOADS, bias_gelu_axpy_ir, matmul_bias_relu2d_ir
+from intent_ir_amd.lowering import gemm_workspace_bytes
 from intent_ir_amd.dtypes import bf16_bits_to_f32, f32_to_bf16_bits, to_compute_f32
 from intent_ir_amd.ir import as_intent
 from oracle.compare import compare_outputs
@@ -481,6 +482,67 @@ def _gemm_abi(hip, A, B, bias, M, N, K, ta=False, tb=False, offset=0):
     return c.cpu().numpy().view(np.uint16).reshape(M, N)
 
 
+def _gemm_ws(hip, A, B, bias, M, N, K, ta=False, tb=False, offset=0, c_offset=0, ws_bytes=None):
+    """C (bf16 bits) through ihip_gemm_bf16_bias_relu_ws with a workspace of ws_bytes (default:
+    ihip_gemm_workspace_size, or room for both operands when a base is misaligned); A, B and C
+    placed offset / c_offset elements past 256-byte aligned allocations."""
+    import ctypes
+
+    import torch
+
+    def dev(bits, off):
+        t = torch.zeros(bits.size + off, dtype=torch.int16, device="cuda")
+        t[off:] = torch.from_numpy(bits.reshape(-1).view(np.int16)).cuda()
+        return t
+
+    a, b = dev(A, offset), dev(B, offset)
+    bt = torch.from_numpy(bias).cuda()
+    c = torch.empty(M * N + c_offset, dtype=torch.int16, device="cuda")
+    if ws_bytes is None:
+        k8 = -(-K // 8) * 8
+        ws_bytes = hip.ihip_gemm_workspace_size(M, N, K, int(ta), int(tb))
+        if offset or c_offset:
+            ws_bytes = 2 * (-(-(M * k8 * 2) // 256) * 256 + -(-(N * k8 * 2) // 256) * 256)
+    ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    st = hip.ihip_gemm_bf16_bias_relu_ws(ctypes.c_void_p(a.data_ptr() + 2 * offset),
+                                         ctypes.c_void_p(b.data_ptr() + 2 * offset), ctypes.c_void_p(bt.data_ptr()),
+                                         ctypes.c_void_p(c.data_ptr() + 2 * c_offset), M, N, K, int(ta), int(tb), 1, 0,
+                                         ctypes.c_void_p(ws.data_ptr() if ws_bytes else None), ws_bytes,
+                                         ctypes.c_void_p(s))
+    assert st == 0, hip.ihip_last_error().decode()
+    torch.cuda.synchronize()
+    return c[c_offset:].cpu().numpy().view(np.uint16).reshape(M, N)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(7, 9, 3), (300, 263, 64), (257, 250, 60), (1000, 1001, 100), (513, 264, 1000),
+                                   (4100, 4099, 72), (4096, 4095, 4095), (31, 4104, 33), (1001, 57, 4104)])
+def test_gemm_packed_path(hip, M, N, K, ta, tb):
+    """Rows that cannot start 16-byte aligned (K % 8 != 0, N % 8 != 0 with B as [K, N], M % 8 != 0
+    with A as [K, M]) are packed into the workspace as K-contiguous rows of K rounded up to 8
+    and run on the tiled kernel: bit for bit the guarded kernel (the same zeros in the same k
+    slots, the same MFMA order), and the oracle's result within the GEMM tolerance.  2-byte
+    aligned bases of A, B or C take the same path when the workspace holds their copies."""
+    w = WORKLOADS["matmul"]
+    b = {"M": M, "N": N, "K": K}
+    inp = w.gen(b, seed=M + 7 * N + 3 * K, sigma=1.0)
+    A = np.ascontiguousarray(inp["A"].T) if ta else inp["A"]
+    B = np.ascontiguousarray(inp["B"].T) if tb else inp["B"]
+    print(f"[case] gemm packed M={M} N={N} K={K} ta={ta} tb={tb}", flush=True)
+    packed = _gemm_ws(hip, A, B, inp["bias"], M, N, K, ta, tb)
+    guarded = _gemm_ws(hip, A, B, inp["bias"], M, N, K, ta, tb, ws_bytes=0)
+    assert np.array_equal(packed, guarded), f"packed and guarded differ in {int((packed != guarded).sum())} elements"
+    if M * N * K <= 1 << 31:
+        ref = oracle_outputs(w.ir(), inp, b)
+        check({"C": bf16_bits_to_f32(packed)}, ref, ["C"], TOL["matmul"], f"packed {b}")
+    if M * N <= 1 << 22:
+        for off, c_off in ((1, 0), (0, 1), (1, 3)):  # misaligned operand or C bases
+            print(f"[case]   offsets {off} {c_off}", flush=True)
+            mis = _gemm_ws(hip, A, B, inp["bias"], M, N, K, ta, tb, offset=off, c_offset=c_off)
+            assert np.array_equal(mis, guarded), f"offsets {off}/{c_off}: {int((mis != guarded).sum())} elements differ"
+
+
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("M,N,K", [(300, 264, 64), (8, 8, 32), (257, 8, 32), (513, 520, 96), (1000, 1000, 256),
                                    (2000, 136, 4096), (300, 264, 1000), (257, 136, 40), (64, 64, 8), (512, 512, 264),
@@ -564,7 +626,9 @@ def test_gemm_transposed_operands(hip, ta, tb, M, N, K):
            "B": np.ascontiguousarray(inp["B"].T) if tb else inp["B"], "bias": inp["bias"]}
     ir = _transposed_ir(ta, tb)
     k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
-    assert k.kernel_id == "ihip_gemm_bf16_bias_relu_t"
+    # rows that cannot start 16-byte aligned (K % 8 != 0) go through the packed path
+    assert k.kernel_id == ("ihip_gemm_bf16_bias_relu_ws" if gemm_workspace_bytes(M, N, K, ta, tb)
+                           else "ihip_gemm_bf16_bias_relu_t")
     out = run_case(ir, tin, b)
     check(out, oracle_outputs(ir, tin, b), ["C"], TOL["matmul_strict"], f"gemm ta={ta} tb={tb} {b}")
     plain = run_case(w.ir(), inp, b)

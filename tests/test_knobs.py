@@ -29,9 +29,9 @@ def test_gemm_tile_binding_knob():
     k = lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 256})
     assert k.kernel_id == "ihip_gemm_bf16_bias_relu_ex"
     assert k.call_args[-3:] == (("i32", 0), ("i32", 1), ("i32", 256))  # transpose_b, relu, tile
-    assert k.launch.grid[0] == 16 and k.launch.lds_bytes == 136192
+    assert k.launch.grid[0] == 16 and k.launch.lds_bytes == 163840
     k = lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 128})
-    assert k.call_args[-1] == ("i32", 128) and k.launch.grid[0] == 64 and k.launch.lds_bytes == 66048
+    assert k.call_args[-1] == ("i32", 128) and k.launch.grid[0] == 64 and k.launch.lds_bytes == 81920
     with pytest.raises(HipLoweringError, match="is not one of"):
         lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 64})
 
@@ -63,15 +63,29 @@ def test_recovered_schedule_is_a_hint_unless_respected():
         lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_RESPECT_SCHEDULE": 1})
 
 
+def test_gemm_tile_knob_on_the_packed_path():
+    ir = WORKLOADS["matmul"].ir()
+    b = {"M": 64, "N": 263, "K": 64}  # N % 8 != 0 with B as [K, N]: B packed, then the tiled kernel
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 256})
+    assert k.kernel_id == "ihip_gemm_bf16_bias_relu_ws" and k.call_args[-2] == ("i32", 256)
+    assert k.call_args[-1] == ("workspace", 263 * 64 * 2 + 256 - 263 * 64 * 2 % 256)
+    assert k.launch.lds_bytes == 163840 and k.launch.grid[0] == 2
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 128})
+    assert k.launch.lds_bytes == 81920 and k.launch.grid[0] == 3
+    auto = lower_intent_to_hip_kernel(ir, shape_bindings=b)  # 2 tiles of 256x256: 128x128 tiles
+    assert auto.launch == k.launch and auto.call_args[-2] == ("i32", 0)
+
+
 def test_gemm_tile_knob_on_the_guarded_kernel():
     ir = WORKLOADS["matmul"].ir()
-    b = {"M": 64, "N": 263, "K": 64}  # N % 8 != 0 with B as [K, N]: the guarded kernel
+    # a ragged K (K % 32 != 0) with operands above 2 GiB, whose rows are 16-byte aligned: the
+    # guarded kernel (the tiled one points ragged k-chunks past every record)
+    b = {"M": 65536, "N": 16384, "K": 40968}
     k = lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 256})
-    assert k.launch.lds_bytes == 147456 and k.launch.grid[0] == 2
+    assert k.kernel_id == "ihip_gemm_bf16_bias_relu_ex"
+    assert k.launch.lds_bytes == 147456 and k.launch.grid[0] == 256 * 64
     k = lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 128})
-    assert k.launch.lds_bytes == 73728 and k.launch.grid[0] == 3
-    auto = lower_intent_to_hip_kernel(ir, shape_bindings=b)  # 2 tiles of 256x256: 128x128 tiles
-    assert auto.launch == k.launch
+    assert k.launch.lds_bytes == 73728 and k.launch.grid[0] == 512 * 128
 
 
 @pytest.mark.parametrize("rows", [1, 2, 4])

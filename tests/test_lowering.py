@@ -11,6 +11,7 @@ import pytest
 
 from intent_ir_amd import HipLoweringError, lower_intent_to_hip_kernel
 from intent_ir_amd.configs import WORKLOADS, matmul_bias_relu2d_ir, softmax_inner_ir
+from intent_ir_amd.lowering import gemm_workspace_bytes
 from intent_ir_amd.ir import IntentFunction, IntentIRValidationError, as_intent
 from intent_ir_amd.macros import expand_macros
 from intent_ir_amd.runtime import LIB_PATH, SIGNATURES
@@ -206,35 +207,58 @@ def test_gemm_forms_and_errors():
     assert lower_intent_to_hip_kernel(ir, shape_bindings=b).call_args[-1] == ("i32", 1)
 
 
-@pytest.mark.parametrize("M,N,K,tile,guarded", [
-    (256, 256, 64, 128, False), (300, 264, 1000, 128, False), (8, 8, 8, 128, False), (4096, 4096, 64, 256, False),
-    (4096, 2048, 64, 128, False), (4096, 2304, 64, 256, False), (4100, 4104, 72, 256, False),
-    (256, 250, 64, 128, True), (256, 256, 60, 128, True), (65536, 16384, 40960, 256, False),
-    (65536, 16384, 40968, 256, True), (5000, 3001, 64, 256, True)])
-def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tile, guarded):
-    """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N (LDS
-    max(4-stage ring, staged C tile) + 256 bias floats), other shapes the guarded kernel (a
-    double-buffered pair of 64-k operand tiles).  Both use 256x256 tiles, or 128x128 tiles when
-    at most 128 tiles of 256x256 (half the CUs) would be busy.  A ragged K needs operands below
-    2 GiB for the tiled kernel."""
+@pytest.mark.parametrize("M,N,K,tile,path", [
+    (256, 256, 64, 128, "fast"), (300, 264, 1000, 128, "fast"), (8, 8, 8, 128, "fast"), (4096, 4096, 64, 256, "fast"),
+    (4096, 2048, 64, 128, "fast"), (4096, 2304, 64, 256, "fast"), (4100, 4104, 72, 256, "fast"),
+    (256, 250, 64, 128, "packed"), (256, 256, 60, 128, "packed"), (65536, 16384, 40960, 256, "fast"),
+    (65536, 16384, 40968, 256, "guarded"), (5000, 3001, 64, 256, "packed"), (7, 9, 3, 128, "packed")])
+def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tile, path):
+    """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N (LDS:
+    three paired-slice A regions and four B stages); other rows are packed into a workspace
+    and then take the tiled kernel; the guarded kernel (a double-buffered pair of 64-k operand
+    tiles) is left for shapes beyond the tiled kernel's limits, such as a ragged K with
+    operands above 2 GiB.  All use 256x256 tiles, or 128x128 tiles when at most 128 tiles of
+    256x256 (half the CUs) would be busy."""
     k = lower_intent_to_hip_kernel(matmul_bias_relu2d_ir(), shape_bindings={"M": M, "N": N, "K": K})
     assert k.launch.grid == (-(-M // tile) * -(-N // tile), 1, 1)
-    assert k.launch.lds_bytes == {(256, False): 136192, (128, False): 66048, (256, True): 147456,
-                                  (128, True): 73728}[(tile, guarded)]
+    assert k.launch.lds_bytes == {(256, "fast"): 163840, (128, "fast"): 81920, (256, "packed"): 163840,
+                                  (128, "packed"): 81920, (256, "guarded"): 147456,
+                                  (128, "guarded"): 73728}[(tile, path)]
+    assert (k.kernel_id == "ihip_gemm_bf16_bias_relu_ws") == (path == "packed")
+    if path == "packed":
+        assert k.call_args[-1] == ("workspace", gemm_workspace_bytes(M, N, K, False, False)) and k.call_args[-1][1] > 0
 
 
-@pytest.mark.parametrize("N,tb,lds", [(50257, True, 136192), (263, True, 66048), (263, False, 73728),
-                                      (50257, False, 147456)])
-def test_gemm_odd_n_takes_the_tiled_kernel_with_b_as_nk(N, tb, lds):
+@pytest.mark.parametrize("N,tb,lds,kid", [(50257, True, 163840, "ihip_gemm_bf16_bias_relu_t"),
+                                          (263, True, 81920, "ihip_gemm_bf16_bias_relu_t"),
+                                          (263, False, 81920, "ihip_gemm_bf16_bias_relu_ws"),
+                                          (50257, False, 163840, "ihip_gemm_bf16_bias_relu_ws")])
+def test_gemm_odd_n_takes_the_tiled_kernel_with_b_as_nk(N, tb, lds, kid):
     """With B given as [N, K] (transpose_b) the rows of A and B stay 16-byte aligned at any N,
-    so the tiled kernel runs (C written with 2-byte stores); B as [K, N] with N % 8 != 0 takes
-    the guarded kernel."""
+    so the tiled kernel runs (C written with 2-byte stores); B as [K, N] with N % 8 != 0 is
+    packed into a workspace as [N, K] first."""
     ir = matmul_bias_relu2d_ir()
     if tb:
         ir["tensors"]["B"]["shape"] = ["N", "K"]
         ir["ops"][0]["attrs"] = {"transpose_b": True}
     k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": 300, "N": N, "K": 64})
-    assert k.launch.lds_bytes == lds
+    assert k.launch.lds_bytes == lds and k.kernel_id == kid
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_gemm_workspace_size_matches_the_library(ta, tb):
+    """The lowering sizes the packed path's workspace by the library's rule
+    (ihip_gemm_workspace_size), pinned here on shapes around every alignment case."""
+    from intent_ir_amd.runtime import load_library
+
+    lib = load_library()
+    for M in (1, 7, 8, 9, 256, 1000, 4099):
+        for N in (1, 8, 263, 264, 50257):
+            for K in (1, 3, 8, 60, 64, 1000, 4095):
+                want = lib.ihip_gemm_workspace_size(M, N, K, int(ta), int(tb))
+                assert gemm_workspace_bytes(M, N, K, ta, tb) == want, (M, N, K, ta, tb)
+    assert lib.ihip_gemm_workspace_size(0, 8, 3, 0, 0) == 0 == gemm_workspace_bytes(0, 8, 3, False, False)
 
 
 def test_unsupported_ops_raise():
