@@ -9,10 +9,10 @@
 //
 // Packing is one HBM pass per packed operand (read R x K, write R x K8 elements):
 //  * a K-contiguous source (A [M, K], B [N, K]) is re-pitched row by row: each thread writes
-//    8 consecutive elements (one 16-byte store) from 2-byte loads, since the source rows
-//    start at any even address;
+//    8 consecutive elements (one 16-byte store) from 4-byte loads when every row starts
+//    4-byte aligned (K even), else from 2-byte loads;
 //  * a K-major source (A [K, M], B [K, N]) is transposed through LDS in 64 x 64 tiles, read
-//    and written along rows of 128 bytes.
+//    along source rows and written in 16-byte stores along destination rows.
 #include "common.hpp"
 
 namespace ihip {
@@ -34,7 +34,9 @@ int64_t align_up(int64_t b) { return (b + kWsAlign - 1) / kWsAlign * kWsAlign; }
 bool shape_packs_a(int64_t M, int64_t K, bool ta) { return K % 8 != 0 || (ta && M % 8 != 0); }
 bool shape_packs_b(int64_t N, int64_t K, bool tb) { return K % 8 != 0 || (!tb && N % 8 != 0); }
 
-// dst [R, K8] from a K-contiguous src [R, K] (leading dimension K).
+// dst [R, K8] from a K-contiguous src [R, K] (leading dimension K); kPairs: every row starts
+// 4-byte aligned (K even, src 4-byte aligned), so pairs of elements load as one dword.
+template <bool kPairs>
 __global__ __launch_bounds__(256) void pack_rows_kc(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                     int64_t R, int64_t K, int64_t K8) {
   const int64_t chunks = K8 / 8;
@@ -46,29 +48,59 @@ __global__ __launch_bounds__(256) void pack_rows_kc(const uint16_t* __restrict__
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int64_t k = k0 + 2 * e;
-    const uint32_t lo = k < K ? s[k] : 0u, hi = k + 1 < K ? s[k + 1] : 0u;
-    w[e] = lo | (hi << 16);
+    if (kPairs) {  // K even: a pair is wholly inside the row or wholly past it
+      w[e] = k < K ? *reinterpret_cast<const uint32_t*>(s + k) : 0u;
+    } else {
+      const uint32_t lo = k < K ? s[k] : 0u, hi = k + 1 < K ? s[k + 1] : 0u;
+      w[e] = lo | (hi << 16);
+    }
   }
   *reinterpret_cast<u32x4*>(dst + r * K8 + k0) = u32x4{w[0], w[1], w[2], w[3]};
 }
 
 // dst [R, K8] from a K-major src [K, R] (leading dimension R): 64 x 64 tiles through LDS.
+// Reads go along src rows (4-byte loads when every row starts 4-byte aligned, kPairs), writes
+// along dst rows in 16-byte stores, 8 lanes per 128-byte row piece.
 constexpr int kT = 64;
+template <bool kPairs>
 __global__ __launch_bounds__(256) void pack_rows_km(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                     int64_t R, int64_t K, int64_t K8) {
   __shared__ uint16_t tile[kT][kT + 2];
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kT, k0 = static_cast<int64_t>(blockIdx.y) * kT;
-  const int c = threadIdx.x & (kT - 1), q = threadIdx.x >> 6;  // 4 row groups of 64 lanes
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   // read: src row k0 + i holds r0 .. r0+63 contiguously
-  for (int i = q; i < kT; i += 4) {
-    const int64_t k = k0 + i, r = r0 + c;
-    tile[i][c] = (k < K && r < R) ? src[k * R + r] : 0;
+  if constexpr (kPairs) {
+    const int c = 2 * (lane & 31);
+    for (int i = 2 * w + (lane >> 5); i < kT; i += 8) {
+      const int64_t k = k0 + i, r = r0 + c;
+      uint32_t v = 0;
+      if (k < K && r + 1 < R) {
+        v = *reinterpret_cast<const uint32_t*>(src + k * R + r);
+      } else if (k < K && r < R) {
+        v = src[k * R + r];
+      }
+      tile[i][c] = static_cast<uint16_t>(v);
+      tile[i][c + 1] = static_cast<uint16_t>(v >> 16);
+    }
+  } else {
+    for (int i = w; i < kT; i += 4) {
+      const int64_t k = k0 + i, r = r0 + lane;
+      tile[i][lane] = (k < K && r < R) ? src[k * R + r] : 0;
+    }
   }
   __syncthreads();
-  // write: dst row r0 + i gets k0 .. k0+63 (zeros past K; K8 may end inside the tile)
-  for (int i = q; i < kT; i += 4) {
-    const int64_t r = r0 + i, k = k0 + c;
-    if (r < R && k < K8) dst[r * K8 + k] = tile[c][i];
+  // write: dst row r0 + i gets k0 .. k0+63 (zeros past K; K8, a multiple of 8, may end inside
+  // the tile), 8 columns per lane
+  const int c8 = lane & 7;
+  for (int i = (lane >> 3) + 8 * w; i < kT; i += 32) {
+    const int64_t r = r0 + i, k = k0 + 8 * c8;
+    if (r < R && k < K8) {
+      uint32_t q[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        q[e] = static_cast<uint32_t>(tile[8 * c8 + 2 * e][i]) | (static_cast<uint32_t>(tile[8 * c8 + 2 * e + 1][i]) << 16);
+      *reinterpret_cast<u32x4*>(dst + r * K8 + k) = u32x4{q[0], q[1], q[2], q[3]};
+    }
   }
 }
 
@@ -76,10 +108,17 @@ hipError_t pack(const uint16_t* src, uint16_t* dst, int64_t R, int64_t K, bool k
   const int64_t K8 = round8(K);
   if (!kmajor) {
     const int64_t threads = R * (K8 / 8);
-    pack_rows_kc<<<dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s>>>(src, dst, R, K, K8);
+    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    if (K % 2 == 0 && (reinterpret_cast<uintptr_t>(src) & 3) == 0)
+      pack_rows_kc<true><<<grid, dim3(256), 0, s>>>(src, dst, R, K, K8);
+    else
+      pack_rows_kc<false><<<grid, dim3(256), 0, s>>>(src, dst, R, K, K8);
   } else {
     const dim3 grid(static_cast<unsigned>((R + kT - 1) / kT), static_cast<unsigned>((K8 + kT - 1) / kT));
-    pack_rows_km<<<grid, dim3(256), 0, s>>>(src, dst, R, K, K8);
+    if (R % 2 == 0 && (reinterpret_cast<uintptr_t>(src) & 3) == 0)
+      pack_rows_km<true><<<grid, dim3(256), 0, s>>>(src, dst, R, K, K8);
+    else
+      pack_rows_km<false><<<grid, dim3(256), 0, s>>>(src, dst, R, K, K8);
   }
   return hipGetLastError();
 }
