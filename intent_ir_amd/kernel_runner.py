@@ -18,12 +18,15 @@ reads come from HBM rather than the Infinity Cache (as in bench.py).  With
 ``--copy-mib`` the run ends with plain device-to-device copies of that size
 (torch ``copy_``), whose FETCH_SIZE/WRITE_SIZE readings calibrate the HBM byte
 counters against a known transfer.  ``--bindings`` replaces the workload's shape
-bindings; ``--transpose-b`` (matmul) gives B as [N, K] with matmul{transpose_b}.
+bindings; ``--transpose-b`` (matmul) gives B as [N, K] with matmul{transpose_b};
+``--no-workspace`` passes an empty workspace, so a GEMM whose operands would be packed runs
+the guarded kernel instead.
 """
 
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import math
 import sys
 
@@ -174,6 +177,8 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-mib", type=int, default=0)
     ap.add_argument("--bindings", default="", help="comma-separated SYMBOL=VALUE overrides, e.g. M=1000,N=4096")
     ap.add_argument("--transpose-b", action="store_true", help="matmul: B given as [N, K] (matmul{transpose_b})")
+    ap.add_argument("--no-workspace", action="store_true",
+                    help="pass an empty workspace (a GEMM that would be packed runs the guarded kernel)")
     args = ap.parse_args(argv)
     if sum(x is not None for x in (args.config, args.ew_chain, args.row_reduce)) != 1:
         ap.error("give exactly one of --config, --ew-chain and --row-reduce")
@@ -204,6 +209,9 @@ def main(argv=None) -> int:
         ir["tensors"]["B"]["shape"] = ["N", "K"]
         ir["ops"][0]["attrs"] = {"transpose_b": True}
     k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    if args.no_workspace:
+        k = dataclasses.replace(k, call_args=tuple(("workspace", 0) if kind == "workspace" else (kind, v)
+                                                   for kind, v in k.call_args))
     shapes = tensor_shapes(k.io_spec, k.bindings)
     per = algorithmic_bytes(args.config, b)
     nsets = 1 if args.config in ("matmul", "gelu") else max(2, math.ceil(ROTATE_MIN_BYTES / per))
