@@ -148,6 +148,9 @@ hipError_t launch_gemm_packed(const uint16_t* A, const uint16_t* B, const float*
   const bool pb = shape_packs_b(N, K, tb) || (reinterpret_cast<uintptr_t>(B) & 15) != 0 || (c_unaligned && !tb);
   const int64_t a_bytes = pa ? align_up(M * K8 * 2) : 0, b_bytes = pb ? align_up(N * K8 * 2) : 0;
   if (a_bytes + b_bytes > ws_bytes) return hipErrorNotSupported;
+  // a transposing copy runs (K8 / 64) x (R / 64) tiles: grid.y holds at most 65535
+  const bool km_copy = (pa && ta) || (pb && !tb);
+  if (km_copy && (K8 + kT - 1) / kT > 65535) return hipErrorNotSupported;
   uint16_t* a_ws = static_cast<uint16_t*>(ws);
   uint16_t* b_ws = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + a_bytes);
   const uint16_t* A2 = pa ? a_ws : A;

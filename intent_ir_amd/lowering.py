@@ -260,7 +260,8 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     K8 = _cdiv(K, 8) * 8
     ta2 = ta and not _gemm_packs_a(M, K, ta)
     tb2 = tb or _gemm_packs_b(N, K, tb)
-    packed = ws > 0 and _gemm_fast_fits(M, N, K8, ta2, tb2, packed=True)
+    km_copy = (ta and not ta2) or (not tb and tb2)  # a transposing copy: (K8 / 64)-tile grid rows
+    packed = ws > 0 and _gemm_fast_fits(M, N, K8, ta2, tb2, packed=True) and not (km_copy and _cdiv(K8, 64) > 65535)
     # 256x256 tiles, or 128x128 tiles when at most 128 tiles of 256x256 (half the CUs) would
     # be busy (gemm_fast_tile_extent)
     t = tile or (128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256)
