@@ -149,7 +149,7 @@ class _Knobs:
             allowed.update(tile_m=(128, 256), tile_n=(128, 256))
         else:  # the binding knob overrides the schedule's tile (as SOFTMAX_THREADS does in the reference)
             self.used |= {"tile_m", "tile_n"}
-        self._fields(allowed, "the GEMM (K slices of 32 in a 4-stage ring, 16-byte copies)")
+        self._fields(allowed, "the GEMM (K slices of 32, 16-byte copies)")
         if knob is not None:
             return knob
         tm, tn = self.sched.get("tile_m"), self.sched.get("tile_n")

@@ -175,6 +175,33 @@ def test_softmax_rows_per_workgroup_knob_gives_identical_results(hip, M, N):
     assert d.ok, d.summary
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 6, 7, 9])
+@pytest.mark.parametrize("N", [4, 64, 100, 512, 1000, 1024])
+def test_softmax_two_rows_per_wave_at_every_row_count(hip, M, N):
+    """Rows of at most 1024 floats run two rows per wave, two waves per workgroup: a wave whose
+    second row is past the last re-reads the last row and must store nothing for it.  Every
+    row count modulo 4 against the one-row-per-wave form (bit for bit) and the oracle; the
+    output buffer's guard rows past M stay untouched."""
+    import torch
+
+    w = WORKLOADS["softmax"]
+    b = {"M": M, "N": N}
+    inp = w.gen(b)
+    k2 = lower_intent_to_hip_kernel(w.ir(), shape_bindings=b)
+    k1 = lower_intent_to_hip_kernel(w.ir(), shape_bindings={**b, "HIP_ROWS_PER_WG": 1})
+    x = torch.from_numpy(inp["input_ptr"]).cuda()
+    outs = []
+    for k in (k2, k1):
+        guard = torch.full((M + 4, N), 7.0, device="cuda")
+        launch_lowered(k, {"input_ptr": x, "output_ptr": guard[:M]})
+        torch.cuda.synchronize()
+        assert torch.all(guard[M:] == 7.0), "a row past M was written"
+        outs.append(guard[:M].cpu().numpy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+    d = compare_outputs({"output_ptr": outs[0]}, _oracle(w.ir(), inp, b), ["output_ptr"], {"atol": 1e-7, "rtol": 1e-5})
+    assert d.ok, d.summary
+
+
 @pytest.mark.parametrize("key", sorted(WORKLOADS))
 def test_run_hip_kernel_called_like_the_reference(hip, key):
     """The call site of the reference smoke test (tests/backends/cuda/test_cuda_backend_smoke.py:55-63),
