@@ -219,6 +219,21 @@ def test_run_hip_kernel_called_like_the_reference(hip, key):
         np.testing.assert_array_equal(out[n], inp[n])
 
 
+def test_run_hip_kernel_with_a_workspace_argument(hip):
+    """A GEMM whose operands are packed carries a ("workspace", bytes) argument in its plan; the
+    reference-shaped call allocates it from io_spec["hip_call"] alone."""
+    w = WORKLOADS["matmul"]
+    b = {"M": 64, "N": 97, "K": 100}
+    k = lower_intent_to_hip_kernel(w.ir(), shape_bindings=b)
+    assert k.kernel_id == "ihip_gemm_bf16_bias_relu_ws" and k.call_args[-1][0] == "workspace"
+    inp = w.gen(b)
+    out = run_hip_kernel(kernel_name=k.kernel_name, kernel_id=k.kernel_id, io_spec=k.io_spec, launch=k.launch,
+                         bindings=k.bindings, inputs_np=inp, output_names=k.output_names)
+    np.testing.assert_array_equal(out["C"], run_lowered(k, inp)["C"])
+    d = compare_outputs({"C": out["C"]}, _oracle(w.ir(), inp, b), ["C"], {"atol": 2e-2, "rtol": 2e-2})
+    assert d.ok, d.summary
+
+
 def test_device_tensor_helpers_round_trip(hip):
     import torch
 
