@@ -142,24 +142,49 @@ int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const floa
                                 int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
                                 void* stream);
 
-/* Workspace bytes ihip_gemm_bf16_bias_relu_ws needs for this shape: 0 when every operand's
- * rows can start 16-byte aligned (K % 8 == 0, N % 8 == 0 with B given as [K, N], M % 8 == 0
- * with A given as [K, M]); else room for K-contiguous copies of the operands that cannot,
- * K rounded up to 8, 256-byte aligned.  Same shapes and layouts as the entries above (the
- * reference allocates nothing for matmul: its kernels take any shape in place,
- * intentir_to_cuda.py:537-985). */
+/* Workspace bytes ihip_gemm_bf16_bias_relu_ws needs for this shape (0: none), 256-byte
+ * aligned pieces in this order:
+ *  - K-contiguous copies, K rounded up to 8, of the operands whose rows cannot start 16-byte
+ *    aligned (K % 8 != 0, N % 8 != 0 with B given as [K, N], M % 8 != 0 with A given as
+ *    [K, M]);
+ *  - split-K partials, S x M x (N rounded up to 4) floats, when the output has fewer than 128
+ *    tiles (256 x 256 tiles, or 128 x 128 tiles when at most 128 of 256 x 256 would be busy):
+ *    S = min(256 / tiles, K8 / 512) segments of a whole number of 64-k steps, K8 = K rounded
+ *    up to 8.
+ * Same shapes and layouts as the entries above (the reference allocates nothing for matmul:
+ * its kernels take any shape in place, intentir_to_cuda.py:537-985). */
 int64_t ihip_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int transpose_a, int transpose_b);
 
 /* ihip_gemm_bf16_bias_relu_ex with a caller workspace (256-byte aligned, workspace_bytes
- * long; NULL / 0 allowed): operands the tiled kernel cannot read in place are copied into
- * it as K-contiguous rows of K rounded up to 8 elements (zeros past K) and the tiled kernel
- * runs on the copies; C rows that are not 16-byte aligned are written with 2-byte stores.
- * Results are bit-identical to the guarded kernel's (the same zeros in the same k slots,
- * the same MFMA order), which runs when the workspace is too small.  The workspace must
- * stay untouched until the launch completes on the stream. */
+ * long; NULL / 0 allowed):
+ *  - operands the tiled kernel cannot read in place are copied into it as K-contiguous rows
+ *    of K rounded up to 8 elements (zeros past K) and the tiled kernel runs on the copies;
+ *    C rows that are not 16-byte aligned are written with 2-byte stores.  Unsplit, results
+ *    are bit-identical to the guarded kernel's (the same zeros in the same k slots, the same
+ *    MFMA order), which runs when the workspace is too small for the copies;
+ *  - a grid of too few tiles (ihip_gemm_workspace_size) is split along K: each segment's
+ *    f32 sums go to the workspace and a second kernel adds the segments in order, then bias
+ *    and activation.  Deterministic; it differs from the unsplit result only by f32
+ *    summation order.  Without room for the partials the launch is unsplit.
+ * The workspace must stay untouched until the launch completes on the stream. */
 int ihip_gemm_bf16_bias_relu_ws(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                                 int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
                                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of a split into `splits` K segments (0: the split rule of
+ * ihip_gemm_workspace_size; 1: none), for operands read in place. */
+int64_t ihip_gemm_splitk_workspace_size(int64_t M, int64_t N, int64_t K, int splits);
+
+/* ihip_gemm_bf16_bias_relu_ex split into `splits` K segments (0: the split rule; 1: unsplit;
+ * at most one per 64 k and at most 1024), for operands the tiled kernel reads in place (K % 8 == 0, M % 8 == 0
+ * with A given as [K, M], N % 8 == 0 with B given as [K, N], A and B 16-byte aligned; any C
+ * alignment), K > 0; IHIP_ERR_INVALID_ARG otherwise or when the workspace (256-byte aligned)
+ * is smaller than ihip_gemm_splitk_workspace_size.  Each segment is a whole number of 64-k
+ * steps.  The split count is a tuning knob with no counterpart in the reference
+ * (intentir_to_cuda.py:537-985 runs one kernel per matmul). */
+int ihip_gemm_bf16_bias_relu_splitk(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                                    int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
+                                    int splits, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Generic element-wise program: any chain of element-wise ops over inputs that

@@ -35,6 +35,9 @@ hipError_t launch_gemm_bf16_bias_relu(const uint16_t*, const uint16_t*, const fl
 hipError_t launch_gemm_bf16_bias_relu_ws(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t,
                                          int64_t, bool, bool, int, int, void*, int64_t, hipStream_t);
 int64_t gemm_workspace_bytes(int64_t, int64_t, int64_t, bool, bool);
+int64_t gemm_splitk_workspace_bytes(int64_t, int64_t, int64_t, int);
+hipError_t launch_gemm_split(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t, int64_t,
+                             bool, bool, int, int, int, void*, int64_t, hipStream_t);
 hipError_t launch_elementwise_program(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*,
                                       int, const int64_t (&)[4], hipStream_t);
 hipError_t launch_elementwise_jit(const ihip_ew_instr*, int, const ihip_ew_operand*, int, const ihip_ew_operand*, int,
@@ -324,6 +327,37 @@ int ihip_gemm_bf16_bias_relu_ws(const uint16_t* A, const uint16_t* B, const floa
                                                     tile, workspace, workspace_bytes,
                                                     static_cast<hipStream_t>(stream)),
                 "gemm_bf16_bias_relu");
+}
+
+int64_t ihip_gemm_splitk_workspace_size(int64_t M, int64_t N, int64_t K, int splits) {
+  if (numel2(M, K) < 0 || numel2(K, N) < 0 || numel2(M, N) < 0 || splits < 0) return 0;
+  return ihip::gemm_splitk_workspace_bytes(M, N, K, splits);
+}
+
+int ihip_gemm_bf16_bias_relu_splitk(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                                    int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
+                                    int splits, void* workspace, int64_t workspace_bytes, void* stream) {
+  IHIP_REQUIRE(numel2(M, K) >= 0 && numel2(K, N) >= 0 && numel2(M, N) >= 0,
+               "gemm_bf16_bias_relu_splitk: invalid shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+               (long long)K);
+  IHIP_REQUIRE(tile == 0 || tile == 128 || tile == 256,
+               "gemm_bf16_bias_relu_splitk: tile %d is not 0 (automatic), 128 or 256", tile);
+  IHIP_REQUIRE(splits >= 0, "gemm_bf16_bias_relu_splitk: splits %d is negative", splits);
+  IHIP_REQUIRE(workspace_bytes >= 0 && (workspace_bytes == 0 || workspace != nullptr),
+               "gemm_bf16_bias_relu_splitk: workspace of %lld bytes at a null pointer", (long long)workspace_bytes);
+  if (M == 0 || N == 0) return 0;
+  IHIP_REQUIRE(K > 0, "gemm_bf16_bias_relu_splitk: K = 0 (nothing to split)");
+  const int64_t need = ihip::gemm_splitk_workspace_bytes(M, N, K, splits);
+  IHIP_REQUIRE(workspace_bytes >= need, "gemm_bf16_bias_relu_splitk: workspace of %lld bytes, %lld needed",
+               (long long)workspace_bytes, (long long)need);
+  IHIP_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
+               "gemm_bf16_bias_relu_splitk: workspace not 256-byte aligned");
+  const hipError_t e = ihip::launch_gemm_split(A, B, bias, C, M, N, K, transpose_a != 0, transpose_b != 0, relu, tile,
+                                               splits, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  IHIP_REQUIRE(e != hipErrorNotSupported,
+               "gemm_bf16_bias_relu_splitk: operands the tiled kernel cannot read in place (K %% 8, a [K, M] A "
+               "with M %% 8, a [K, N] B with N %% 8, or a base not 16-byte aligned)");
+  return finish(e, "gemm_bf16_bias_relu_splitk");
 }
 
 int ihip_gemm_bf16_bias_relu_t(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,

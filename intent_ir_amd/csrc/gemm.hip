@@ -244,6 +244,9 @@ hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* b
 hipError_t launch_gemm_packed(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                               int64_t N, int64_t K, bool ta, bool tb, int relu, int tile, void* ws, int64_t ws_bytes,
                               hipStream_t s);
+hipError_t launch_gemm_split(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                             int64_t N, int64_t K, bool ta, bool tb, int relu, int tile, int splits, void* ws,
+                             int64_t ws_bytes, hipStream_t s);
 
 template <bool kTA, bool kTB, int TB>
 static hipError_t launch_guarded(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
@@ -280,15 +283,18 @@ hipError_t launch_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, cons
 }
 
 // The same with a workspace (ws, ws_bytes; may be null / 0): operands the tiled kernel cannot
-// read in place are packed into it and the tiled kernel runs on the copies (gemm_pack.hip);
-// without a large enough workspace the guarded kernel runs, as above.
+// read in place are packed into it and the tiled kernel runs on the copies, and a grid of too
+// few tiles is split along K with f32 partials in it (gemm_pack.hip); without a large enough
+// workspace the unsplit tiled kernel or the guarded kernel runs, as above.
 hipError_t launch_gemm_bf16_bias_relu_ws(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C,
                                          int64_t M, int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu,
                                          int tile, void* ws, int64_t ws_bytes, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
+  // split-K by the split rule when the workspace holds the partials, else unsplit
+  hipError_t e = launch_gemm_split(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, 0, ws, ws_bytes, s);
+  if (e != hipErrorNotSupported) return e;
   if (!gemm_fast_fits(M, N, K, transpose_a, transpose_b, A, B, C)) {
-    const hipError_t e =
-        launch_gemm_packed(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, ws, ws_bytes, s);
+    e = launch_gemm_packed(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, ws, ws_bytes, s);
     if (e != hipErrorNotSupported) return e;
   }
   return launch_gemm_bf16_bias_relu(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, tile, s);

@@ -63,8 +63,18 @@ typedef __attribute__((address_space(3))) char lds_char_t;
 typedef __attribute__((address_space(3))) char lds_wchar_t;
 typedef __attribute__((address_space(3))) u32x2 lds_u32x2_t;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4_t;
+typedef __attribute__((address_space(3))) f32x4_t lds_f32x4_t;
 
 constexpr int kGroupRows = 8;  // tile-rows per raster group
+
+// The K loop of a launch: KL k from the operands' bases (which a split-K launch offsets into
+// the tensors), and one past each tensor's last element (edge copies are range-checked
+// against the whole tensor).
+struct GemmKRange {
+  const uint16_t* a_end;
+  const uint16_t* b_end;
+  int64_t KL;
+};
 
 typedef __bf16 bf16x2_pk_t __attribute__((ext_vector_type(2)));
 
@@ -277,11 +287,12 @@ struct FastGemm {
   // One operand's share of a K slice: tile rows x0.. (K-contiguous) or k-rows k0.. (K-major).
   template <bool kKMajor, int kInstrOp>
   static __device__ __forceinline__ void copy_operand(const uint16_t* __restrict__ X, const uint16_t* end, int64_t ld,
-                                                      int64_t K, int64_t x0, int64_t k0, uint32_t dst, int wave,
-                                                      const uint32_t (&voff)[4], int chunk_k) {
+                                                      int64_t K, int64_t KL, int64_t x0, int64_t k0, uint32_t dst,
+                                                      int wave, const uint32_t (&voff)[4], int chunk_k) {
     const uint16_t* base = slice_base<kKMajor>(X, ld, K, x0, k0);
 #pragma unroll
-    for (int i = 0; i < kInstrOp; ++i) copy_one<kKMajor>(base, end, voff[i], K - k0, chunk_k, dst + (4 * i + wave) * 1024);
+    for (int i = 0; i < kInstrOp; ++i)
+      copy_one<kKMajor>(base, end, voff[i], KL - k0, chunk_k, dst + (4 * i + wave) * 1024);
   }
 
   // With an odd number of K slices (more than one) the last A pair holds a single slice.
@@ -303,10 +314,11 @@ struct FastGemm {
     const int pr = P < last ? P : last;
     return static_cast<int64_t>(pr) * 2 * DK - (pr == single ? DK : 0);
   }
-  // rows: A + (m0 + h*TILE/2)*K; k0: pair_k0 of the pair; region: where the pair goes.
-  static __device__ __forceinline__ PairSrc pair_src(const uint16_t* rows, int64_t K, int64_t k0, int region, int h,
+  // rows: A + (m0 + h*TILE/2)*K; KL: the k extent of the launch's K loop; k0: pair_k0 of the
+  // pair; region: where the pair goes.
+  static __device__ __forceinline__ PairSrc pair_src(const uint16_t* rows, int64_t KL, int64_t k0, int region, int h,
                                                      uint32_t lds_addr) {
-    return {rows + k0, K - k0, lds_addr + static_cast<uint32_t>(region * kRegionA + h * (TILE / 2) * kRowP)};
+    return {rows + k0, KL - k0, lds_addr + static_cast<uint32_t>(region * kRegionA + h * (TILE / 2) * kRowP)};
   }
 
   // Copy instruction i (rows of instruction j = 4i + wave) of a pair half (end: one past A's
@@ -322,11 +334,11 @@ struct FastGemm {
 
   // All of this wave's instructions of A pair P (both halves) into region P (prologue: P < 3).
   static __device__ __forceinline__ void copy_pair_all(const uint16_t* rows0, const uint16_t* rows1,
-                                                       const uint16_t* end, int64_t K, int P, int last, int single,
+                                                       const uint16_t* end, int64_t KL, int P, int last, int single,
                                                        int wave, const Lane& L, uint32_t lds_addr) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const PairSrc ps = pair_src(h ? rows1 : rows0, K, pair_k0(P, last, single), P, h, lds_addr);
+      const PairSrc ps = pair_src(h ? rows1 : rows0, KL, pair_k0(P, last, single), P, h, lds_addr);
 #pragma unroll
       for (int i = 0; i < kInstrA; ++i) copy_pair(ps, end, i, wave, L);
     }
@@ -334,14 +346,14 @@ struct FastGemm {
 
   // This wave's share of K slice s of B (and of an unpaired A).
   static __device__ __forceinline__ void copy_b(const uint16_t* __restrict__ B, int64_t N, int64_t K, int64_t n0, int s,
-                                                int wave, const Lane& L, uint32_t lds_addr) {
-    copy_operand<BKM, kInstrB>(B, B + K * N, N, K, n0, static_cast<int64_t>(s) * DK, lds_addr + b_stage(s), wave, L.bi,
-                               L.kb);
+                                                int wave, const Lane& L, uint32_t lds_addr, const GemmKRange& R) {
+    copy_operand<BKM, kInstrB>(B, R.b_end, N, K, R.KL, n0, static_cast<int64_t>(s) * DK, lds_addr + b_stage(s), wave,
+                               L.bi, L.kb);
   }
   static __device__ __forceinline__ void copy_a(const uint16_t* __restrict__ A, int64_t M, int64_t K, int64_t m0, int s,
-                                                int wave, const Lane& L, uint32_t lds_addr) {
-    copy_operand<AKM, kInstrA>(A, A + M * K, M, K, m0, static_cast<int64_t>(s) * DK, lds_addr + a_region(s), wave, L.ai,
-                               L.ka);
+                                                int wave, const Lane& L, uint32_t lds_addr, const GemmKRange& R) {
+    copy_operand<AKM, kInstrA>(A, R.a_end, M, K, R.KL, m0, static_cast<int64_t>(s) * DK, lds_addr + a_region(s), wave,
+                               L.ai, L.ka);
   }
 
   // Wait until at most `pending` slices of this wave's copies are still in flight
@@ -440,18 +452,18 @@ struct FastGemm {
   static __device__ __forceinline__ void copy_instr(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                     int64_t M, int64_t N, int64_t K, int64_t m0, int64_t n0, int kt,
                                                     const PairSrc& ps, uint32_t lds_addr, int wave, const Lane& L,
-                                                    int i) {
+                                                    int i, const GemmKRange& R) {
     const int nt = kt + STAGES - 1;
     const int64_t k0 = static_cast<int64_t>(nt) * DK;
     if (i < kInstrA) {
       if constexpr (kPairA)
-        copy_pair(ps, A + M * K, i, wave, L);
+        copy_pair(ps, R.a_end, i, wave, L);
       else
-        copy_one<AKM>(slice_base<AKM>(A, M, K, m0, k0), A + M * K, L.ai[i], K - k0, L.ka,
+        copy_one<AKM>(slice_base<AKM>(A, M, K, m0, k0), R.a_end, L.ai[i], R.KL - k0, L.ka,
                       lds_addr + a_region(nt) + (4 * i + wave) * 1024);
     } else {
       const int ib = i - kInstrA;
-      copy_one<BKM>(slice_base<BKM>(B, N, K, n0, k0), B + K * N, L.bi[ib], K - k0, L.kb,
+      copy_one<BKM>(slice_base<BKM>(B, N, K, n0, k0), R.b_end, L.bi[ib], R.KL - k0, L.kb,
                     lds_addr + b_stage(nt) + (4 * ib + wave) * 1024);
     }
   }
@@ -482,11 +494,14 @@ constexpr int fast_lds_bytes() {
 
 // One TILE x TILE C tile at (m0, n0); lds_raw is the kernel's LDS.  CU: C rows are not 16-byte
 // aligned (N % 8 != 0, only with B given as [N, K]); C is then written with 2-byte stores.
-template <int DK, int STAGES, bool AKM, bool BKM, bool EDGE, int TILE, bool CU>
+// kPartial (split-K): the tile's f32 sums over R's K segment go to P (row-major, ldp floats
+// per row) instead of bias + activation into C.
+template <int DK, int STAGES, bool AKM, bool BKM, bool EDGE, int TILE, bool CU, bool kPartial = false>
 __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                const float* __restrict__ bias, uint16_t* __restrict__ C, int64_t M,
                                                int64_t N, int64_t K, int relu, int64_t m0, int64_t n0,
-                                               char* lds_raw) {
+                                               char* lds_raw, const GemmKRange& R, float* __restrict__ P = nullptr,
+                                               int64_t ldp = 0) {
   using G = FastGemm<DK, STAGES, AKM, BKM, EDGE, TILE>;
   constexpr int kBlk = G::kBlk;
   constexpr int kCPitch = c_pitch<TILE>();
@@ -509,7 +524,7 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
       threadIdx.x < TILE && bias != nullptr && (!EDGE || n0 + threadIdx.x < N) ? bias[n0 + threadIdx.x] : 0.0f;
 
   const typename G::Lane L = G::lane_plan(M, N, K, wave, wm, wn, lane);
-  const int KT = static_cast<int>((K + DK - 1) / DK);  // a ragged last slice only in edge instances
+  const int KT = static_cast<int>((R.KL + DK - 1) / DK);  // a ragged last slice only in edge instances
   // Slice kt's copies fill the stage slice kt-1 used, so a copy is issued kLead slices ahead.
   constexpr int kLead = STAGES - 1;
   // Paired A: row bases of the two halves of the tile, the last pair, and the last pair (or
@@ -524,12 +539,12 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
     // [pair 0, B 0] [B 1] [pair 1, B 2], then the first group must land.  With the steady
     // loop's kInstr copies per slice, the waits below stay exact: when slice kt+1 must land,
     // every copy issued up to slice kt-2 (B slice kt+1, pair (kt+1)/2) is complete.
-    G::copy_pair_all(a_rows0, a_rows1, A + M * K, K, 0, last_pair, single_pair, wave, L, lds_addr);
-    G::copy_b(B, N, K, n0, 0, wave, L, lds_addr);
-    if (KT > 1) G::copy_b(B, N, K, n0, 1, wave, L, lds_addr);
+    G::copy_pair_all(a_rows0, a_rows1, R.a_end, R.KL, 0, last_pair, single_pair, wave, L, lds_addr);
+    G::copy_b(B, N, K, n0, 0, wave, L, lds_addr, R);
+    if (KT > 1) G::copy_b(B, N, K, n0, 1, wave, L, lds_addr, R);
     if (KT > 2) {
-      G::copy_pair_all(a_rows0, a_rows1, A + M * K, K, 1, last_pair, single_pair, wave, L, lds_addr);
-      G::copy_b(B, N, K, n0, 2, wave, L, lds_addr);
+      G::copy_pair_all(a_rows0, a_rows1, R.a_end, R.KL, 1, last_pair, single_pair, wave, L, lds_addr);
+      G::copy_b(B, N, K, n0, 2, wave, L, lds_addr, R);
       G::template wait_vm<2 * G::kInstr>();
     } else if (KT > 1) {
       G::template wait_vm<G::kInstrB>();
@@ -541,8 +556,8 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
 #pragma unroll
     for (int s = 0; s < kLead; ++s)
       if (s < KT) {
-        G::copy_a(A, M, K, m0, s, wave, L, lds_addr);
-        G::copy_b(B, N, K, n0, s, wave, L, lds_addr);
+        G::copy_a(A, M, K, m0, s, wave, L, lds_addr, R);
+        G::copy_b(B, N, K, n0, s, wave, L, lds_addr, R);
       }
     G::wait_copies((KT < kLead ? KT : kLead) - 1);
   }
@@ -592,7 +607,7 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
     // A copies of this slice: half kt & 1 of pair kt/2 + 2, into the region pair kt/2 - 1 used
     typename G::PairSrc ps{};
     if constexpr (kCopy && G::kPairA)
-      ps = G::pair_src(odd ? a_rows1 : a_rows0, K, a_k0, pa == 0 ? 2 : pa - 1, odd, lds_addr);
+      ps = G::pair_src(odd ? a_rows1 : a_rows0, R.KL, a_k0, pa == 0 ? 2 : pa - 1, odd, lds_addr);
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       typename G::Frag& cur = f[kk & 1];
@@ -633,7 +648,7 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
         if constexpr (kCopy) {
           if (q < kPerStep) {
             __builtin_amdgcn_sched_barrier(0);
-            G::copy_instr(A, B, M, N, K, m0, n0, kt, ps, lds_addr, wave, L, kk * kPerStep + q);
+            G::copy_instr(A, B, M, N, K, m0, n0, kt, ps, lds_addr, wave, L, kk * kPerStep + q, R);
           }
         }
       }
@@ -659,6 +674,50 @@ __device__ __forceinline__ void gemm_fast_tile(const uint16_t* __restrict__ A, c
   for (; kt < KT; ++kt) {
     slice(kt, pa, 0, std::false_type{}, AnyPar{}, kt + 1 < KT ? KT - 2 - kt : -1);
     if (kt & 1) pa = pa == 2 ? 0 : pa + 1;
+  }
+
+  if constexpr (kPartial) {
+    // Split-K partial sums in f32, staged through LDS TILE / 2 rows at a time (pass h: the
+    // rows of the two waves with wm == h) and stored as whole rows of TILE floats, TILE / 4
+    // lanes of 16 bytes per row; stored straight
+    // from the MFMA layout, each instruction would write 32 bytes into each of 32 rows.  Rows
+    // past M and 4-column groups at or past N are skipped (ldp, a multiple of 4, covers the
+    // last group).  LDS rows are padded by 16 bytes against bank conflicts.
+    constexpr int kPitchF = TILE + 4;
+    constexpr int kChunkRows = TILE / 2;
+    static_assert(kChunkRows * kPitchF * 4 <= fast_lds_bytes<DK, STAGES, AKM, BKM, TILE>(), "LDS");
+    constexpr int kLanesPerRow = TILE / 4;
+    constexpr int kRowsPerInstr = 64 / kLanesPerRow;
+    lds_f32x4_t* const pt = (lds_f32x4_t*)lds_raw;  // viewed in 16-byte units: kPitchF / 4 per row
+    const int c4 = lane % kLanesPerRow;
+    __syncthreads();  // every wave's last fragment reads are done before the rings are overwritten
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (wm == h) {
+#pragma unroll
+        for (int ni = 0; ni < kBlk; ++ni)
+#pragma unroll
+          for (int mi = 0; mi < kBlk; ++mi) {
+            const int ml = mi * 32 + (lane & 31);
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const int nl = wn * 32 + ni * 64 + g4 * 8 + (lane >> 5) * 4;
+              pt[(ml * kPitchF + nl) / 4] = f32x4_t{acc[ni][mi][g4 * 4], acc[ni][mi][g4 * 4 + 1],
+                                                   acc[ni][mi][g4 * 4 + 2], acc[ni][mi][g4 * 4 + 3]};
+            }
+          }
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int i = 0; i < kChunkRows / (4 * kRowsPerInstr); ++i) {
+        const int row = (i * 4 + wave) * kRowsPerInstr + lane / kLanesPerRow;
+        const int64_t m = m0 + h * kChunkRows + row, n = n0 + c4 * 4;
+        const f32x4_t v = pt[(row * kPitchF) / 4 + c4];
+        if (!EDGE || (m < M && n < N)) *reinterpret_cast<f32x4_t*>(P + m * ldp + n) = v;
+      }
+      if (h == 0) __syncthreads();
+    }
+    return;
   }
 
   // Epilogue.  The tile is staged in LDS as bf16 rows and then written out in full 512-byte
@@ -744,10 +803,91 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
   // Uniform per workgroup: edge tiles (and every tile when K is not a whole number of K steps,
   // or, with a paired A, a single K step, whose pair would reach past K) run the range-checked
   // instance of the tile code.
+  const GemmKRange R{A + M * K, B + K * N, K};
   if (m0 + TILE <= M && n0 + TILE <= N && K % DK == 0 && (AKM || K > DK))
-    gemm_fast_tile<DK, STAGES, AKM, BKM, false, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw);
+    gemm_fast_tile<DK, STAGES, AKM, BKM, false, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, R);
   else
-    gemm_fast_tile<DK, STAGES, AKM, BKM, true, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw);
+    gemm_fast_tile<DK, STAGES, AKM, BKM, true, TILE, CU>(A, B, bias, C, M, N, K, relu, m0, n0, lds_raw, R);
+}
+
+// Split-K: workgroup (tile, s) multiplies K segment s, k in [s * kseg, min((s + 1) * kseg, K)),
+// into the f32 partials P + s * M * ldp.  kseg is a multiple of 64, so every segment but the
+// last is a whole number of A pairs and reads nothing past its end.  One-dimensional grid of
+// tiles x segments: workgroups are dispatched to the XCDs round robin (bid % 8), and each
+// XCD (whose L2 is its own) is given a contiguous run of the segment-major order, tiles in
+// groups of kGroupRows tile-rows walked column by column, so that it reads a compact slab of
+// A and B rather than all of them.
+template <int DK, int STAGES, bool AKM, bool BKM, int TILE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_splitk_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ P,
+                             int64_t M, int64_t N, int64_t K, int64_t kseg, int64_t ldp, int tiles_m, int tiles_n) {
+  constexpr int kLdsBytes = fast_lds_bytes<DK, STAGES, AKM, BKM, TILE>();
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) char lds_raw[kLdsBytes];
+
+  // XCD x runs bids x, x + 8, ...: G / 8 of them, one more for x < G % 8
+  const int G = gridDim.x, xcd = blockIdx.x % kNumXcd;
+  const int bid = xcd * (G / kNumXcd) + (xcd < G % kNumXcd ? xcd : G % kNumXcd) + blockIdx.x / kNumXcd;
+  const int T = tiles_m * tiles_n;
+  const int seg = bid / T, t = bid % T;
+  const int per_group = kGroupRows * tiles_n;
+  const int first_m = (t / per_group) * kGroupRows;
+  const int gsz = (tiles_m - first_m) < kGroupRows ? (tiles_m - first_m) : kGroupRows;
+  const int tm = first_m + (t % per_group) % gsz, tn = (t % per_group) / gsz;
+  const int64_t m0 = static_cast<int64_t>(tm) * TILE, n0 = static_cast<int64_t>(tn) * TILE;
+  const int64_t kb = static_cast<int64_t>(seg) * kseg;
+  const int64_t KL = K - kb < kseg ? K - kb : kseg;
+  const uint16_t* As = AKM ? A + kb * M : A + kb;
+  const uint16_t* Bs = BKM ? B + kb * N : B + kb;
+  float* Ps = P + static_cast<int64_t>(seg) * M * ldp;
+  const GemmKRange R{A + M * K, B + K * N, KL};
+  if (m0 + TILE <= M && n0 + TILE <= N && KL % DK == 0 && (AKM || KL > DK))
+    gemm_fast_tile<DK, STAGES, AKM, BKM, false, TILE, false, true>(As, Bs, nullptr, nullptr, M, N, K, 0, m0, n0,
+                                                                    lds_raw, R, Ps, ldp);
+  else
+    gemm_fast_tile<DK, STAGES, AKM, BKM, true, TILE, false, true>(As, Bs, nullptr, nullptr, M, N, K, 0, m0, n0,
+                                                                   lds_raw, R, Ps, ldp);
+}
+
+// C = act(sum over the S segments of P + bias) in bf16 (round to nearest even), segments added
+// in order 0 .. S-1; one thread per 4 consecutive columns of a row.  C rows are written with
+// one 8-byte store where 8-byte aligned, else with 2-byte stores.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(const float* __restrict__ P, int S, int64_t M, int64_t N,
+                                                          int64_t ldp, const float* __restrict__ bias, int relu,
+                                                          uint16_t* __restrict__ C) {
+  const int64_t groups = ldp / 4;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= M * groups) return;
+  const int64_t m = t / groups, n = (t % groups) * 4;
+  if (n >= N) return;
+  const int64_t plane = M * ldp;
+  const f32x4_t* const src = reinterpret_cast<const f32x4_t*>(P + m * ldp + n);
+  const auto part = [&](int s) { return src[s * (plane / 4)]; };
+  // loads four segments ahead of the additions, which stay in segment order
+  f32x4_t sum = part(0);
+  int s = 1;
+  for (; s + 3 < S; s += 4) {
+    const f32x4_t p1 = part(s), p2 = part(s + 1), p3 = part(s + 2), p4 = part(s + 3);
+    sum += p1;
+    sum += p2;
+    sum += p3;
+    sum += p4;
+  }
+  for (; s < S; ++s) sum += part(s);
+  const float floor_v = relu ? 0.0f : -__builtin_inff();
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    v[q] = __builtin_elementwise_maximum(sum[q] + (bias != nullptr && n + q < N ? bias[n + q] : 0.0f), floor_v);
+  uint16_t* dst = C + m * N + n;
+  const u32x2 pk = {pack_bf16x2_rne(v[0], v[1]), pack_bf16x2_rne(v[2], v[3])};
+  if (n + 4 <= N && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+    *reinterpret_cast<u32x2*>(dst) = pk;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (n + q < N) dst[q] = static_cast<uint16_t>(pk[q >> 1] >> (16 * (q & 1)));
+  }
 }
 
 // K step and ring depth of the fast path.
@@ -821,6 +961,41 @@ hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* b
     launch_tiles<256, true>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
   else
     launch_tiles<256, false>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
+  return hipGetLastError();
+}
+
+// Split-K with S segments of kseg k (gemm_split_k): the tiled kernel writes f32 partials to P
+// (S x M x ldp floats) and gemm_splitk_reduce adds them in order with bias and activation.
+// Same operand conditions as launch_gemm_fast; C may have any alignment.
+template <int TILE>
+static void launch_splitk_tiles(const uint16_t* A, const uint16_t* B, float* P, int64_t M, int64_t N, int64_t K,
+                                int64_t kseg, int S, int64_t ldp, bool ta, bool tb, hipStream_t s) {
+  const int64_t tm = (M + TILE - 1) / TILE, tn = (N + TILE - 1) / TILE;
+  const dim3 grid(static_cast<unsigned>(tm * tn * S)), block(256);
+  const int itm = static_cast<int>(tm), itn = static_cast<int>(tn);
+  constexpr int DK = kFastDK, ST = kFastStages;
+  if (!ta && !tb)
+    gemm_bf16_splitk_kernel<DK, ST, false, true, TILE><<<grid, block, 0, s>>>(A, B, P, M, N, K, kseg, ldp, itm, itn);
+  else if (!ta)
+    gemm_bf16_splitk_kernel<DK, ST, false, false, TILE><<<grid, block, 0, s>>>(A, B, P, M, N, K, kseg, ldp, itm, itn);
+  else if (!tb)
+    gemm_bf16_splitk_kernel<DK, ST, true, true, TILE><<<grid, block, 0, s>>>(A, B, P, M, N, K, kseg, ldp, itm, itn);
+  else
+    gemm_bf16_splitk_kernel<DK, ST, true, false, TILE><<<grid, block, 0, s>>>(A, B, P, M, N, K, kseg, ldp, itm, itn);
+}
+
+hipError_t launch_gemm_splitk(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                              int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, int S,
+                              int64_t kseg, float* P, int64_t ldp, hipStream_t s) {
+  if (tile == 256)
+    launch_splitk_tiles<256>(A, B, P, M, N, K, kseg, S, ldp, transpose_a, transpose_b, s);
+  else
+    launch_splitk_tiles<128>(A, B, P, M, N, K, kseg, S, ldp, transpose_a, transpose_b, s);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t threads = M * (ldp / 4);
+  gemm_splitk_reduce<<<dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s>>>(P, S, M, N, ldp, bias,
+                                                                                             relu, C);
   return hipGetLastError();
 }
 

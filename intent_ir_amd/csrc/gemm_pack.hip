@@ -13,6 +13,14 @@
 //    4-byte aligned (K even), else from 2-byte loads;
 //  * a K-major source (A [K, M], B [K, N]) is transposed through LDS in 64 x 64 tiles, read
 //    along source rows and written in 16-byte stores along destination rows.
+//
+// Split-K: when the output has too few tiles to occupy the CUs, K is cut into S segments, the
+// tiled kernel runs (tile, segment) workgroups that write f32 partial sums into the workspace,
+// and a reduce kernel adds the S partials in segment order, then bias and activation.  The
+// result is deterministic; it differs from the unsplit kernel's only in the f32 summation
+// order.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace ihip {
@@ -22,6 +30,10 @@ bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, bool tran
 hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
                             int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s,
                             bool c_unaligned);
+hipError_t launch_gemm_splitk(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                              int64_t N, int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, int S,
+                              int64_t kseg, float* P, int64_t ldp, hipStream_t s);
+int gemm_fast_tile_extent(int64_t M, int64_t N);
 
 namespace {
 
@@ -29,6 +41,84 @@ constexpr int64_t kWsAlign = 256;
 
 int64_t round8(int64_t k) { return (k + 7) / 8 * 8; }
 int64_t align_up(int64_t b) { return (b + kWsAlign - 1) / kWsAlign * kWsAlign; }
+
+// Split rule.  Grids of 256x256 tiles (more than 128 of them) are not split.  For 128x128
+// tiles the rule picks the S (segments of at least kSplitMinK k, at most 512 workgroups) of
+// least estimated time, in integer nanoseconds:
+//   tile-steps (tiles x 32-k steps) / rate(tiles x S)
+//   + for S > 1: kSplitFixedNs (reduce launch) + S x M x ldp x 8 bytes (partials written and
+//     read back) at kSplitBytesPerNs,
+// where rate(G), tile-steps per microsecond with G workgroups, is interpolated from
+// kSplitRate (measured on MI355X: the rate per workgroup falls as more CUs draw on the power
+// budget and the shared caches) and, past 256 workgroups, scaled by the last wave's fill.
+// Ties go to the smaller S.
+constexpr int64_t kSplitMinK = 512;
+constexpr int64_t kSplitMax = 1024;  // segments at most
+constexpr int64_t kSplitMaxGrid = 512;
+constexpr int64_t kSplitRate[5] = {0, 305, 533, 680, 800};  // at 0, 64, 128, 192, 256 workgroups
+constexpr int64_t kSplitFixedNs = 3500;
+constexpr int64_t kSplitBytesPerNs = 6000;
+
+int64_t split_rate(int64_t G) {
+  if (G >= 256) {
+    const int64_t waves = (G + 255) / 256;
+    return kSplitRate[4] * G / (waves * 256);
+  }
+  const int64_t i = G / 64, f = G % 64;
+  return kSplitRate[i] + (kSplitRate[i + 1] - kSplitRate[i]) * f / 64;
+}
+
+int64_t split_cost_ns(int64_t tiles, int64_t M, int64_t N, int64_t K, int64_t S) {
+  const int64_t rate = std::max<int64_t>(1, split_rate(tiles * S));
+  int64_t ns = tiles * ((K + 31) / 32) * 1000 / rate;
+  if (S > 1) ns += kSplitFixedNs + S * M * ((N + 3) / 4 * 4) * 8 / kSplitBytesPerNs;
+  return ns;
+}
+
+struct SplitPlan {
+  int S;         // segments (1: no split)
+  int64_t kseg;  // k per segment, a multiple of 64 (the last segment may be shorter)
+};
+
+// splits: 0 = by the rule above, else the number asked for (at most one per 64 k, and at
+// most kSplitMax).
+SplitPlan plan_of(int64_t K, int64_t S) {
+  S = std::max<int64_t>(1, std::min<int64_t>({S, (K + 63) / 64, kSplitMax}));
+  const int64_t kseg = ((K + S - 1) / S + 63) / 64 * 64;
+  return {static_cast<int>((K + kseg - 1) / kseg), kseg};
+}
+
+SplitPlan split_plan(int64_t M, int64_t N, int64_t K, int splits) {
+  if (K <= 0) return {1, K};
+  if (splits > 0) return plan_of(K, splits);
+  if (gemm_fast_tile_extent(M, N) != 128) return {1, K};
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  const int64_t smax = std::max<int64_t>(1, std::min({K / kSplitMinK, kSplitMax, kSplitMaxGrid / tiles}));
+  SplitPlan best = {1, K};
+  int64_t best_ns = split_cost_ns(tiles, M, N, K, 1);
+  for (int64_t s = 2; s <= smax; ++s) {
+    const SplitPlan p = plan_of(K, s);
+    const int64_t ns = split_cost_ns(tiles, M, N, K, p.S);
+    if (ns < best_ns) best = p, best_ns = ns;
+  }
+  return best;
+}
+
+// f32 partials of a split: S planes of M rows of N rounded up to 4 floats.
+int64_t split_ldp(int64_t N) { return (N + 3) / 4 * 4; }
+int64_t split_bytes(int64_t M, int64_t N, int S) { return S > 1 ? align_up(S * M * split_ldp(N) * 4) : 0; }
+
+// The tiled kernel on operands it reads in place, split by `plan` when the workspace (ws,
+// ws_bytes) holds the partials, else unsplit.
+hipError_t launch_tiled(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
+                        int64_t K, bool ta, bool tb, int relu, int tile, bool c_unaligned, const SplitPlan& plan,
+                        void* ws, int64_t ws_bytes, hipStream_t s) {
+  if (plan.S > 1 && ws != nullptr && (reinterpret_cast<uintptr_t>(ws) & (kWsAlign - 1)) == 0 &&
+      split_bytes(M, N, plan.S) <= ws_bytes)
+    return launch_gemm_splitk(A, B, bias, C, M, N, K, ta, tb, relu, tile == 0 ? gemm_fast_tile_extent(M, N) : tile,
+                              plan.S, plan.kseg, static_cast<float*>(ws), split_ldp(N), s);
+  return launch_gemm_fast(A, B, bias, C, M, N, K, ta, tb, relu, tile, s, c_unaligned);
+}
 
 // Which operands the shape alone sends through a packed copy (pointer alignment aside).
 bool shape_packs_a(int64_t M, int64_t K, bool ta) { return K % 8 != 0 || (ta && M % 8 != 0); }
@@ -125,13 +215,37 @@ hipError_t pack(const uint16_t* src, uint16_t* dst, int64_t R, int64_t K, bool k
 
 }  // namespace
 
-// Workspace bytes the packed path needs for this shape (0: the shape needs no packed copy;
-// operands whose only problem is a 2-byte aligned base are packed too when the workspace
-// passed at launch is large enough for them).
+// Workspace bytes for this shape: the packed copies it needs, then the split-K partials
+// (0: neither; operands whose only problem is a 2-byte aligned base are packed too when the
+// workspace passed at launch is large enough for them).
 int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool ta, bool tb) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const int64_t K8 = round8(K);
-  return (shape_packs_a(M, K, ta) ? align_up(M * K8 * 2) : 0) + (shape_packs_b(N, K, tb) ? align_up(N * K8 * 2) : 0);
+  return (shape_packs_a(M, K, ta) ? align_up(M * K8 * 2) : 0) + (shape_packs_b(N, K, tb) ? align_up(N * K8 * 2) : 0) +
+         split_bytes(M, N, split_plan(M, N, K8, 0).S);
+}
+
+// Workspace bytes of a split into `splits` segments (0: by the split rule).
+int64_t gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return split_bytes(M, N, split_plan(M, N, K, splits).S);
+}
+
+// The tiled kernel split into `splits` segments (1: unsplit; 0: by the split rule) on
+// operands it reads in place; hipErrorNotSupported when it cannot read them in place or the
+// workspace does not hold the partials.  A split writes C through the reduce kernel, which
+// takes any C alignment; unsplit, a C base that is not 16-byte aligned needs B as [N, K].
+hipError_t launch_gemm_split(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
+                             int64_t N, int64_t K, bool ta, bool tb, int relu, int tile, int splits, void* ws,
+                             int64_t ws_bytes, hipStream_t s) {
+  if (!gemm_fast_fits(M, N, K, ta, tb, A, B, A)) return hipErrorNotSupported;  // C checked below
+  const bool c_unaligned = (reinterpret_cast<uintptr_t>(C) & 15) != 0;
+  const SplitPlan plan = split_plan(M, N, K, splits);
+  if (plan.S > 1 && (ws == nullptr || (reinterpret_cast<uintptr_t>(ws) & (kWsAlign - 1)) != 0 ||
+                     split_bytes(M, N, plan.S) > ws_bytes))
+    return hipErrorNotSupported;
+  if (plan.S == 1 && c_unaligned && !tb) return hipErrorNotSupported;
+  return launch_tiled(A, B, bias, C, M, N, K, ta, tb, relu, tile, c_unaligned, plan, ws, ws_bytes, s);
 }
 
 // The packed path, or hipErrorNotSupported when it does not apply (then the caller runs the
@@ -163,7 +277,8 @@ hipError_t launch_gemm_packed(const uint16_t* A, const uint16_t* B, const float*
   if (pa) e = pack(A, a_ws, M, K, ta, s);
   if (e == hipSuccess && pb) e = pack(B, b_ws, N, K, !tb, s);
   if (e != hipSuccess) return e;
-  return launch_gemm_fast(A2, B2, bias, C, M, N, K8, ta2, tb2, relu, tile, s, c_unaligned);
+  return launch_tiled(A2, B2, bias, C, M, N, K8, ta2, tb2, relu, tile, c_unaligned, split_plan(M, N, K8, 0),
+                      static_cast<char*>(ws) + a_bytes + b_bytes, ws_bytes - a_bytes - b_bytes, s);
 }
 
 }  // namespace ihip

@@ -254,23 +254,27 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     args += [("i32", int(relu))] + ([("i32", tile)] if tile else [])
     # tiled fast path (any M and N; rows 16-byte aligned), packed copies then the tiled path
     # (rows that cannot start 16-byte aligned), or the guarded kernel, as gemm_fast_fits and
-    # launch_gemm_packed decide for 16-byte aligned tensors
+    # launch_gemm_packed decide for 16-byte aligned tensors; the tiled path split along K into
+    # S segments when the grid has too few tiles (gemm_pack.hip split_plan)
     full = _gemm_fast_fits(M, N, K, ta, tb)
-    ws = 0 if full else gemm_workspace_bytes(M, N, K, ta, tb)
+    pack_ws = 0 if full else gemm_pack_bytes(M, N, K, ta, tb)
     K8 = _cdiv(K, 8) * 8
     ta2 = ta and not _gemm_packs_a(M, K, ta)
     tb2 = tb or _gemm_packs_b(N, K, tb)
     km_copy = (ta and not ta2) or (not tb and tb2)  # a transposing copy: (K8 / 64)-tile grid rows
-    packed = ws > 0 and _gemm_fast_fits(M, N, K8, ta2, tb2, packed=True) and not (km_copy and _cdiv(K8, 64) > 65535)
+    packed = (pack_ws > 0 and _gemm_fast_fits(M, N, K8, ta2, tb2, packed=True)
+              and not (km_copy and _cdiv(K8, 64) > 65535))
+    S = gemm_split_plan(M, N, K8)[0] if (full or packed) else 1
+    ws = pack_ws + _gemm_split_bytes(M, N, S) if (full or packed) else 0
     # 256x256 tiles, or 128x128 tiles when at most 128 tiles of 256x256 (half the CUs) would
     # be busy (gemm_fast_tile_extent)
-    t = tile or (128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256)
-    grid = (max(1, _cdiv(M, t) * _cdiv(N, t)), 1, 1)
+    t = tile or _gemm_tile_extent(M, N)
+    grid = (max(1, _cdiv(M, t) * _cdiv(N, t)) * S, 1, 1)  # a split: tiles x segments workgroups
     if full or packed:
         launch = HipLaunch(grid, (256, 1, 1), _gemm_fast_lds(t, ta2 if packed else ta))
     else:  # guarded kernel: the same tile choice, a double-buffered {A, Bt} tile pair of 64-k slices
         launch = HipLaunch(grid, (256, 1, 1), 147456 if t == 256 else 73728)
-    if packed:
+    if ws > 0:
         args = [("tensor", a), ("tensor", b), ("tensor", env["bias"][1]) if has_bias else ("null", None),
                 ("tensor", oname), ("i64", M), ("i64", N), ("i64", K), ("i32", int(ta)), ("i32", int(tb)),
                 ("i32", int(relu)), ("i32", tile), ("workspace", ws)]
@@ -307,15 +311,86 @@ def _gemm_packs_b(N: int, K: int, tb: bool) -> bool:
     return K % 8 != 0 or (not tb and N % 8 != 0)
 
 
-def gemm_workspace_bytes(M: int, N: int, K: int, ta: bool, tb: bool) -> int:
-    """Workspace bytes of ihip_gemm_bf16_bias_relu_ws (gemm_pack.hip gemm_workspace_bytes): a
-    K-contiguous copy, K rounded up to 8 and 256-byte aligned, of each operand whose rows cannot
-    start 16-byte aligned; 0 when none is needed."""
+def _al256(n: int) -> int:
+    return _cdiv(n, 256) * 256
+
+
+def _gemm_tile_extent(M: int, N: int) -> int:
+    """gemm_fast.hip gemm_fast_tile_extent: 128x128 tiles when at most 128 tiles of 256x256
+    (half the CUs) would be busy, else 256x256."""
+    return 128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256
+
+
+_SPLIT_RATE = (0, 305, 533, 680, 800)  # tile-steps per microsecond at 0, 64, 128, 192, 256 workgroups
+
+
+def _split_rate(G: int) -> int:
+    if G >= 256:
+        waves = _cdiv(G, 256)
+        return _SPLIT_RATE[4] * G // (waves * 256)
+    i, f = divmod(G, 64)
+    return _SPLIT_RATE[i] + (_SPLIT_RATE[i + 1] - _SPLIT_RATE[i]) * f // 64
+
+
+def _split_cost_ns(tiles: int, M: int, N: int, K: int, S: int) -> int:
+    ns = tiles * _cdiv(K, 32) * 1000 // max(1, _split_rate(tiles * S))
+    if S > 1:
+        ns += 3500 + S * M * (_cdiv(N, 4) * 4) * 8 // 6000
+    return ns
+
+
+def _split_plan_of(K: int, S: int) -> Tuple[int, int]:
+    S = max(1, min(S, _cdiv(K, 64), 1024))
+    kseg = _cdiv(_cdiv(K, S), 64) * 64
+    return _cdiv(K, kseg), kseg
+
+
+def gemm_split_plan(M: int, N: int, K: int, splits: int = 0) -> Tuple[int, int]:
+    """(S, kseg) of gemm_pack.hip split_plan.  splits > 0: that many segments (at most one per
+    64 k and at most 1024), each but the last of kseg k, a multiple of 64.  splits = 0: grids
+    of 256x256 tiles stay unsplit; for 128x128 tiles, the S (segments of at least 512 k, at
+    most 512 workgroups) of least estimated time: tile-steps over the measured rate at
+    tiles x S workgroups, plus the reduce launch and the partials' round trip; ties go to the
+    smaller S."""
+    if K <= 0:
+        return 1, K
+    if splits > 0:
+        return _split_plan_of(K, splits)
+    if _gemm_tile_extent(M, N) != 128:
+        return 1, K
+    tiles = _cdiv(M, 128) * _cdiv(N, 128)
+    smax = max(1, min(K // 512, 1024, 512 // tiles))
+    best, best_ns = (1, K), _split_cost_ns(tiles, M, N, K, 1)
+    for s in range(2, smax + 1):
+        p = _split_plan_of(K, s)
+        ns = _split_cost_ns(tiles, M, N, K, p[0])
+        if ns < best_ns:
+            best, best_ns = p, ns
+    return best
+
+
+def _gemm_split_bytes(M: int, N: int, S: int) -> int:
+    """f32 partials of a split: S planes of M rows of N rounded up to 4 floats."""
+    return _al256(S * M * _cdiv(N, 4) * 4 * 4) if S > 1 else 0
+
+
+def gemm_pack_bytes(M: int, N: int, K: int, ta: bool, tb: bool) -> int:
+    """Workspace bytes of the packed copies: a K-contiguous copy, K rounded up to 8 and
+    256-byte aligned, of each operand whose rows cannot start 16-byte aligned."""
     if M <= 0 or N <= 0 or K <= 0:
         return 0
     k8 = _cdiv(K, 8) * 8
-    al = lambda n: _cdiv(n, 256) * 256  # noqa: E731
-    return (al(M * k8 * 2) if _gemm_packs_a(M, K, ta) else 0) + (al(N * k8 * 2) if _gemm_packs_b(N, K, tb) else 0)
+    return ((_al256(M * k8 * 2) if _gemm_packs_a(M, K, ta) else 0)
+            + (_al256(N * k8 * 2) if _gemm_packs_b(N, K, tb) else 0))
+
+
+def gemm_workspace_bytes(M: int, N: int, K: int, ta: bool, tb: bool) -> int:
+    """Workspace bytes of ihip_gemm_bf16_bias_relu_ws (gemm_pack.hip gemm_workspace_bytes): the
+    packed copies, then the split-K partials of the split rule on K rounded up to 8; 0 when
+    neither is needed."""
+    if M <= 0 or N <= 0 or K <= 0:
+        return 0
+    return gemm_pack_bytes(M, N, K, ta, tb) + _gemm_split_bytes(M, N, gemm_split_plan(M, N, _cdiv(K, 8) * 8)[0])
 
 
 def _match_reduce_any(c: _Ctx) -> Optional[HipLoweredKernel]:

@@ -53,6 +53,9 @@ SIGNATURES: Dict[str, Tuple[Any, Tuple[Any, ...]]] = {
     "ihip_gemm_bf16_bias_relu_ex": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P)),
     "ihip_gemm_workspace_size": (_I64, (_I64, _I64, _I64, _I32, _I32)),
     "ihip_gemm_bf16_bias_relu_ws": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _I64, _P)),
+    "ihip_gemm_splitk_workspace_size": (_I64, (_I64, _I64, _I64, _I32)),
+    "ihip_gemm_bf16_bias_relu_splitk": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P,
+                                                _I64, _P)),
     "ihip_elementwise_program": (_I32, (_P, _I32, _P, _I32, _P, _I32, _P, _I32, _P)),
     "ihip_elementwise_mode": (_I32, (_I32,)),
     "ihip_elementwise_prepare": (_I32, (_P, _I32, _P, _I32, _P, _I32)),

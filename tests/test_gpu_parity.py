@@ -28,7 +28,7 @@ import pytest
 
 from intent_ir_amd import lower_intent_to_hip_kernel, run_lowered
 from intent_ir_amd.configs import WORKLOADS, bias_gelu_axpy_ir, matmul_bias_relu2d_ir
-from intent_ir_amd.lowering import gemm_workspace_bytes
+from intent_ir_amd.lowering import gemm_pack_bytes, gemm_split_plan, gemm_workspace_bytes
 from intent_ir_amd.dtypes import bf16_bits_to_f32, f32_to_bf16_bits, to_compute_f32
 from intent_ir_amd.ir import as_intent
 from oracle.compare import compare_outputs
@@ -501,8 +501,8 @@ def _gemm_ws(hip, A, B, bias, M, N, K, ta=False, tb=False, offset=0, c_offset=0,
     if ws_bytes is None:
         k8 = -(-K // 8) * 8
         ws_bytes = hip.ihip_gemm_workspace_size(M, N, K, int(ta), int(tb))
-        if offset or c_offset:
-            ws_bytes = 2 * (-(-(M * k8 * 2) // 256) * 256 + -(-(N * k8 * 2) // 256) * 256)
+        if offset or c_offset:  # room for copies of both operands, none for split-K partials
+            ws_bytes = -(-(M * k8 * 2) // 256) * 256 + -(-(N * k8 * 2) // 256) * 256
     ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device="cuda")
     s = torch.cuda.current_stream().cuda_stream
     st = hip.ihip_gemm_bf16_bias_relu_ws(ctypes.c_void_p(a.data_ptr() + 2 * offset),
@@ -513,6 +513,121 @@ def _gemm_ws(hip, A, B, bias, M, N, K, ta=False, tb=False, offset=0, c_offset=0,
     assert st == 0, hip.ihip_last_error().decode()
     torch.cuda.synchronize()
     return c[c_offset:].cpu().numpy().view(np.uint16).reshape(M, N)
+
+
+def _assert_near_unsplit(split, unsplit):
+    """A split-K result against the unsplit kernel's: the two differ only in the order of f32
+    additions, so after rounding to bf16 an element moves by at most a unit or two in its last
+    place (plus a hair of the output's scale where cancellation leaves a small value)."""
+    a, b = bf16_bits_to_f32(split).astype(np.float64), bf16_bits_to_f32(unsplit).astype(np.float64)
+    scale = max(1e-30, float(np.abs(b).max()))
+    bad = np.abs(a - b) > 2.0 ** -7 * np.abs(b) + 1e-5 * scale
+    assert not bad.any(), f"split and unsplit differ beyond rounding in {int(bad.sum())} elements"
+
+
+def _gemm_splitk(hip, A, B, bias, M, N, K, ta, tb, splits, tile=0, c_offset=0):
+    """C (bf16 bits) through ihip_gemm_bf16_bias_relu_splitk with a workspace of exactly
+    ihip_gemm_splitk_workspace_size bytes; C placed c_offset elements past an aligned base."""
+    import ctypes
+
+    import torch
+
+    a = torch.from_numpy(A.reshape(-1).view(np.int16)).cuda()
+    b = torch.from_numpy(B.reshape(-1).view(np.int16)).cuda()
+    bt = torch.from_numpy(bias).cuda()
+    c = torch.full((M * N + c_offset,), 0x7FC0, dtype=torch.int16, device="cuda")  # NaN: unwritten shows
+    wb = hip.ihip_gemm_splitk_workspace_size(M, N, K, splits)
+    ws = torch.full((max(1, wb),), 0xFF, dtype=torch.uint8, device="cuda")  # NaN partials if one is not written
+    s = torch.cuda.current_stream().cuda_stream
+    st = hip.ihip_gemm_bf16_bias_relu_splitk(ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+                                             ctypes.c_void_p(bt.data_ptr()), ctypes.c_void_p(c.data_ptr() + 2 * c_offset),
+                                             M, N, K, int(ta), int(tb), 1, tile, splits,
+                                             ctypes.c_void_p(ws.data_ptr() if wb else None), wb, ctypes.c_void_p(s))
+    assert st == 0, hip.ihip_last_error().decode()
+    torch.cuda.synchronize()
+    return c[c_offset:].cpu().numpy().view(np.uint16).reshape(M, N)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K,splits", [
+    (1024, 1024, 8192, 0),   # the split rule: 64 tiles of 128x128, 4 segments of 2048
+    (1000, 1000, 1000, 3),   # segments 384, 384, 232: the last one ends inside a 32-k step; edge tiles
+    (8, 8, 4096, 64),        # one 64-k step per segment on a one-tile grid
+    (256, 136, 520, 5),      # segments of 128, the last of 8 k (a single ragged K step)
+    (304, 264, 96, 2),       # segments 64 and 32
+    (128, 4104, 2048, 0),    # the rule: 33 tiles, 4 segments
+    (1400, 8, 65536, 0),     # the rule: 11 tiles, 23 segments of 2880 (the last 2176)
+    (4096, 4096, 1024, 2),   # 256x256 tiles, split on request
+])
+def test_gemm_split_k(hip, M, N, K, splits, ta, tb):
+    """Split-K: K cut into segments of whole 64-k steps, each (tile, segment) workgroup's f32
+    sums written to the workspace, then added in segment order with bias and ReLU.  Judged
+    against the oracle, against the unsplit tiled kernel (equal up to f32 summation order),
+    run to run (bit for bit), across the 128 and 256 tile knobs (bit for bit: the same
+    segments in the same MFMA order) and with a 2-byte aligned C (bit for bit)."""
+    w = WORKLOADS["matmul"]
+    b = {"M": M, "N": N, "K": K}
+    inp = w.gen(b, seed=M + 5 * N + 7 * K + splits, sigma=1.0)
+    A = np.ascontiguousarray(inp["A"].T) if ta else inp["A"]
+    B = np.ascontiguousarray(inp["B"].T) if tb else inp["B"]
+    S = gemm_split_plan(M, N, K, splits)[0]
+    print(f"[case] gemm split-K M={M} N={N} K={K} splits={splits} (S={S}) ta={ta} tb={tb}", flush=True)
+    assert S > 1
+    split = _gemm_splitk(hip, A, B, inp["bias"], M, N, K, ta, tb, splits)
+    ref = oracle_outputs(w.ir(), inp, b)
+    check({"C": bf16_bits_to_f32(split)}, ref, ["C"], TOL["matmul"], f"split {b}")
+    check({"C": bf16_bits_to_f32(split)}, ref, ["C"], TOL["matmul_strict"], f"split strict {b}")
+    unsplit = _gemm_splitk(hip, A, B, inp["bias"], M, N, K, ta, tb, 1)
+    assert np.array_equal(unsplit, _gemm_abi(hip, A, B, inp["bias"], M, N, K, ta, tb)), "splits=1 is the tiled kernel"
+    _assert_near_unsplit(split, unsplit)
+    assert np.array_equal(split, _gemm_splitk(hip, A, B, inp["bias"], M, N, K, ta, tb, splits)), "run to run"
+    for tile in (128, 256):
+        other = _gemm_splitk(hip, A, B, inp["bias"], M, N, K, ta, tb, splits, tile=tile)
+        assert np.array_equal(split, other), f"tile {tile}: {int((split != other).sum())} elements differ"
+    assert np.array_equal(split, _gemm_splitk(hip, A, B, inp["bias"], M, N, K, ta, tb, splits, c_offset=1))
+    if splits == 0:  # the workspace entry applies the same rule
+        assert np.array_equal(split, _gemm_ws(hip, A, B, inp["bias"], M, N, K, ta, tb))
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 1001, 4096), (64, 3, 8192), (200, 4097, 4096)])
+def test_gemm_split_k_odd_n_with_b_as_nk(hip, M, N, K):
+    """With B given as [N, K] any N runs in place; the partial rows are padded to a multiple of
+    4 floats and the reduce writes C with 2-byte stores where a row is not 8-byte aligned."""
+    w = WORKLOADS["matmul"]
+    b = {"M": M, "N": N, "K": K}
+    inp = w.gen(b, seed=M + N + K, sigma=1.0)
+    B = np.ascontiguousarray(inp["B"].T)
+    print(f"[case] gemm split-K odd N M={M} N={N} K={K}", flush=True)
+    assert gemm_split_plan(M, N, K)[0] > 1
+    split = _gemm_splitk(hip, inp["A"], B, inp["bias"], M, N, K, False, True, 0)
+    check({"C": bf16_bits_to_f32(split)}, oracle_outputs(w.ir(), inp, b), ["C"], TOL["matmul"], f"split {b}")
+    _assert_near_unsplit(split, _gemm_abi(hip, inp["A"], B, inp["bias"], M, N, K, False, True))
+    assert np.array_equal(split, _gemm_ws(hip, inp["A"], B, inp["bias"], M, N, K, False, True))
+
+
+def test_gemm_split_k_rejects_what_it_cannot_read_in_place(hip):
+    """The explicit split entry takes operands the tiled kernel reads in place only, K > 0, and
+    a workspace of at least ihip_gemm_splitk_workspace_size bytes: anything else is an
+    argument error, with nothing launched."""
+    import ctypes
+
+    import torch
+
+    a = torch.zeros(64 * 1024, dtype=torch.int16, device="cuda")
+    c = torch.zeros(64 * 64, dtype=torch.int16, device="cuda")
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    P = ctypes.c_void_p
+    s = P(torch.cuda.current_stream().cuda_stream)
+    call = lambda M, N, K, tb, splits, wsp, wb: hip.ihip_gemm_bf16_bias_relu_splitk(  # noqa: E731
+        P(a.data_ptr()), P(a.data_ptr()), None, P(c.data_ptr()), M, N, K, 0, tb, 0, 0, splits, wsp, wb, s)
+    assert call(64, 64, 1020, 0, 2, P(ws.data_ptr()), 1 << 20) != 0  # K % 8 != 0
+    assert call(64, 60, 1024, 0, 2, P(ws.data_ptr()), 1 << 20) != 0  # B as [K, N], N % 8 != 0
+    assert call(64, 64, 1024, 0, 2, P(ws.data_ptr()), 100) != 0      # workspace too small
+    assert call(64, 64, 1024, 0, 2, P(ws.data_ptr() + 16), 1 << 19) != 0  # workspace not 256-byte aligned
+    assert call(64, 64, 0, 0, 2, P(ws.data_ptr()), 1 << 20) != 0     # K = 0
+    assert call(64, 64, 1024, 0, -1, P(ws.data_ptr()), 1 << 20) != 0
+    assert call(64, 64, 1024, 0, 2, P(ws.data_ptr()), 1 << 20) == 0
+    torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
@@ -530,17 +645,26 @@ def test_gemm_packed_path(hip, M, N, K, ta, tb):
     A = np.ascontiguousarray(inp["A"].T) if ta else inp["A"]
     B = np.ascontiguousarray(inp["B"].T) if tb else inp["B"]
     print(f"[case] gemm packed M={M} N={N} K={K} ta={ta} tb={tb}", flush=True)
-    packed = _gemm_ws(hip, A, B, inp["bias"], M, N, K, ta, tb)
+    # a workspace for the copies only: the packed path unsplit
+    packed = _gemm_ws(hip, A, B, inp["bias"], M, N, K, ta, tb, ws_bytes=gemm_pack_bytes(M, N, K, ta, tb))
     guarded = _gemm_ws(hip, A, B, inp["bias"], M, N, K, ta, tb, ws_bytes=0)
     assert np.array_equal(packed, guarded), f"packed and guarded differ in {int((packed != guarded).sum())} elements"
-    if M * N * K <= 1 << 31:
-        ref = oracle_outputs(w.ir(), inp, b)
+    ref = oracle_outputs(w.ir(), inp, b) if M * N * K <= 1 << 31 else None
+    if ref is not None:
         check({"C": bf16_bits_to_f32(packed)}, ref, ["C"], TOL["matmul"], f"packed {b}")
+    if gemm_split_plan(M, N, -(-K // 8) * 8)[0] > 1:  # the full workspace: packed, then split along K
+        split = _gemm_ws(hip, A, B, inp["bias"], M, N, K, ta, tb)
+        if ref is not None:
+            check({"C": bf16_bits_to_f32(split)}, ref, ["C"], TOL["matmul"], f"packed split {b}")
+        _assert_near_unsplit(split, packed)
     if M * N <= 1 << 22:
         for off, c_off in ((1, 0), (0, 1), (1, 3)):  # misaligned operand or C bases
             print(f"[case]   offsets {off} {c_off}", flush=True)
             mis = _gemm_ws(hip, A, B, inp["bias"], M, N, K, ta, tb, offset=off, c_offset=c_off)
-            assert np.array_equal(mis, guarded), f"offsets {off}/{c_off}: {int((mis != guarded).sum())} elements differ"
+            if gemm_split_plan(M, N, -(-K // 8) * 8)[0] > 1:  # split where the workspace holds the partials
+                _assert_near_unsplit(mis, guarded)
+            else:
+                assert np.array_equal(mis, guarded), f"offsets {off}/{c_off}: {int((mis != guarded).sum())} elements differ"
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])

@@ -211,22 +211,36 @@ def test_gemm_forms_and_errors():
     (256, 256, 64, 128, "fast"), (300, 264, 1000, 128, "fast"), (8, 8, 8, 128, "fast"), (4096, 4096, 64, 256, "fast"),
     (4096, 2048, 64, 128, "fast"), (4096, 2304, 64, 256, "fast"), (4100, 4104, 72, 256, "fast"),
     (256, 250, 64, 128, "packed"), (256, 256, 60, 128, "packed"), (65536, 16384, 40960, 256, "fast"),
-    (65536, 16384, 40968, 256, "guarded"), (5000, 3001, 64, 256, "packed"), (7, 9, 3, 128, "packed")])
+    (65536, 16384, 40968, 256, "guarded"), (5000, 3001, 64, 256, "packed"), (7, 9, 3, 128, "packed"),
+    (1024, 1024, 8192, 128, "split4"), (1000, 1000, 4100, 128, "packed+split4"), (128, 64, 65536, 128, "split128"),
+    (1536, 1408, 8192, 128, "fast"), (1408, 1408, 1024, 128, "fast"), (64, 64, 4096, 128, "split8"),
+    (512, 512, 16384, 128, "split16"), (1024, 1024, 2048, 128, "fast")])
 def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tile, path):
     """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N (LDS:
     three paired-slice A regions and four B stages); other rows are packed into a workspace
     and then take the tiled kernel; the guarded kernel (a double-buffered pair of 64-k operand
     tiles) is left for shapes beyond the tiled kernel's limits, such as a ragged K with
     operands above 2 GiB.  All use 256x256 tiles, or 128x128 tiles when at most 128 tiles of
-    256x256 (half the CUs) would be busy."""
+    256x256 (half the CUs) would be busy.  A grid of 128x128 tiles may be split along K into S
+    segments (tiles x S workgroups), its f32 partials in the workspace, where the split rule
+    estimates a gain: 64 tiles with K = 8192 take 4 segments, 16 tiles with K = 16384 take 16,
+    one tile with K = 65536 takes 128 segments of 512; 132 tiles (1536 x 1408) would need a
+    second wave to split, 121 tiles with K = 1024 and 64 tiles with K = 2048 gain too little
+    over the partials' round trip."""
     k = lower_intent_to_hip_kernel(matmul_bias_relu2d_ir(), shape_bindings={"M": M, "N": N, "K": K})
-    assert k.launch.grid == (-(-M // tile) * -(-N // tile), 1, 1)
+    S = int(path.split("split")[1]) if "split" in path else 1
+    assert k.launch.grid == (-(-M // tile) * -(-N // tile) * S, 1, 1)
+    base = path.split("+")[0] if "+" in path else ("fast" if path.startswith("split") else path)
     assert k.launch.lds_bytes == {(256, "fast"): 163840, (128, "fast"): 81920, (256, "packed"): 163840,
                                   (128, "packed"): 81920, (256, "guarded"): 147456,
-                                  (128, "guarded"): 73728}[(tile, path)]
-    assert (k.kernel_id == "ihip_gemm_bf16_bias_relu_ws") == (path == "packed")
-    if path == "packed":
+                                  (128, "guarded"): 73728}[(tile, base)]
+    uses_ws = base == "packed" or S > 1
+    assert (k.kernel_id == "ihip_gemm_bf16_bias_relu_ws") == uses_ws
+    if uses_ws:
         assert k.call_args[-1] == ("workspace", gemm_workspace_bytes(M, N, K, False, False)) and k.call_args[-1][1] > 0
+    if S > 1:
+        partials = S * M * (-(-N // 4) * 4) * 4
+        assert gemm_workspace_bytes(M, N, K, False, False) >= partials
 
 
 @pytest.mark.parametrize("N,tb,lds,kid", [(50257, True, 163840, "ihip_gemm_bf16_bias_relu_t"),
@@ -255,10 +269,32 @@ def test_gemm_workspace_size_matches_the_library(ta, tb):
     lib = load_library()
     for M in (1, 7, 8, 9, 256, 1000, 4099):
         for N in (1, 8, 263, 264, 50257):
-            for K in (1, 3, 8, 60, 64, 1000, 4095):
+            for K in (1, 3, 8, 60, 64, 1000, 1024, 4095, 16383, 65536):
                 want = lib.ihip_gemm_workspace_size(M, N, K, int(ta), int(tb))
                 assert gemm_workspace_bytes(M, N, K, ta, tb) == want, (M, N, K, ta, tb)
     assert lib.ihip_gemm_workspace_size(0, 8, 3, 0, 0) == 0 == gemm_workspace_bytes(0, 8, 3, False, False)
+
+
+def test_gemm_split_plan_matches_the_library():
+    """The split rule and an explicit split count size the partials as the library does
+    (ihip_gemm_splitk_workspace_size), and every plan covers K with segments of whole 64-k
+    steps, the last one non-empty."""
+    from intent_ir_amd.lowering import gemm_split_plan
+    from intent_ir_amd.runtime import load_library
+
+    lib = load_library()
+    for M, N in ((1, 1), (128, 64), (1000, 1001), (1024, 1024), (1408, 1408), (1536, 1408), (4096, 4096)):
+        for K in (8, 64, 520, 1024, 4100, 8192, 65536):
+            for splits in (0, 1, 2, 3, 7, 64, 1025, 5000):
+                S, kseg = gemm_split_plan(M, N, K, splits)
+                assert (S == 1 or kseg % 64 == 0) and (S - 1) * kseg < K <= S * kseg, (M, N, K, splits, S, kseg)
+                assert S <= max(1, splits) or splits == 0
+                want = -(-S * M * (-(-N // 4) * 4) * 4 // 256) * 256 if S > 1 else 0
+                assert lib.ihip_gemm_splitk_workspace_size(M, N, K, splits) == want, (M, N, K, splits)
+    assert gemm_split_plan(1024, 1024, 8192) == (4, 2048)
+    assert gemm_split_plan(4096, 4096, 8192) == (1, 8192)   # 256x256 tiles: never split
+    assert gemm_split_plan(128, 64, 131072) == (256, 512)   # one tile: 256 segments fill the CUs
+    assert gemm_split_plan(1000, 1000, 200) == (1, 200)     # K under two segments of 512
 
 
 def test_unsupported_ops_raise():
