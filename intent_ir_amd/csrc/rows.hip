@@ -960,6 +960,123 @@ __global__ __launch_bounds__(64 * kW) void layernorm_rows_f16_skew(
   }
 }
 
+// Rows of at most 4096 + 7 halves that do not all start 16-byte aligned, one wave per row, as
+// in layernorm_rows_f16_skew<8, 1, .>, with w and b realigned once per workgroup instead of per
+// row: the rows r = c, c + 8, c + 16, ... start at the same offset modulo 16 bytes (8 rows are
+// 8N halves = 16N bytes apart), so they share the head and the shift that brings w and b to
+// the body's 16-byte vectors.  Workgroup g takes class c = g % 8; its kWaves waves take that
+// class's rows t = g / 8 + J (kWaves i + wave) (J = gridDim.x / 8), after staging w and b,
+// shifted by the class's head, in LDS (8 KiB each).  The body arithmetic is the aligned
+// one-wave kernel's (v_dot2_f32_f16 for the sum, v_fma_mix_f32 for x - mean, recomputed in
+// the output pass), which keeps a row at half the registers of layernorm_rows_f16_skew (that
+// kernel converts all 64 halves of a lane to f32 once and keeps them: 127 VGPRs, 4 waves per
+// SIMD, 46% of HBM peak at [8192, 4099]).
+constexpr int kLnLdsWaves = 4;
+constexpr int kLnLdsMaxVec = 512;  // body vectors of a row of N <= 4096 + 7
+// kVpl body vectors per lane: rows of at most 512 kVpl + 7 halves.
+template <int kVpl, bool kAlignedWB>
+__global__ __launch_bounds__(64 * kLnLdsWaves) __attribute__((amdgpu_waves_per_eu(6, 6))) void layernorm_rows_f16_skew_lds(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b,
+    uint16_t* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t M, int64_t N,
+    float eps) {
+  static_assert(kVpl * kWave <= kLnLdsMaxVec, "w and b staging");
+  __shared__ u32x4 w_s[kLnLdsMaxVec], b_s[kLnLdsMaxVec];
+  const int lane = threadIdx.x & 63, v = threadIdx.x >> 6;
+  const int64_t c = blockIdx.x % 8, j = blockIdx.x / 8, J = gridDim.x / 8;
+  if (c >= M) return;  // uniform per workgroup
+  // N <= 4096 + 7: head, body and tail counts fit 32 bits
+  const int n = static_cast<int>(N);
+  const int to_edge = static_cast<int>((8 - ((reinterpret_cast<uintptr_t>(x + c * N) >> 1) & 7)) & 7);
+  const int head = to_edge < n ? to_edge : n;
+  const int nb = (n - head) >> 3;
+  const int tail = n - head - 8 * nb;
+  for (int k = threadIdx.x; k < nb; k += 64 * kLnLdsWaves) {
+    f16x8_t wv, bv;
+    if (kAlignedWB) {
+      wv = f16x8_at(w, N, k, head);
+      bv = f16x8_at(b, N, k, head);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        wv[e] = __builtin_bit_cast(_Float16, w[head + 8 * k + e]);
+        bv[e] = __builtin_bit_cast(_Float16, b[head + 8 * k + e]);
+      }
+    }
+    w_s[k] = __builtin_bit_cast(u32x4, wv);
+    b_s[k] = __builtin_bit_cast(u32x4, bv);
+  }
+  __syncthreads();
+  // head and tail w, b of this lane (the same for every row of the class)
+  const float hw = lane < head ? f16_to_f32(w[lane]) : 0.0f, hb = lane < head ? f16_to_f32(b[lane]) : 0.0f;
+  const int te = head + 8 * nb + lane;
+  const float tw = lane < tail ? f16_to_f32(w[te]) : 0.0f, tb = lane < tail ? f16_to_f32(b[te]) : 0.0f;
+  for (int64_t t = j + J * v;; t += J * kLnLdsWaves) {
+    const int64_t row = c + 8 * t;
+    if (row >= M) break;  // uniform per wave: waves take their own rows, no barrier below
+    const uint16_t* xr = x + row * N;
+    uint16_t* yr = y + row * N;
+    const u32x4* xb = reinterpret_cast<const u32x4*>(xr + head) + lane;
+    u32x4* yb = reinterpret_cast<u32x4*>(yr + head) + lane;
+    f16x8_t xv[kVpl];
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i)
+      xv[i] = __builtin_bit_cast(f16x8_t, lane + i * kWave < nb ? __builtin_nontemporal_load(xb + i * kWave)
+                                                                 : u32x4(0u));
+    const float hx = lane < head ? f16_to_f32(xr[lane]) : 0.0f;
+    const float tx = lane < tail ? f16_to_f32(xr[te]) : 0.0f;
+    float s = hx + tx;  // padding is +0
+    const f16x2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2_t pr = {xv[i][2 * e], xv[i][2 * e + 1]};
+        s = __builtin_amdgcn_fdot2(pr, one, s, false);
+      }
+    s = wave_sum(s);
+    const float mean = s / static_cast<float>(N);
+    // an opaque 1.0: x * unit - mean stays one v_fma_mix_f32 (f16 operand widened inside)
+    float unit;
+    asm volatile("v_mov_b32 %0, 1.0" : "=v"(unit));
+    float q = 0.f;
+    if (lane < head) q = (hx - mean) * (hx - mean);
+    if (lane < tail) q = __builtin_fmaf(tx - mean, tx - mean, q);
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i) {
+      const bool in = lane + i * kWave < nb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = __builtin_fmaf(static_cast<float>(xv[i][e]), unit, -mean);
+        q = __builtin_fmaf(d, in ? d : 0.f, q);
+      }
+    }
+    q = wave_sum(q);
+    const float rstd = 1.0f / sqrtf(q / static_cast<float>(N) + eps);
+    float unit2;  // a second opaque 1.0: d is recomputed below, not kept across the reduction
+    asm volatile("v_mov_b32 %0, 1.0" : "=v"(unit2));
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i) {
+      const int k = lane + i * kWave;
+      if (k < nb) {
+        const f16x8_t wv = __builtin_bit_cast(f16x8_t, w_s[k]), bv = __builtin_bit_cast(f16x8_t, b_s[k]);
+        f16x8_t o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = __builtin_fmaf(static_cast<float>(xv[i][e]), unit2, -mean);
+          o[e] = static_cast<_Float16>(__builtin_fmaf(d * rstd, static_cast<float>(wv[e]), static_cast<float>(bv[e])));
+        }
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), yb + i * kWave);
+      }
+    }
+    if (lane < head) yr[lane] = f32_to_f16_rne(__builtin_fmaf((hx - mean) * rstd, hw, hb));
+    if (lane < tail) yr[te] = f32_to_f16_rne(__builtin_fmaf((tx - mean) * rstd, tw, tb));
+    if (lane == 0) {
+      if (mean_out != nullptr) mean_out[row] = mean;
+      if (rstd_out != nullptr) rstd_out[row] = rstd;
+    }
+  }
+}
+
 // Any N: one workgroup per row, three passes over the row.
 __global__ __launch_bounds__(256) void layernorm_rows_f16_any(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                               const uint16_t* __restrict__ b, uint16_t* __restrict__ y,
@@ -1041,10 +1158,30 @@ hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const
                     ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(y)) & 15) == 0;
   if (skew) {
     const bool wb16 = ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
-    if (wb16)
+    if (N <= 4096 + 7) {
+      // 8 row classes x J workgroups of kLnLdsWaves waves (J <= 128: 4 workgroups per CU,
+      // which measured 2-8% ahead of 8), then more rows per wave
+      const int64_t per_class = (M + 7) / 8;
+      const int64_t J = std::min<int64_t>(128, (per_class + kLnLdsWaves - 1) / kLnLdsWaves);
+      const dim3 grid(static_cast<unsigned>(8 * J)), block(64 * kLnLdsWaves);
+      const auto go = [&](auto vpl) {
+        constexpr int kV = decltype(vpl)::value;
+        if (wb16)
+          layernorm_rows_f16_skew_lds<kV, true><<<grid, block, 0, s>>>(x, w, b, y, mean, rstd, M, N, eps);
+        else
+          layernorm_rows_f16_skew_lds<kV, false><<<grid, block, 0, s>>>(x, w, b, y, mean, rstd, M, N, eps);
+      };
+      if (N <= 1024 + 7)
+        go(std::integral_constant<int, 2>{});
+      else if (N <= 2048 + 7)
+        go(std::integral_constant<int, 4>{});
+      else
+        go(std::integral_constant<int, 8>{});
+    } else if (wb16) {
       launch_layernorm_skew<true>(x, w, b, y, mean, rstd, M, N, eps, s);
-    else
+    } else {
       launch_layernorm_skew<false>(x, w, b, y, mean, rstd, M, N, eps, s);
+    }
     return hipGetLastError();
   }
   if (!vec) {
