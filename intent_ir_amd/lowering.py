@@ -529,6 +529,9 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     elif N % 8 == 0 and N <= 65536:  # kW waves per row, one row per workgroup
         kw = 2 if N <= 16384 else 4 if N <= 32768 else 8
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
+    elif 0 < N <= 4096 + 7:  # N % 8 != 0: 8 row classes x J workgroups of 4 waves, w and b per class in LDS
+        J = min(128, _cdiv(_cdiv(M, 8), 4))
+        launch = HipLaunch((8 * max(1, J), 1, 1), (256, 1, 1), 2 * 512 * 16)
     elif 0 < N <= 65536 + 7:  # N % 8 != 0: head / 16-byte body / tail, kW waves per row, one row per workgroup
         kw = next(k for k in (1, 2, 4, 8, 16) if N <= 4096 * k + 7)
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)

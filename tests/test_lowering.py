@@ -344,3 +344,14 @@ def test_library_rejects_bad_arguments_without_a_device():
     assert st == -1 and b"rows_per_wg 3" in lib.ihip_last_error()
     st = lib.ihip_gemm_bf16_bias_relu_ex(None, None, None, None, 0, 0, 0, 0, 0, 1, 64, None)
     assert st == -1 and b"tile 64" in lib.ihip_last_error()
+
+
+@pytest.mark.parametrize("M,N,grid,block,lds", [
+    (8192, 4099, 1024, 256, 16384), (3, 1029, 8, 256, 16384), (64, 7, 16, 256, 16384),
+    (8192, 4104, 1024, 1024, 128), (8192, 8191, 8192, 128, 16), (5, 65537, 5, 1024, 128), (5, 65545, 5, 256, 16)])
+def test_layernorm_launch_descriptor(M, N, grid, block, lds):
+    """Rows not 16-byte aligned up to N = 4096 + 7 run as 8 row classes of workgroups with w and b
+    staged per class (grid 8 x min(128, ceil(ceil(M / 8) / 4))); longer ones one row per
+    workgroup of 1-16 waves; beyond 65536 + 7 the three-pass kernel."""
+    k = lower_intent_to_hip_kernel(WORKLOADS["layernorm"].ir(), shape_bindings={"M": M, "N": N})
+    assert (k.launch.grid[0], k.launch.block[0], k.launch.lds_bytes) == (grid, block, lds)
