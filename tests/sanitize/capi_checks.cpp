@@ -95,6 +95,32 @@ static void row_kernels() {
   EXPECT(ihip_gemm_workspace_size(1LL << 40, 1LL << 40, 1LL << 40, 0, 0) == 0, "gemm workspace size overflow");
   EXPECT(ihip_gemm_workspace_size(7, 9, 3, 0, 0) == 256 + 256, "gemm workspace size 7x9x3");
   EXPECT(ihip_gemm_workspace_size(64, 263, 64, 0, 1) == 0, "gemm workspace size with B as [N, K]");
+  // split-K: sizes, and argument errors caught before any launch (no device needed)
+  EXPECT(ihip_gemm_workspace_size(1024, 1024, 8192, 0, 0) == 4LL * 1024 * 1024 * 4, "gemm split-K workspace (4 segments)");
+  EXPECT(ihip_gemm_splitk_workspace_size(1024, 1024, 8192, 1) == 0, "no partials unsplit");
+  // 2 segments x 8 rows x 4 floats (N = 3 padded to 4) x 4 bytes = 256; 2 x 3 x 12 x 4 = 288 -> 512
+  EXPECT(ihip_gemm_splitk_workspace_size(8, 3, 4096, 2) == 256, "partials padded to 4 columns");
+  EXPECT(ihip_gemm_splitk_workspace_size(3, 12, 4096, 2) == 512, "partials 256-byte aligned");
+  EXPECT(ihip_gemm_splitk_workspace_size(8, 8, 4096, -1) == 0, "negative split count");
+  EXPECT(ihip_gemm_splitk_workspace_size(1LL << 40, 1LL << 40, 1LL << 40, 0) == 0, "split-K size overflow");
+  EXPECT(ihip_gemm_bf16_bias_relu_splitk(nullptr, nullptr, nullptr, nullptr, 8, 8, 64, 0, 0, 1, 64, 2, nullptr, 0,
+                                         nullptr) == IHIP_ERR_INVALID_ARG,
+         "split-K tile 64");
+  EXPECT(ihip_gemm_bf16_bias_relu_splitk(nullptr, nullptr, nullptr, nullptr, 8, 8, 64, 0, 0, 1, 0, -2, nullptr, 0,
+                                         nullptr) == IHIP_ERR_INVALID_ARG,
+         "split-K negative count");
+  EXPECT(ihip_gemm_bf16_bias_relu_splitk(nullptr, nullptr, nullptr, nullptr, 8, 8, 0, 0, 0, 1, 0, 2, nullptr, 0,
+                                         nullptr) == IHIP_ERR_INVALID_ARG,
+         "split-K with K = 0");
+  EXPECT(ihip_gemm_bf16_bias_relu_splitk(nullptr, nullptr, nullptr, nullptr, 8, 8, 4096, 0, 0, 1, 0, 2, nullptr, 100,
+                                         nullptr) == IHIP_ERR_INVALID_ARG,
+         "split-K workspace bytes at a null pointer");
+  EXPECT(ihip_gemm_bf16_bias_relu_splitk(nullptr, nullptr, nullptr, nullptr, 8, 8, 4096, 0, 0, 1, 0, 2, nullptr, 0,
+                                         nullptr) == IHIP_ERR_INVALID_ARG,
+         "split-K workspace too small");
+  EXPECT(ihip_gemm_bf16_bias_relu_splitk(nullptr, nullptr, nullptr, nullptr, 0, 8, 4096, 0, 0, 1, 0, 2, nullptr, 0,
+                                         nullptr) == 0,
+         "split-K with M = 0 is a no-op");
 }
 
 static void program_checker() {
