@@ -99,6 +99,24 @@ int ihip_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, void* 
  * not depend on rows_per_wg. */
 int ihip_softmax_rows_f32_ex(const float* x, float* y, int64_t M, int64_t N, int rows_per_wg, void* stream);
 
+/* Bytes of workspace ihip_softmax_rows_f32_ws uses for an [M, N] softmax: 2 * M * S floats
+ * when rows are longer than 65536 floats (vocabulary-width rows) and split into S <= 256
+ * segments, else 0 (the rows are not split).  Depends on M and N only.  Same softmax as
+ * ihip_softmax_rows_f32, whose long-row kernel it speeds up (the reference lowers every N
+ * through _kernel_softmax_2d_last_f32, backends/cuda/codegen/intentir_to_cuda.py:1103-1247). */
+int64_t ihip_softmax_rows_f32_workspace_size(int64_t M, int64_t N);
+
+/* ihip_softmax_rows_f32 with a caller-owned device workspace (the library still allocates
+ * nothing): when ihip_softmax_rows_f32_workspace_size(M, N) > 0 and the rows of x and y start
+ * at the same offset modulo 16 bytes (4-byte aligned), each row is split over S workgroups;
+ * one kernel writes each segment's maximum and sum of exponentials to the workspace and a
+ * second combines a row's S partials in segment order and writes y.  Results are
+ * reproducible; the sum's rounding order differs from the unsplit form.  workspace may be
+ * NULL (exactly ihip_softmax_rows_f32); otherwise it must hold at least workspace_size
+ * bytes, 8-byte aligned, and stay untouched until the work on `stream` completes. */
+int ihip_softmax_rows_f32_ws(const float* x, float* y, int64_t M, int64_t N, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
 /* LayerNorm forward over the last axis: x, y f16 [M, N]; w, b f16 [N];
  * mean, rstd f32 [M] (either may be NULL: that statistic is then not written);
  * f32 statistics, rstd = 1/sqrt(var + eps).  Replaces

@@ -24,7 +24,7 @@ hipError_t launch_reduce_any_rows_f32(const float*, uint8_t*, int64_t, int64_t, 
 hipError_t launch_reduce_any_rows_u8(const uint8_t*, uint8_t*, int64_t, int64_t, hipStream_t);
 hipError_t launch_reduce_rows_f32(const float*, float*, int64_t, int64_t, int, float*, hipStream_t);
 int reduce_rows_segments(int64_t, int64_t);
-hipError_t launch_softmax_rows_f32(const float*, float*, int64_t, int64_t, int, hipStream_t);
+hipError_t launch_softmax_rows_f32(const float*, float*, int64_t, int64_t, int, hipStream_t, float*);
 bool softmax_rows_per_wg_form(const float*, const float*, int64_t);
 hipError_t launch_layernorm_rows_f16(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, float*,
                                      int64_t, int64_t, float, hipStream_t);
@@ -266,8 +266,32 @@ int ihip_softmax_rows_f32_ex(const float* x, float* y, int64_t M, int64_t N, int
                "softmax_rows_f32: rows_per_wg %d needs the one-wave-per-row form (N %% 4 == 0, N <= 4096, "
                "16-byte aligned x and y); N = %lld runs one row per workgroup",
                rows_per_wg, (long long)N);
-  return finish(ihip::launch_softmax_rows_f32(x, y, M, N, rows_per_wg, static_cast<hipStream_t>(stream)),
+  return finish(ihip::launch_softmax_rows_f32(x, y, M, N, rows_per_wg, static_cast<hipStream_t>(stream), nullptr),
                 "softmax_rows_f32");
+}
+
+int64_t ihip_softmax_rows_f32_workspace_size(int64_t M, int64_t N) {
+  if (numel2(M, N) < 0) return 0;
+  const ihip::SoftmaxSplit p = ihip::softmax_split_plan(M, N);
+  return p.S > 0 ? 2 * M * p.S * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
+int ihip_softmax_rows_f32_ws(const float* x, float* y, int64_t M, int64_t N, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  const int64_t n = numel2(M, N);
+  IHIP_REQUIRE(n >= 0, "softmax_rows_f32_ws: invalid shape [%lld, %lld]", (long long)M, (long long)N);
+  IHIP_REQUIRE(n == 0 || (x != nullptr && y != nullptr), "softmax_rows_f32_ws: null pointer");
+  IHIP_REQUIRE(workspace_bytes >= 0, "softmax_rows_f32_ws: negative workspace size %lld", (long long)workspace_bytes);
+  IHIP_REQUIRE(workspace != nullptr || workspace_bytes == 0,
+               "softmax_rows_f32_ws: workspace of %lld bytes at a null pointer", (long long)workspace_bytes);
+  const int64_t need = ihip_softmax_rows_f32_workspace_size(M, N);
+  IHIP_REQUIRE(workspace == nullptr || workspace_bytes >= need,
+               "softmax_rows_f32_ws: workspace of %lld bytes, [%lld, %lld] needs %lld", (long long)workspace_bytes,
+               (long long)M, (long long)N, (long long)need);
+  IHIP_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 7) == 0, "softmax_rows_f32_ws: workspace not 8-byte aligned");
+  float* part = need > 0 ? static_cast<float*>(workspace) : nullptr;
+  return finish(ihip::launch_softmax_rows_f32(x, y, M, N, 0, static_cast<hipStream_t>(stream), part),
+                "softmax_rows_f32_ws");
 }
 
 int ihip_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, void* stream) {

@@ -119,4 +119,12 @@ __device__ __forceinline__ float block_max_nan(float v, float* scratch) {
   return r;
 }
 
+// Row split of a long-row softmax (rows.hip): S segments per row of 256 * vpl 16-byte
+// vectors, two floats of workspace per segment; S = 0 when rows are not split.
+struct SoftmaxSplit {
+  int S;
+  int vpl;
+};
+SoftmaxSplit softmax_split_plan(int64_t M, int64_t N);
+
 }  // namespace ihip

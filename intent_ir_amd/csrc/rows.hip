@@ -559,6 +559,168 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restr
   for (int64_t i = threadIdx.x; i < N; i += blockDim.x) yr[i] = expf(xr[i] - mx) / s;
 }
 
+// ------------------------------------------------------------- long rows, split over workgroups
+// Rows longer than 65536 floats are cut into S segments of kSplitThreads * kVpl 16-byte vectors
+// of the row's body, one workgroup each, and run in two launches:
+//   softmax_split_stats: segment j's maximum m_j and s_j = sum(exp(x - m_j)) over the segment,
+//     written to part[2 * (row * S + j) + {0, 1}];
+//   softmax_split_write: the row's maximum mx = max_j m_j and sum = sum_j s_j * exp(m_j - mx),
+//     added in segment order (a segment whose maximum is -inf, all of it masked, adds 0), then
+//     y = exp(x - mx) * (1 / sum) over the segment.
+// x is read twice and y written once (the workgroup-per-row kernel reads x three times), every
+// CU is busy for few rows, and each element's arithmetic is that of the register-resident
+// kernels: only the sum's rounding order differs.  Special values come out as numpy's: a NaN
+// anywhere gives a NaN maximum and NaN everywhere; +inf gives inf - inf = NaN in its segment's
+// s_j and so everywhere; a row of -inf gives mx = -inf and NaN.
+// kSkew: rows start 4-byte aligned, x and y at the same offset modulo 16 bytes, and every row
+// splits into a head of up to 3 elements before its first 16-byte boundary, the body, and a
+// tail of up to 3; head and tail belong to segment 0.  Without kSkew rows are 16-byte aligned
+// (N % 4 == 0).  Launch: grid M * S, block kSplitThreads; blockIdx.x = row * S + j, so both
+// launches place a segment on the same XCD (workgroups go to the XCDs round robin).  The first
+// launch reads x with ordinary loads, so that the caches keep what they can of it for the
+// second (non-temporal) read: 2-6 points of HBM peak at 33-130 MB of x against non-temporal
+// loads in both, and no worse at 1 GiB.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitMaxSegments = 256;
+
+struct SplitRow {
+  int64_t head, nb, tail;  // elements before the body, body vectors, elements after it
+};
+
+template <bool kSkew>
+__device__ __forceinline__ SplitRow split_row(const float* xr, int64_t N) {
+  if (!kSkew) return {0, N >> 2, 0};
+  const int64_t to_edge = (4 - ((reinterpret_cast<uintptr_t>(xr) >> 2) & 3)) & 3;
+  const int64_t head = to_edge < N ? to_edge : N;
+  const int64_t nb = (N - head) >> 2;
+  return {head, nb, N - head - 4 * nb};
+}
+
+template <int kVpl, bool kSkew>
+__global__ __launch_bounds__(kSplitThreads) void softmax_split_stats(const float* __restrict__ x,
+                                                                     float* __restrict__ part, int64_t N, int S) {
+  constexpr int kW = kSplitThreads / kWave;
+  __shared__ float part_m[kW], part_s[kW];
+  const int tid = threadIdx.x, lane = tid & 63, v = tid >> 6;
+  const int64_t row = blockIdx.x / S;
+  const int seg = static_cast<int>(blockIdx.x % S);
+  const float* xr = x + row * N;
+  const SplitRow r = split_row<kSkew>(xr, N);
+  const int64_t first = static_cast<int64_t>(seg) * (kSplitThreads * kVpl) + tid;
+  const f32x4* xb = reinterpret_cast<const f32x4*>(xr + r.head) + first;
+  const float ninf = -__builtin_inff();
+  f32x4 xv[kVpl];
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+    xv[i] = first + i * kSplitThreads < r.nb ? xb[i * kSplitThreads] : f32x4{ninf, ninf, ninf, ninf};
+  const bool ht = kSkew && seg == 0;  // uniform: this segment holds the head and the tail
+  float hv = ht && tid < r.head ? xr[tid] : ninf;
+  float tv = ht && tid < r.tail ? xr[r.head + 4 * r.nb + tid] : ninf;
+  float mx = max_nan(hv, tv);
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) mx = max_nan(max_nan(mx, xv[i].x), max_nan(max_nan(xv[i].y, xv[i].z), xv[i].w));
+  mx = wave_max_nan(mx);
+  if (lane == 0) part_m[v] = mx;
+  __syncthreads();
+  mx = part_m[0];
+#pragma unroll
+  for (int k = 1; k < kW; ++k) mx = max_nan(mx, part_m[k]);
+  float sum = (ht && tid < r.head ? exp_nonpos(hv - mx) : 0.f) + (ht && tid < r.tail ? exp_nonpos(tv - mx) : 0.f);
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    const float e = (exp_nonpos(xv[i].x - mx) + exp_nonpos(xv[i].y - mx)) +
+                    (exp_nonpos(xv[i].z - mx) + exp_nonpos(xv[i].w - mx));
+    if (first + i * kSplitThreads < r.nb) sum += e;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) part_s[v] = sum;
+  __syncthreads();
+  if (tid == 0) {
+    float tot = 0.f;
+#pragma unroll
+    for (int k = 0; k < kW; ++k) tot += part_s[k];
+    part[2 * static_cast<int64_t>(blockIdx.x)] = mx;
+    part[2 * static_cast<int64_t>(blockIdx.x) + 1] = tot;
+  }
+}
+
+template <int kVpl, bool kSkew>
+__global__ __launch_bounds__(kSplitThreads) void softmax_split_write(const float* __restrict__ x,
+                                                                     float* __restrict__ y,
+                                                                     const float* __restrict__ part, int64_t N,
+                                                                     int S) {
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x / S;
+  const int seg = static_cast<int>(blockIdx.x % S);
+  const float* xr = x + row * N;
+  float* yr = y + row * N;
+  const SplitRow r = split_row<kSkew>(xr, N);
+  const int64_t first = static_cast<int64_t>(seg) * (kSplitThreads * kVpl) + tid;
+  const f32x4* xb = reinterpret_cast<const f32x4*>(xr + r.head) + first;
+  f32x4* yb = reinterpret_cast<f32x4*>(yr + r.head) + first;
+  const float ninf = -__builtin_inff();
+  f32x4 xv[kVpl];
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i)
+    xv[i] = first + i * kSplitThreads < r.nb ? __builtin_nontemporal_load(xb + i * kSplitThreads)
+                                             : f32x4{ninf, ninf, ninf, ninf};
+  const bool ht = kSkew && seg == 0;
+  const float hv = ht && tid < r.head ? xr[tid] : ninf;
+  const float tv = ht && tid < r.tail ? xr[r.head + 4 * r.nb + tid] : ninf;
+  // the row's statistics from its S partials (uniform: every workgroup of the row gets the same)
+  const float* pr = part + 2 * row * S;
+  float mx = pr[0];
+  for (int j = 1; j < S; ++j) mx = max_nan(mx, pr[2 * j]);
+  float tot = 0.f;
+  for (int j = 0; j < S; ++j) {
+    const float m = pr[2 * j];
+    tot += m == ninf ? 0.f : pr[2 * j + 1] * exp_nonpos(m - mx);
+  }
+  const float inv = 1.0f / tot;
+#pragma unroll
+  for (int i = 0; i < kVpl; ++i) {
+    if (first + i * kSplitThreads < r.nb) {
+      const f32x4 e = {exp_nonpos(xv[i].x - mx), exp_nonpos(xv[i].y - mx), exp_nonpos(xv[i].z - mx),
+                       exp_nonpos(xv[i].w - mx)};
+      __builtin_nontemporal_store(e * inv, yb + i * kSplitThreads);
+    }
+  }
+  if (ht && tid < r.head) yr[tid] = exp_nonpos(hv - mx) * inv;
+  if (ht && tid < r.tail) yr[r.head + 4 * r.nb + tid] = exp_nonpos(tv - mx) * inv;
+}
+
+// Split of an [M, N] softmax: S segments per row of 256 * vpl vectors, or S = 0 (not split:
+// rows of at most 65536 floats, or more than kSplitMaxSegments segments).  The longest segments
+// (16 vectors per thread) unless that leaves fewer than 512 workgroups.  Shape only.
+SoftmaxSplit softmax_split_plan(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 65536) return {0, 0};
+  const int64_t n4 = N / 4;  // body vectors of a row, at most
+  int vpl = 16;
+  int64_t S = (n4 + kSplitThreads * vpl - 1) / (kSplitThreads * vpl);
+  while (vpl > 4 && M * S < 512) {
+    vpl /= 2;
+    S = (n4 + kSplitThreads * vpl - 1) / (kSplitThreads * vpl);
+  }
+  if (S > kSplitMaxSegments || M * S > 0x7fffffffLL) return {0, 0};
+  return {static_cast<int>(S), vpl};
+}
+
+template <bool kSkew>
+static void launch_softmax_split(const float* x, float* y, int64_t M, int64_t N, const SoftmaxSplit& p, float* part,
+                                 hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(M * p.S)), block(kSplitThreads);
+  if (p.vpl == 16) {
+    softmax_split_stats<16, kSkew><<<grid, block, 0, s>>>(x, part, N, p.S);
+    softmax_split_write<16, kSkew><<<grid, block, 0, s>>>(x, y, part, N, p.S);
+  } else if (p.vpl == 8) {
+    softmax_split_stats<8, kSkew><<<grid, block, 0, s>>>(x, part, N, p.S);
+    softmax_split_write<8, kSkew><<<grid, block, 0, s>>>(x, y, part, N, p.S);
+  } else {
+    softmax_split_stats<4, kSkew><<<grid, block, 0, s>>>(x, part, N, p.S);
+    softmax_split_write<4, kSkew><<<grid, block, 0, s>>>(x, y, part, N, p.S);
+  }
+}
+
 // rows: rows per workgroup, 1, 2 or 4 (the kernel reads its waves from blockDim).  Four rows of
 // at most 1024 floats run as two waves of two rows each, otherwise one wave per row.
 template <int kVpl>
@@ -584,9 +746,25 @@ bool softmax_rows_per_wg_form(const float* x, const float* y, int64_t N) {
   return vec && N / 4 <= 1024;
 }
 
-// rows_per_wg: 0 = automatic (4), else 1, 2 or 4 for the one-wave-per-row form.
-hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, int rows_per_wg, hipStream_t s) {
+// rows_per_wg: 0 = automatic (4), else 1, 2 or 4 for the one-wave-per-row form.  part: workspace
+// of 2 * M * softmax_split_plan(M, N).S floats, or null: rows longer than 65536 floats are then
+// split over several workgroups each (16-byte aligned rows, or rows at the same offset modulo 16
+// bytes in x and y), else they take the workgroup-per-row kernel.
+hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, int rows_per_wg, hipStream_t s,
+                                   float* part) {
   if (M == 0 || N == 0) return hipSuccess;
+  if (part != nullptr) {
+    const SoftmaxSplit p = softmax_split_plan(M, N);
+    const uintptr_t xa = reinterpret_cast<uintptr_t>(x), ya = reinterpret_cast<uintptr_t>(y);
+    if (p.S > 0 && N % 4 == 0 && ((xa | ya) & 15) == 0) {
+      launch_softmax_split<false>(x, y, M, N, p, part, s);
+      return hipGetLastError();
+    }
+    if (p.S > 0 && ((xa | ya) & 3) == 0 && ((xa ^ ya) & 15) == 0) {
+      launch_softmax_split<true>(x, y, M, N, p, part, s);
+      return hipGetLastError();
+    }
+  }
   const int rows = rows_per_wg > 0 ? rows_per_wg : 4;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // grid.x limit of the row-per-workgroup fallback
   const bool vec = (N % 4 == 0) && (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0);

@@ -20,7 +20,8 @@ reads come from HBM rather than the Infinity Cache (as in bench.py).  With
 counters against a known transfer.  ``--bindings`` replaces the workload's shape
 bindings; ``--transpose-b`` (matmul) gives B as [N, K] with matmul{transpose_b};
 ``--no-workspace`` passes an empty workspace, so a GEMM whose operands would be packed runs
-the guarded kernel instead.
+the guarded kernel instead, and a softmax over rows longer than 65536 floats the
+workgroup-per-row kernel instead of the split one.
 """
 
 from __future__ import annotations
@@ -178,7 +179,8 @@ def main(argv=None) -> int:
     ap.add_argument("--bindings", default="", help="comma-separated SYMBOL=VALUE overrides, e.g. M=1000,N=4096")
     ap.add_argument("--transpose-b", action="store_true", help="matmul: B given as [N, K] (matmul{transpose_b})")
     ap.add_argument("--no-workspace", action="store_true",
-                    help="pass an empty workspace (a GEMM that would be packed runs the guarded kernel)")
+                    help="pass an empty workspace (a GEMM that would be packed runs the guarded kernel, a long-row "
+                         "softmax the workgroup-per-row kernel)")
     args = ap.parse_args(argv)
     if sum(x is not None for x in (args.config, args.ew_chain, args.row_reduce)) != 1:
         ap.error("give exactly one of --config, --ew-chain and --row-reduce")

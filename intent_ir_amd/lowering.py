@@ -476,7 +476,30 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
     if rows:
         return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32_ex", c.io([x, oname]), launch, [oname], dict(c.b),
                                 args + (("i32", rows),))
+    segs, _ = softmax_split_plan(M, N)
+    if segs:  # rows longer than 65536 floats: S workgroups per row, two floats of partials each
+        launch = HipLaunch((M * segs, 1, 1), (256, 1, 1), 32)
+        return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32_ws", c.io([x, oname]), launch, [oname], dict(c.b),
+                                args + (("workspace", 8 * M * segs),))
     return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b), args)
+
+
+def softmax_split_plan(M: int, N: int) -> Tuple[int, int]:
+    """(S, vpl) of the split long-row softmax (rows.hip softmax_split_plan): rows longer than
+    65536 floats are cut into S segments of 256 * vpl 16-byte vectors, vpl = 16 unless that
+    leaves fewer than 512 workgroups (then 8, then 4); (0, 0) = not split, also when S would
+    exceed 256."""
+    if M <= 0 or N <= 65536:
+        return 0, 0
+    n4 = N // 4
+    vpl = 16
+    s = _cdiv(n4, 256 * vpl)
+    while vpl > 4 and M * s < 512:
+        vpl //= 2
+        s = _cdiv(n4, 256 * vpl)
+    if s > 256 or M * s > 0x7FFFFFFF:
+        return 0, 0
+    return s, vpl
 
 
 def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
@@ -767,4 +790,4 @@ def lower_intent_to_hip_kernel(intent, *, shape_bindings: Mapping[str, Any],
 
 
 __all__ = ["HipLoweringError", "HipLaunch", "HipLoweredKernel", "KNOBS", "call_args_from_json", "call_args_to_json",
-           "lower_intent_to_hip_kernel", "reduce_rows_segments"]
+           "lower_intent_to_hip_kernel", "reduce_rows_segments", "softmax_split_plan"]

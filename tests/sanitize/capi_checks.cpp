@@ -78,6 +78,29 @@ static void row_kernels() {
   EXPECT(ihip_softmax_rows_f32_ex(nullptr, nullptr, 0, 8, 3, nullptr) == IHIP_ERR_INVALID_ARG, "rows_per_wg 3");
   EXPECT(ihip_softmax_rows_f32_ex((float*)fake(64), (float*)fake(128), 4, 8192, 2, nullptr) == IHIP_ERR_INVALID_ARG,
          "rows_per_wg on a multi-wave row");
+  // long rows: 8 segments of 4096 vectors per 128256-float row at 64 rows, 2 floats each
+  EXPECT(ihip_softmax_rows_f32_workspace_size(64, 128256) == 64 * 8 * 8, "softmax split workspace");
+  EXPECT(ihip_softmax_rows_f32_workspace_size(64, 65536) == 0, "softmax rows not split");
+  EXPECT(ihip_softmax_rows_f32_workspace_size(1, 1048580) == 0, "softmax split past 256 segments");
+  EXPECT(ihip_softmax_rows_f32_workspace_size(-1, 128256) == 0, "softmax split negative");
+  EXPECT(ihip_softmax_rows_f32_workspace_size(1LL << 40, 1LL << 40) == 0, "softmax split overflow");
+  EXPECT(ihip_softmax_rows_f32_ws((float*)fake(64), (float*)fake(64), 64, 128256, fake(256), 8, nullptr) ==
+             IHIP_ERR_INVALID_ARG, "softmax workspace too small");
+  EXPECT(ihip_softmax_rows_f32_ws((float*)fake(64), (float*)fake(64), 64, 128256, fake(260), 4096, nullptr) ==
+             IHIP_ERR_INVALID_ARG, "softmax workspace alignment");
+  EXPECT(ihip_softmax_rows_f32_ws((float*)fake(64), (float*)fake(64), 64, 128256, nullptr, 4096, nullptr) ==
+             IHIP_ERR_INVALID_ARG, "softmax workspace null with bytes");
+  EXPECT(ihip_softmax_rows_f32_ws((float*)fake(64), (float*)fake(64), 64, 128256, fake(256), -8, nullptr) ==
+             IHIP_ERR_INVALID_ARG, "softmax workspace negative");
+  EXPECT(ihip_softmax_rows_f32_ws(nullptr, nullptr, 3, -2, nullptr, 0, nullptr) == IHIP_ERR_INVALID_ARG,
+         "softmax ws shape");
+  EXPECT(ihip_softmax_rows_f32_ws(nullptr, nullptr, 0, 128256, nullptr, 0, nullptr) == IHIP_OK, "softmax ws M = 0");
+  for (int64_t m : {0LL, 1LL, 31LL, 4096LL, 1LL << 30, 1LL << 40})
+    for (int64_t n : {0LL, 65536LL, 65537LL, 1LL << 20, 1LL << 22, 1LL << 40}) {
+      const int64_t w = ihip_softmax_rows_f32_workspace_size(m, n);
+      EXPECT(w >= 0 && (w == 0 || w % (8 * m) == 0) && w / 8 <= 0x7fffffffLL, "softmax workspace %lld for [%lld, %lld]",
+             (long long)w, (long long)m, (long long)n);
+    }
   EXPECT(ihip_layernorm_rows_f16(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 4, 8, 1e-5f, nullptr) ==
              IHIP_ERR_INVALID_ARG, "layernorm null");
   EXPECT(ihip_bias_gelu_tanh_axpy_bf16(nullptr, nullptr, nullptr, -2, 8, 0.5f, nullptr) == IHIP_ERR_INVALID_ARG,
