@@ -100,17 +100,19 @@ int ihip_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, void* 
 int ihip_softmax_rows_f32_ex(const float* x, float* y, int64_t M, int64_t N, int rows_per_wg, void* stream);
 
 /* Bytes of workspace ihip_softmax_rows_f32_ws uses for an [M, N] softmax: 2 * M * S floats
- * when rows are longer than 65536 floats (vocabulary-width rows) and split into S <= 256
- * segments, else 0 (the rows are not split).  Depends on M and N only.  Same softmax as
- * ihip_softmax_rows_f32, whose long-row kernel it speeds up (the reference lowers every N
- * through _kernel_softmax_2d_last_f32, backends/cuda/codegen/intentir_to_cuda.py:1103-1247). */
+ * when rows are longer than 65536 floats (vocabulary-width rows) and too few for a workgroup
+ * per row to fill the GPU (fewer than 192, or a last round of at most 160 rows after one or
+ * two full rounds of 256), split into S segments each; else 0 (the rows are not split).
+ * Depends on M and N only.  Same softmax as ihip_softmax_rows_f32, whose long-row kernel it
+ * speeds up on such shapes (the reference lowers every N through
+ * _kernel_softmax_2d_last_f32, backends/cuda/codegen/intentir_to_cuda.py:1103-1247). */
 int64_t ihip_softmax_rows_f32_workspace_size(int64_t M, int64_t N);
 
 /* ihip_softmax_rows_f32 with a caller-owned device workspace (the library still allocates
  * nothing): when ihip_softmax_rows_f32_workspace_size(M, N) > 0 and the rows of x and y start
  * at the same offset modulo 16 bytes (4-byte aligned), each row is split over S workgroups;
  * one kernel writes each segment's maximum and sum of exponentials to the workspace and a
- * second combines a row's S partials in segment order and writes y.  Results are
+ * second folds a row's S partials in a fixed order and writes y.  Results are
  * reproducible; the sum's rounding order differs from the unsplit form.  workspace may be
  * NULL (exactly ihip_softmax_rows_f32); otherwise it must hold at least workspace_size
  * bytes, 8-byte aligned, and stay untouched until the work on `stream` completes. */

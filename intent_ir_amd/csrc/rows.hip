@@ -544,19 +544,98 @@ __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_skew(const float* __
   if (tid < tail) yr[head + 4 * nb + tid] = tv * inv;
 }
 
-// Any N: one workgroup per row, three passes (max, sum, write) over the row.
-__global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restrict__ x, float* __restrict__ y, int64_t N) {
-  __shared__ float scratch[4];
+// (m, s) <- the statistics of the union of two sets of elements: maxima m and m2, sums of
+// exponentials s = sum(exp(x - m)) and s2 = sum(exp(x - m2)).  A set whose maximum is -inf
+// (empty, or all of it masked) adds 0; a NaN maximum propagates.  Commutative, so a
+// butterfly over a wave leaves every lane with the same pair.
+__device__ __forceinline__ void softmax_fold(float& m, float& s, float m2, float s2) {
+  const float ninf = -__builtin_inff();
+  const float nm = max_nan(m, m2);
+  s = (m == ninf ? 0.f : s * exp_nonpos(m - nm)) + (m2 == ninf ? 0.f : s2 * exp_nonpos(m2 - nm));
+  m = nm;
+}
+
+// Folds every thread's (m, s) into the workgroup's, in a fixed order (xor butterfly within each
+// wave, then the waves in order through LDS); every thread returns the same pair.
+template <int kW>
+__device__ __forceinline__ void block_softmax_fold(float& m, float& s, float* fm, float* fs) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) softmax_fold(m, s, __shfl_xor(m, off, kWave), __shfl_xor(s, off, kWave));
+  const int lane = threadIdx.x & 63, v = threadIdx.x >> 6;
+  if (lane == 0) fm[v] = m, fs[v] = s;
+  __syncthreads();
+  m = fm[0];
+  s = fs[0];
+#pragma unroll
+  for (int k = 1; k < kW; ++k) softmax_fold(m, s, fm[k], fs[k]);
+}
+
+// Rows no other form holds (longer than 65536 floats without a workspace, or x and y at
+// different offsets modulo 16 bytes): one 1024-thread workgroup per row, two passes over x.
+// The first keeps a running maximum and sum of exponentials per thread (the sum rescaled by
+// exp(old - new) when the maximum grows) and folds them over the workgroup; the second writes
+// exp(x - max) * (1 / sum) with the register kernels' arithmetic.  kVec: x and y 4-byte
+// aligned at the same offset modulo 16 bytes: a head and tail of < 4 elements on the first
+// threads around 16-byte loads of the body; otherwise 4-byte loads throughout.
+template <bool kVec>
+__global__ __launch_bounds__(1024) void softmax_rows_f32_online(const float* __restrict__ x, float* __restrict__ y,
+                                                                int64_t N) {
+  constexpr int kW = 16, kT = 1024, kU = 4;
+  __shared__ float fm[kW], fs[kW];
+  const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const float* xr = x + row * N;
   float* yr = y + row * N;
-  float mx = -__builtin_inff();
-  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) mx = max_nan(mx, xr[i]);
-  mx = block_max_nan(mx, scratch);
-  float s = 0.f;
-  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) s += expf(xr[i] - mx);
-  s = block_sum(s, scratch);
-  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) yr[i] = expf(xr[i] - mx) / s;
+  const float ninf = -__builtin_inff();
+  float m = ninf, s = 0.f;
+  // adds four elements (-inf for none) to the thread's running pair
+  auto add4 = [&](float a, float b, float c, float d) {
+    const float nm = max_nan(m, max_nan(max_nan(a, b), max_nan(c, d)));
+    if (nm != ninf) {
+      s = (m == ninf ? 0.f : s * exp_nonpos(m - nm)) +
+          ((exp_nonpos(a - nm) + exp_nonpos(b - nm)) + (exp_nonpos(c - nm) + exp_nonpos(d - nm)));
+      m = nm;
+    }
+  };
+  if constexpr (kVec) {
+    const int64_t to_edge = (4 - ((reinterpret_cast<uintptr_t>(xr) >> 2) & 3)) & 3;
+    const int64_t head = to_edge < N ? to_edge : N;
+    const int64_t nb = (N - head) >> 2, tail = N - head - 4 * nb;
+    const f32x4* xb = reinterpret_cast<const f32x4*>(xr + head);
+    f32x4* yb = reinterpret_cast<f32x4*>(yr + head);
+    for (int64_t i = tid; i < nb; i += kU * kT) {
+      f32x4 q[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) q[u] = i + u * kT < nb ? xb[i + u * kT] : f32x4{ninf, ninf, ninf, ninf};
+#pragma unroll
+      for (int u = 0; u < kU; ++u) add4(q[u].x, q[u].y, q[u].z, q[u].w);
+    }
+    add4(tid < head ? xr[tid] : ninf, tid < tail ? xr[head + 4 * nb + tid] : ninf, ninf, ninf);
+    block_softmax_fold<kW>(m, s, fm, fs);
+    const float inv = 1.0f / s;
+    for (int64_t i = tid; i < nb; i += kU * kT) {
+      f32x4 q[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (i + u * kT < nb) q[u] = __builtin_nontemporal_load(xb + i + u * kT);
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (i + u * kT < nb) {
+          const f32x4 e = {exp_nonpos(q[u].x - m), exp_nonpos(q[u].y - m), exp_nonpos(q[u].z - m),
+                           exp_nonpos(q[u].w - m)};
+          __builtin_nontemporal_store(e * inv, yb + i + u * kT);
+        }
+    }
+    if (tid < head) yr[tid] = exp_nonpos(xr[tid] - m) * inv;
+    if (tid < tail) yr[head + 4 * nb + tid] = exp_nonpos(xr[head + 4 * nb + tid] - m) * inv;
+  } else {
+    for (int64_t i = tid; i < N; i += 4 * kT)
+      add4(xr[i], i + kT < N ? xr[i + kT] : ninf, i + 2 * kT < N ? xr[i + 2 * kT] : ninf,
+           i + 3 * kT < N ? xr[i + 3 * kT] : ninf);
+    block_softmax_fold<kW>(m, s, fm, fs);
+    const float inv = 1.0f / s;
+    for (int64_t i = tid; i < N; i += kT) yr[i] = exp_nonpos(xr[i] - m) * inv;
+  }
 }
 
 // ------------------------------------------------------------- long rows, split over workgroups
@@ -565,10 +644,10 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restr
 //   softmax_split_stats: segment j's maximum m_j and s_j = sum(exp(x - m_j)) over the segment,
 //     written to part[2 * (row * S + j) + {0, 1}];
 //   softmax_split_write: the row's maximum mx = max_j m_j and sum = sum_j s_j * exp(m_j - mx),
-//     added in segment order (a segment whose maximum is -inf, all of it masked, adds 0), then
-//     y = exp(x - mx) * (1 / sum) over the segment.
-// x is read twice and y written once (the workgroup-per-row kernel reads x three times), every
-// CU is busy for few rows, and each element's arithmetic is that of the register-resident
+//     folded in a fixed order (softmax_fold: a segment whose maximum is -inf, all of it masked,
+//     adds 0), then y = exp(x - mx) * (1 / sum) over the segment.
+// x is read twice and y written once, as by the workgroup-per-row kernel, but every CU is
+// busy for few rows, and each element's arithmetic is that of the register-resident
 // kernels: only the sum's rounding order differs.  Special values come out as numpy's: a NaN
 // anywhere gives a NaN maximum and NaN everywhere; +inf gives inf - inf = NaN in its segment's
 // s_j and so everywhere; a row of -inf gives mx = -inf and NaN.
@@ -581,7 +660,7 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_any(const float* __restr
 // second (non-temporal) read: 2-6 points of HBM peak at 33-130 MB of x against non-temporal
 // loads in both, and no worse at 1 GiB.
 constexpr int kSplitThreads = 256;
-constexpr int kSplitMaxSegments = 256;
+constexpr int64_t kSplitMaxSegments = 1 << 20;
 
 struct SplitRow {
   int64_t head, nb, tail;  // elements before the body, body vectors, elements after it
@@ -667,15 +746,13 @@ __global__ __launch_bounds__(kSplitThreads) void softmax_split_write(const float
   const bool ht = kSkew && seg == 0;
   const float hv = ht && tid < r.head ? xr[tid] : ninf;
   const float tv = ht && tid < r.tail ? xr[r.head + 4 * r.nb + tid] : ninf;
-  // the row's statistics from its S partials (uniform: every workgroup of the row gets the same)
+  // the row's statistics from its S partials, folded in a fixed order (partials j = t, t + 256,
+  // ... by thread t, then the workgroup), so every workgroup of the row gets the same pair
+  __shared__ float fm[kSplitThreads / kWave], fs[kSplitThreads / kWave];
   const float* pr = part + 2 * row * S;
-  float mx = pr[0];
-  for (int j = 1; j < S; ++j) mx = max_nan(mx, pr[2 * j]);
-  float tot = 0.f;
-  for (int j = 0; j < S; ++j) {
-    const float m = pr[2 * j];
-    tot += m == ninf ? 0.f : pr[2 * j + 1] * exp_nonpos(m - mx);
-  }
+  float mx = ninf, tot = 0.f;
+  for (int j = tid; j < S; j += kSplitThreads) softmax_fold(mx, tot, pr[2 * j], pr[2 * j + 1]);
+  block_softmax_fold<kSplitThreads / kWave>(mx, tot, fm, fs);
   const float inv = 1.0f / tot;
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
@@ -689,11 +766,17 @@ __global__ __launch_bounds__(kSplitThreads) void softmax_split_write(const float
   if (ht && tid < r.tail) yr[r.head + 4 * r.nb + tid] = exp_nonpos(tv - mx) * inv;
 }
 
-// Split of an [M, N] softmax: S segments per row of 256 * vpl vectors, or S = 0 (not split:
-// rows of at most 65536 floats, or more than kSplitMaxSegments segments).  The longest segments
-// (16 vectors per thread) unless that leaves fewer than 512 workgroups.  Shape only.
+// Split of an [M, N] softmax: S segments per row of 256 * vpl vectors, or S = 0 (not split).
+// Rows of at most 65536 floats stay in registers.  Longer rows are split when the workgroup-per-
+// row kernel would leave CUs idle: fewer than 192 rows, or a last round of at most 160 rows
+// after one or two full rounds of 256 (measured on MI355X at N = 65540, 128256 and 262144: the
+// split is 5-20% faster there and 2-12% slower elsewhere, where both read x twice but the
+// row kernel finds more of its second read in the caches).  The longest segments (16 vectors
+// per thread) unless that leaves fewer than 512 workgroups.  Depends on the shape only.
 SoftmaxSplit softmax_split_plan(int64_t M, int64_t N) {
   if (M <= 0 || N <= 65536) return {0, 0};
+  const bool idle = M < 192 || (M > 256 && M < 640 && M % 256 != 0 && M % 256 <= 160);
+  if (!idle) return {0, 0};
   const int64_t n4 = N / 4;  // body vectors of a row, at most
   int vpl = 16;
   int64_t S = (n4 + kSplitThreads * vpl - 1) / (kSplitThreads * vpl);
@@ -815,8 +898,10 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
     softmax_rows_f32_regs<64, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x, y, M, N);
   else if (!vec && N <= 64 * 64 * 16)
     softmax_rows_f32_regs<64, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, M, N);
+  else if (skew || vec)
+    softmax_rows_f32_online<true><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, N);
   else
-    softmax_rows_f32_any<<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, N);
+    softmax_rows_f32_online<false><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, N);
   return hipGetLastError();
 }
 

@@ -486,10 +486,13 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
 
 def softmax_split_plan(M: int, N: int) -> Tuple[int, int]:
     """(S, vpl) of the split long-row softmax (rows.hip softmax_split_plan): rows longer than
-    65536 floats are cut into S segments of 256 * vpl 16-byte vectors, vpl = 16 unless that
-    leaves fewer than 512 workgroups (then 8, then 4); (0, 0) = not split, also when S would
-    exceed 256."""
+    65536 floats are cut into S segments of 256 * vpl 16-byte vectors when a workgroup per row
+    would leave CUs idle (fewer than 192 rows, or a last round of at most 160 rows after one or
+    two full rounds of 256); vpl = 16 unless that leaves fewer than 512 workgroups (then 8, then
+    4); (0, 0) = not split, also when S would exceed 2**20 or the grid 2**31 - 1 workgroups."""
     if M <= 0 or N <= 65536:
+        return 0, 0
+    if not (M < 192 or (256 < M < 640 and 0 < M % 256 <= 160)):
         return 0, 0
     n4 = N // 4
     vpl = 16
@@ -497,7 +500,7 @@ def softmax_split_plan(M: int, N: int) -> Tuple[int, int]:
     while vpl > 4 and M * s < 512:
         vpl //= 2
         s = _cdiv(n4, 256 * vpl)
-    if s > 256 or M * s > 0x7FFFFFFF:
+    if s > 1 << 20 or M * s > 0x7FFFFFFF:
         return 0, 0
     return s, vpl
 

@@ -81,7 +81,8 @@ static void row_kernels() {
   // long rows: 8 segments of 4096 vectors per 128256-float row at 64 rows, 2 floats each
   EXPECT(ihip_softmax_rows_f32_workspace_size(64, 128256) == 64 * 8 * 8, "softmax split workspace");
   EXPECT(ihip_softmax_rows_f32_workspace_size(64, 65536) == 0, "softmax rows not split");
-  EXPECT(ihip_softmax_rows_f32_workspace_size(1, 1048580) == 0, "softmax split past 256 segments");
+  EXPECT(ihip_softmax_rows_f32_workspace_size(1, 1048580) == 257 * 8, "softmax split: 257 segments of 1024 vectors");
+  EXPECT(ihip_softmax_rows_f32_workspace_size(1LL << 20, 1LL << 30) == 0, "softmax split grid past 2^31");
   EXPECT(ihip_softmax_rows_f32_workspace_size(-1, 128256) == 0, "softmax split negative");
   EXPECT(ihip_softmax_rows_f32_workspace_size(1LL << 40, 1LL << 40) == 0, "softmax split overflow");
   EXPECT(ihip_softmax_rows_f32_ws((float*)fake(64), (float*)fake(64), 64, 128256, fake(256), 8, nullptr) ==

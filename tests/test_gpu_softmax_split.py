@@ -33,7 +33,8 @@ def _check(out, ref, what):
 
 
 @pytest.mark.parametrize("M,N", [(1, 65540), (3, 128256), (64, 151936), (257, 100000), (5, 262144),
-                                 (2, 1 << 20), (4, 65537), (3, 100003), (1, 1048580)])
+                                 (2, 1 << 20), (4, 65537), (3, 100003), (1, 1048580), (1, 1 << 24),
+                                 (512, 65540), (448, 100003)])
 def test_split_softmax_matches_the_oracle(hip, M, N):
     w = WORKLOADS["softmax"]
     b = {"M": M, "N": N}
@@ -64,8 +65,9 @@ def _run(hip, x, y, M, N, ws=None, off=(0, 0)):
 
 @pytest.mark.parametrize("M,N", [(8, 151936), (6, 131073)])
 def test_split_and_unsplit_forms_agree(hip, M, N):
-    """Through the C-ABI: no workspace (a workgroup per row, three passes) against the split,
-    with special values in the rows; the split repeats bit for bit."""
+    """Through the C-ABI: no workspace (a workgroup per row, two passes; 16-byte loads, and
+    4-byte loads with y one float off x's alignment) against the split, with special values
+    in the rows; the split repeats bit for bit."""
     import torch
 
     rng = np.random.default_rng(N)
@@ -81,18 +83,21 @@ def test_split_and_unsplit_forms_agree(hip, M, N):
     y = torch.empty(M * N, device="cuda")
     print(f"[case] softmax split vs unsplit M={M} N={N} ws={ws.numel()}", flush=True)
     a = _run(hip, x, y, M, N)
+    a4 = _run(hip, x, torch.empty(M * N + 1, device="cuda"), M, N, off=(0, 1))
     b1 = _run(hip, x, y, M, N, ws)
     b2 = _run(hip, x, y, M, N, ws)
     np.testing.assert_array_equal(b1, b2)
     with np.errstate(invalid="ignore", over="ignore"):
         ref = execute_intent(WORKLOADS["softmax"].ir(), {"input_ptr": xh}, {"M": M, "N": N})["output_ptr"]
-    for got in (a, b1):
+    for got in (a, a4, b1):
         np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+        assert (got[2, : 3 * N // 4] == 0.0).all()
     assert np.isnan(b1[[0, 1, 3]]).all() and not np.isnan(b1[[2, 4, 5]]).any()
     assert (b1[2, : 3 * N // 4] == 0.0).all()
     fin = ~np.isnan(ref)
     _check(np.where(fin, b1, 0), np.where(fin, ref, 0), "split")
     _check(np.where(fin, b1, 0), np.where(fin, a, 0), "split against unsplit")
+    _check(np.where(fin, a4, 0), np.where(fin, ref, 0), "unsplit, 4-byte loads")
 
 
 @pytest.mark.parametrize("N", [65539, 100003, 131072])

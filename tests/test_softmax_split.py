@@ -16,15 +16,17 @@ from intent_ir_amd.configs import WORKLOADS
 from intent_ir_amd.lowering import softmax_split_plan
 from intent_ir_amd.runtime import load_library
 
-SHAPES = [(m, n) for m in (0, 1, 2, 3, 17, 31, 32, 33, 64, 255, 256, 1000, 4096)
-          for n in (0, 1, 4096, 65536, 65537, 65540, 100003, 128256, 151936, 262144, 1 << 20, 1048576 + 4, 1 << 22)]
+SHAPES = [(m, n) for m in (0, 1, 2, 3, 17, 31, 32, 33, 64, 191, 192, 255, 256, 257, 300, 416, 417, 512, 513, 639,
+                          640, 1000, 4096)
+          for n in (0, 1, 4096, 65536, 65537, 65540, 100003, 128256, 151936, 262144, 1 << 20, 1048576 + 4, 1 << 22,
+                    1 << 30)]
 
 
 def test_python_split_plan_matches_the_library():
     lib = load_library()
     for M, N in SHAPES:
         s, vpl = softmax_split_plan(M, N)
-        assert (s == 0) == (vpl == 0) and vpl in (0, 4, 8, 16) and 0 <= s <= 256
+        assert (s == 0) == (vpl == 0) and vpl in (0, 4, 8, 16) and 0 <= s <= 1 << 20
         if s:
             # the segments cover the longest body a row can have, and no segment is empty
             assert s * 256 * vpl >= N // 4 > (s - 1) * 256 * vpl
@@ -32,8 +34,12 @@ def test_python_split_plan_matches_the_library():
 
 
 @pytest.mark.parametrize("M,N,S,vpl", [(64, 128256, 8, 16), (1, 128256, 32, 4), (16, 151936, 38, 4),
-                                       (32, 151936, 19, 8), (4096, 65540, 5, 16), (2, 1 << 20, 256, 4),
-                                       (1, 1048580, 0, 0), (100, 65536, 0, 0)])
+                                       (32, 151936, 19, 8), (4096, 65540, 0, 0), (2, 1 << 20, 256, 4),
+                                       (191, 128256, 8, 16), (192, 128256, 0, 0), (256, 128256, 0, 0),
+                                       (257, 100000, 7, 16), (416, 128256, 8, 16), (417, 128256, 0, 0),
+                                       (512, 128256, 0, 0), (639, 70000, 5, 16), (640, 70000, 0, 0),
+                                       (1, 1048580, 257, 4), (1, 1 << 26, 4096, 16), (100, 65536, 0, 0),
+                                       (1 << 20, 1 << 30, 0, 0)])
 def test_lowering_selects_the_split_form(M, N, S, vpl):
     assert softmax_split_plan(M, N) == (S, vpl)
     k = lower_intent_to_hip_kernel(WORKLOADS["softmax"].ir(), shape_bindings={"M": M, "N": N})
