@@ -324,6 +324,12 @@ def test_library_exports_every_declared_symbol():
     lib.ihip_abi_version.restype = ctypes.c_int
     assert lib.ihip_abi_version() == 2
     lib.ihip_last_error.restype = ctypes.c_char_p
+    # the message is per thread and survives until the next call: other tests in this process
+    # may have left one, and a successful call (an empty softmax needs no device) clears it
+    lib.ihip_softmax_rows_f32.restype = ctypes.c_int
+    lib.ihip_softmax_rows_f32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_void_p]
+    assert lib.ihip_softmax_rows_f32(None, None, 0, 0, None) == 0
     assert lib.ihip_last_error() == b""
 
 
