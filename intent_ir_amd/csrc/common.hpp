@@ -119,6 +119,15 @@ __device__ __forceinline__ float block_max_nan(float v, float* scratch) {
   return r;
 }
 
+// Workgroup b of a G-workgroup launch runs on XCD b % 8 (workgroups are dispatched to the XCDs
+// round robin).  Its position in an order where every XCD holds one contiguous run (G / 8
+// workgroups, one more on the first G % 8 XCDs), so that the tiles an XCD runs together are
+// neighbours in the tile order and share that XCD's L2.  A bijection on [0, G).
+__device__ __forceinline__ int xcd_contiguous(int b, int G) {
+  const int x = b % kNumXcd, q = G / kNumXcd, r = G % kNumXcd;
+  return x * q + (x < r ? x : r) + b / kNumXcd;
+}
+
 // Row split of a long-row softmax (rows.hip): S segments per row of 256 * vpl 16-byte
 // vectors, two floats of workspace per segment; S = 0 when rows are not split.
 struct SoftmaxSplit {

@@ -152,9 +152,7 @@ void gemm_bf16_bias_relu_kernel(const uint16_t* __restrict__ A, const uint16_t* 
   const int wm = wave & 1, wn = wave >> 1;
 
   // ---- tile schedule: XCD-contiguous, then grouped raster inside each XCD's range
-  int bid = blockIdx.x;
-  const int T = gridDim.x;
-  if (T % kNumXcd == 0) bid = (bid % kNumXcd) * (T / kNumXcd) + bid / kNumXcd;
+  const int bid = xcd_contiguous(blockIdx.x, gridDim.x);
   const int per_group = kGroupM * tiles_n;
   const int g = bid / per_group, first_m = g * kGroupM;
   const int gsz = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;

@@ -791,9 +791,7 @@ void gemm_bf16_fast_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) char lds_raw[kLdsBytes];
 
-  int bid = blockIdx.x;
-  const int T = gridDim.x;
-  if (T % kNumXcd == 0) bid = (bid % kNumXcd) * (T / kNumXcd) + bid / kNumXcd;
+  const int bid = xcd_contiguous(blockIdx.x, gridDim.x);
   const int per_group = kGroupRows * tiles_n;
   const int grp = bid / per_group, first_m = grp * kGroupRows;
   const int gsz = (tiles_m - first_m) < kGroupRows ? (tiles_m - first_m) : kGroupRows;
@@ -825,9 +823,7 @@ void gemm_bf16_splitk_kernel(const uint16_t* __restrict__ A, const uint16_t* __r
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) char lds_raw[kLdsBytes];
 
-  // XCD x runs bids x, x + 8, ...: G / 8 of them, one more for x < G % 8
-  const int G = gridDim.x, xcd = blockIdx.x % kNumXcd;
-  const int bid = xcd * (G / kNumXcd) + (xcd < G % kNumXcd ? xcd : G % kNumXcd) + blockIdx.x / kNumXcd;
+  const int bid = xcd_contiguous(blockIdx.x, gridDim.x);
   const int T = tiles_m * tiles_n;
   const int seg = bid / T, t = bid % T;
   const int per_group = kGroupRows * tiles_n;
@@ -896,8 +892,12 @@ constexpr int kFastStages = 4;
 // At most this many 256x256 tiles (half of the 256 CUs busy) the launch uses 128x128 tiles:
 // measured 0.74-0.99 PF/s on such grids against 0.4-0.8 with 256x256 tiles; from 144 tiles up
 // the 256x256 kernel is faster (fewer busy CUs also run at a higher clock on this power-limited
-// chip).
+// chip).  Skinny products (M <= 128, the rows of a decode step) with more than one round of
+// 256x256 tiles also take 128x128 tiles: a 256-row tile computes at least twice the rows it
+// stores, and halving that waste was 10-18% faster at M = 32-128 with N = 128256, K = 4096
+// (with a single round, 16 x 50257 x 4096, the 256x256 tiles stayed 15% faster).
 constexpr int64_t kSmallGridTiles = 128;
+constexpr int64_t kSkinnyRows = 128;
 
 // Any M, N and K (edge tiles are copied through the descriptor's range check and stored under
 // masks) as long as every row of A and B starts 16 bytes aligned: K % 8 == 0, M % 8 == 0 when
@@ -919,7 +919,7 @@ bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, bool tran
 
 int gemm_fast_tile_extent(int64_t M, int64_t N) {
   const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
-  return tiles256 <= kSmallGridTiles ? 128 : 256;
+  return tiles256 <= kSmallGridTiles || (M <= kSkinnyRows && tiles256 > 256) ? 128 : 256;
 }
 
 template <int TILE, bool CU>

@@ -317,8 +317,9 @@ def _al256(n: int) -> int:
 
 def _gemm_tile_extent(M: int, N: int) -> int:
     """gemm_fast.hip gemm_fast_tile_extent: 128x128 tiles when at most 128 tiles of 256x256
-    (half the CUs) would be busy, else 256x256."""
-    return 128 if _cdiv(M, 256) * _cdiv(N, 256) <= 128 else 256
+    (half the CUs) would be busy, or for M <= 128 with more than 256 such tiles, else 256x256."""
+    tiles256 = _cdiv(M, 256) * _cdiv(N, 256)
+    return 128 if tiles256 <= 128 or (M <= 128 and tiles256 > 256) else 256
 
 
 _SPLIT_RATE = (0, 305, 533, 680, 800)  # tile-steps per microsecond at 0, 64, 128, 192, 256 workgroups

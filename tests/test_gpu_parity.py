@@ -548,6 +548,24 @@ def _gemm_splitk(hip, A, B, bias, M, N, K, ta, tb, splits, tile=0, c_offset=0):
     return c[c_offset:].cpu().numpy().view(np.uint16).reshape(M, N)
 
 
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("M,N,K", [(16, 65792, 512), (128, 66048, 256), (100, 65800, 200)])
+def test_gemm_skinny_products_take_128_tiles(hip, M, N, K, tb):
+    """M <= 128 with more than 256 tiles of 256x256 (N > 65536, a vocabulary projection in a
+    decode step) runs 128x128 tiles by default: the same bits as either tile size on request
+    (same MFMA over the same k order), and the oracle's values."""
+    w = WORKLOADS["matmul"]
+    b = {"M": M, "N": N, "K": K}
+    inp = w.gen(b, seed=M + N + K, sigma=1.0)
+    B = np.ascontiguousarray(inp["B"].T) if tb else inp["B"]
+    print(f"[case] gemm skinny M={M} N={N} K={K} tb={tb}", flush=True)
+    auto = _gemm_splitk(hip, inp["A"], B, inp["bias"], M, N, K, False, tb, 1)
+    for tile in (128, 256):
+        assert np.array_equal(auto, _gemm_splitk(hip, inp["A"], B, inp["bias"], M, N, K, False, tb, 1, tile=tile))
+    ref = oracle_outputs(w.ir(), inp, b)
+    check({"C": bf16_bits_to_f32(auto)}, ref, ["C"], TOL["matmul_strict"], f"skinny {b}")
+
+
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("M,N,K,splits", [
     (1024, 1024, 8192, 0),   # the split rule: 64 tiles of 128x128, 4 segments of 2048

@@ -214,14 +214,17 @@ def test_gemm_forms_and_errors():
     (65536, 16384, 40968, 256, "guarded"), (5000, 3001, 64, 256, "packed"), (7, 9, 3, 128, "packed"),
     (1024, 1024, 8192, 128, "split4"), (1000, 1000, 4100, 128, "packed+split4"), (128, 64, 65536, 128, "split128"),
     (1536, 1408, 8192, 128, "fast"), (1408, 1408, 1024, 128, "fast"), (64, 64, 4096, 128, "split8"),
-    (512, 512, 16384, 128, "split16"), (1024, 1024, 2048, 128, "fast")])
+    (512, 512, 16384, 128, "split16"), (1024, 1024, 2048, 128, "fast"),
+    # skinny (M <= 128) with more than one round of 256x256 tiles: 128x128; with one round: 256x256
+    (32, 131072, 4096, 128, "fast"), (128, 65792, 4096, 128, "fast"), (129, 131072, 4096, 256, "fast"),
+    (64, 65536, 8192, 256, "fast"), (16, 50256, 4096, 256, "fast")])
 def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tile, path):
     """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N (LDS:
     three paired-slice A regions and four B stages); other rows are packed into a workspace
     and then take the tiled kernel; the guarded kernel (a double-buffered pair of 64-k operand
     tiles) is left for shapes beyond the tiled kernel's limits, such as a ragged K with
     operands above 2 GiB.  All use 256x256 tiles, or 128x128 tiles when at most 128 tiles of
-    256x256 (half the CUs) would be busy.  A grid of 128x128 tiles may be split along K into S
+    256x256 (half the CUs) would be busy, or when M <= 128 and more than 256 such tiles run.  A grid of 128x128 tiles may be split along K into S
     segments (tiles x S workgroups), its f32 partials in the workspace, where the split rule
     estimates a gain: 64 tiles with K = 8192 take 4 segments, 16 tiles with K = 16384 take 16,
     one tile with K = 65536 takes 128 segments of 512; 132 tiles (1536 x 1408) would need a
