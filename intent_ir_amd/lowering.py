@@ -489,8 +489,8 @@ def softmax_split_plan(M: int, N: int) -> Tuple[int, int]:
     """(S, vpl) of the split long-row softmax (rows.hip softmax_split_plan): rows longer than
     65536 floats are cut into S segments of 256 * vpl 16-byte vectors when a workgroup per row
     would leave CUs idle (fewer than 192 rows, or a last round of at most 160 rows after one or
-    two full rounds of 256); vpl = 16 unless that leaves fewer than 512 workgroups (then 8, then
-    4); (0, 0) = not split, also when S would exceed 2**20 or the grid 2**31 - 1 workgroups."""
+    two full rounds of 256); vpl = 16 unless that leaves fewer than 4096 workgroups (then 8,
+    then 4); (0, 0) = not split, also when S would exceed 2**20 or the grid 2**31 - 1 workgroups."""
     if M <= 0 or N <= 65536:
         return 0, 0
     if not (M < 192 or (256 < M < 640 and 0 < M % 256 <= 160)):
@@ -498,7 +498,7 @@ def softmax_split_plan(M: int, N: int) -> Tuple[int, int]:
     n4 = N // 4
     vpl = 16
     s = _cdiv(n4, 256 * vpl)
-    while vpl > 4 and M * s < 512:
+    while vpl > 4 and M * s < 4096:
         vpl //= 2
         s = _cdiv(n4, 256 * vpl)
     if s > 1 << 20 or M * s > 0x7FFFFFFF:

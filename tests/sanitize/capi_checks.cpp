@@ -78,8 +78,8 @@ static void row_kernels() {
   EXPECT(ihip_softmax_rows_f32_ex(nullptr, nullptr, 0, 8, 3, nullptr) == IHIP_ERR_INVALID_ARG, "rows_per_wg 3");
   EXPECT(ihip_softmax_rows_f32_ex((float*)fake(64), (float*)fake(128), 4, 8192, 2, nullptr) == IHIP_ERR_INVALID_ARG,
          "rows_per_wg on a multi-wave row");
-  // long rows: 8 segments of 4096 vectors per 128256-float row at 64 rows, 2 floats each
-  EXPECT(ihip_softmax_rows_f32_workspace_size(64, 128256) == 64 * 8 * 8, "softmax split workspace");
+  // long rows: 32 segments of 1024 vectors per 128256-float row at 64 rows, 2 floats each
+  EXPECT(ihip_softmax_rows_f32_workspace_size(64, 128256) == 64 * 32 * 8, "softmax split workspace");
   EXPECT(ihip_softmax_rows_f32_workspace_size(64, 65536) == 0, "softmax rows not split");
   EXPECT(ihip_softmax_rows_f32_workspace_size(1, 1048580) == 257 * 8, "softmax split: 257 segments of 1024 vectors");
   EXPECT(ihip_softmax_rows_f32_workspace_size(1LL << 20, 1LL << 30) == 0, "softmax split grid past 2^31");
@@ -87,7 +87,7 @@ static void row_kernels() {
   EXPECT(ihip_softmax_rows_f32_workspace_size(1LL << 40, 1LL << 40) == 0, "softmax split overflow");
   EXPECT(ihip_softmax_rows_f32_ws((float*)fake(64), (float*)fake(64), 64, 128256, fake(256), 8, nullptr) ==
              IHIP_ERR_INVALID_ARG, "softmax workspace too small");
-  EXPECT(ihip_softmax_rows_f32_ws((float*)fake(64), (float*)fake(64), 64, 128256, fake(260), 4096, nullptr) ==
+  EXPECT(ihip_softmax_rows_f32_ws((float*)fake(64), (float*)fake(64), 64, 128256, fake(260), 16384, nullptr) ==
              IHIP_ERR_INVALID_ARG, "softmax workspace alignment");
   EXPECT(ihip_softmax_rows_f32_ws((float*)fake(64), (float*)fake(64), 64, 128256, nullptr, 4096, nullptr) ==
              IHIP_ERR_INVALID_ARG, "softmax workspace null with bytes");

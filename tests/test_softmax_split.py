@@ -33,11 +33,12 @@ def test_python_split_plan_matches_the_library():
         assert lib.ihip_softmax_rows_f32_workspace_size(M, N) == 8 * M * s, (M, N)
 
 
-@pytest.mark.parametrize("M,N,S,vpl", [(64, 128256, 8, 16), (1, 128256, 32, 4), (16, 151936, 38, 4),
-                                       (32, 151936, 19, 8), (4096, 65540, 0, 0), (2, 1 << 20, 256, 4),
-                                       (191, 128256, 8, 16), (192, 128256, 0, 0), (256, 128256, 0, 0),
-                                       (257, 100000, 7, 16), (416, 128256, 8, 16), (417, 128256, 0, 0),
-                                       (512, 128256, 0, 0), (639, 70000, 5, 16), (640, 70000, 0, 0),
+@pytest.mark.parametrize("M,N,S,vpl", [(64, 128256, 32, 4), (1, 128256, 32, 4), (16, 151936, 38, 4),
+                                       (32, 151936, 38, 4), (4096, 65540, 0, 0), (2, 1 << 20, 256, 4),
+                                       (191, 128256, 32, 4), (192, 128256, 0, 0), (256, 128256, 0, 0),
+                                       (257, 100000, 25, 4), (416, 128256, 16, 8), (417, 128256, 0, 0),
+                                       (512, 128256, 0, 0), (639, 70000, 9, 8), (640, 70000, 0, 0),
+                                       (300, 262144, 16, 16),
                                        (1, 1048580, 257, 4), (1, 1 << 26, 4096, 16), (100, 65536, 0, 0),
                                        (1 << 20, 1 << 30, 0, 0)])
 def test_lowering_selects_the_split_form(M, N, S, vpl):
@@ -54,9 +55,9 @@ def test_workspace_argument_checks_without_a_device():
     lib = load_library()
     p = ctypes.c_void_p(256)  # never dereferenced: the checks return before any HIP call
     need = lib.ihip_softmax_rows_f32_workspace_size(64, 128256)
-    assert need == 8 * 64 * 8
+    assert need == 8 * 64 * 32
     st = lib.ihip_softmax_rows_f32_ws(p, p, 64, 128256, p, need - 8, None)
-    assert st == -1 and b"needs 4096" in lib.ihip_last_error()
+    assert st == -1 and b"needs 16384" in lib.ihip_last_error()
     st = lib.ihip_softmax_rows_f32_ws(p, p, 64, 128256, ctypes.c_void_p(260), need, None)
     assert st == -1 and b"aligned" in lib.ihip_last_error()
     st = lib.ihip_softmax_rows_f32_ws(p, p, 64, 128256, None, 64, None)
