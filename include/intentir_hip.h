@@ -134,6 +134,15 @@ int ihip_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const uint16_t
 int ihip_bias_gelu_tanh_axpy_bf16(const uint16_t* x, const uint16_t* bias, uint16_t* y, int64_t M, int64_t N,
                                   float alpha, void* stream);
 
+/* out[i] = inp[row_idx[i], col_idx[i]] for i < L, with inp f32 [M, N], row_idx and col_idx
+ * int32 [L], out f32 [L]; an index pair outside [0, M) x [0, N) (negative indices included)
+ * gives other_value.  Replaces _kernel_gather2d_f32
+ * (backends/cuda/codegen/intentir_to_cuda.py:1779-1832, dispatched at :2155-2156), with the
+ * out-of-range rule its test pins (tests/backends/cuda/test_cuda_backend_smoke.py:292-336).
+ * inp may be NULL when M * N == 0 (every index is then out of range). */
+int ihip_gather2d_f32(const float* inp, const int32_t* row_idx, const int32_t* col_idx, float* out, int64_t M,
+                      int64_t N, int64_t L, float other_value, void* stream);
+
 /* C = act(A @ B + bias) with A bf16 [M, K], B bf16 [K, N], bias f32 [N] or NULL,
  * act = ReLU when relu != 0 else identity; f32 accumulation on MFMA, C bf16
  * (round to nearest even).  Replaces _kernel_matmul_f32 / wmma_matmul_f32_tf32

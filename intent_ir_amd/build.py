@@ -14,8 +14,8 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libintentir_hip.so"
-SOURCES = ["capi.hip", "rows.hip", "elementwise.hip", "gemm.hip", "gemm_fast.hip", "gemm_pack.hip", "ewprog.hip",
-           "ewjit.hip"]
+SOURCES = ["capi.hip", "rows.hip", "elementwise.hip", "gather.hip", "gemm.hip", "gemm_fast.hip", "gemm_pack.hip",
+           "ewprog.hip", "ewjit.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

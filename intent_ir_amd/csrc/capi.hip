@@ -30,6 +30,8 @@ hipError_t launch_layernorm_rows_f16(const uint16_t*, const uint16_t*, const uin
                                      int64_t, int64_t, float, hipStream_t);
 hipError_t launch_bias_gelu_axpy_bf16(const uint16_t*, const uint16_t*, uint16_t*, int64_t, int64_t, float,
                                       hipStream_t);
+hipError_t launch_gather2d_f32(const float*, const int32_t*, const int32_t*, float*, int64_t, int64_t, int64_t, float,
+                               hipStream_t);
 hipError_t launch_gemm_bf16_bias_relu(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t,
                                       int64_t, bool, bool, int, int, hipStream_t);
 hipError_t launch_gemm_bf16_bias_relu_ws(const uint16_t*, const uint16_t*, const float*, uint16_t*, int64_t, int64_t,
@@ -315,6 +317,18 @@ int ihip_bias_gelu_tanh_axpy_bf16(const uint16_t* x, const uint16_t* bias, uint1
   IHIP_REQUIRE(n == 0 || (x != nullptr && bias != nullptr && y != nullptr), "bias_gelu_tanh_axpy_bf16: null pointer");
   return finish(ihip::launch_bias_gelu_axpy_bf16(x, bias, y, M, N, alpha, static_cast<hipStream_t>(stream)),
                 "bias_gelu_tanh_axpy_bf16");
+}
+
+int ihip_gather2d_f32(const float* inp, const int32_t* row_idx, const int32_t* col_idx, float* out, int64_t M,
+                      int64_t N, int64_t L, float other_value, void* stream) {
+  const int64_t n = numel2(M, N);
+  IHIP_REQUIRE(n >= 0 && L >= 0, "gather2d_f32: invalid shape inp [%lld, %lld], L = %lld", (long long)M, (long long)N,
+               (long long)L);
+  IHIP_REQUIRE(L == 0 || (row_idx != nullptr && col_idx != nullptr && out != nullptr), "gather2d_f32: null pointer");
+  IHIP_REQUIRE(L == 0 || n == 0 || inp != nullptr, "gather2d_f32: inp is null");
+  return finish(ihip::launch_gather2d_f32(inp, row_idx, col_idx, out, M, N, L, other_value,
+                                          static_cast<hipStream_t>(stream)),
+                "gather2d_f32");
 }
 
 int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,

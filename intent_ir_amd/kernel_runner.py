@@ -4,6 +4,7 @@
     python -m intent_ir_amd.kernel_runner --config matmul --bindings M=4096,N=50257,K=4096 --transpose-b
     python -m intent_ir_amd.kernel_runner --ew-chain all --launches 20
     python -m intent_ir_amd.kernel_runner --row-reduce sum --bindings M=64,N=1048576 --launches 20
+    python -m intent_ir_amd.kernel_runner --gather --bindings M=8192,N=8192,L=16777216 --launches 20
 
 ``--ew-chain`` runs generic element-wise programs (ihip_elementwise_program, native code)
 on 8192 x 8192 operands and prints each chain's rate: per launch, every input's bytes
@@ -12,6 +13,8 @@ read once and every output's written once, over the median of 5 timed rounds of
 times reduce_sum / reduce_max over the last axis of an f32 [M, N] tensor the same way
 (rotating buffer sets over > 640 MiB), default [64, 1048576]: few long rows, which the
 library splits over several workgroups per row with partial results in a workspace.
+``--gather`` times gather2d (ihip_gather2d_f32) over L uniformly random index pairs into an
+f32 [M, N] tensor (default 8192 x 8192, L = 2^24), 16 algorithmic bytes per element.
 
 Inputs are generated on the GPU; launches rotate over enough buffer sets that
 reads come from HBM rather than the Infinity Cache (as in bench.py).  With
@@ -168,12 +171,53 @@ def run_row_reduce(kind, bindings, launches, torch) -> int:
     return 0
 
 
+def run_gather(bindings, launches, torch) -> int:
+    """gather(inp [M, N] f32, row [L] i32, col [L] i32) -> out [L] (ihip_gather2d_f32) with
+    uniformly random in-range indices; algorithmic bytes 16 per element (two indices, one inp
+    value, one output), index and output sets rotated over >= 640 MiB."""
+    import statistics  # noqa: PLC0415
+
+    from . import lower_intent_to_hip_kernel  # noqa: PLC0415
+    from .runtime import launch_lowered  # noqa: PLC0415
+
+    ir = {"name": "gather2d", "tensors": {"A": _t("f32", "M", "N"), "row": _t("i32", "L"), "col": _t("i32", "L"),
+                                          "Out": _t("f32", "L")},
+          "ops": [_op("gather", ["A", "row", "col"], "Out", other_value=0.0)], "outputs": ["Out"]}
+    b = {"M": 8192, "N": 8192, "L": 1 << 24, **bindings}
+    k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    per = 16 * b["L"]
+    nsets = max(2, math.ceil(ROTATE_MIN_BYTES / (12 * b["L"])))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    A = torch.randn((b["M"], b["N"]), generator=g, device="cuda")
+    sets = [{"A": A, "row": torch.randint(0, b["M"], (b["L"],), generator=g, device="cuda", dtype=torch.int32),
+             "col": torch.randint(0, b["N"], (b["L"],), generator=g, device="cuda", dtype=torch.int32),
+             "Out": torch.empty(b["L"], device="cuda")} for _ in range(nsets)]
+    for i in range(nsets):
+        launch_lowered(k, sets[i])
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(5):
+        t0.record()
+        for i in range(launches):
+            launch_lowered(k, sets[i % nsets])
+        t1.record()
+        torch.cuda.synchronize()
+        times.append(t0.elapsed_time(t1) / launches)
+    ms = statistics.median(times)
+    print(f"[runner] gather {b}: {k.kernel_id}, {ms * 1e3:.1f} us/launch, {per / (ms * 1e-3) / 1e12:.2f} TB/s "
+          f"algorithmic, {b['L'] / (ms * 1e-3) / 1e9:.2f} G elements/s", flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", choices=["any", "softmax", "layernorm", "gelu", "matmul"])
     ap.add_argument("--ew-chain", choices=sorted(EW_CHAINS) + ["all"],
                     help="time a generic element-wise program chain (or all of them)")
     ap.add_argument("--row-reduce", choices=["sum", "max"], help="time a row reduction (f32 [M, N], --bindings)")
+    ap.add_argument("--gather", action="store_true", help="time gather2d (inp f32 [M, N], L random index pairs)")
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--copy-mib", type=int, default=0)
     ap.add_argument("--bindings", default="", help="comma-separated SYMBOL=VALUE overrides, e.g. M=1000,N=4096")
@@ -182,8 +226,8 @@ def main(argv=None) -> int:
                     help="pass an empty workspace (a GEMM that would be packed runs the guarded kernel, a long-row "
                          "softmax the workgroup-per-row kernel)")
     args = ap.parse_args(argv)
-    if sum(x is not None for x in (args.config, args.ew_chain, args.row_reduce)) != 1:
-        ap.error("give exactly one of --config, --ew-chain and --row-reduce")
+    if sum(x is not None for x in (args.config, args.ew_chain, args.row_reduce)) + args.gather != 1:
+        ap.error("give exactly one of --config, --ew-chain, --row-reduce and --gather")
     if args.transpose_b and args.config != "matmul":
         ap.error("--transpose-b applies to --config matmul only")
 
@@ -191,8 +235,10 @@ def main(argv=None) -> int:
 
     if args.ew_chain:
         return run_ew_chains(sorted(EW_CHAINS) if args.ew_chain == "all" else [args.ew_chain], args.launches, torch)
-    if args.row_reduce:
+    if args.row_reduce or args.gather:
         rb = {n: int(v) for n, _, v in (item.partition("=") for item in filter(None, args.bindings.split(",")))}
+        if args.gather:
+            return run_gather(rb, args.launches, torch)
         return run_row_reduce(args.row_reduce, rb, args.launches, torch)
 
     from . import lower_intent_to_hip_kernel

@@ -506,6 +506,44 @@ def softmax_split_plan(M: int, N: int) -> Tuple[int, int]:
     return s, vpl
 
 
+def _match_gather(fn: IntentFunction, b: Dict[str, Any]) -> Optional[HipLoweredKernel]:
+    """A lone gather(inp [M, N] f32, row [L] i32, col [L] i32) -> out [L] f32: the CUDA
+    backend's gather2d (intentir_to_cuda.py:1779-1832), which it dispatches for a single-op IR
+    (:2155-2156).  An index pair outside [0, M) x [0, N) gives attrs.other_value (default 0),
+    as there (tests/backends/cuda/test_cuda_backend_smoke.py:292-336).  Any other use of gather
+    is rejected."""
+    gathers = [o for o in fn.ops if o.op == "gather"]
+    if not gathers:
+        return None
+    form = ("HIP lowering unsupported gather form: gather is lowered as a lone op: "
+            "gather(inp [M, N] f32, row [L] i32, col [L] i32) -> out [L] f32")
+    if len(fn.ops) != 1 or len(gathers[0].inputs) != 3 or list(fn.outputs) != [gathers[0].output]:
+        raise HipLoweringError(form)
+    op = gathers[0]
+    inp, row, col = op.inputs
+    out = op.output
+    t = fn.tensors
+    if (t[inp].dtype, t[row].dtype, t[col].dtype, t[out].dtype) != ("f32", "i32", "i32", "f32"):
+        raise HipLoweringError(form + f"; got {t[inp].dtype}, {t[row].dtype}, {t[col].dtype} -> {t[out].dtype}")
+    try:
+        shp = {n: resolve_shape(t[n], b) for n in (inp, row, col, out)}
+    except KeyError as e:
+        raise HipLoweringError(f"missing binding for gather: {e}") from e
+    if len(shp[inp]) != 2 or len(shp[row]) != 1 or shp[col] != shp[row] or shp[out] != shp[row]:
+        raise HipLoweringError(form + f"; got shapes {[list(shp[n]) for n in (inp, row, col, out)]}")
+    (M, N), (L,) = shp[inp], shp[row]
+    try:
+        other = float((op.attrs or {}).get("other_value", 0.0))
+    except (TypeError, ValueError) as e:
+        raise HipLoweringError(f"gather other_value must be a number: {e}") from e
+    io = {"arg_names": [inp, row, col, out], "scalars": {},
+          "tensors": {n: {"dtype": t[n].dtype, "shape": t[n].dims()} for n in (inp, row, col, out)}}
+    launch = HipLaunch((max(1, _cdiv(L, 1024)), 1, 1), (256, 1, 1), 0)  # 4 elements per thread
+    return HipLoweredKernel(fn.name, "ihip_gather2d_f32", io, launch, [out], dict(b),
+                            (("tensor", inp), ("tensor", row), ("tensor", col), ("tensor", out), ("i64", M),
+                             ("i64", N), ("i64", L), ("f32", other)))
+
+
 def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     X = ("?in", "x")
     MEAN = ("div", ("rsum", X, (1,)), ("?c", "n1"))
@@ -778,6 +816,11 @@ def lower_intent_to_hip_kernel(intent, *, shape_bindings: Mapping[str, Any],
     unsupported = sorted({o.op for o in fn.ops} - HIP_SUPPORTED_OPS)
     if unsupported:
         raise HipLoweringError(f"HIP lowering unsupported ops {unsupported} in {fn.name}")
+    k = _match_gather(fn, bindings)
+    if k is not None:
+        _Knobs(fn, bindings).check_used(k.kernel_id)
+        k.io_spec["hip_call"] = call_args_to_json(k.call_args)
+        return k
     try:
         ctx = _Ctx(fn, bindings)
     except PatternError as e:

@@ -38,7 +38,7 @@ ELEMENTWISE_OPS: frozenset = frozenset({
 }) | VIEW_OPS
 
 HIP_SUPPORTED_OPS: frozenset = ELEMENTWISE_OPS | frozenset({
-    "reduce_sum", "reduce_max", "reduce_any", "softmax", "matmul",
+    "reduce_sum", "reduce_max", "reduce_any", "softmax", "matmul", "gather",
 })
 
 __all__ = ["CORE_OPS", "EXPERIMENTAL_OPS", "MACRO_OPS", "SUPPORTED_OPS", "VIEW_OPS", "ELEMENTWISE_OPS",

@@ -104,6 +104,15 @@ static void row_kernels() {
     }
   EXPECT(ihip_layernorm_rows_f16(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 4, 8, 1e-5f, nullptr) ==
              IHIP_ERR_INVALID_ARG, "layernorm null");
+  EXPECT(ihip_gather2d_f32((float*)fake(64), (int32_t*)fake(64), (int32_t*)fake(64), (float*)fake(64), 7, 9, -1, 0.f,
+                           nullptr) == IHIP_ERR_INVALID_ARG, "gather negative L");
+  EXPECT(ihip_gather2d_f32((float*)fake(64), nullptr, (int32_t*)fake(64), (float*)fake(64), 7, 9, 32, 0.f,
+                           nullptr) == IHIP_ERR_INVALID_ARG, "gather null index");
+  EXPECT(ihip_gather2d_f32(nullptr, (int32_t*)fake(64), (int32_t*)fake(64), (float*)fake(64), 7, 9, 32, 0.f,
+                           nullptr) == IHIP_ERR_INVALID_ARG, "gather null inp");
+  EXPECT(ihip_gather2d_f32((float*)fake(64), (int32_t*)fake(64), (int32_t*)fake(64), (float*)fake(64), 1LL << 40,
+                           1LL << 40, 32, 0.f, nullptr) == IHIP_ERR_INVALID_ARG, "gather overflow");
+  EXPECT(ihip_gather2d_f32(nullptr, nullptr, nullptr, nullptr, 7, 9, 0, 0.f, nullptr) == IHIP_OK, "gather L = 0");
   EXPECT(ihip_bias_gelu_tanh_axpy_bf16(nullptr, nullptr, nullptr, -2, 8, 0.5f, nullptr) == IHIP_ERR_INVALID_ARG,
          "gelu shape");
   EXPECT(ihip_gemm_bf16_bias_relu(nullptr, nullptr, nullptr, nullptr, 2, 2, 2, 1, nullptr) == IHIP_ERR_INVALID_ARG,
