@@ -72,16 +72,25 @@ __global__ __launch_bounds__(256) void reduce_any_rows_f32_scalar(const float* _
   if (lane == 0) out[row] = acc != 0u;
 }
 
-// bool/u8 input: out[m] = any(x[m, :] != 0).  Vector form (N % 16 == 0, 16-byte aligned
-// base): a wave per row ORs 16-byte words, 16 loads per lane in flight, as the f32 kernel.
+// bool/u8 input: out[m] = any(x[m, :] != 0).  A wave per row ORs 16-byte words of the row's
+// aligned body, 16 loads per lane in flight, as the f32 kernel; the head (bytes before the row's
+// first 16-byte boundary) and the tail (after its last) are < 16 bytes each, one byte per lane
+// on the first lanes, so any N and any base alignment take the vector form.
 template <int kUnroll>
-__global__ __launch_bounds__(64) void reduce_any_rows_u8_vec(const u32x4* __restrict__ x, uint8_t* __restrict__ out,
-                                                             int64_t M, int64_t n16) {
+__global__ __launch_bounds__(64) void reduce_any_rows_u8_vec(const uint8_t* __restrict__ x, uint8_t* __restrict__ out,
+                                                             int64_t M, int64_t N) {
   const int lane = threadIdx.x & 63;
   const int64_t row = blockIdx.x;
   if (row >= M) return;
-  const u32x4* xr = x + row * n16;
+  const uint8_t* rowp = x + row * N;
+  const int64_t to_edge = (16 - (reinterpret_cast<uintptr_t>(rowp) & 15)) & 15;
+  const int64_t head = to_edge < N ? to_edge : N;
+  const int64_t n16 = (N - head) >> 4;
+  const int64_t tail = N - head - 16 * n16;
+  const u32x4* xr = reinterpret_cast<const u32x4*>(rowp + head);
   uint32_t acc = 0;
+  if (lane < head) acc |= rowp[lane];
+  if (lane < tail) acc |= rowp[head + 16 * n16 + lane];
   for (int64_t base = lane; base < n16; base += kWave * kUnroll) {
     u32x4 v[kUnroll];
 #pragma unroll
@@ -92,18 +101,6 @@ __global__ __launch_bounds__(64) void reduce_any_rows_u8_vec(const u32x4* __rest
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) acc |= v[u].x | v[u].y | v[u].z | v[u].w;
   }
-  acc = wave_or(acc);
-  if (lane == 0) out[row] = acc != 0u;
-}
-
-__global__ __launch_bounds__(256) void reduce_any_rows_u8(const uint8_t* __restrict__ x, uint8_t* __restrict__ out,
-                                                          int64_t M, int64_t N) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (row >= M) return;
-  const uint8_t* xr = x + row * N;
-  uint32_t acc = 0;
-  for (int64_t i = lane; i < N; i += kWave) acc |= xr[i];
   acc = wave_or(acc);
   if (lane == 0) out[row] = acc != 0u;
 }
@@ -137,11 +134,11 @@ hipError_t launch_reduce_any_rows_f32(const float* x, uint8_t* out, int64_t M, i
 hipError_t launch_reduce_any_rows_u8(const uint8_t* x, uint8_t* out, int64_t M, int64_t N, hipStream_t s) {
   if (M == 0) return hipSuccess;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row in the vector form
-  if (N % 16 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0)
-    reduce_any_rows_u8_vec<16><<<dim3(static_cast<unsigned>(M)), dim3(kStreamBlock), 0, s>>>(
-        reinterpret_cast<const u32x4*>(x), out, M, N / 16);
+  const dim3 grid(static_cast<unsigned>(M)), block(kStreamBlock);
+  if (N / 16 >= kWave * 16)
+    reduce_any_rows_u8_vec<16><<<grid, block, 0, s>>>(x, out, M, N);
   else
-    reduce_any_rows_u8<<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(x, out, M, N);
+    reduce_any_rows_u8_vec<4><<<grid, block, 0, s>>>(x, out, M, N);
   return hipGetLastError();
 }
 

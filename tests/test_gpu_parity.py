@@ -100,10 +100,12 @@ def test_reduce_any_special_values(hip):
     assert out["out"].tolist() == [False, False, True, True, True, True, False, True]
 
 
-@pytest.mark.parametrize("M,N", [(1, 16), (3, 4096), (17, 4112), (33, 17), (5, 4100), (2, 65536), (300, 1024)])
+@pytest.mark.parametrize("M,N", [(1, 16), (3, 4096), (17, 4112), (33, 17), (5, 4100), (2, 65536), (300, 1024),
+                                 (4, 15), (7, 1), (64, 16385), (9, 20001)])
 def test_reduce_any_bool_input(hip, M, N):
-    """reduce_any over an i1 tensor (interpreter.py:489-494): the 16-byte vector form for
-    N % 16 == 0, the byte-wise form otherwise; rows with a single true at either end."""
+    """reduce_any over an i1 tensor (interpreter.py:489-494): 16-byte words over each row's
+    aligned body, a head and tail of < 16 bytes when rows do not start 16-byte aligned (N % 16
+    != 0); rows with a single true at either end."""
     ir = {"name": "anyb", "tensors": {"x": {"dtype": "i1", "shape": ["M", "N"]}, "out": {"dtype": "i1", "shape": ["M"]}},
           "ops": [{"op": "reduce_any", "inputs": ["x"], "output": "out", "attrs": {"dims": [1]}}], "outputs": ["out"]}
     rng = np.random.default_rng(M * 31 + N)
@@ -118,6 +120,33 @@ def test_reduce_any_bool_input(hip, M, N):
     out = run_case(ir, {"x": x}, {"M": M, "N": N})
     np.testing.assert_array_equal(out["out"], oracle_outputs(ir, {"x": x}, {"M": M, "N": N})["out"])
     np.testing.assert_array_equal(out["out"], x.any(axis=1))
+
+
+@pytest.mark.parametrize("N", [1, 15, 16, 17, 31, 1000, 16401])
+@pytest.mark.parametrize("off", [0, 1, 7, 15])
+def test_reduce_any_bool_at_every_alignment(hip, N, off):
+    """Through the C-ABI with x placed off bytes past a 256-byte aligned base: each row's head,
+    body and tail move with the offset; a single true byte at every position class (head, body,
+    tail) of some row, and rows of all zeros, give exactly numpy's any."""
+    import ctypes
+
+    import torch
+
+    M = 48
+    x = np.zeros((M, N), dtype=np.uint8)
+    for r in range(1, M, 2):
+        x[r, (r * 7919) % N] = 1 + (r % 5)  # any non-zero byte counts as true
+    x[2, 0] = 1
+    x[4, N - 1] = 1
+    buf = torch.zeros(M * N + off, dtype=torch.uint8, device="cuda")
+    buf[off:] = torch.from_numpy(x.reshape(-1)).cuda()
+    out = torch.full((M,), 9, dtype=torch.uint8, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    print(f"[case] reduce_any_rows_u8 N={N} offset={off}", flush=True)
+    assert hip.ihip_reduce_any_rows_u8(ctypes.c_void_p(buf.data_ptr() + off), ctypes.c_void_p(out.data_ptr()), M, N,
+                                       ctypes.c_void_p(s)) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), (x != 0).any(axis=1).astype(np.uint8))
 
 
 def test_reduce_any_ne_form_with_nonzero_constant(hip):
