@@ -1338,33 +1338,100 @@ __global__ __launch_bounds__(64 * kLnLdsWaves) __attribute__((amdgpu_waves_per_e
   }
 }
 
-// Any N: one workgroup per row, three passes over the row.
-__global__ __launch_bounds__(256) void layernorm_rows_f16_any(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                              const uint16_t* __restrict__ b, uint16_t* __restrict__ y,
-                                                              float* __restrict__ mean_out, float* __restrict__ rstd_out,
-                                                              int64_t N, float eps) {
+// Rows no other form holds (longer than 65543 halves, x and y at different offsets modulo 16
+// bytes, bases not 2-byte aligned): one workgroup per row (kT threads: 1024, or 256 for rows of
+// at most 16384 halves, which leave a larger one idle) and the reference's three
+// passes (sum; sum of squared deviations from the mean; the output), in f32 with the IR's op
+// order and no contraction.  kVec: N % 8 == 0 and x, y, w, b 16-byte aligned, 16-byte accesses
+// (8 halves), two per thread in flight; otherwise 2-byte accesses.  Between passes the row is
+// read again, mostly from L2 (a 64K-half row is 128 KiB).
+__device__ __forceinline__ float sum_f16x8(const u32x4& v) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    s += f16_to_f32(static_cast<uint16_t>(v[k] & 0xffffu)) + f16_to_f32(static_cast<uint16_t>(v[k] >> 16));
+  return s;
+}
+
+__device__ __forceinline__ float sq_dev_f16x8(const u32x4& v, float mean) {
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float a = f16_to_f32(static_cast<uint16_t>(v[k] & 0xffffu)) - mean;
+    const float c = f16_to_f32(static_cast<uint16_t>(v[k] >> 16)) - mean;
+    q += a * a + c * c;
+  }
+  return q;
+}
+
+__device__ __forceinline__ uint16_t ln_out(uint16_t xh, uint16_t wh, uint16_t bh, float mean, float rstd) {
+  const float d = f16_to_f32(xh) - mean;
+  const float xhat = d * rstd;
+  const float scaled = xhat * f16_to_f32(wh);
+  return f32_to_f16_rne(scaled + f16_to_f32(bh));
+}
+
+template <bool kVec, int kT>
+__global__ __launch_bounds__(kT) void layernorm_rows_f16_long(const uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ w,
+                                                                const uint16_t* __restrict__ b, uint16_t* __restrict__ y,
+                                                                float* __restrict__ mean_out,
+                                                                float* __restrict__ rstd_out, int64_t N, float eps) {
 #pragma clang fp contract(off)
-  __shared__ float scratch[4];
+  __shared__ float scratch[kT / kWave];
+  const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * N;
   uint16_t* yr = y + row * N;
+  const int64_t n8 = N / 8;
+  const u32x4* x8 = reinterpret_cast<const u32x4*>(xr);
   float s = 0.f;
-  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) s += f16_to_f32(xr[i]);
+  if constexpr (kVec) {
+    for (int64_t i = tid; i < n8; i += 2 * kT) {
+      const u32x4 v0 = x8[i];
+      const u32x4 v1 = i + kT < n8 ? x8[i + kT] : u32x4(0u);
+      s += sum_f16x8(v0) + sum_f16x8(v1);
+    }
+  } else {
+    for (int64_t i = tid; i < N; i += kT) s += f16_to_f32(xr[i]);
+  }
   const float mean = block_sum(s, scratch) / static_cast<float>(N);
   float q = 0.f;
-  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) {
-    const float d = f16_to_f32(xr[i]) - mean;
-    q += d * d;
+  if constexpr (kVec) {
+    for (int64_t i = tid; i < n8; i += 2 * kT) {
+      const u32x4 v0 = x8[i];
+      q += sq_dev_f16x8(v0, mean);
+      if (i + kT < n8) q += sq_dev_f16x8(x8[i + kT], mean);
+    }
+  } else {
+    for (int64_t i = tid; i < N; i += kT) {
+      const float d = f16_to_f32(xr[i]) - mean;
+      q += d * d;
+    }
   }
   const float var = block_sum(q, scratch) / static_cast<float>(N);
   const float rstd = 1.0f / sqrtf(var + eps);
-  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) {
-    const float d = f16_to_f32(xr[i]) - mean;
-    const float xhat = d * rstd;
-    const float scaled = xhat * f16_to_f32(w[i]);
-    yr[i] = f32_to_f16_rne(scaled + f16_to_f32(b[i]));
+  if constexpr (kVec) {
+    const u32x4* w8 = reinterpret_cast<const u32x4*>(w);
+    const u32x4* b8 = reinterpret_cast<const u32x4*>(b);
+    u32x4* y8 = reinterpret_cast<u32x4*>(yr);
+    for (int64_t i = tid; i < n8; i += kT) {
+      const u32x4 v = __builtin_nontemporal_load(x8 + i), wv = w8[i], bv = b8[i];
+      u32x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = ln_out(static_cast<uint16_t>(v[k] & 0xffffu), static_cast<uint16_t>(wv[k] & 0xffffu),
+                                   static_cast<uint16_t>(bv[k] & 0xffffu), mean, rstd);
+        const uint32_t hi = ln_out(static_cast<uint16_t>(v[k] >> 16), static_cast<uint16_t>(wv[k] >> 16),
+                                   static_cast<uint16_t>(bv[k] >> 16), mean, rstd);
+        o[k] = lo | (hi << 16);
+      }
+      __builtin_nontemporal_store(o, y8 + i);
+    }
+  } else {
+    for (int64_t i = tid; i < N; i += kT) yr[i] = ln_out(xr[i], w[i], b[i], mean, rstd);
   }
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     if (mean_out != nullptr) mean_out[row] = mean;
     if (rstd_out != nullptr) rstd_out[row] = rstd;
   }
@@ -1446,7 +1513,13 @@ hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const
     return hipGetLastError();
   }
   if (!vec) {
-    layernorm_rows_f16_any<<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, w, b, y, mean, rstd, N, eps);
+    const dim3 grid(static_cast<unsigned>(M));
+    if (N % 8 == 0 && (al & 15) == 0)  // N > 65536
+      layernorm_rows_f16_long<true, 1024><<<grid, dim3(1024), 0, s>>>(x, w, b, y, mean, rstd, N, eps);
+    else if (N > 16384)
+      layernorm_rows_f16_long<false, 1024><<<grid, dim3(1024), 0, s>>>(x, w, b, y, mean, rstd, N, eps);
+    else
+      layernorm_rows_f16_long<false, 256><<<grid, dim3(256), 0, s>>>(x, w, b, y, mean, rstd, N, eps);
     return hipGetLastError();
   }
   const int n8 = static_cast<int>(N / 8);

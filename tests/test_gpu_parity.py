@@ -286,10 +286,12 @@ def _check_ln(out, ref, what):
 
 
 @pytest.mark.parametrize("M", [1, 3, 17])
-@pytest.mark.parametrize("N", EDGE + [64, 1000, 1024, 4096, 4104, 8192, 8200, 16384, 20000, 65536, 65544])
+@pytest.mark.parametrize("N", EDGE + [64, 1000, 1024, 4096, 4104, 8192, 8200, 16384, 20000, 65536, 65544, 65545, 100000,
+                                      100003, 262144])
 def test_layernorm_edge_shapes(hip, M, N):
     """One wave per row up to N = 4096; 2-16 waves per row up to 65536 (rows per workgroup
-    16 / waves, so M = 17 leaves waves past the last row); the three-pass kernel beyond."""
+    16 / waves, so M = 17 leaves waves past the last row); beyond, a 1024-thread workgroup per
+    row with 16-byte accesses (N % 8 == 0) or 2-byte ones (65545, 100003)."""
     w = WORKLOADS["layernorm"]
     b = {"M": M, "N": N}
     inp = w.gen(b, seed=M * 7 + N)
@@ -307,13 +309,14 @@ def test_layernorm_rows_not_16_byte_aligned(hip, M, N):
     _check_ln(run_case(w.ir(), inp, b), oracle_outputs(w.ir(), inp, b), f"LN {b}")
 
 
-@pytest.mark.parametrize("N", [1000, 4099, 8200])
+@pytest.mark.parametrize("N", [1000, 4099, 8200, 70000])
 @pytest.mark.parametrize("ox,oy,ow", [(1, 1, 0), (3, 3, 0), (7, 7, 0), (1, 2, 0), (0, 5, 0), (3, 3, 1), (0, 0, 3)])
 def test_layernorm_at_every_alignment(hip, N, ox, oy, ow):
     """Through the C-ABI with x and y offset by ox, oy halves from a 16-byte boundary: equal
-    offsets take the head/body/tail form, unequal ones the three-pass kernel; w and b offset by
-    ow halves are read element by element instead of as realigned 16-byte vectors.  All against
-    the oracle."""
+    offsets take the head/body/tail form (up to 65543 halves), unequal ones (and N = 70000 at
+    any offset) the workgroup-per-row kernel with 2-byte accesses; w and b offset by ow halves
+    are read element by element instead of as realigned 16-byte vectors.  All against the
+    oracle."""
     import ctypes
 
     import torch
