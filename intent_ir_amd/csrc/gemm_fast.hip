@@ -919,7 +919,11 @@ bool gemm_fast_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, bool tran
 
 int gemm_fast_tile_extent(int64_t M, int64_t N) {
   const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
-  return tiles256 <= kSmallGridTiles || (M <= kSkinnyRows && tiles256 > 256) ? 128 : 256;
+  const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
+  // one row of 256x256 tiles holding 129-256 rows: 128x128 tiles would take two rounds for a
+  // second tile-row of at most half the rows (256 x 32000 x 4096: 7-17% slower than 256x256)
+  const bool one_full_row = M > kSkinnyRows && M <= 256 && tiles128 > 256;
+  return (tiles256 <= kSmallGridTiles && !one_full_row) || (M <= kSkinnyRows && tiles256 > 256) ? 128 : 256;
 }
 
 template <int TILE, bool CU>

@@ -317,9 +317,12 @@ def _al256(n: int) -> int:
 
 def _gemm_tile_extent(M: int, N: int) -> int:
     """gemm_fast.hip gemm_fast_tile_extent: 128x128 tiles when at most 128 tiles of 256x256
-    (half the CUs) would be busy, or for M <= 128 with more than 256 such tiles, else 256x256."""
+    (half the CUs) would be busy, unless M is 129-256 and the 128x128 grid needs more than
+    one round, or for M <= 128 with more than 256 such tiles; else 256x256."""
     tiles256 = _cdiv(M, 256) * _cdiv(N, 256)
-    return 128 if tiles256 <= 128 or (M <= 128 and tiles256 > 256) else 256
+    tiles128 = _cdiv(M, 128) * _cdiv(N, 128)
+    one_full_row = 128 < M <= 256 and tiles128 > 256
+    return 128 if (tiles256 <= 128 and not one_full_row) or (M <= 128 and tiles256 > 256) else 256
 
 
 _SPLIT_RATE = (0, 305, 533, 680, 800)  # tile-steps per microsecond at 0, 64, 128, 192, 256 workgroups

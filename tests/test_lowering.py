@@ -217,7 +217,9 @@ def test_gemm_forms_and_errors():
     (512, 512, 16384, 128, "split16"), (1024, 1024, 2048, 128, "fast"),
     # skinny (M <= 128) with more than one round of 256x256 tiles: 128x128; with one round: 256x256
     (32, 131072, 4096, 128, "fast"), (128, 65792, 4096, 128, "fast"), (129, 131072, 4096, 256, "fast"),
-    (64, 65536, 8192, 256, "fast"), (16, 50256, 4096, 256, "fast")])
+    (64, 65536, 8192, 256, "fast"), (16, 50256, 4096, 256, "fast"),
+    # one row of 256x256 tiles with 129-256 rows and more than a round of 128x128 tiles: 256x256
+    (256, 32000, 4096, 256, "fast"), (200, 33024, 1024, 256, "fast"), (256, 16384, 8192, 128, "fast")])
 def test_gemm_launch_descriptor_follows_the_fast_path(M, N, K, tile, path):
     """Rows 16-byte aligned (N % 8 == 0, K % 8 == 0) take the tiled kernel at any M and N (LDS:
     three paired-slice A regions and four B stages); other rows are packed into a workspace
