@@ -105,6 +105,72 @@ __global__ __launch_bounds__(64) void reduce_any_rows_u8_vec(const uint8_t* __re
   if (lane == 0) out[row] = acc != 0u;
 }
 
+// Short rows (at most 64 16-byte vectors): G lanes per row (G = 4 .. 32, a power of two), 64 / G
+// rows per wave, about two vectors per lane, the row's head and tail elements (before its first
+// 16-byte boundary and after its last) on the group's first lanes, and an OR over the group.
+// kEsz: element bytes (4: f32 compared with c, or by its bits when kZero; 1: u8, any non-zero).
+template <int G, int kEsz, bool kZero>
+__global__ __launch_bounds__(256) void reduce_any_rows_grouped(const void* __restrict__ x, uint8_t* __restrict__ out,
+                                                               int64_t M, int64_t N, float c) {
+  constexpr int kPerVec = 16 / kEsz;
+  const int lig = threadIdx.x & (G - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / G) + threadIdx.x / G;
+  auto test = [&](const char* p) -> uint32_t {
+    if constexpr (kEsz == 1) {
+      return *reinterpret_cast<const uint8_t*>(p);
+    } else {
+      const float v = *reinterpret_cast<const float*>(p);
+      return kZero ? (__float_as_uint(v) & 0x7fffffffu) : static_cast<uint32_t>(v != c);
+    }
+  };
+  uint32_t acc = 0;
+  if (row < M) {  // no early return: the group's shuffles below need every lane
+    const char* rowp = reinterpret_cast<const char*>(x) + row * N * kEsz;
+    const int64_t to_edge = ((16 - (reinterpret_cast<uintptr_t>(rowp) & 15)) & 15) / kEsz;
+    const int64_t head = to_edge < N ? to_edge : N;
+    const int64_t nb = (N - head) / kPerVec;
+    const int64_t tail = N - head - nb * kPerVec;
+    for (int64_t t = lig; t < head; t += G) acc |= test(rowp + t * kEsz);
+    for (int64_t t = lig; t < tail; t += G) acc |= test(rowp + (head + nb * kPerVec + t) * kEsz);
+    const u32x4* body = reinterpret_cast<const u32x4*>(rowp + head * kEsz);
+    for (int64_t v = lig; v < nb; v += G) {
+      const u32x4 w = __builtin_nontemporal_load(body + v);
+      if constexpr (kEsz == 1) {
+        acc |= w.x | w.y | w.z | w.w;
+      } else if constexpr (kZero) {
+        acc |= (w.x | w.y | w.z | w.w) & 0x7fffffffu;
+      } else {
+        acc |= static_cast<uint32_t>(__uint_as_float(w.x) != c) | static_cast<uint32_t>(__uint_as_float(w.y) != c) |
+               static_cast<uint32_t>(__uint_as_float(w.z) != c) | static_cast<uint32_t>(__uint_as_float(w.w) != c);
+      }
+    }
+  }
+#pragma unroll
+  for (int off = G / 2; off > 0; off >>= 1) acc |= __shfl_xor(acc, off, kWave);
+  if (row < M && lig == 0) out[row] = acc != 0u;
+}
+
+// Lanes per row for a row of `bytes` bytes in the grouped form: about two 16-byte vectors per
+// lane, 4 .. 32; 0 when the row is long enough for a wave of its own (more than 64 vectors).
+static int any_group_lanes(int64_t bytes) {
+  const int64_t nvec = bytes / 16;
+  if (nvec > 64) return 0;
+  int g = 4;
+  while (g < 32 && 2 * g < nvec) g *= 2;
+  return g;
+}
+
+template <int kEsz, bool kZero>
+static void launch_any_grouped(const void* x, uint8_t* out, int64_t M, int64_t N, float c, int g, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((M * g + 255) / 256)), block(256);
+  switch (g) {
+    case 4: reduce_any_rows_grouped<4, kEsz, kZero><<<grid, block, 0, s>>>(x, out, M, N, c); break;
+    case 8: reduce_any_rows_grouped<8, kEsz, kZero><<<grid, block, 0, s>>>(x, out, M, N, c); break;
+    case 16: reduce_any_rows_grouped<16, kEsz, kZero><<<grid, block, 0, s>>>(x, out, M, N, c); break;
+    default: reduce_any_rows_grouped<32, kEsz, kZero><<<grid, block, 0, s>>>(x, out, M, N, c); break;
+  }
+}
+
 // Row kernels take the number of rows per workgroup from blockDim.x / 64.  Streaming kernels
 // launch one-wave workgroups (measured 2-3% faster than four-wave ones on MI355X at 128 MiB).
 constexpr int kStreamBlock = 64;
@@ -115,7 +181,13 @@ hipError_t launch_reduce_any_rows_f32(const float* x, uint8_t* out, int64_t M, i
   const dim3 grid(static_cast<unsigned>(M)), block(kStreamBlock);
   // 16-byte loads over each row's aligned body whenever x is 4-byte aligned (any N)
   const bool vec = (reinterpret_cast<uintptr_t>(x) & 3) == 0;
-  if (!vec) {
+  const int g = vec ? any_group_lanes(4 * N) : 0;
+  if (g > 0) {  // short rows: several per wave
+    if (c == 0.0f)
+      launch_any_grouped<4, true>(x, out, M, N, c, g, s);
+    else
+      launch_any_grouped<4, false>(x, out, M, N, c, g, s);
+  } else if (!vec) {
     reduce_any_rows_f32_scalar<<<grid, block, 0, s>>>(x, out, M, N, c);
   } else if (c == 0.0f) {
     if (N / 4 >= kWave * 16)
@@ -135,7 +207,10 @@ hipError_t launch_reduce_any_rows_u8(const uint8_t* x, uint8_t* out, int64_t M, 
   if (M == 0) return hipSuccess;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row in the vector form
   const dim3 grid(static_cast<unsigned>(M)), block(kStreamBlock);
-  if (N / 16 >= kWave * 16)
+  const int g = any_group_lanes(N);
+  if (g > 0)  // short rows: several per wave
+    launch_any_grouped<1, false>(x, out, M, N, 0.0f, g, s);
+  else if (N / 16 >= kWave * 16)
     reduce_any_rows_u8_vec<16><<<grid, block, 0, s>>>(x, out, M, N);
   else
     reduce_any_rows_u8_vec<4><<<grid, block, 0, s>>>(x, out, M, N);

@@ -122,7 +122,7 @@ def test_reduce_any_bool_input(hip, M, N):
     np.testing.assert_array_equal(out["out"], x.any(axis=1))
 
 
-@pytest.mark.parametrize("N", [1, 15, 16, 17, 31, 1000, 16401])
+@pytest.mark.parametrize("N", [1, 15, 16, 17, 31, 64, 129, 1000, 1023, 1025, 16401])
 @pytest.mark.parametrize("off", [0, 1, 7, 15])
 def test_reduce_any_bool_at_every_alignment(hip, N, off):
     """Through the C-ABI with x placed off bytes past a 256-byte aligned base: each row's head,
@@ -147,6 +147,36 @@ def test_reduce_any_bool_at_every_alignment(hip, N, off):
                                        ctypes.c_void_p(s)) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), (x != 0).any(axis=1).astype(np.uint8))
+
+
+@pytest.mark.parametrize("N", [1, 3, 4, 5, 63, 64, 65, 255, 256, 1023, 1025])
+@pytest.mark.parametrize("off", [0, 1, 3])
+@pytest.mark.parametrize("c", [0.0, 1.0])
+def test_reduce_any_f32_short_rows(hip, N, off, c):
+    """Rows of at most 64 16-byte vectors run several per wave (4-32 lanes per row); through the
+    C-ABI with x placed off floats past an aligned base, rows equal to c everywhere but one
+    position (head, body or tail of the row), rows of -0.0 (equal to 0), NaN, against numpy."""
+    import ctypes
+
+    import torch
+
+    M = 77
+    x = np.full((M, N), c, dtype=np.float32)
+    if c == 0.0:
+        x[1::4] = -0.0
+    for r in range(2, M, 3):
+        x[r, (r * 131) % N] = 2.5 if r % 2 else np.nan
+    x[5, 0] = -7.0
+    x[8, N - 1] = 1e-45
+    buf = torch.zeros(M * N + off, dtype=torch.float32, device="cuda")
+    buf[off:] = torch.from_numpy(x.reshape(-1)).cuda()
+    out = torch.full((M,), 9, dtype=torch.uint8, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    print(f"[case] reduce_any_rows_f32 N={N} offset={off} c={c}", flush=True)
+    assert hip.ihip_reduce_any_rows_f32(ctypes.c_void_p(buf.data_ptr() + 4 * off), ctypes.c_void_p(out.data_ptr()), M,
+                                        N, ctypes.c_float(c), ctypes.c_void_p(s)) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), (x != np.float32(c)).any(axis=1).astype(np.uint8))
 
 
 def test_reduce_any_ne_form_with_nonzero_constant(hip):
