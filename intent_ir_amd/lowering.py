@@ -462,7 +462,12 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
     if rows > 1 and not (N % 4 == 0 and N <= 4096):
         raise HipLoweringError(f"{rows} rows per workgroup needs the one-wave-per-row softmax (N % 4 == 0, "
                                f"N <= 4096); N = {N} runs one row per workgroup")
-    if N % 4 == 0 and N <= 4096:  # 4 rows per workgroup unless a knob says otherwise: a wave per
+    if 0 < N <= 128 and N % 4 == 0 and not rows:  # short rows: g lanes per row (one vector each)
+        g = 1
+        while g < N // 4:
+            g *= 2
+        launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
+    elif N % 4 == 0 and N <= 4096:  # 4 rows per workgroup unless a knob says otherwise: a wave per
         # row, or for N <= 1024 and 4 rows two waves of two rows each
         launch = _row_launch(M, rows or 4)
         if N <= 1024 and (rows or 4) == 4:
@@ -589,7 +594,12 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     args = (("tensor", x), ("tensor", w), ("tensor", b), ("tensor", y), stat("mean"), stat("rstd"), ("i64", M),
             ("i64", N), ("f32", float(env["eps"][1])))
     names = [x, w, b, y] + [inv[r] for r in ("mean", "rstd") if r in inv]
-    if N % 8 == 0 and 0 < N <= 4096:  # 16 rows per 1024-thread workgroup; w and b staged in LDS
+    if N % 8 == 0 and 0 < N <= 256:  # short rows: g lanes per row (one 16-byte vector each)
+        g = 1
+        while g < N // 8:
+            g *= 2
+        launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
+    elif N % 8 == 0 and 0 < N <= 4096:  # 16 rows per 1024-thread workgroup; w and b staged in LDS
         kvpl = next(v for v in (1, 2, 4, 8) if N // 8 <= 64 * v)
         launch = HipLaunch((max(1, _cdiv(M, 16)), 1, 1), (1024, 1, 1), 2 * kvpl * 64 * 16)
     elif N % 8 == 0 and N <= 8192:  # 2 waves per row, 8 rows per 1024-thread workgroup, partials in LDS
@@ -662,7 +672,12 @@ def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
         launch = HipLaunch((M * segs, 1, 1), (1024, 1, 1), 64)
         return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32_ws", c.io([x, oname]), launch, [oname], dict(c.b),
                                 args + (("workspace", 4 * M * segs),))
-    if N > 0:  # 16-byte body loads (a head and tail of < 4 elements around them when rows are
+    if 0 < N and N // 4 <= 128:  # short rows: g lanes per row (two to four vectors each), several per wave
+        g = 1
+        while g < 32 and 2 * g < N // 4:
+            g *= 2
+        launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
+    elif N > 0:  # 16-byte body loads (a head and tail of < 4 elements around them when rows are
         # not 16-byte aligned): a wave per row, or 16 waves per row for few long rows
         few_long = M < 2048 and N // 4 > 256
         launch = HipLaunch((max(1, M), 1, 1), (1024 if few_long else 64, 1, 1), 64 if few_long else 0)

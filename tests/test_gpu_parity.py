@@ -213,7 +213,8 @@ def _row_reduce_ir(op: str) -> dict:
 
 
 ROW_REDUCE_SHAPES = ([(m, n) for m in (1, 3, 17) for n in EDGE + [64, 255, 256, 1023, 1025, 4096, 4100, 65536]]
-                     + [(2048, 256), (2048, 4100), (4096, 1024), (1000, 2048), (2048, 4099), (64, 65537)])
+                     + [(2048, 256), (2048, 4100), (4096, 1024), (1000, 2048), (2048, 4099), (64, 65537),
+                        (65536, 32), (20001, 61), (100, 257), (3000, 512), (77, 515)])
 
 
 @pytest.mark.parametrize("op", ["reduce_sum", "reduce_max"])
@@ -266,12 +267,22 @@ def test_row_reduce_full_size(hip):
 
 # ------------------------------------------------------------------ softmax
 @pytest.mark.parametrize("M", [1, 7, 33])
-@pytest.mark.parametrize("N", EDGE + [64, 256, 1000, 1001, 1024, 1025, 4096, 4097, 4100, 5000, 8191, 8192, 8196, 16384,
-                                      32000, 32768, 50257, 65535, 65536, 65537, 65540])
+@pytest.mark.parametrize("N", EDGE + [4, 12, 64, 100, 128, 132, 256, 1000, 1001, 1024, 1025, 4096, 4097, 4100, 5000, 8191,
+                                      8192, 8196, 16384, 32000, 32768, 50257, 65535, 65536, 65537, 65540])
 def test_softmax_edge_shapes(hip, M, N):
     """N % 4 == 0: one wave per row up to N = 4096, 2-16 waves per row up to 65536 (4100, 8196:
     the first size past a form's capacity).  N % 4 != 0: the row in registers through 4-byte
     loads up to 65535 (1025, 4097: past a form's capacity).  The three-pass kernel beyond."""
+    w = WORKLOADS["softmax"]
+    b = {"M": M, "N": N}
+    inp = w.gen(b, seed=M + N)
+    check(run_case(w.ir(), inp, b), oracle_outputs(w.ir(), inp, b), ["output_ptr"], TOL["softmax"], f"softmax {b}")
+
+
+@pytest.mark.parametrize("M,N", [(65536, 64), (100003, 32), (4099, 128), (777, 4)])
+def test_softmax_many_short_rows(hip, M, N):
+    """Rows of at most 32 16-byte vectors run several per wave (N / 4 rounded up to a power of
+    two lanes each): many rows, row counts that leave a partial wave, against the oracle."""
     w = WORKLOADS["softmax"]
     b = {"M": M, "N": N}
     inp = w.gen(b, seed=M + N)
@@ -315,9 +326,9 @@ def _check_ln(out, ref, what):
     check(out, ref, ["out_mean_ptr", "out_rstd_ptr"], TOL["ln_stats"], what + " stats")
 
 
-@pytest.mark.parametrize("M", [1, 3, 17])
-@pytest.mark.parametrize("N", EDGE + [64, 1000, 1024, 4096, 4104, 8192, 8200, 16384, 20000, 65536, 65544, 65545, 100000,
-                                      100003, 262144])
+@pytest.mark.parametrize("M", [1, 3, 17, 777])
+@pytest.mark.parametrize("N", EDGE + [64, 120, 256, 264, 1000, 1024, 4096, 4104, 8192, 8200, 16384, 20000, 65536, 65544,
+                                      65545, 100000, 100003, 262144])
 def test_layernorm_edge_shapes(hip, M, N):
     """One wave per row up to N = 4096; 2-16 waves per row up to 65536 (rows per workgroup
     16 / waves, so M = 17 leaves waves past the last row); beyond, a 1024-thread workgroup per
