@@ -54,11 +54,16 @@ __device__ __forceinline__ uint32_t bf16x2_apply(uint32_t xw, float b0, float b1
   return pack_bf16x2_rne(y0, y1);
 }
 
-// a: 1/alpha when kFolded, else alpha.
+// a: 1/alpha when kFolded, else alpha.  lanes: threads per row of the workgroup (256, or for rows
+// of fewer than 256 vectors n8 rounded up to a power of two, so that 256 / lanes rows share the
+// workgroup instead of leaving most threads idle: N = 64 ran at 17% of HBM peak); thread t takes
+// column t % lanes of rows (t / lanes) + r * (256 / lanes), r < kRows, of its row block.
 template <int kRows, bool kFolded>
 __global__ __launch_bounds__(256) void bias_gelu_axpy_bf16_vec(const u32x4* __restrict__ x, const u32x4* __restrict__ bias,
-                                                               u32x4* __restrict__ y, int64_t M, int64_t n8, float a) {
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+                                                               u32x4* __restrict__ y, int64_t M, int64_t n8, float a,
+                                                               int lanes) {
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * lanes + (threadIdx.x & (lanes - 1));
+  const int64_t sub = threadIdx.x / lanes, per = 256 / lanes;  // row within a group of per rows
   if (col >= n8) return;
   const u32x4 bw = bias[col];
   float bf[8];
@@ -67,17 +72,17 @@ __global__ __launch_bounds__(256) void bias_gelu_axpy_bf16_vec(const u32x4* __re
     bf[2 * j] = __uint_as_float(bw[j] << 16);
     bf[2 * j + 1] = __uint_as_float(bw[j] & 0xffff0000u);
   }
-  for (int64_t row0 = static_cast<int64_t>(blockIdx.y) * kRows; row0 < M;
-       row0 += static_cast<int64_t>(gridDim.y) * kRows) {
+  for (int64_t row0 = static_cast<int64_t>(blockIdx.y) * kRows * per + sub; row0 < M;
+       row0 += static_cast<int64_t>(gridDim.y) * kRows * per) {
     u32x4 v[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-      const int64_t row = row0 + r;
+      const int64_t row = row0 + r * per;
       if (row < M) v[r] = __builtin_nontemporal_load(x + row * n8 + col);
     }
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-      const int64_t row = row0 + r;
+      const int64_t row = row0 + r * per;
       if (row < M) {
         u32x4 o;
 #pragma unroll
@@ -106,17 +111,20 @@ hipError_t launch_bias_gelu_axpy_bf16(const uint16_t* x, const uint16_t* bias, u
   if (N % 8 == 0 && (al & 15) == 0) {
     constexpr int kRows = 8;
     const int64_t n8 = N / 8;
-    int64_t row_blocks = (M + kRows - 1) / kRows;
+    int lanes = 1;
+    while (lanes < 256 && lanes < n8) lanes *= 2;
+    const int64_t per = 256 / lanes;
+    int64_t row_blocks = (M + kRows * per - 1) / (kRows * per);
     if (row_blocks > 65535) row_blocks = 65535;  // grid.y limit; the kernel strides over the rest
-    const dim3 grid(static_cast<unsigned>((n8 + 255) / 256), static_cast<unsigned>(row_blocks));
+    const dim3 grid(static_cast<unsigned>((n8 + lanes - 1) / lanes), static_cast<unsigned>(row_blocks));
     const u32x4* x8 = reinterpret_cast<const u32x4*>(x);
     const u32x4* b8 = reinterpret_cast<const u32x4*>(bias);
     u32x4* y8 = reinterpret_cast<u32x4*>(y);
     const float ia = 1.0f / alpha;
     if (alpha != 0.0f && __builtin_isfinite(ia) && __builtin_isfinite(alpha))
-      bias_gelu_axpy_bf16_vec<kRows, true><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, ia);
+      bias_gelu_axpy_bf16_vec<kRows, true><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, ia, lanes);
     else
-      bias_gelu_axpy_bf16_vec<kRows, false><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, alpha);
+      bias_gelu_axpy_bf16_vec<kRows, false><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, alpha, lanes);
   } else {
     const int64_t total = M * N;
     int64_t blocks = (total + 255) / 256;

@@ -641,8 +641,12 @@ def _match_gelu_axpy(c: _Ctx) -> Optional[HipLoweredKernel]:
     M, N = c.rows(x)
     if c.fn.tensors[x].rank != 2 or c.shape(bias) != (N,):
         return None
-    if N % 8 == 0:
-        launch = HipLaunch((max(1, _cdiv(N // 8, 256)), max(1, min(65535, _cdiv(M, 8))), 1), (256, 1, 1), 0)
+    if N % 8 == 0:  # lanes per row: 256, or N / 8 rounded up to a power of two, 256 / lanes rows per workgroup
+        lanes = 1
+        while lanes < 256 and lanes < N // 8:
+            lanes *= 2
+        launch = HipLaunch((max(1, _cdiv(N // 8, lanes)), max(1, min(65535, _cdiv(M, 8 * (256 // lanes)))), 1),
+                           (256, 1, 1), 0)
     else:
         launch = HipLaunch((max(1, min(65536, _cdiv(M * N, 256))), 1, 1), (256, 1, 1), 0)
     return HipLoweredKernel(c.fn.name, "ihip_bias_gelu_tanh_axpy_bf16", c.io([x, bias, oname]), launch, [oname],

@@ -466,6 +466,20 @@ def test_gelu_matches_tanh_form(hip):
     np.testing.assert_allclose(out, 0.5 * gelu + xf, rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("M,N", [(100001, 64), (4097, 8), (777, 120), (20000, 264), (3, 2048), (5, 2056)])
+def test_gelu_short_and_ragged_rows(hip, M, N):
+    """Rows of fewer than 256 16-byte vectors share a workgroup (N / 8 rounded up to a power of
+    two lanes per row, 256 / lanes rows per workgroup), with row counts that leave partial
+    groups; checked in full against the oracle."""
+    w = WORKLOADS["gelu"]
+    b = {"M": M, "N": N}
+    inp = w.gen(b, seed=M + N)
+    out = run_case(w.ir(), inp, b)
+    ref = oracle_outputs(w.ir(), inp, b)
+    check(out, ref, ["y"], TOL["gelu"], f"gelu {b}")
+    check(out, ref, ["y"], TOL["gelu_strict"], f"gelu strict {b}")
+
+
 def test_gelu_full_config(hip):
     import torch
 
