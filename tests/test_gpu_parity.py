@@ -279,10 +279,12 @@ def test_softmax_edge_shapes(hip, M, N):
     check(run_case(w.ir(), inp, b), oracle_outputs(w.ir(), inp, b), ["output_ptr"], TOL["softmax"], f"softmax {b}")
 
 
-@pytest.mark.parametrize("M,N", [(65536, 64), (100003, 32), (4099, 128), (777, 4)])
+@pytest.mark.parametrize("M,N", [(65536, 64), (100003, 32), (4099, 128), (777, 4), (65537, 31), (3001, 127), (999, 1),
+                                 (20000, 99)])
 def test_softmax_many_short_rows(hip, M, N):
-    """Rows of at most 32 16-byte vectors run several per wave (N / 4 rounded up to a power of
-    two lanes each): many rows, row counts that leave a partial wave, against the oracle."""
+    """Rows of at most 128 floats run several per wave (N / 4 rounded up to a power of two lanes
+    each for N % 4 == 0, up to 4 elements per lane otherwise): many rows, row counts that leave
+    a partial wave, against the oracle."""
     w = WORKLOADS["softmax"]
     b = {"M": M, "N": N}
     inp = w.gen(b, seed=M + N)
@@ -327,8 +329,8 @@ def _check_ln(out, ref, what):
 
 
 @pytest.mark.parametrize("M", [1, 3, 17, 777])
-@pytest.mark.parametrize("N", EDGE + [64, 120, 256, 264, 1000, 1024, 4096, 4104, 8192, 8200, 16384, 20000, 65536, 65544,
-                                      65545, 100000, 100003, 262144])
+@pytest.mark.parametrize("N", EDGE + [64, 100, 120, 129, 255, 256, 257, 264, 1000, 1024, 4096, 4104, 8192, 8200, 16384,
+                                      20000, 65536, 65544, 65545, 100000, 100003, 262144])
 def test_layernorm_edge_shapes(hip, M, N):
     """One wave per row up to N = 4096; 2-16 waves per row up to 65536 (rows per workgroup
     16 / waves, so M = 17 leaves waves past the last row); beyond, a 1024-thread workgroup per

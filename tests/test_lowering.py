@@ -358,11 +358,14 @@ def test_library_rejects_bad_arguments_without_a_device():
 
 
 @pytest.mark.parametrize("M,N,grid,block,lds", [
-    (8192, 4099, 1024, 256, 16384), (3, 1029, 8, 256, 16384), (64, 7, 16, 256, 16384),
+    (8192, 4099, 1024, 256, 16384), (3, 1029, 8, 256, 16384), (64, 7, 1, 256, 0), (1000, 100, 63, 256, 0),
+    (1000, 256, 125, 256, 0), (1000, 257, 256, 256, 16384),
     (8192, 4104, 1024, 1024, 128), (8192, 8191, 8192, 128, 16), (5, 65537, 5, 1024, 128), (5, 65545, 5, 256, 16)])
 def test_layernorm_launch_descriptor(M, N, grid, block, lds):
-    """Rows not 16-byte aligned up to N = 4096 + 7 run as 8 row classes of workgroups with w and b
-    staged per class (grid 8 x min(128, ceil(ceil(M / 8) / 4))); longer ones one row per
-    workgroup of 1-16 waves; beyond 65536 + 7 the three-pass kernel."""
+    """Short rows (up to 256 halves) run several per wave: N / 8 lanes per row rounded up to a
+    power of two for aligned rows, one lane per 8 elements for the others.  Rows not 16-byte
+    aligned up to N = 4096 + 7 run as 8 row classes of workgroups with w and b staged per class
+    (grid 8 x min(128, ceil(ceil(M / 8) / 4))); longer ones one row per workgroup of 1-16
+    waves; beyond 65536 + 7 a 256- or 1024-thread workgroup per row."""
     k = lower_intent_to_hip_kernel(WORKLOADS["layernorm"].ir(), shape_bindings={"M": M, "N": N})
     assert (k.launch.grid[0], k.launch.block[0], k.launch.lds_bytes) == (grid, block, lds)
