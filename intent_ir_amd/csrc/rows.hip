@@ -984,6 +984,133 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_grouped_any(const float*
   }
 }
 
+// ---------------------------------------------------------------- LDS-staged short rows
+// A block of consecutive short rows is one contiguous run of n elements in memory, whatever the
+// row length.  stage_in copies it to LDS with 16-byte loads: element e goes to dst[h + e], where
+// h = (address of src & 15) / sizeof(T), so src's 16-byte boundaries fall on 16-byte boundaries
+// of dst and every whole vector moves with one load and one ds_write_b128; the at most two
+// partial vectors at the ends move element by element.  stage_out is the reverse.  src and dst
+// must be aligned to their element size.
+template <typename T, int kT>
+__device__ __forceinline__ void stage_in(const T* __restrict__ src, int n, T* dst, int h) {
+  constexpr int kE = 16 / sizeof(T);
+  const u32x4* base = reinterpret_cast<const u32x4*>(reinterpret_cast<uintptr_t>(src) & ~uintptr_t{15});
+  const int nv = (h + n + kE - 1) / kE;
+  for (int v = threadIdx.x; v < nv; v += kT) {
+    const int e0 = v * kE - h;
+    if (e0 >= 0 && e0 + kE <= n) {
+      reinterpret_cast<u32x4*>(dst)[v] = __builtin_nontemporal_load(base + v);
+    } else {  // every load issued before the first is used: clamped indices, no branches
+      T t[kE];
+#pragma unroll
+      for (int k = 0; k < kE; ++k) t[k] = src[min(max(e0 + k, 0), n - 1)];
+#pragma unroll
+      for (int k = 0; k < kE; ++k)
+        if (e0 + k >= 0 && e0 + k < n) dst[v * kE + k] = t[k];
+    }
+  }
+}
+
+template <typename T, int kT>
+__device__ __forceinline__ void stage_out(const T* src, int h, int n, T* __restrict__ dst) {
+  constexpr int kE = 16 / sizeof(T);
+  u32x4* base = reinterpret_cast<u32x4*>(reinterpret_cast<uintptr_t>(dst) & ~uintptr_t{15});
+  const int nv = (h + n + kE - 1) / kE;
+  for (int v = threadIdx.x; v < nv; v += kT) {
+    const int e0 = v * kE - h;
+    if (e0 >= 0 && e0 + kE <= n) {
+      __builtin_nontemporal_store(reinterpret_cast<const u32x4*>(src)[v], base + v);
+    } else {  // the slot's LDS words read together (v * kE + kE <= the buffer's size)
+      T t[kE];
+#pragma unroll
+      for (int k = 0; k < kE; ++k) t[k] = src[v * kE + k];
+#pragma unroll
+      for (int k = 0; k < kE; ++k)
+        if (e0 + k >= 0 && e0 + k < n) dst[e0 + k] = t[k];
+    }
+  }
+}
+
+// Rows per workgroup of the LDS-staged short-row kernels: kShortRpt (softmax) or kLnShortRpt
+// (LayerNorm) rows per group of G lanes.
+constexpr int kShortRpt = 2;
+constexpr int kLnShortRpt = 4;
+
+// Short rows of any length (N <= 128) with x and y 4-byte aligned: the rows of a workgroup
+// (kShortRpt * 256 / G of them, at most 8 KiB) are staged through LDS with 16-byte accesses
+// (softmax_rows_f32_grouped_any's per-element 4-byte accesses of rows that straddle vectors
+// ran at 55-66% of HBM peak), then each group of G lanes takes a row with
+// softmax_rows_f32_grouped_any's element mapping and arithmetic, so the results are identical.
+// y goes back into the same LDS slots when x and y share their offset modulo 16 bytes (each
+// lane rewrites only the slots it read), after a barrier otherwise.
+template <int G>
+__global__ __launch_bounds__(256) void softmax_rows_f32_short_lds(const float* __restrict__ x, float* __restrict__ y,
+                                                                  int64_t M, int N) {
+  constexpr int kRows = kShortRpt * (256 / G);
+  __shared__ __align__(16) float buf[kRows * 4 * G + 4];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
+  const int rows = static_cast<int>(M - r0 < kRows ? M - r0 : kRows);
+  const int n = rows * N;
+  const float* xb = x + r0 * N;
+  float* yb = y + r0 * N;
+  const int hx = static_cast<int>((reinterpret_cast<uintptr_t>(xb) & 15) >> 2);
+  const int hy = static_cast<int>((reinterpret_cast<uintptr_t>(yb) & 15) >> 2);
+  stage_in<float, 256>(xb, n, buf, hx);
+  __syncthreads();
+  const int lig = threadIdx.x & (G - 1);
+  const float ninf = -__builtin_inff();
+  float v[kShortRpt][4];
+  float inv[kShortRpt];
+#pragma unroll
+  for (int rr = 0; rr < kShortRpt; ++rr) {
+    const int lr = rr * (256 / G) + static_cast<int>(threadIdx.x) / G;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      // read unconditionally (index < hx + kRows * N <= the buffer's size), so that the reads
+      // are not serialised behind one branch each
+      const float t = buf[hx + lr * N + lig + k * G];
+      v[rr][k] = lr < rows && lig + k * G < N ? t : ninf;
+    }
+    float mx = max_nan(max_nan(v[rr][0], v[rr][1]), max_nan(v[rr][2], v[rr][3]));
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) mx = max_nan(mx, __shfl_xor(mx, off, kWave));
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[rr][k] = exp_nonpos(v[rr][k] - mx);
+      if (lig + k * G < N) sum += v[rr][k];
+    }
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    inv[rr] = 1.0f / sum;
+  }
+  if (hx != hy) __syncthreads();  // uniform over the workgroup
+#pragma unroll
+  for (int rr = 0; rr < kShortRpt; ++rr) {
+    const int lr = rr * (256 / G) + static_cast<int>(threadIdx.x) / G;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (lr < rows && lig + k * G < N) buf[hy + lr * N + lig + k * G] = v[rr][k] * inv[rr];
+  }
+  __syncthreads();
+  stage_out<float, 256>(buf, hy, n, yb);
+}
+
+static void launch_softmax_short_lds(const float* x, float* y, int64_t M, int N, hipStream_t s) {
+  int g = 1;
+  while (4 * g < N) g *= 2;
+  const int rows = kShortRpt * (256 / g);
+  const dim3 grid(static_cast<unsigned>((M + rows - 1) / rows)), block(256);
+  switch (g) {
+    case 1: softmax_rows_f32_short_lds<1><<<grid, block, 0, s>>>(x, y, M, N); break;
+    case 2: softmax_rows_f32_short_lds<2><<<grid, block, 0, s>>>(x, y, M, N); break;
+    case 4: softmax_rows_f32_short_lds<4><<<grid, block, 0, s>>>(x, y, M, N); break;
+    case 8: softmax_rows_f32_short_lds<8><<<grid, block, 0, s>>>(x, y, M, N); break;
+    case 16: softmax_rows_f32_short_lds<16><<<grid, block, 0, s>>>(x, y, M, N); break;
+    default: softmax_rows_f32_short_lds<32><<<grid, block, 0, s>>>(x, y, M, N); break;
+  }
+}
+
 static void launch_softmax_grouped_any(const float* x, float* y, int64_t M, int64_t N, hipStream_t s) {
   int g = 1;
   while (4 * g < N) g *= 2;
@@ -1086,6 +1213,9 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
     softmax_rows_f32_multi<16, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x4, y4, M, n4i);
   else if (vec && n4 <= 16384)
     softmax_rows_f32_multi<16, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x4, y4, M, n4i);
+  else if (!vec && N <= 128 && rows_per_wg == 0 &&
+           ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 3) == 0)
+    launch_softmax_short_lds(x, y, M, static_cast<int>(N), s);  // short rows at any length: staged in LDS
   else if (!vec && N <= 128 && rows_per_wg == 0)  // short rows at any alignment: several per wave
     launch_softmax_grouped_any(x, y, M, N, s);
   else if (!vec && N <= 64 * 16)
@@ -1749,6 +1879,132 @@ __global__ __launch_bounds__(256) void layernorm_rows_f16_grouped_any(
   }
 }
 
+// Short rows of any length (N <= 256 halves) with x and y 2-byte aligned: the rows of a workgroup
+// (kShortRpt * 256 / G of them, at most 8 KiB) are staged through LDS with 16-byte accesses, w and
+// b once per workgroup (three 2-byte loads per element held layernorm_rows_f16_grouped_any to
+// 18-25% of HBM peak), then each group of G lanes takes a row with that kernel's element mapping
+// and arithmetic, so the results are identical.  y goes back into the same LDS slots as in the
+// staged softmax.
+template <int G, int K>
+__global__ __launch_bounds__(256) void layernorm_rows_f16_short_lds(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b,
+    uint16_t* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t M, int N, float eps) {
+  constexpr int kRows = kLnShortRpt * (256 / G);
+  __shared__ __align__(16) uint16_t buf[kRows * K * G + 8];
+  __shared__ float wl[8 * G], bl[8 * G];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
+  const int rows = static_cast<int>(M - r0 < kRows ? M - r0 : kRows);
+  const int n = rows * N;
+  const uint16_t* xb = x + r0 * N;
+  uint16_t* yb = y + r0 * N;
+  const int hx = static_cast<int>((reinterpret_cast<uintptr_t>(xb) & 15) >> 1);
+  const int hy = static_cast<int>((reinterpret_cast<uintptr_t>(yb) & 15) >> 1);
+  if (static_cast<int>(threadIdx.x) < N) {  // N <= 256 = blockDim.x
+    wl[threadIdx.x] = f16_to_f32(w[threadIdx.x]);
+    bl[threadIdx.x] = f16_to_f32(b[threadIdx.x]);
+  }
+  stage_in<uint16_t, 256>(xb, n, buf, hx);
+  __syncthreads();
+  const int lig = threadIdx.x & (G - 1);
+  float v[kLnShortRpt][K];
+  float mean[kLnShortRpt], rstd[kLnShortRpt];
+  // Each row's divisions and square root (about 30 VALU instructions) are the same on all G lanes
+  // of its group: with G >= kLnShortRpt, lane rr of a group computes them for its row rr and
+  // broadcasts the result, one set of instructions for all the thread's rows.
+  constexpr bool kOneLane = G >= kLnShortRpt;
+  const int lead = (static_cast<int>(threadIdx.x) & (kWave - 1)) & ~(G - 1);
+  float sum[kLnShortRpt];
+#pragma unroll
+  for (int rr = 0; rr < kLnShortRpt; ++rr) {
+    const int lr = rr * (256 / G) + static_cast<int>(threadIdx.x) / G;
+    sum[rr] = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float t = f16_to_f32(buf[hx + lr * N + lig + k * G]);  // in the buffer: read unconditionally
+      v[rr][k] = lr < rows && lig + k * G < N ? t : 0.f;
+      sum[rr] += v[rr][k];
+    }
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) sum[rr] += __shfl_xor(sum[rr], off, kWave);
+  }
+  if constexpr (kOneLane) {
+    float sel = sum[0];
+#pragma unroll
+    for (int rr = 1; rr < kLnShortRpt; ++rr) sel = lig == rr ? sum[rr] : sel;
+    const float m = sel / static_cast<float>(N);
+#pragma unroll
+    for (int rr = 0; rr < kLnShortRpt; ++rr) mean[rr] = __shfl(m, lead + rr, kWave);
+  } else {
+#pragma unroll
+    for (int rr = 0; rr < kLnShortRpt; ++rr) mean[rr] = sum[rr] / static_cast<float>(N);
+  }
+  float q[kLnShortRpt];
+#pragma unroll
+  for (int rr = 0; rr < kLnShortRpt; ++rr) {
+    q[rr] = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float d = v[rr][k] - mean[rr];
+      if (lig + k * G < N) q[rr] = __builtin_fmaf(d, d, q[rr]);
+    }
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) q[rr] += __shfl_xor(q[rr], off, kWave);
+  }
+  if constexpr (kOneLane) {
+    float sel = q[0];
+#pragma unroll
+    for (int rr = 1; rr < kLnShortRpt; ++rr) sel = lig == rr ? q[rr] : sel;
+    const float r = 1.0f / sqrtf(sel / static_cast<float>(N) + eps);
+#pragma unroll
+    for (int rr = 0; rr < kLnShortRpt; ++rr) rstd[rr] = __shfl(r, lead + rr, kWave);
+  } else {
+#pragma unroll
+    for (int rr = 0; rr < kLnShortRpt; ++rr) rstd[rr] = 1.0f / sqrtf(q[rr] / static_cast<float>(N) + eps);
+  }
+  if (hx != hy) __syncthreads();  // uniform over the workgroup
+#pragma unroll
+  for (int rr = 0; rr < kLnShortRpt; ++rr) {
+    const int lr = rr * (256 / G) + static_cast<int>(threadIdx.x) / G;
+    if (lr < rows) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int c = lig + k * G;
+        if (c < N)
+          buf[hy + lr * N + c] = f32_to_f16_rne(__builtin_fmaf((v[rr][k] - mean[rr]) * rstd[rr], wl[c], bl[c]));
+      }
+      if (lig == 0) {  // null statistics pointers: not wanted, not written
+        if (mean_out != nullptr) mean_out[r0 + lr] = mean[rr];
+        if (rstd_out != nullptr) rstd_out[r0 + lr] = rstd[rr];
+      }
+    }
+  }
+  __syncthreads();
+  stage_out<uint16_t, 256>(buf, hy, n, yb);
+}
+
+static void launch_layernorm_short_lds(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y,
+                                       float* mean, float* rstd, int64_t M, int N, float eps, hipStream_t s) {
+  int g = 1;
+  while (8 * g < N) g *= 2;
+  const int rows = kLnShortRpt * (256 / g);
+  const dim3 grid(static_cast<unsigned>((M + rows - 1) / rows)), block(256);
+  // up to 5 or 8 elements per lane: rows of 4G + 1 .. 5G elements leave fewer idle slots with 5
+#define IHIP_LN_SHORT(G)                                                                         \
+  if (N <= 5 * (G))                                                                              \
+    layernorm_rows_f16_short_lds<G, 5><<<grid, block, 0, s>>>(x, w, b, y, mean, rstd, M, N, eps); \
+  else                                                                                           \
+    layernorm_rows_f16_short_lds<G, 8><<<grid, block, 0, s>>>(x, w, b, y, mean, rstd, M, N, eps)
+  switch (g) {
+    case 1: IHIP_LN_SHORT(1); break;
+    case 2: IHIP_LN_SHORT(2); break;
+    case 4: IHIP_LN_SHORT(4); break;
+    case 8: IHIP_LN_SHORT(8); break;
+    case 16: IHIP_LN_SHORT(16); break;
+    default: IHIP_LN_SHORT(32); break;
+  }
+#undef IHIP_LN_SHORT
+}
+
 static void launch_layernorm_grouped_any(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y,
                                          float* mean, float* rstd, int64_t M, int64_t N, float eps, hipStream_t s) {
   int g = 1;
@@ -1826,8 +2082,11 @@ hipError_t launch_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const
   // so any N qualifies); w and b are read per element
   const bool skew = !vec && N > 0 && N <= 65536 + 7 && (al & 1) == 0 &&
                     ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(y)) & 15) == 0;
-  if (!vec && N > 0 && N <= 256) {  // short rows at any alignment: several per wave
-    launch_layernorm_grouped_any(x, w, b, y, mean, rstd, M, N, eps, s);
+  if (!vec && N > 0 && N <= 256) {  // short rows: several per wave
+    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 1) == 0)
+      launch_layernorm_short_lds(x, w, b, y, mean, rstd, M, static_cast<int>(N), eps, s);  // staged in LDS
+    else
+      launch_layernorm_grouped_any(x, w, b, y, mean, rstd, M, N, eps, s);
     return hipGetLastError();
   }
   if (skew) {

@@ -467,11 +467,12 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
         while g < N // 4:
             g *= 2
         launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
-    elif 0 < N <= 128 and not rows:  # short rows, N % 4 != 0: g lanes per row, up to 4 elements each
+    elif 0 < N <= 128 and not rows:  # short rows, N % 4 != 0: g lanes per row, up to 4 elements
+        # each, 2 rows per group; the workgroup's rows staged in LDS (8 KiB + 16 B)
         g = 1
         while 4 * g < N:
             g *= 2
-        launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
+        launch = HipLaunch((max(1, _cdiv(M * g, 512)), 1, 1), (256, 1, 1), 4 * (2048 + 4))
     elif N % 4 == 0 and N <= 4096:  # 4 rows per workgroup unless a knob says otherwise: a wave per
         # row, or for N <= 1024 and 4 rows two waves of two rows each
         launch = _row_launch(M, rows or 4)
@@ -612,11 +613,13 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     elif N % 8 == 0 and N <= 65536:  # kW waves per row, one row per workgroup
         kw = 2 if N <= 16384 else 4 if N <= 32768 else 8
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
-    elif 0 < N <= 256:  # short rows, N % 8 != 0: g lanes per row, up to 8 elements each
+    elif 0 < N <= 256:  # short rows, N % 8 != 0: g lanes per row, up to 5 (N <= 5g) or 8 elements
+        # each, 4 rows per group; the workgroup's rows staged in LDS and w, b as f32 (8g each)
         g = 1
         while 8 * g < N:
             g *= 2
-        launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
+        slots = 5 if N <= 5 * g else 8
+        launch = HipLaunch((max(1, _cdiv(M * g, 1024)), 1, 1), (256, 1, 1), 2 * (1024 * slots + 8) + 2 * 4 * 8 * g)
     elif 0 < N <= 4096 + 7:  # N % 8 != 0: 8 row classes x J workgroups of 4 waves, w and b per class in LDS
         J = min(128, _cdiv(_cdiv(M, 8), 4))
         launch = HipLaunch((8 * max(1, J), 1, 1), (256, 1, 1), 2 * 512 * 16)

@@ -352,7 +352,7 @@ def test_layernorm_rows_not_16_byte_aligned(hip, M, N):
     _check_ln(run_case(w.ir(), inp, b), oracle_outputs(w.ir(), inp, b), f"LN {b}")
 
 
-@pytest.mark.parametrize("N", [1000, 4099, 8200, 70000])
+@pytest.mark.parametrize("N", [33, 200, 1000, 4099, 8200, 70000])
 @pytest.mark.parametrize("ox,oy,ow", [(1, 1, 0), (3, 3, 0), (7, 7, 0), (1, 2, 0), (0, 5, 0), (3, 3, 1), (0, 0, 3)])
 def test_layernorm_at_every_alignment(hip, N, ox, oy, ow):
     """Through the C-ABI with x and y offset by ox, oy halves from a 16-byte boundary: equal
@@ -503,7 +503,7 @@ def test_gelu_full_config(hip):
     np.testing.assert_allclose(out, yref, rtol=1e-2, atol=1e-3)
 
 
-@pytest.mark.parametrize("N", [1029, 4099, 8195, 50257, 65533])
+@pytest.mark.parametrize("N", [31, 127, 1029, 4099, 8195, 50257, 65533])
 @pytest.mark.parametrize("ox,oy", [(0, 0), (1, 1), (2, 2), (3, 3), (1, 2), (0, 3)])
 def test_softmax_odd_rows_at_every_alignment(hip, N, ox, oy):
     """N % 4 != 0 through the C-ABI with x and y placed ox, oy floats past 256-byte aligned
@@ -531,6 +531,58 @@ def test_softmax_odd_rows_at_every_alignment(hip, N, ox, oy):
     assert (yh[:oy] == 7.0).all() and (yh[oy + M * N:] == 7.0).all(), "write outside y"
     ref = oracle_outputs(w.ir(), inp, b)
     check({out: yh[oy:oy + M * N].reshape(M, N)}, ref, [out], TOL["softmax"], f"softmax N={N} {ox},{oy}")
+
+
+@pytest.mark.parametrize("kind,N", [("softmax", 31), ("softmax", 97), ("layernorm", 33), ("layernorm", 200)])
+@pytest.mark.parametrize("ox,oy", [(0, 0), (1, 2), (3, 3), (2, 7)])
+def test_short_rows_staged_in_lds_at_offsets(hip, kind, N, ox, oy):
+    """Short rows of other lengths are staged through LDS a workgroup's rows at a time (16-byte
+    accesses from each block's own offset modulo 16 bytes; y rewritten in place when x and y share
+    it, after a barrier otherwise): 3001 rows (many workgroups, a partial last one) with x and y
+    placed ox, oy elements past aligned allocations, against the oracle, with nothing written
+    outside y."""
+    import ctypes
+
+    import torch
+
+    w = WORKLOADS[kind]
+    M = 3001
+    b = {"M": M, "N": N}
+    inp = w.gen(b, seed=N + 10 * ox + oy)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    print(f"[case] staged short rows {kind} N={N} ox={ox} oy={oy}", flush=True)
+    if kind == "softmax":
+        ox, oy = ox % 4, oy % 4  # floats: offsets within one 16-byte vector
+        xt = torch.empty(M * N + ox, dtype=torch.float32, device="cuda")
+        xt[ox:] = torch.from_numpy(inp["input_ptr"].reshape(-1)).cuda()
+        yt = torch.full((M * N + oy + 4,), 7.0, dtype=torch.float32, device="cuda")
+        st = hip.ihip_softmax_rows_f32(ctypes.c_void_p(xt.data_ptr() + 4 * ox), ctypes.c_void_p(yt.data_ptr() + 4 * oy),
+                                       M, N, s)
+        assert st == 0, hip.ihip_last_error().decode()
+        torch.cuda.synchronize()
+        yh = yt.cpu().numpy()
+        assert (yh[:oy] == 7.0).all() and (yh[oy + M * N:] == 7.0).all(), "write outside y"
+        out = w.ir()["outputs"][0]
+        check({out: yh[oy:oy + M * N].reshape(M, N)}, oracle_outputs(w.ir(), inp, b), [out], TOL["softmax"],
+              f"softmax N={N} {ox},{oy}")
+        return
+    xs = torch.zeros(M * N + 16, dtype=torch.float16, device="cuda")
+    ys = torch.zeros(M * N + 16, dtype=torch.float16, device="cuda")
+    xs[ox:ox + M * N] = torch.from_numpy(inp["in_ptr"].reshape(-1)).cuda()
+    wt = torch.from_numpy(inp["weight_ptr"]).cuda()
+    bt = torch.from_numpy(inp["bias_ptr"]).cuda()
+    mean = torch.empty(M, device="cuda")
+    rstd = torch.empty(M, device="cuda")
+    st = hip.ihip_layernorm_rows_f16(ctypes.c_void_p(xs.data_ptr() + 2 * ox), ctypes.c_void_p(wt.data_ptr()),
+                                     ctypes.c_void_p(bt.data_ptr()), ctypes.c_void_p(ys.data_ptr() + 2 * oy),
+                                     ctypes.c_void_p(mean.data_ptr()), ctypes.c_void_p(rstd.data_ptr()), M, N,
+                                     ctypes.c_float(1e-5), s)
+    assert st == 0, hip.ihip_last_error()
+    torch.cuda.synchronize()
+    out = {"out_ptr": ys[oy:oy + M * N].cpu().numpy().reshape(M, N).astype(np.float32),
+           "out_mean_ptr": mean.cpu().numpy(), "out_rstd_ptr": rstd.cpu().numpy()}
+    _check_ln(out, oracle_outputs(w.ir(), inp, b), f"LN N={N} offsets {ox},{oy}")
+    assert (ys[:oy] == 0).all() and (ys[oy + M * N:] == 0).all(), "writes outside y"
 
 
 # ------------------------------------------------------------------ GEMM
