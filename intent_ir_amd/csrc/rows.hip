@@ -357,8 +357,8 @@ int reduce_rows_segments(int64_t M, int64_t N) {
   return static_cast<int>(S);
 }
 
-// Short rows (at most 128 16-byte vectors): G lanes per row (G = 1 .. 32, about two vectors per
-// lane, four at 65-128 vectors), 64 / G rows per wave, the row's head and tail elements on the
+// Short rows (at most 128 16-byte vectors): G lanes per row (G = 1 .. 32; one vector per lane up
+// to 8 vectors, then about two, four at 65-128 vectors), 64 / G rows per wave, the row's head and tail elements on the
 // group's first lanes, and
 // the group's values combined with xor shuffles (a wave per row left most lanes idle: N = 32
 // ran at 5% of HBM peak, 128 at 19%).  kKind 0: sum, 1: NaN-propagating max.
@@ -391,8 +391,10 @@ __global__ __launch_bounds__(256) void reduce_rows_f32_grouped(const float* __re
 template <int kKind>
 static void launch_reduce_grouped(const float* x, float* out, int64_t M, int64_t N, hipStream_t s) {
   const int64_t nvec = N / 4;
+  // one vector per lane for rows of at most 8 (N = 16: 45% -> 59% of HBM peak, 32: 45% -> 61%),
+  // two for longer ones (one per lane measured 12-18% slower at 16-32 vectors)
   int g = 1;
-  while (g < 32 && 2 * g < nvec) g *= 2;
+  while (g < 32 && (nvec <= 8 ? g < nvec : 2 * g < nvec)) g *= 2;
   const dim3 grid(static_cast<unsigned>((M * g + 255) / 256)), block(256);
   switch (g) {
     case 1: reduce_rows_f32_grouped<kKind, 1><<<grid, block, 0, s>>>(x, out, M, N); break;
