@@ -600,11 +600,11 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     args = (("tensor", x), ("tensor", w), ("tensor", b), ("tensor", y), stat("mean"), stat("rstd"), ("i64", M),
             ("i64", N), ("f32", float(env["eps"][1])))
     names = [x, w, b, y] + [inv[r] for r in ("mean", "rstd") if r in inv]
-    if N % 8 == 0 and 0 < N <= 256:  # short rows: g lanes per row (one 16-byte vector each)
+    if N % 8 == 0 and 0 < N <= 256:  # short rows: g lanes per row (one 16-byte vector each), 2 rows per group
         g = 1
         while g < N // 8:
             g *= 2
-        launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
+        launch = HipLaunch((max(1, _cdiv(M * g, 512)), 1, 1), (256, 1, 1), 0)
     elif N % 8 == 0 and 0 < N <= 4096:  # 16 rows per 1024-thread workgroup; w and b staged in LDS
         kvpl = next(v for v in (1, 2, 4, 8) if N // 8 <= 64 * v)
         launch = HipLaunch((max(1, _cdiv(M, 16)), 1, 1), (1024, 1, 1), 2 * kvpl * 64 * 16)

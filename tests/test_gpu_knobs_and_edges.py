@@ -34,7 +34,7 @@ def _oracle(ir, inputs, b):
     return execute_intent(ir, {n: to_compute_f32(v, fn.tensors[n].dtype) for n, v in inputs.items()}, b)
 
 
-@pytest.mark.parametrize("N", [8, 64, 100, 128, 1000, 1029, 4096, 4099, 8192, 50257, 128256, 100003])
+@pytest.mark.parametrize("N", [8, 31, 64, 100, 127, 128, 1000, 1029, 4096, 4099, 8192, 50257, 128256, 100003])
 def test_softmax_rows_with_minus_inf(hip, N):
     w = WORKLOADS["softmax"]
     M = 6

@@ -359,11 +359,11 @@ def test_library_rejects_bad_arguments_without_a_device():
 
 @pytest.mark.parametrize("M,N,grid,block,lds", [
     (8192, 4099, 1024, 256, 16384), (3, 1029, 8, 256, 16384), (64, 7, 1, 256, 16464), (1000, 100, 16, 256, 17424), (1000, 33, 8, 256, 10768),
-    (1000, 256, 125, 256, 0), (1000, 257, 256, 256, 16384),
+    (1000, 256, 63, 256, 0), (1000, 64, 16, 256, 0), (1000, 257, 256, 256, 16384),
     (8192, 4104, 1024, 1024, 128), (8192, 8191, 8192, 128, 16), (5, 65537, 5, 1024, 128), (5, 65545, 5, 256, 16)])
 def test_layernorm_launch_descriptor(M, N, grid, block, lds):
     """Short rows (up to 256 halves) run several per wave: N / 8 lanes per row rounded up to a
-    power of two for aligned rows; for the others one lane per 8 elements (5 when N <= 5 lanes' worth),
+    power of two and two rows per group for aligned rows; for the others one lane per 8 elements (5 when N <= 5 lanes' worth),
     four rows per group and the workgroup's rows staged in LDS (with w and b as f32).  Rows not 16-byte
     aligned up to N = 4096 + 7 run as 8 row classes of workgroups with w and b staged per class
     (grid 8 x min(128, ceil(ceil(M / 8) / 4))); longer ones one row per workgroup of 1-16
