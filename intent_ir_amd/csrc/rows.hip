@@ -105,8 +105,8 @@ __global__ __launch_bounds__(64) void reduce_any_rows_u8_vec(const uint8_t* __re
   if (lane == 0) out[row] = acc != 0u;
 }
 
-// Short rows (at most 64 16-byte vectors): G lanes per row (G = 4 .. 32, a power of two), 64 / G
-// rows per wave, about two vectors per lane, the row's head and tail elements (before its first
+// Short rows (at most 64 16-byte vectors): G lanes per row (G = 2 .. 32 for f32, 4 .. 32 for u8), 64 / G
+// rows per wave, at most two vectors per lane loaded together, the row's head and tail elements (before its first
 // 16-byte boundary and after its last) on the group's first lanes, and an OR over the group.
 // kEsz: element bytes (4: f32 compared with c, or by its bits when kZero; 1: u8, any non-zero).
 template <int G, int kEsz, bool kZero>
@@ -133,8 +133,19 @@ __global__ __launch_bounds__(256) void reduce_any_rows_grouped(const void* __res
     for (int64_t t = lig; t < head; t += G) acc |= test(rowp + t * kEsz);
     for (int64_t t = lig; t < tail; t += G) acc |= test(rowp + (head + nb * kPerVec + t) * kEsz);
     const u32x4* body = reinterpret_cast<const u32x4*>(rowp + head * kEsz);
-    for (int64_t v = lig; v < nb; v += G) {
-      const u32x4 w = __builtin_nontemporal_load(body + v);
+    // at most 2 vectors per lane (G >= nb / 2), both loads issued before either is used
+    u32x4 q[2] = {u32x4(0u), u32x4(0u)};
+    if (nb > 0) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int64_t v = lig + i * G;
+        q[i] = __builtin_nontemporal_load(body + (v < nb ? v : nb - 1));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (lig + i * G >= nb) continue;
+      const u32x4 w = q[i];
       if constexpr (kEsz == 1) {
         acc |= w.x | w.y | w.z | w.w;
       } else if constexpr (kZero) {
@@ -151,11 +162,11 @@ __global__ __launch_bounds__(256) void reduce_any_rows_grouped(const void* __res
 }
 
 // Lanes per row for a row of `bytes` bytes in the grouped form: about two 16-byte vectors per
-// lane, 4 .. 32; 0 when the row is long enough for a wave of its own (more than 64 vectors).
-static int any_group_lanes(int64_t bytes) {
+// lane, min_g .. 32; 0 when the row is long enough for a wave of its own (more than 64 vectors).
+static int any_group_lanes(int64_t bytes, int min_g) {
   const int64_t nvec = bytes / 16;
   if (nvec > 64) return 0;
-  int g = 4;
+  int g = min_g;
   while (g < 32 && 2 * g < nvec) g *= 2;
   return g;
 }
@@ -164,6 +175,7 @@ template <int kEsz, bool kZero>
 static void launch_any_grouped(const void* x, uint8_t* out, int64_t M, int64_t N, float c, int g, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((M * g + 255) / 256)), block(256);
   switch (g) {
+    case 2: reduce_any_rows_grouped<2, kEsz, kZero><<<grid, block, 0, s>>>(x, out, M, N, c); break;
     case 4: reduce_any_rows_grouped<4, kEsz, kZero><<<grid, block, 0, s>>>(x, out, M, N, c); break;
     case 8: reduce_any_rows_grouped<8, kEsz, kZero><<<grid, block, 0, s>>>(x, out, M, N, c); break;
     case 16: reduce_any_rows_grouped<16, kEsz, kZero><<<grid, block, 0, s>>>(x, out, M, N, c); break;
@@ -181,7 +193,7 @@ hipError_t launch_reduce_any_rows_f32(const float* x, uint8_t* out, int64_t M, i
   const dim3 grid(static_cast<unsigned>(M)), block(kStreamBlock);
   // 16-byte loads over each row's aligned body whenever x is 4-byte aligned (any N)
   const bool vec = (reinterpret_cast<uintptr_t>(x) & 3) == 0;
-  const int g = vec ? any_group_lanes(4 * N) : 0;
+  const int g = vec ? any_group_lanes(4 * N, 2) : 0;  // f32: a head and tail of at most 3 elements
   if (g > 0) {  // short rows: several per wave
     if (c == 0.0f)
       launch_any_grouped<4, true>(x, out, M, N, c, g, s);
@@ -207,7 +219,7 @@ hipError_t launch_reduce_any_rows_u8(const uint8_t* x, uint8_t* out, int64_t M, 
   if (M == 0) return hipSuccess;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row in the vector form
   const dim3 grid(static_cast<unsigned>(M)), block(kStreamBlock);
-  const int g = any_group_lanes(N);
+  const int g = any_group_lanes(N, 4);  // u8: a head and tail of up to 15 bytes over the group's lanes
   if (g > 0)  // short rows: several per wave
     launch_any_grouped<1, false>(x, out, M, N, 0.0f, g, s);
   else if (N / 16 >= kWave * 16)
@@ -357,12 +369,13 @@ int reduce_rows_segments(int64_t M, int64_t N) {
   return static_cast<int>(S);
 }
 
-// Short rows (at most 128 16-byte vectors): G lanes per row (G = 1 .. 32; one vector per lane up
-// to 8 vectors, then about two, four at 65-128 vectors), 64 / G rows per wave, the row's head and tail elements on the
+// Short rows (at most 128 16-byte vectors): G lanes per row (G = 1 .. 32, about two vectors per
+// lane, four at 65-128 vectors, loaded together: a loop with one load per trip ran N = 16-32 at
+// 45% of HBM peak, against 69-71% now), 64 / G rows per wave, the row's head and tail elements on the
 // group's first lanes, and
 // the group's values combined with xor shuffles (a wave per row left most lanes idle: N = 32
 // ran at 5% of HBM peak, 128 at 19%).  kKind 0: sum, 1: NaN-propagating max.
-template <int kKind, int G>
+template <int kKind, int G, int kV>
 __global__ __launch_bounds__(256) void reduce_rows_f32_grouped(const float* __restrict__ x, float* __restrict__ out,
                                                                int64_t M, int64_t N) {
   const int lig = threadIdx.x & (G - 1);
@@ -378,9 +391,16 @@ __global__ __launch_bounds__(256) void reduce_rows_f32_grouped(const float* __re
     for (int64_t t = lig; t < head; t += G) acc = op(acc, rowp[t]);
     for (int64_t t = lig; t < tail; t += G) acc = op(acc, rowp[head + 4 * nb + t]);
     const f32x4* body = reinterpret_cast<const f32x4*>(rowp + head);
-    for (int64_t v = lig; v < nb; v += G) {
-      const f32x4 q = __builtin_nontemporal_load(body + v);
-      acc = op(acc, op(op(q.x, q.y), op(q.z, q.w)));
+    if (nb > 0) {  // at most kV vectors per lane, all loads issued before the first is used
+      f32x4 q[kV];
+#pragma unroll
+      for (int i = 0; i < kV; ++i) {
+        const int64_t v = lig + i * G;
+        q[i] = __builtin_nontemporal_load(body + (v < nb ? v : nb - 1));
+      }
+#pragma unroll
+      for (int i = 0; i < kV; ++i)
+        if (lig + i * G < nb) acc = op(acc, op(op(q[i].x, q[i].y), op(q[i].z, q[i].w)));
     }
   }
 #pragma unroll
@@ -388,21 +408,33 @@ __global__ __launch_bounds__(256) void reduce_rows_f32_grouped(const float* __re
   if (row < M && lig == 0) out[row] = acc;
 }
 
+template <int kKind, int G>
+static void launch_reduce_grouped_g(const float* x, float* out, int64_t M, int64_t N, int kv, dim3 grid,
+                                    hipStream_t s) {
+  if (kv <= 1)
+    reduce_rows_f32_grouped<kKind, G, 1><<<grid, dim3(256), 0, s>>>(x, out, M, N);
+  else if (kv <= 2)
+    reduce_rows_f32_grouped<kKind, G, 2><<<grid, dim3(256), 0, s>>>(x, out, M, N);
+  else
+    reduce_rows_f32_grouped<kKind, G, 4><<<grid, dim3(256), 0, s>>>(x, out, M, N);
+}
+
 template <int kKind>
 static void launch_reduce_grouped(const float* x, float* out, int64_t M, int64_t N, hipStream_t s) {
   const int64_t nvec = N / 4;
-  // one vector per lane for rows of at most 8 (N = 16: 45% -> 59% of HBM peak, 32: 45% -> 61%),
-  // two for longer ones (one per lane measured 12-18% slower at 16-32 vectors)
+  // about two vectors per lane (four at 65-128 vectors); one per lane measured 12-18% slower at
+  // 16-32 vectors and, with the loads issued together, 14-16% slower at 4-8
   int g = 1;
-  while (g < 32 && (nvec <= 8 ? g < nvec : 2 * g < nvec)) g *= 2;
-  const dim3 grid(static_cast<unsigned>((M * g + 255) / 256)), block(256);
+  while (g < 32 && 2 * g < nvec) g *= 2;
+  const int kv = static_cast<int>((nvec + g - 1) / g);  // body vectors per lane at most (<= 4)
+  const dim3 grid(static_cast<unsigned>((M * g + 255) / 256));
   switch (g) {
-    case 1: reduce_rows_f32_grouped<kKind, 1><<<grid, block, 0, s>>>(x, out, M, N); break;
-    case 2: reduce_rows_f32_grouped<kKind, 2><<<grid, block, 0, s>>>(x, out, M, N); break;
-    case 4: reduce_rows_f32_grouped<kKind, 4><<<grid, block, 0, s>>>(x, out, M, N); break;
-    case 8: reduce_rows_f32_grouped<kKind, 8><<<grid, block, 0, s>>>(x, out, M, N); break;
-    case 16: reduce_rows_f32_grouped<kKind, 16><<<grid, block, 0, s>>>(x, out, M, N); break;
-    default: reduce_rows_f32_grouped<kKind, 32><<<grid, block, 0, s>>>(x, out, M, N); break;
+    case 1: launch_reduce_grouped_g<kKind, 1>(x, out, M, N, kv, grid, s); break;
+    case 2: launch_reduce_grouped_g<kKind, 2>(x, out, M, N, kv, grid, s); break;
+    case 4: launch_reduce_grouped_g<kKind, 4>(x, out, M, N, kv, grid, s); break;
+    case 8: launch_reduce_grouped_g<kKind, 8>(x, out, M, N, kv, grid, s); break;
+    case 16: launch_reduce_grouped_g<kKind, 16>(x, out, M, N, kv, grid, s); break;
+    default: launch_reduce_grouped_g<kKind, 32>(x, out, M, N, kv, grid, s); break;
   }
 }
 

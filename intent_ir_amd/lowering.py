@@ -689,10 +689,9 @@ def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
         launch = HipLaunch((M * segs, 1, 1), (1024, 1, 1), 64)
         return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32_ws", c.io([x, oname]), launch, [oname], dict(c.b),
                                 args + (("workspace", 4 * M * segs),))
-    if 0 < N and N // 4 <= 128:  # short rows: g lanes per row (one vector each up to 8 vectors, then
-        # two to four), several per wave
+    if 0 < N and N // 4 <= 128:  # short rows: g lanes per row (two to four vectors each), several per wave
         g = 1
-        while g < 32 and (g < N // 4 if N // 4 <= 8 else 2 * g < N // 4):
+        while g < 32 and 2 * g < N // 4:
             g *= 2
         launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
     elif N > 0:  # 16-byte body loads (a head and tail of < 4 elements around them when rows are

@@ -46,12 +46,12 @@ def test_lowering_selects_the_split_form(M, N, S):
             assert k.kernel_id == "ihip_reduce_rows_f32"
 
 
-@pytest.mark.parametrize("M,N,grid", [(1000, 4, 4), (1000, 16, 16), (1000, 32, 32), (1000, 33, 32), (1000, 64, 32),
+@pytest.mark.parametrize("M,N,grid", [(1000, 4, 4), (1000, 16, 8), (1000, 32, 16), (1000, 33, 16), (1000, 64, 32),
                                       (1000, 512, 125), (1000, 513, 125), (1000, 516, 1000)])
 def test_short_row_launch_descriptor(M, N, grid):
-    """Rows of at most 128 16-byte vectors run several per wave: one vector per lane up to 8
-    vectors, then two (four at 65-128), g lanes per row a power of two up to 32, 256 threads per
-    workgroup; longer rows a wave each."""
+    """Rows of at most 128 16-byte vectors run several per wave: about two vectors per lane (four
+    at 65-128), g lanes per row a power of two up to 32, 256 threads per workgroup; longer rows a
+    wave each."""
     for op in ("reduce_sum", "reduce_max"):
         k = lower_intent_to_hip_kernel(_ir(op), shape_bindings={"M": M, "N": N})
         assert k.launch.grid[0] == grid, (op, M, N)
