@@ -426,10 +426,16 @@ def _match_reduce_any(c: _Ctx) -> Optional[HipLoweredKernel]:
         kid = "ihip_reduce_any_rows_u8"
     else:
         raise HipLoweringError(f"reduce_any input dtype {dt} is not lowered")
-    if kid == "ihip_reduce_any_rows_f32" or N % 16 == 0:  # a wave per row (bool: 16-byte vector form)
-        launch = _row_launch(M, 1)
+    # rows of at most 64 16-byte vectors: g lanes per row (about two vectors each; at least 2 lanes
+    # for f32, 4 for bool), 256-thread workgroups; longer rows a one-wave workgroup each
+    nvec = N // 4 if kid == "ihip_reduce_any_rows_f32" else N // 16
+    if nvec <= 64:
+        g = 2 if kid == "ihip_reduce_any_rows_f32" else 4
+        while g < 32 and 2 * g < nvec:
+            g *= 2
+        launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
     else:
-        launch = _row_launch(M)
+        launch = _row_launch(M, 1)
     return HipLoweredKernel(c.fn.name, kid, c.io([x, oname]), launch, [oname], dict(c.b), args)
 
 

@@ -372,6 +372,19 @@ def test_layernorm_launch_descriptor(M, N, grid, block, lds):
     assert (k.launch.grid[0], k.launch.block[0], k.launch.lds_bytes) == (grid, block, lds)
 
 
+@pytest.mark.parametrize("dt,M,N,grid,block", [
+    ("f32", 1000, 4096, 1000, 64), ("f32", 1000, 16, 8, 256), ("f32", 1000, 256, 125, 256), ("f32", 1000, 260, 1000, 64),
+    ("bool", 1000, 64, 16, 256), ("bool", 1000, 1025, 125, 256), ("bool", 1000, 2000, 1000, 64)])
+def test_reduce_any_launch_descriptor(dt, M, N, grid, block):
+    """Rows of at most 64 16-byte vectors run several per wave (g lanes per row, about two vectors
+    each, at least 2 for f32 and 4 for bool, whose head and tail hold up to 15 bytes); longer rows a
+    one-wave workgroup each."""
+    ir = {"name": "any_rows", "tensors": {"x": {"dtype": dt, "shape": ["M", "N"]}, "out": {"dtype": "bool", "shape": ["M"]}},
+          "ops": [{"op": "reduce_any", "inputs": ["x"], "output": "out", "attrs": {"dims": [1]}}], "outputs": ["out"]}
+    k = lower_intent_to_hip_kernel(ir, shape_bindings={"M": M, "N": N})
+    assert (k.launch.grid[0], k.launch.block[0]) == (grid, block)
+
+
 @pytest.mark.parametrize("M,N,grid,block,lds", [
     (1000, 31, 16, 256, 8208), (1000, 127, 63, 256, 8208), (5, 1, 1, 256, 8208), (1000, 32, 32, 256, 0),
     (1000, 128, 125, 256, 0), (1000, 129, 1000, 64, 0)])
