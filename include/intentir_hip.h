@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define IHIP_ABI_VERSION 2
+#define IHIP_ABI_VERSION 3
 
 #define IHIP_OK 0
 #define IHIP_ERR_INVALID_ARG (-1)
@@ -74,6 +74,13 @@ int64_t ihip_reduce_rows_f32_workspace_size(int64_t M, int64_t N);
  * hold at least workspace_size bytes, 4-byte aligned, and stay untouched until the work on
  * `stream` completes.  Same semantics as ihip_reduce_rows_f32 (verify/interpreter.py:478-500). */
 int ihip_reduce_rows_f32_ws(const float* x, float* out, int64_t M, int64_t N, int kind, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/* ihip_reduce_rows_f32_ws with a result scale: out[m] = reduce(x[m, :]) * scale, one f32
+ * multiply of the row's result (scale 1.0 is ihip_reduce_rows_f32_ws exactly).  The
+ * interpreter's reduce_sum{scale} (verify/interpreter.py:478-488, :646-673), e.g. a row mean
+ * written as sum * (1/N) (pipeline/cuda/core.py:509-511). */
+int ihip_reduce_rows_f32_ex(const float* x, float* out, int64_t M, int64_t N, int kind, float scale, void* workspace,
                             int64_t workspace_bytes, void* stream);
 
 /* ihip_reduce_rows_f32_ws without a workspace argument and without any allocation: no
@@ -119,13 +126,32 @@ int64_t ihip_softmax_rows_f32_workspace_size(int64_t M, int64_t N);
 int ihip_softmax_rows_f32_ws(const float* x, float* y, int64_t M, int64_t N, void* workspace, int64_t workspace_bytes,
                              void* stream);
 
-/* LayerNorm forward over the last axis: x, y f16 [M, N]; w, b f16 [N];
+/* ihip_softmax_rows_f32_ws that also writes each row's statistics: row_max[m] = max(x[m, :])
+ * (NaN-propagating) and row_sum[m] = sum(exp(x[m, :] - row_max[m])), the values the softmax
+ * divides by, from the same launch (no second pass over x).  Either pointer may be NULL (not
+ * written).  Rows of length 0 have no maximum: N == 0 with a non-NULL statistic is
+ * IHIP_ERR_INVALID_ARG.  The reference's softmax IR with those outputs
+ * (pipeline/cuda/core.py:453-493, softmax_inner: output_ptr, row_max_ptr, row_sum_ptr). */
+int ihip_softmax_rows_f32_stats(const float* x, float* y, float* row_max, float* row_sum, int64_t M, int64_t N,
+                                void* workspace, int64_t workspace_bytes, void* stream);
+
+/* LayerNorm forward over the last axis with f16 data: x, y f16 [M, N]; w, b f16 [N];
  * mean, rstd f32 [M] (either may be NULL: that statistic is then not written);
- * f32 statistics, rstd = 1/sqrt(var + eps).  Replaces
- * _kernel_layernorm_2d_f32 (backends/cuda/codegen/intentir_to_cuda.py:1250-1338,
- * backends/cuda/runtime/kernels/layernorm.cuh:11-98), extended to f16 I/O. */
+ * f32 statistics, rstd = 1/sqrt(var + eps), y rounded to f16.  The reference has no f16
+ * LayerNorm kernel (its CUDA lowering types f32 only, intentir_to_cuda.py:159-175); this
+ * entry runs the reference LayerNorm IR (pipeline/tilelang/core.py:1322-1384) when it
+ * declares x, w, b, y as f16, with the op order of ihip_layernorm_rows_f32. */
 int ihip_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y, float* mean,
                             float* rstd, int64_t M, int64_t N, float eps, void* stream);
+
+/* LayerNorm forward in f32: x, y f32 [M, N]; w, b f32 [N]; mean, rstd f32 [M] (either may
+ * be NULL: not written).  mean = sum(x)/N, d = x - mean, var = sum(d*d)/N,
+ * rstd = 1/sqrt(var + eps), y = ((d*rstd)*w) + b, each step a separately rounded f32
+ * operation.  Any N and alignment; M < 2^31.  Replaces _kernel_layernorm_2d_f32
+ * (backends/cuda/codegen/intentir_to_cuda.py:1250-1338, dispatched at :2163-2164;
+ * backends/cuda/runtime/kernels/layernorm.cuh:11-98). */
+int ihip_layernorm_rows_f32(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
+                            int64_t M, int64_t N, float eps, void* stream);
 
 /* y = alpha * gelu_tanh(x + bias[col]) + x for x, y bf16 [M, N], bias bf16 [N],
  * f32 arithmetic, one pass.  Replaces the fused element-wise lowering
@@ -145,14 +171,29 @@ int ihip_gather2d_f32(const float* inp, const int32_t* row_idx, const int32_t* c
 
 /* C = act(A @ B + bias) with A bf16 [M, K], B bf16 [K, N], bias f32 [N] or NULL,
  * act = ReLU when relu != 0 else identity; f32 accumulation on MFMA, C bf16
- * (round to nearest even).  Replaces _kernel_matmul_f32 / wmma_matmul_f32_tf32
- * (backends/cuda/codegen/intentir_to_cuda.py:537-985,
- * backends/cuda/runtime/kernels/wmma_matmul.cuh:124-565), which lower matmul
- * only as a lone op (:2137-2140).  Any shape: rows that all start 16-byte aligned
+ * (round to nearest even).  The reference lowers f32 matmul only, as a lone op
+ * (backends/cuda/codegen/intentir_to_cuda.py:537-985, :2137-2140); this entry runs the
+ * reference matmul IR (pipeline/tilelang/core.py:886-910, with its bias + ReLU epilogue)
+ * when A, B and C are declared bf16.  The f32 IR runs on ihip_gemm_f32_bias_relu.
+ * Any shape: rows that all start 16-byte aligned
  * (N % 8 == 0, K % 8 == 0, 16-byte aligned A, B, C) run the tiled MFMA kernel at any
  * M, N, K; other shapes a slower guarded kernel with the same accumulation order. */
 int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                              int64_t N, int64_t K, int relu, void* stream);
+
+/* C = act(op(A) @ op(B) + bias) in f32: A f32 [M, K] (or [K, M] when transpose_a), B f32
+ * [K, N] (or [N, K] when transpose_b), bias f32 [N] or NULL, C f32 [M, N]; act = ReLU
+ * (numpy's maximum(x, 0): NaN and -0.0 pass through) when relu != 0.  Exact f32 products
+ * and f32 accumulation on the fp32 matrix cores (no reduced-precision inputs, so the
+ * reference's opt-in ALLOW_TF32 is never needed).  Any M, N, K and alignment.  tile = 0
+ * chooses automatically (128x128 C tiles, 64x64 when fewer than 256 tiles of 128x128 would
+ * run); 64 or 128 fixes it; C does not depend on tile.  Replaces _kernel_matmul_f32 and
+ * its device code (backends/cuda/codegen/intentir_to_cuda.py:537-985, dispatched at
+ * :2137-2140; backends/cuda/runtime/kernels/matmul_fallback.cuh:8-73,
+ * wmma_matmul.cuh:124-565), and also takes the bias + ReLU epilogue the reference's
+ * builders emit (pipeline/tilelang/core.py:886-910) in the same launch. */
+int ihip_gemm_f32_bias_relu(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
+                            int64_t K, int transpose_a, int transpose_b, int relu, int tile, void* stream);
 
 /* The same with matmul's transpose flags (verify/interpreter.py:507-520): when transpose_a,
  * A is given as [K, M] and the product uses its transpose; when transpose_b, B is given as
@@ -225,11 +266,22 @@ int ihip_gemm_bf16_bias_relu_splitk(const uint16_t* A, const uint16_t* B, const 
  * same instruction stream (uniform branches), on 4 consecutive elements per lane.
  * Values are f32 inside the program; bool is 0.0 / 1.0.
  * ------------------------------------------------------------------------- */
+/* Limits of the interpreter kernel (a fixed register file and instruction buffer). */
 #define IHIP_EW_MAX_CODE 64
 #define IHIP_EW_MAX_REGS 8
 #define IHIP_EW_MAX_INPUTS 8
 #define IHIP_EW_MAX_OUTPUTS 4
 #define IHIP_EW_MAX_RANK 4
+/* Limits of the native (hiprtc-compiled, straight-line) form, where registers are plain
+ * variables and the instruction list becomes code: a program within the interpreter limits
+ * above runs in every mode; a larger one, up to these, runs only as native code (modes AUTO
+ * and NATIVE), and in INTERP mode or when its compilation fails the call returns an error
+ * instead of falling back to the interpreter.  The reference generates one kernel per chain
+ * with no such limits (backends/cuda/codegen/intentir_to_cuda.py:229-534). */
+#define IHIP_EW_NATIVE_MAX_CODE 1024
+#define IHIP_EW_NATIVE_MAX_REGS 255
+#define IHIP_EW_NATIVE_MAX_INPUTS 32
+#define IHIP_EW_NATIVE_MAX_OUTPUTS 8
 
 /* Operand element types. */
 #define IHIP_DT_F32 0

@@ -22,12 +22,16 @@
 namespace ihip {
 hipError_t launch_reduce_any_rows_f32(const float*, uint8_t*, int64_t, int64_t, float, hipStream_t);
 hipError_t launch_reduce_any_rows_u8(const uint8_t*, uint8_t*, int64_t, int64_t, hipStream_t);
-hipError_t launch_reduce_rows_f32(const float*, float*, int64_t, int64_t, int, float*, hipStream_t);
+hipError_t launch_reduce_rows_f32(const float*, float*, int64_t, int64_t, int, float, float*, hipStream_t);
 int reduce_rows_segments(int64_t, int64_t);
-hipError_t launch_softmax_rows_f32(const float*, float*, int64_t, int64_t, int, hipStream_t, float*);
+hipError_t launch_softmax_rows_f32(const float*, float*, int64_t, int64_t, int, hipStream_t, float*, float*, float*);
 bool softmax_rows_per_wg_form(const float*, const float*, int64_t);
 hipError_t launch_layernorm_rows_f16(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, float*,
                                      int64_t, int64_t, float, hipStream_t);
+hipError_t launch_layernorm_rows_f32(const float*, const float*, const float*, float*, float*, float*, int64_t, int64_t,
+                                     float, hipStream_t);
+hipError_t launch_gemm_f32_bias_relu(const float*, const float*, const float*, float*, int64_t, int64_t, int64_t, bool,
+                                     bool, int, int, hipStream_t);
 hipError_t launch_bias_gelu_axpy_bf16(const uint16_t*, const uint16_t*, uint16_t*, int64_t, int64_t, float,
                                       hipStream_t);
 hipError_t launch_gather2d_f32(const float*, const int32_t*, const int32_t*, float*, int64_t, int64_t, int64_t, float,
@@ -138,13 +142,13 @@ bool ew_dtype_ok(int dt) { return dt >= IHIP_DT_F32 && dt <= IHIP_DT_I32; }
 // Data-flow check of an element-wise program: known opcodes, registers in range and written
 // before read, operands in range, every output stored exactly once.  0 or a failure code.
 int check_program(const ihip_ew_instr* code, int n_code, int n_inputs, int n_outputs) {
-  bool written[IHIP_EW_MAX_REGS] = {};
-  int stored[IHIP_EW_MAX_OUTPUTS] = {};
+  bool written[IHIP_EW_NATIVE_MAX_REGS] = {};
+  int stored[IHIP_EW_NATIVE_MAX_OUTPUTS] = {};
   for (int pc = 0; pc < n_code; ++pc) {
     const ihip_ew_instr& in = code[pc];
     const EwForm f = ew_form(in.op);
     IHIP_REQUIRE(f != kEwBad, "elementwise_program: instruction %d has unknown opcode %d", pc, (int)in.op);
-    const auto reg_ok = [&](int r) { return r < IHIP_EW_MAX_REGS && written[r]; };
+    const auto reg_ok = [&](int r) { return r < IHIP_EW_NATIVE_MAX_REGS && written[r]; };
     switch (f) {
       case kEwLoad:
         IHIP_REQUIRE(in.a < n_inputs, "elementwise_program: instruction %d loads input %d of %d", pc, (int)in.a,
@@ -172,14 +176,29 @@ int check_program(const ihip_ew_instr* code, int n_code, int n_inputs, int n_out
         break;
     }
     if (f != kEwStore) {
-      IHIP_REQUIRE(in.dst < IHIP_EW_MAX_REGS, "elementwise_program: instruction %d writes register %d of %d", pc,
-                   (int)in.dst, IHIP_EW_MAX_REGS);
+      IHIP_REQUIRE(in.dst < IHIP_EW_NATIVE_MAX_REGS, "elementwise_program: instruction %d writes register %d of %d",
+                   pc, (int)in.dst, IHIP_EW_NATIVE_MAX_REGS);
       written[in.dst] = true;
     }
   }
   for (int k = 0; k < n_outputs; ++k)
     IHIP_REQUIRE(stored[k] == 1, "elementwise_program: output %d is stored %d times (must be once)", k, stored[k]);
   return 0;
+}
+
+// True when a (checked) program fits the interpreter kernel: its instruction buffer, operand
+// tables and register file.  Larger programs run only as native code.
+bool fits_interpreter(const ihip_ew_instr* code, int n_code, int n_inputs, int n_outputs) {
+  if (n_code > IHIP_EW_MAX_CODE || n_inputs > IHIP_EW_MAX_INPUTS || n_outputs > IHIP_EW_MAX_OUTPUTS) return false;
+  for (int pc = 0; pc < n_code; ++pc) {
+    const ihip_ew_instr& in = code[pc];
+    const EwForm f = ew_form(in.op);
+    if (f != kEwStore && in.dst >= IHIP_EW_MAX_REGS) return false;
+    if ((f == kEwUnary || f == kEwBinary || f == kEwWhere || f == kEwStore) && in.a >= IHIP_EW_MAX_REGS) return false;
+    if ((f == kEwBinary || f == kEwWhere) && in.b >= IHIP_EW_MAX_REGS) return false;
+    if (f == kEwWhere && in.c >= IHIP_EW_MAX_REGS) return false;
+  }
+  return true;
 }
 
 }  // namespace
@@ -225,6 +244,11 @@ static int check_reduce_rows(const char* who, const float* x, float* out, int64_
 
 int ihip_reduce_rows_f32_ws(const float* x, float* out, int64_t M, int64_t N, int kind, void* workspace,
                             int64_t workspace_bytes, void* stream) {
+  return ihip_reduce_rows_f32_ex(x, out, M, N, kind, 1.0f, workspace, workspace_bytes, stream);
+}
+
+int ihip_reduce_rows_f32_ex(const float* x, float* out, int64_t M, int64_t N, int kind, float scale, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
   const int bad = check_reduce_rows("reduce_rows_f32", x, out, M, N, kind);
   if (bad) return bad;
   const int64_t need = ihip_reduce_rows_f32_workspace_size(M, N);
@@ -233,7 +257,7 @@ int ihip_reduce_rows_f32_ws(const float* x, float* out, int64_t M, int64_t N, in
                (long long)M, (long long)N, (long long)need);
   IHIP_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 3) == 0, "reduce_rows_f32: workspace not 4-byte aligned");
   float* part = need > 0 ? static_cast<float*>(workspace) : nullptr;
-  return finish(ihip::launch_reduce_rows_f32(x, out, M, N, kind, part, static_cast<hipStream_t>(stream)),
+  return finish(ihip::launch_reduce_rows_f32(x, out, M, N, kind, scale, part, static_cast<hipStream_t>(stream)),
                 "reduce_rows_f32");
 }
 
@@ -254,7 +278,7 @@ int ihip_reduce_rows_f32_noalloc(const float* x, float* out, int64_t M, int64_t 
     if (e != hipSuccess) return fail(static_cast<int>(e), "reduce_rows_f32_noalloc: scratch address: %s",
                                      hipGetErrorString(e));
   }
-  return finish(ihip::launch_reduce_rows_f32(x, out, M, N, kind, part, static_cast<hipStream_t>(stream)),
+  return finish(ihip::launch_reduce_rows_f32(x, out, M, N, kind, 1.0f, part, static_cast<hipStream_t>(stream)),
                 "reduce_rows_f32_noalloc");
 }
 
@@ -268,7 +292,8 @@ int ihip_softmax_rows_f32_ex(const float* x, float* y, int64_t M, int64_t N, int
                "softmax_rows_f32: rows_per_wg %d needs the one-wave-per-row form (N %% 4 == 0, N <= 4096, "
                "16-byte aligned x and y); N = %lld runs one row per workgroup",
                rows_per_wg, (long long)N);
-  return finish(ihip::launch_softmax_rows_f32(x, y, M, N, rows_per_wg, static_cast<hipStream_t>(stream), nullptr),
+  return finish(ihip::launch_softmax_rows_f32(x, y, M, N, rows_per_wg, static_cast<hipStream_t>(stream), nullptr,
+                                              nullptr, nullptr),
                 "softmax_rows_f32");
 }
 
@@ -280,20 +305,27 @@ int64_t ihip_softmax_rows_f32_workspace_size(int64_t M, int64_t N) {
 
 int ihip_softmax_rows_f32_ws(const float* x, float* y, int64_t M, int64_t N, void* workspace, int64_t workspace_bytes,
                              void* stream) {
+  return ihip_softmax_rows_f32_stats(x, y, nullptr, nullptr, M, N, workspace, workspace_bytes, stream);
+}
+
+int ihip_softmax_rows_f32_stats(const float* x, float* y, float* row_max, float* row_sum, int64_t M, int64_t N,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   const int64_t n = numel2(M, N);
-  IHIP_REQUIRE(n >= 0, "softmax_rows_f32_ws: invalid shape [%lld, %lld]", (long long)M, (long long)N);
-  IHIP_REQUIRE(n == 0 || (x != nullptr && y != nullptr), "softmax_rows_f32_ws: null pointer");
-  IHIP_REQUIRE(workspace_bytes >= 0, "softmax_rows_f32_ws: negative workspace size %lld", (long long)workspace_bytes);
+  IHIP_REQUIRE(M <= 0 || N > 0 || (row_max == nullptr && row_sum == nullptr),
+               "softmax_rows_f32_stats: rows of length 0 have no maximum");
+  IHIP_REQUIRE(n >= 0, "softmax_rows_f32_stats: invalid shape [%lld, %lld]", (long long)M, (long long)N);
+  IHIP_REQUIRE(n == 0 || (x != nullptr && y != nullptr), "softmax_rows_f32_stats: null pointer");
+  IHIP_REQUIRE(workspace_bytes >= 0, "softmax_rows_f32_stats: negative workspace size %lld", (long long)workspace_bytes);
   IHIP_REQUIRE(workspace != nullptr || workspace_bytes == 0,
-               "softmax_rows_f32_ws: workspace of %lld bytes at a null pointer", (long long)workspace_bytes);
+               "softmax_rows_f32_stats: workspace of %lld bytes at a null pointer", (long long)workspace_bytes);
   const int64_t need = ihip_softmax_rows_f32_workspace_size(M, N);
   IHIP_REQUIRE(workspace == nullptr || workspace_bytes >= need,
-               "softmax_rows_f32_ws: workspace of %lld bytes, [%lld, %lld] needs %lld", (long long)workspace_bytes,
+               "softmax_rows_f32_stats: workspace of %lld bytes, [%lld, %lld] needs %lld", (long long)workspace_bytes,
                (long long)M, (long long)N, (long long)need);
-  IHIP_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 7) == 0, "softmax_rows_f32_ws: workspace not 8-byte aligned");
+  IHIP_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 7) == 0, "softmax_rows_f32_stats: workspace not 8-byte aligned");
   float* part = need > 0 ? static_cast<float*>(workspace) : nullptr;
-  return finish(ihip::launch_softmax_rows_f32(x, y, M, N, 0, static_cast<hipStream_t>(stream), part),
-                "softmax_rows_f32_ws");
+  return finish(ihip::launch_softmax_rows_f32(x, y, M, N, 0, static_cast<hipStream_t>(stream), part, row_max, row_sum),
+                "softmax_rows_f32_stats");
 }
 
 int ihip_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, void* stream) {
@@ -308,6 +340,17 @@ int ihip_layernorm_rows_f16(const uint16_t* x, const uint16_t* w, const uint16_t
                "layernorm_rows_f16: null pointer");
   return finish(ihip::launch_layernorm_rows_f16(x, w, b, y, mean, rstd, M, N, eps, static_cast<hipStream_t>(stream)),
                 "layernorm_rows_f16");
+}
+
+int ihip_layernorm_rows_f32(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
+                            int64_t M, int64_t N, float eps, void* stream) {
+  const int64_t n = numel2(M, N);
+  IHIP_REQUIRE(n >= 0, "layernorm_rows_f32: invalid shape [%lld, %lld]", (long long)M, (long long)N);
+  IHIP_REQUIRE(n == 0 || (x != nullptr && y != nullptr && w != nullptr && b != nullptr),
+               "layernorm_rows_f32: null pointer");
+  IHIP_REQUIRE(M <= 0x7fffffffLL, "layernorm_rows_f32: M = %lld exceeds 2^31 - 1 rows", (long long)M);
+  return finish(ihip::launch_layernorm_rows_f32(x, w, b, y, mean, rstd, M, N, eps, static_cast<hipStream_t>(stream)),
+                "layernorm_rows_f32");
 }
 
 int ihip_bias_gelu_tanh_axpy_bf16(const uint16_t* x, const uint16_t* bias, uint16_t* y, int64_t M, int64_t N,
@@ -343,6 +386,19 @@ int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const floa
   return finish(ihip::launch_gemm_bf16_bias_relu(A, B, bias, C, M, N, K, transpose_a != 0, transpose_b != 0, relu,
                                                  tile, static_cast<hipStream_t>(stream)),
                 "gemm_bf16_bias_relu");
+}
+
+int ihip_gemm_f32_bias_relu(const float* A, const float* B, const float* bias, float* C, int64_t M, int64_t N,
+                            int64_t K, int transpose_a, int transpose_b, int relu, int tile, void* stream) {
+  IHIP_REQUIRE(numel2(M, K) >= 0 && numel2(K, N) >= 0 && numel2(M, N) >= 0,
+               "gemm_f32_bias_relu: invalid shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  IHIP_REQUIRE(M == 0 || N == 0 || C != nullptr, "gemm_f32_bias_relu: C is null");
+  IHIP_REQUIRE(M == 0 || N == 0 || K == 0 || (A != nullptr && B != nullptr), "gemm_f32_bias_relu: A or B is null");
+  IHIP_REQUIRE(tile == 0 || tile == 64 || tile == 128, "gemm_f32_bias_relu: tile %d is not 0 (automatic), 64 or 128",
+               tile);
+  return finish(ihip::launch_gemm_f32_bias_relu(A, B, bias, C, M, N, K, transpose_a != 0, transpose_b != 0, relu, tile,
+                                                static_cast<hipStream_t>(stream)),
+                "gemm_f32_bias_relu");
 }
 
 int64_t ihip_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int transpose_a, int transpose_b) {
@@ -413,12 +469,12 @@ int ihip_gemm_bf16_bias_relu(const uint16_t* A, const uint16_t* B, const float* 
 static int check_ew_launch(const char* who, const ihip_ew_instr* code, int32_t n_code, const ihip_ew_operand* inputs,
                            int32_t n_inputs, const ihip_ew_operand* outputs, int32_t n_outputs, const int64_t* shape,
                            int32_t rank, int64_t (&sh)[4], int64_t* total) {
-  IHIP_REQUIRE(code != nullptr && n_code >= 1 && n_code <= IHIP_EW_MAX_CODE,
-               "%s: need 1..%d instructions, got %d", who, IHIP_EW_MAX_CODE, (int)n_code);
-  IHIP_REQUIRE(n_inputs >= 0 && n_inputs <= IHIP_EW_MAX_INPUTS && (n_inputs == 0 || inputs != nullptr),
-               "%s: need 0..%d inputs, got %d", who, IHIP_EW_MAX_INPUTS, (int)n_inputs);
-  IHIP_REQUIRE(n_outputs >= 1 && n_outputs <= IHIP_EW_MAX_OUTPUTS && outputs != nullptr,
-               "%s: need 1..%d outputs, got %d", who, IHIP_EW_MAX_OUTPUTS, (int)n_outputs);
+  IHIP_REQUIRE(code != nullptr && n_code >= 1 && n_code <= IHIP_EW_NATIVE_MAX_CODE,
+               "%s: need 1..%d instructions, got %d", who, IHIP_EW_NATIVE_MAX_CODE, (int)n_code);
+  IHIP_REQUIRE(n_inputs >= 0 && n_inputs <= IHIP_EW_NATIVE_MAX_INPUTS && (n_inputs == 0 || inputs != nullptr),
+               "%s: need 0..%d inputs, got %d", who, IHIP_EW_NATIVE_MAX_INPUTS, (int)n_inputs);
+  IHIP_REQUIRE(n_outputs >= 1 && n_outputs <= IHIP_EW_NATIVE_MAX_OUTPUTS && outputs != nullptr,
+               "%s: need 1..%d outputs, got %d", who, IHIP_EW_NATIVE_MAX_OUTPUTS, (int)n_outputs);
   IHIP_REQUIRE(rank >= 0 && rank <= IHIP_EW_MAX_RANK && (rank == 0 || shape != nullptr),
                "%s: rank %d outside 0..%d", who, (int)rank, IHIP_EW_MAX_RANK);
   for (int d = 0; d < 4; ++d) sh[d] = 1;
@@ -449,11 +505,17 @@ int ihip_elementwise_program(const ihip_ew_instr* code, int32_t n_code, const ih
   if (total == 0) return finish(hipSuccess, "elementwise_program");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int mode = g_ew_mode.load();
+  const bool interp_ok = fits_interpreter(code, n_code, n_inputs, n_outputs);
+  IHIP_REQUIRE(interp_ok || mode != IHIP_EW_MODE_INTERP,
+               "elementwise_program: %d instructions, %d inputs, %d outputs exceed the interpreter kernel's limits "
+               "(%d, %d, %d, registers < %d): such a program runs only as native code (mode AUTO or NATIVE)",
+               (int)n_code, (int)n_inputs, (int)n_outputs, IHIP_EW_MAX_CODE, IHIP_EW_MAX_INPUTS, IHIP_EW_MAX_OUTPUTS,
+               IHIP_EW_MAX_REGS);
   if (mode != IHIP_EW_MODE_INTERP) {
     std::string why;
     const hipError_t e = ihip::launch_elementwise_jit(code, n_code, inputs, n_inputs, outputs, n_outputs, sh, s, &why);
     if (e != hipErrorNotSupported || why.empty()) return finish(e, "elementwise_program (native)");
-    if (mode == IHIP_EW_MODE_NATIVE)
+    if (mode == IHIP_EW_MODE_NATIVE || !interp_ok)
       return fail(static_cast<int>(e), "elementwise_program: native code unavailable: %s", why.c_str());
   }
   return finish(ihip::launch_elementwise_program(code, n_code, inputs, n_inputs, outputs, n_outputs, sh, s),
@@ -462,13 +524,13 @@ int ihip_elementwise_program(const ihip_ew_instr* code, int32_t n_code, const ih
 
 int ihip_elementwise_prepare(const ihip_ew_instr* code, int32_t n_code, const int32_t* input_dtypes, int32_t n_inputs,
                              const int32_t* output_dtypes, int32_t n_outputs) {
-  IHIP_REQUIRE(code != nullptr && n_code >= 1 && n_code <= IHIP_EW_MAX_CODE,
-               "elementwise_prepare: need 1..%d instructions, got %d", IHIP_EW_MAX_CODE, (int)n_code);
-  IHIP_REQUIRE(n_inputs >= 0 && n_inputs <= IHIP_EW_MAX_INPUTS && (n_inputs == 0 || input_dtypes != nullptr),
-               "elementwise_prepare: need 0..%d inputs, got %d", IHIP_EW_MAX_INPUTS, (int)n_inputs);
-  IHIP_REQUIRE(n_outputs >= 1 && n_outputs <= IHIP_EW_MAX_OUTPUTS && output_dtypes != nullptr,
-               "elementwise_prepare: need 1..%d outputs, got %d", IHIP_EW_MAX_OUTPUTS, (int)n_outputs);
-  int in_dt[IHIP_EW_MAX_INPUTS] = {}, out_dt[IHIP_EW_MAX_OUTPUTS] = {};
+  IHIP_REQUIRE(code != nullptr && n_code >= 1 && n_code <= IHIP_EW_NATIVE_MAX_CODE,
+               "elementwise_prepare: need 1..%d instructions, got %d", IHIP_EW_NATIVE_MAX_CODE, (int)n_code);
+  IHIP_REQUIRE(n_inputs >= 0 && n_inputs <= IHIP_EW_NATIVE_MAX_INPUTS && (n_inputs == 0 || input_dtypes != nullptr),
+               "elementwise_prepare: need 0..%d inputs, got %d", IHIP_EW_NATIVE_MAX_INPUTS, (int)n_inputs);
+  IHIP_REQUIRE(n_outputs >= 1 && n_outputs <= IHIP_EW_NATIVE_MAX_OUTPUTS && output_dtypes != nullptr,
+               "elementwise_prepare: need 1..%d outputs, got %d", IHIP_EW_NATIVE_MAX_OUTPUTS, (int)n_outputs);
+  int in_dt[IHIP_EW_NATIVE_MAX_INPUTS] = {}, out_dt[IHIP_EW_NATIVE_MAX_OUTPUTS] = {};
   for (int k = 0; k < n_inputs; ++k) {
     IHIP_REQUIRE(ew_dtype_ok(input_dtypes[k]), "elementwise_prepare: input %d has unknown dtype %d", k,
                  (int)input_dtypes[k]);

@@ -128,6 +128,18 @@ __device__ __forceinline__ int xcd_contiguous(int b, int G) {
   return x * q + (x < r ? x : r) + b / kNumXcd;
 }
 
+// Optional per-row outputs of a softmax: the row maximum and the sum of exp(x - max) over
+// the row (the statistics the kernels compute anyway); a null pointer is not written.
+struct SoftmaxStats {
+  float* max;
+  float* sum;
+};
+
+__device__ __forceinline__ void put_softmax_stats(const SoftmaxStats& st, int64_t row, float mx, float sum) {
+  if (st.max != nullptr) st.max[row] = mx;
+  if (st.sum != nullptr) st.sum[row] = sum;
+}
+
 // Row split of a long-row softmax (rows.hip): S segments per row of 256 * vpl 16-byte
 // vectors, two floats of workspace per segment; S = 0 when rows are not split.
 struct SoftmaxSplit {

@@ -26,6 +26,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/intentir_hip.h"
 #include "common.hpp"
@@ -33,9 +34,9 @@
 namespace ihip {
 
 struct EwJitArgs {
-  const void* in_ptr[IHIP_EW_MAX_INPUTS];
-  int64_t in_stride[IHIP_EW_MAX_INPUTS][4];
-  void* out_ptr[IHIP_EW_MAX_OUTPUTS];
+  const void* in_ptr[IHIP_EW_NATIVE_MAX_INPUTS];
+  int64_t in_stride[IHIP_EW_NATIVE_MAX_INPUTS][4];
+  void* out_ptr[IHIP_EW_NATIVE_MAX_OUTPUTS];
   int64_t shape[4];
   int64_t rows;
   int64_t nvec;  // ceil(D3 / V): lanes own V = 4 or 8 elements
@@ -53,9 +54,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef u32 u32x4 __attribute__((ext_vector_type(4)));
 typedef u32 u32x2 __attribute__((ext_vector_type(2)));
 struct EwJitArgs {
-  const void* in_ptr[8];
-  i64 in_stride[8][4];
-  void* out_ptr[4];
+  const void* in_ptr[32];
+  i64 in_stride[32][4];
+  void* out_ptr[8];
   i64 shape[4];
   i64 rows;
   i64 nvec;
@@ -283,7 +284,7 @@ std::string fmt(const char* f, ...) {
 
 }  // namespace
 
-// Kernel source of a validated program (registers < IHIP_EW_MAX_REGS, operands in range).
+// Kernel source of a validated program (registers < IHIP_EW_NATIVE_MAX_REGS, operands in range).
 // Elements per lane: 8 when every operand is 16-bit or narrower (one 16-byte access each),
 // else 4 (16-byte f32/i32 accesses).
 int ew_jit_width(int n_inputs, const int* in_dt, int n_outputs, const int* out_dt) {
@@ -365,16 +366,17 @@ static void ew_plan_logistic(const ihip_ew_instr* code, int n_code, int* fuse_u,
   }
 }
 
-// Program body: the instruction list as straight-line code over r[8][EW_V].  Inputs and
+// Program body: the instruction list as straight-line code over r[EW_NREG][EW_V].  Inputs and
 // outputs are accessed in their form (in_kind / out_kind, see ldk); in the tiled form
 // (`tiled`) staged inputs ('v', 't') are read from their LDS tile (slot = their rank among
 // the staged inputs) and the other inputs from the registers they were prefetched into.
 static std::string ew_jit_body(const ihip_ew_instr* code, int n_code, const int* in_dt, const int* out_dt,
                                const char* in_kind, const char* out_kind, bool tiled, const char* ind) {
   std::string s;
-  int fuse_u[IHIP_EW_MAX_CODE];
-  bool skip[IHIP_EW_MAX_CODE];
-  ew_plan_logistic(code, n_code, fuse_u, skip);
+  std::vector<int> fuse_u(n_code);
+  std::vector<char> skip_v(n_code);
+  bool* skip = reinterpret_cast<bool*>(skip_v.data());
+  ew_plan_logistic(code, n_code, fuse_u.data(), skip);
   for (int pc = 0; pc < n_code; ++pc) {
     const ihip_ew_instr& in = code[pc];
     if (skip[pc]) continue;
@@ -441,7 +443,10 @@ static std::string ew_jit_body(const ihip_ew_instr* code, int n_code, const int*
 std::string ew_jit_source(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
                           const int* out_dt, const char* in_kind, const char* out_kind) {
   const int V = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt);
-  std::string s = fmt("#define EW_V %d\n", V);
+  int nreg = IHIP_EW_MAX_REGS;  // registers the program writes: r[0 .. nreg - 1]
+  for (int pc = 0; pc < n_code; ++pc)
+    if (code[pc].op != IHIP_EW_STORE && code[pc].dst + 1 > nreg) nreg = code[pc].dst + 1;
+  std::string s = fmt("#define EW_V %d\n#define EW_NREG %d\n", V, nreg);
   s += kPrelude;
   int nt = 0;
   for (int k = 0; k < n_inputs; ++k) nt += is_tiled(in_kind[k]);
@@ -454,7 +459,7 @@ std::string ew_jit_source(const ihip_ew_instr* code, int n_code, int n_inputs, c
          "    for (i64 vec = (i64)blockIdx.x * blockDim.x + threadIdx.x; vec < a.nvec; vec += (i64)gridDim.x * blockDim.x) {\n"
          "      const i64 c3 = vec * EW_V;\n"
          "      const int valid = D3 - c3 < EW_V ? (int)(D3 - c3) : EW_V;\n"
-         "      float r[8][EW_V];\n";
+         "      float r[EW_NREG][EW_V];\n";
     s += ew_jit_body(code, n_code, in_dt, out_dt, in_kind, out_kind, false, "      ");
     s += "    }\n  }\n}\n";
     return s;
@@ -563,7 +568,7 @@ std::string ew_jit_source(const ihip_ew_instr* code, int n_code, int n_inputs, c
        "        const int l2 = pass * 4 * EW_V + tid / (64 / EW_V);\n"
        "        const i64 c2 = c2_0 + l2, row = (c0 * D1 + c1) * D2 + c2;\n"
        "        if (c2 < D2 && c3 < D3) {\n"
-       "          float r[8][EW_V];\n";
+       "          float r[EW_NREG][EW_V];\n";
   s += ew_jit_body(code, n_code, in_dt, out_dt, in_kind, out_kind, true, "          ");
   s += "        }\n      }\n    }\n  }\n}\n";
   return s;
@@ -634,7 +639,7 @@ bool plan_jit(const ihip_ew_instr* code, int n_code, const ihip_ew_operand* inpu
               const ihip_ew_operand* outputs, int n_outputs, const int64_t (&shape)[4], JitPlan& pl) {
   EwJitArgs& a = pl.a;
   for (int d = 0; d < 4; ++d) a.shape[d] = shape[d];
-  int in_dt[IHIP_EW_MAX_INPUTS] = {}, out_dt[IHIP_EW_MAX_OUTPUTS] = {};
+  int in_dt[IHIP_EW_NATIVE_MAX_INPUTS] = {}, out_dt[IHIP_EW_NATIVE_MAX_OUTPUTS] = {};
   for (int k = 0; k < n_inputs; ++k) in_dt[k] = inputs[k].dtype;
   for (int k = 0; k < n_outputs; ++k) out_dt[k] = outputs[k].dtype;
   const int V = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt);
@@ -663,7 +668,7 @@ bool plan_jit(const ihip_ew_instr* code, int n_code, const ihip_ew_operand* inpu
     return shape[2] % vs == 0 && st[3] % vs == 0 && (st[0] % vs == 0 || shape[0] == 1) &&
            (st[1] % vs == 0 || shape[1] == 1) && reinterpret_cast<uintptr_t>(inputs[k].ptr) % 16 == 0;
   };
-  char in_kind[IHIP_EW_MAX_INPUTS + 1] = {}, out_kind[IHIP_EW_MAX_OUTPUTS + 1] = {};
+  char in_kind[IHIP_EW_NATIVE_MAX_INPUTS + 1] = {}, out_kind[IHIP_EW_NATIVE_MAX_OUTPUTS + 1] = {};
   for (int k = 0; k < n_inputs; ++k) {
     a.in_ptr[k] = inputs[k].ptr;
     for (int d = 0; d < 4; ++d) a.in_stride[k][d] = inputs[k].stride[d];
@@ -711,7 +716,7 @@ bool compile_checked(const std::string& src, std::string* why) {
 bool prepare_elementwise_jit(const ihip_ew_instr* code, int n_code, int n_inputs, const int* in_dt, int n_outputs,
                              const int* out_dt, std::string* why) {
   const char w = ew_jit_width(n_inputs, in_dt, n_outputs, out_dt) == 8 ? '8' : '4';
-  char in_kind[IHIP_EW_MAX_INPUTS + 1] = {}, out_kind[IHIP_EW_MAX_OUTPUTS + 1] = {};
+  char in_kind[IHIP_EW_NATIVE_MAX_INPUTS + 1] = {}, out_kind[IHIP_EW_NATIVE_MAX_OUTPUTS + 1] = {};
   for (int k = 0; k < n_inputs; ++k) in_kind[k] = w;
   for (int k = 0; k < n_outputs; ++k) out_kind[k] = w;
   return compile_checked(ew_jit_source(code, n_code, n_inputs, in_dt, n_outputs, out_dt, in_kind, out_kind), why);

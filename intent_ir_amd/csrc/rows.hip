@@ -249,9 +249,11 @@ __device__ __forceinline__ float red_op(float a, float b) {
 // blockIdx.x % S of row blockIdx.x / S, i.e. aligned vectors [seg*per, (seg+1)*per) of the
 // row's body (segment 0 also the head, segment S-1 the tail), and writes its partial to
 // part[row * S + seg] instead of out[row]; reduce_rows_combine then folds the S partials.
+// scale multiplies the row's result as it is written (reduce_sum{scale}); split partials are
+// written unscaled and reduce_rows_combine scales their fold.
 template <int kKind, int W, int kUnroll, int kAcc, bool kSplit = false>
 __global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const float* __restrict__ x, float* __restrict__ out,
-                                                              int64_t M, int64_t N, int S = 1,
+                                                              int64_t M, int64_t N, float scale, int S = 1,
                                                               float* __restrict__ part = nullptr) {
   static_assert(kUnroll % kAcc == 0 && (kAcc & (kAcc - 1)) == 0, "loads fold evenly into a power-of-two of partials");
   const float id = kKind == 0 ? 0.0f : -__builtin_inff();
@@ -308,6 +310,7 @@ __global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const float* __res
   }
   r = kKind == 0 ? wave_sum(r) : wave_max_nan(r);
   float* dst = kSplit ? part + row * S + seg : out + row;
+  const float f = kSplit ? 1.0f : scale;
   if (W > 1) {
     __shared__ float wpart[W];
     if (lane == 0) wpart[wave] = r;
@@ -316,10 +319,10 @@ __global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const float* __res
       float t = wpart[0];
 #pragma unroll
       for (int i = 1; i < W; ++i) t = red_op<kKind>(t, wpart[i]);
-      *dst = t;
+      *dst = t * f;
     }
   } else if (lane == 0) {
-    *dst = r;
+    *dst = r * f;
   }
 }
 
@@ -327,19 +330,19 @@ __global__ __launch_bounds__(64 * W) void reduce_rows_f32_vec(const float* __res
 // l holding partial l; the xor-shuffle tree fixes the order, so results are reproducible.
 template <int kKind>
 __global__ __launch_bounds__(256) void reduce_rows_combine(const float* __restrict__ part, float* __restrict__ out,
-                                                           int64_t M, int S) {
+                                                           int64_t M, int S, float scale) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
   float r = lane < S ? part[row * S + lane] : (kKind == 0 ? 0.0f : -__builtin_inff());
   r = kKind == 0 ? wave_sum(r) : wave_max_nan(r);
-  if (lane == 0) out[row] = r;
+  if (lane == 0) out[row] = r * scale;
 }
 
 // Scalar form for rows the vector form cannot take (N % 4 != 0 or a base not 16-byte aligned).
 template <int kKind>
 __global__ __launch_bounds__(256) void reduce_rows_f32(const float* __restrict__ x, float* __restrict__ out, int64_t M,
-                                                       int64_t N) {
+                                                       int64_t N, float scale) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
@@ -347,7 +350,7 @@ __global__ __launch_bounds__(256) void reduce_rows_f32(const float* __restrict__
   float acc = kKind == 0 ? 0.0f : -__builtin_inff();
   for (int64_t i = lane; i < N; i += kWave) acc = red_op<kKind>(acc, xr[i]);
   acc = kKind == 0 ? wave_sum(acc) : wave_max_nan(acc);
-  if (lane == 0) out[row] = acc;
+  if (lane == 0) out[row] = acc * scale;
 }
 
 // Loads in flight per lane in the one-wave form (8 measured level with 16 on [8192, 4096]).
@@ -377,7 +380,7 @@ int reduce_rows_segments(int64_t M, int64_t N) {
 // ran at 5% of HBM peak, 128 at 19%).  kKind 0: sum, 1: NaN-propagating max.
 template <int kKind, int G, int kV>
 __global__ __launch_bounds__(256) void reduce_rows_f32_grouped(const float* __restrict__ x, float* __restrict__ out,
-                                                               int64_t M, int64_t N) {
+                                                               int64_t M, int64_t N, float scale) {
   const int lig = threadIdx.x & (G - 1);
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / G) + threadIdx.x / G;
   auto op = [](float a, float b) { return kKind == 0 ? a + b : max_nan(a, b); };
@@ -405,22 +408,22 @@ __global__ __launch_bounds__(256) void reduce_rows_f32_grouped(const float* __re
   }
 #pragma unroll
   for (int off = G / 2; off > 0; off >>= 1) acc = op(acc, __shfl_xor(acc, off, kWave));
-  if (row < M && lig == 0) out[row] = acc;
+  if (row < M && lig == 0) out[row] = acc * scale;
 }
 
 template <int kKind, int G>
-static void launch_reduce_grouped_g(const float* x, float* out, int64_t M, int64_t N, int kv, dim3 grid,
+static void launch_reduce_grouped_g(const float* x, float* out, int64_t M, int64_t N, float scale, int kv, dim3 grid,
                                     hipStream_t s) {
   if (kv <= 1)
-    reduce_rows_f32_grouped<kKind, G, 1><<<grid, dim3(256), 0, s>>>(x, out, M, N);
+    reduce_rows_f32_grouped<kKind, G, 1><<<grid, dim3(256), 0, s>>>(x, out, M, N, scale);
   else if (kv <= 2)
-    reduce_rows_f32_grouped<kKind, G, 2><<<grid, dim3(256), 0, s>>>(x, out, M, N);
+    reduce_rows_f32_grouped<kKind, G, 2><<<grid, dim3(256), 0, s>>>(x, out, M, N, scale);
   else
-    reduce_rows_f32_grouped<kKind, G, 4><<<grid, dim3(256), 0, s>>>(x, out, M, N);
+    reduce_rows_f32_grouped<kKind, G, 4><<<grid, dim3(256), 0, s>>>(x, out, M, N, scale);
 }
 
 template <int kKind>
-static void launch_reduce_grouped(const float* x, float* out, int64_t M, int64_t N, hipStream_t s) {
+static void launch_reduce_grouped(const float* x, float* out, int64_t M, int64_t N, float scale, hipStream_t s) {
   const int64_t nvec = N / 4;
   // about two vectors per lane (four at 65-128 vectors); one per lane measured 12-18% slower at
   // 16-32 vectors and, with the loads issued together, 14-16% slower at 4-8
@@ -429,47 +432,48 @@ static void launch_reduce_grouped(const float* x, float* out, int64_t M, int64_t
   const int kv = static_cast<int>((nvec + g - 1) / g);  // body vectors per lane at most (<= 4)
   const dim3 grid(static_cast<unsigned>((M * g + 255) / 256));
   switch (g) {
-    case 1: launch_reduce_grouped_g<kKind, 1>(x, out, M, N, kv, grid, s); break;
-    case 2: launch_reduce_grouped_g<kKind, 2>(x, out, M, N, kv, grid, s); break;
-    case 4: launch_reduce_grouped_g<kKind, 4>(x, out, M, N, kv, grid, s); break;
-    case 8: launch_reduce_grouped_g<kKind, 8>(x, out, M, N, kv, grid, s); break;
-    case 16: launch_reduce_grouped_g<kKind, 16>(x, out, M, N, kv, grid, s); break;
-    default: launch_reduce_grouped_g<kKind, 32>(x, out, M, N, kv, grid, s); break;
+    case 1: launch_reduce_grouped_g<kKind, 1>(x, out, M, N, scale, kv, grid, s); break;
+    case 2: launch_reduce_grouped_g<kKind, 2>(x, out, M, N, scale, kv, grid, s); break;
+    case 4: launch_reduce_grouped_g<kKind, 4>(x, out, M, N, scale, kv, grid, s); break;
+    case 8: launch_reduce_grouped_g<kKind, 8>(x, out, M, N, scale, kv, grid, s); break;
+    case 16: launch_reduce_grouped_g<kKind, 16>(x, out, M, N, scale, kv, grid, s); break;
+    default: launch_reduce_grouped_g<kKind, 32>(x, out, M, N, scale, kv, grid, s); break;
   }
 }
 
 template <int kKind>
-static void launch_reduce_rows(const float* x, float* out, int64_t M, int64_t N, float* part, int S, hipStream_t s) {
+static void launch_reduce_rows(const float* x, float* out, int64_t M, int64_t N, float scale, float* part, int S,
+                               hipStream_t s) {
   // 16-byte loads over each row's aligned body whenever x is 4-byte aligned (any N)
   if ((reinterpret_cast<uintptr_t>(x) & 3) != 0 || N == 0) {
-    reduce_rows_f32<kKind><<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(x, out, M, N);
+    reduce_rows_f32<kKind><<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(x, out, M, N, scale);
     return;
   }
   const int64_t n4 = N / 4;
   const dim3 grid(static_cast<unsigned>(M));
   if (S > 1 && part != nullptr) {  // few long rows split over S workgroups each, then combined
     reduce_rows_f32_vec<kKind, 16, 8, 4, true><<<dim3(static_cast<unsigned>(M * S)), dim3(1024), 0, s>>>(
-        x, out, M, N, S, part);
-    reduce_rows_combine<kKind><<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(part, out, M, S);
+        x, out, M, N, scale, S, part);
+    reduce_rows_combine<kKind><<<dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, s>>>(part, out, M, S, scale);
   } else if (n4 <= 2 * kWave) {  // short rows: several per wave
-    launch_reduce_grouped<kKind>(x, out, M, N, s);
+    launch_reduce_grouped<kKind>(x, out, M, N, scale, s);
   } else if (M >= 2048 || n4 <= 4 * kWave) {  // enough rows for the CUs, or short rows: a wave per row
-    reduce_rows_f32_vec<kKind, 1, kRedUnroll, 4><<<grid, dim3(64), 0, s>>>(x, out, M, N);
+    reduce_rows_f32_vec<kKind, 1, kRedUnroll, 4><<<grid, dim3(64), 0, s>>>(x, out, M, N, scale);
   } else {  // few long rows: 16 waves per row
-    reduce_rows_f32_vec<kKind, 16, 8, 4><<<grid, dim3(1024), 0, s>>>(x, out, M, N);
+    reduce_rows_f32_vec<kKind, 16, 8, 4><<<grid, dim3(1024), 0, s>>>(x, out, M, N, scale);
   }
 }
 
 // part: workspace of M * reduce_rows_segments(M, N) floats, or null (no row split).
-hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, float* part,
-                                  hipStream_t s) {
+hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t N, int kind, float scale,
+                                  float* part, hipStream_t s) {
   if (M == 0) return hipSuccess;
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // one workgroup per row
   const int S = part != nullptr ? reduce_rows_segments(M, N) : 1;
   if (kind == 0)
-    launch_reduce_rows<0>(x, out, M, N, part, S, s);
+    launch_reduce_rows<0>(x, out, M, N, scale, part, S, s);
   else
-    launch_reduce_rows<1>(x, out, M, N, part, S, s);
+    launch_reduce_rows<1>(x, out, M, N, scale, part, S, s);
   return hipGetLastError();
 }
 
@@ -487,7 +491,7 @@ hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t
 // cost 4%).
 template <int kVpl, bool kFull, int kR>
 __global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restrict__ x, f32x4* __restrict__ y,
-                                                            int64_t M, int n4) {
+                                                            int64_t M, int n4, SoftmaxStats st) {
   const int lane = threadIdx.x & 63;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * kR;
   if (row0 >= M) return;
@@ -521,6 +525,7 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restr
       if (kFull || lane + i * kWave < n4) sum += (v[r][i].x + v[r][i].y) + (v[r][i].z + v[r][i].w);
     }
     sum = wave_sum(sum);
+    if (lane == 0 && (kR == 1 || row0 + r < M)) put_softmax_stats(st, row0 + r, mx, sum);
     const float inv = 1.0f / sum;
 #pragma unroll
     for (int i = 0; i < kVpl; ++i) {
@@ -543,7 +548,7 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restr
 // the kW partials in the same order.  Same arithmetic per element as the one-wave kernel.
 template <int kVpl, int kW>
 __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_multi(const f32x4* __restrict__ x, f32x4* __restrict__ y,
-                                                                  int64_t M, int n4) {
+                                                                  int64_t M, int n4, SoftmaxStats st) {
   __shared__ float part_m[kW], part_s[kW];
   const int lane = threadIdx.x & 63, v = threadIdx.x >> 6;
   const int64_t row = blockIdx.x;
@@ -580,6 +585,7 @@ __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_multi(const f32x4* _
   float tot = 0.f;
 #pragma unroll
   for (int k = 0; k < kW; ++k) tot += part_s[k];
+  if (threadIdx.x == 0) put_softmax_stats(st, row, mx, tot);
   const float inv = 1.0f / tot;
 #pragma unroll
   for (int i = 0; i < kVpl; ++i)
@@ -592,7 +598,7 @@ __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_multi(const f32x4* _
 // bytes; kW waves per row, partials through LDS as in the vector multi-wave form.
 template <int kEpl, int kW>
 __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_regs(const float* __restrict__ x, float* __restrict__ y,
-                                                                 int64_t M, int64_t N) {
+                                                                 int64_t M, int64_t N, SoftmaxStats st) {
   __shared__ float part_m[kW], part_s[kW];
   const int lane = threadIdx.x & 63, v = threadIdx.x >> 6;
   const int64_t row = blockIdx.x;
@@ -629,6 +635,7 @@ __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_regs(const float* __
 #pragma unroll
     for (int k = 0; k < kW; ++k) sum += part_s[k];
   }
+  if (threadIdx.x == 0) put_softmax_stats(st, row, mx, sum);
   const float inv = 1.0f / sum;
 #pragma unroll
   for (int i = 0; i < kEpl; ++i)
@@ -643,7 +650,7 @@ __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_regs(const float* __
 // vector k < nb covers elements h + 4k .. h + 4k + 3 < h + 4nb <= N.
 template <int kVpl, int kW>
 __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_skew(const float* __restrict__ x, float* __restrict__ y,
-                                                                 int64_t M, int64_t N) {
+                                                                 int64_t M, int64_t N, SoftmaxStats st) {
   __shared__ float part_m[kW], part_s[kW];
   const int lane = threadIdx.x & 63, v = threadIdx.x >> 6, tid = threadIdx.x;
   const int64_t row = blockIdx.x;
@@ -691,6 +698,7 @@ __global__ __launch_bounds__(64 * kW) void softmax_rows_f32_skew(const float* __
   float tot = 0.f;
 #pragma unroll
   for (int k = 0; k < kW; ++k) tot += part_s[k];
+  if (tid == 0) put_softmax_stats(st, row, mx, tot);
   const float inv = 1.0f / tot;
 #pragma unroll
   for (int i = 0; i < kVpl; ++i)
@@ -734,7 +742,7 @@ __device__ __forceinline__ void block_softmax_fold(float& m, float& s, float* fm
 // threads around 16-byte loads of the body; otherwise 4-byte loads throughout.
 template <bool kVec>
 __global__ __launch_bounds__(1024) void softmax_rows_f32_online(const float* __restrict__ x, float* __restrict__ y,
-                                                                int64_t N) {
+                                                                int64_t N, SoftmaxStats st) {
   constexpr int kW = 16, kT = 1024, kU = 4;
   __shared__ float fm[kW], fs[kW];
   const int tid = threadIdx.x;
@@ -767,6 +775,7 @@ __global__ __launch_bounds__(1024) void softmax_rows_f32_online(const float* __r
     }
     add4(tid < head ? xr[tid] : ninf, tid < tail ? xr[head + 4 * nb + tid] : ninf, ninf, ninf);
     block_softmax_fold<kW>(m, s, fm, fs);
+    if (tid == 0) put_softmax_stats(st, row, m, s);
     const float inv = 1.0f / s;
     for (int64_t i = tid; i < nb; i += kU * kT) {
       f32x4 q[kU];
@@ -788,6 +797,7 @@ __global__ __launch_bounds__(1024) void softmax_rows_f32_online(const float* __r
       add4(xr[i], i + kT < N ? xr[i + kT] : ninf, i + 2 * kT < N ? xr[i + 2 * kT] : ninf,
            i + 3 * kT < N ? xr[i + 3 * kT] : ninf);
     block_softmax_fold<kW>(m, s, fm, fs);
+    if (tid == 0) put_softmax_stats(st, row, m, s);
     const float inv = 1.0f / s;
     for (int64_t i = tid; i < N; i += kT) yr[i] = exp_nonpos(xr[i] - m) * inv;
   }
@@ -882,7 +892,7 @@ template <int kVpl, bool kSkew>
 __global__ __launch_bounds__(kSplitThreads) void softmax_split_write(const float* __restrict__ x,
                                                                      float* __restrict__ y,
                                                                      const float* __restrict__ part, int64_t N,
-                                                                     int S) {
+                                                                     int S, SoftmaxStats st) {
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x / S;
   const int seg = static_cast<int>(blockIdx.x % S);
@@ -908,6 +918,7 @@ __global__ __launch_bounds__(kSplitThreads) void softmax_split_write(const float
   float mx = ninf, tot = 0.f;
   for (int j = tid; j < S; j += kSplitThreads) softmax_fold(mx, tot, pr[2 * j], pr[2 * j + 1]);
   block_softmax_fold<kSplitThreads / kWave>(mx, tot, fm, fs);
+  if (seg == 0 && tid == 0) put_softmax_stats(st, row, mx, tot);
   const float inv = 1.0f / tot;
 #pragma unroll
   for (int i = 0; i < kVpl; ++i) {
@@ -946,17 +957,17 @@ SoftmaxSplit softmax_split_plan(int64_t M, int64_t N) {
 
 template <bool kSkew>
 static void launch_softmax_split(const float* x, float* y, int64_t M, int64_t N, const SoftmaxSplit& p, float* part,
-                                 hipStream_t s) {
+                                 const SoftmaxStats& st, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(M * p.S)), block(kSplitThreads);
   if (p.vpl == 16) {
     softmax_split_stats<16, kSkew><<<grid, block, 0, s>>>(x, part, N, p.S);
-    softmax_split_write<16, kSkew><<<grid, block, 0, s>>>(x, y, part, N, p.S);
+    softmax_split_write<16, kSkew><<<grid, block, 0, s>>>(x, y, part, N, p.S, st);
   } else if (p.vpl == 8) {
     softmax_split_stats<8, kSkew><<<grid, block, 0, s>>>(x, part, N, p.S);
-    softmax_split_write<8, kSkew><<<grid, block, 0, s>>>(x, y, part, N, p.S);
+    softmax_split_write<8, kSkew><<<grid, block, 0, s>>>(x, y, part, N, p.S, st);
   } else {
     softmax_split_stats<4, kSkew><<<grid, block, 0, s>>>(x, part, N, p.S);
-    softmax_split_write<4, kSkew><<<grid, block, 0, s>>>(x, y, part, N, p.S);
+    softmax_split_write<4, kSkew><<<grid, block, 0, s>>>(x, y, part, N, p.S, st);
   }
 }
 
@@ -966,7 +977,7 @@ static void launch_softmax_split(const float* x, float* y, int64_t M, int64_t N,
 // max and the sum are reduced over the group with xor shuffles.
 template <int G>
 __global__ __launch_bounds__(256) void softmax_rows_f32_grouped(const f32x4* __restrict__ x, f32x4* __restrict__ y,
-                                                                int64_t M, int n4) {
+                                                                int64_t M, int n4, SoftmaxStats st) {
   const int lig = threadIdx.x & (G - 1);
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / G) + threadIdx.x / G;
   const bool valid = row < M && lig < n4;  // no early return: the group's shuffles need every lane
@@ -982,6 +993,7 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_grouped(const f32x4* __r
   float sum = valid ? (v.x + v.y) + (v.z + v.w) : 0.f;
 #pragma unroll
   for (int off = G / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+  if (row < M && lig == 0) put_softmax_stats(st, row, mx, sum);
   const float inv = 1.0f / sum;
   if (valid) __builtin_nontemporal_store(v * inv, y + row * n4 + lig);
 }
@@ -991,7 +1003,7 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_grouped(const f32x4* __r
 // at 10% of HBM peak with a wave per row).
 template <int G>
 __global__ __launch_bounds__(256) void softmax_rows_f32_grouped_any(const float* __restrict__ x, float* __restrict__ y,
-                                                                    int64_t M, int64_t N) {
+                                                                    int64_t M, int64_t N, SoftmaxStats st) {
   const int lig = threadIdx.x & (G - 1);
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / G) + threadIdx.x / G;
   const float ninf = -__builtin_inff();
@@ -1010,6 +1022,7 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_grouped_any(const float*
   }
 #pragma unroll
   for (int off = G / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+  if (row < M && lig == 0) put_softmax_stats(st, row, mx, sum);
   const float inv = 1.0f / sum;
   if (row < M) {
 #pragma unroll
@@ -1079,7 +1092,7 @@ constexpr int kLnShortRpt = 4;
 // lane rewrites only the slots it read), after a barrier otherwise.
 template <int G>
 __global__ __launch_bounds__(256) void softmax_rows_f32_short_lds(const float* __restrict__ x, float* __restrict__ y,
-                                                                  int64_t M, int N) {
+                                                                  int64_t M, int N, SoftmaxStats st) {
   constexpr int kRows = kShortRpt * (256 / G);
   __shared__ __align__(16) float buf[kRows * 4 * G + 4];
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
@@ -1116,6 +1129,7 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_short_lds(const float* _
     }
 #pragma unroll
     for (int off = G / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    if (lr < rows && lig == 0) put_softmax_stats(st, r0 + lr, mx, sum);
     inv[rr] = 1.0f / sum;
   }
   if (hx != hy) __syncthreads();  // uniform over the workgroup
@@ -1130,64 +1144,68 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_short_lds(const float* _
   stage_out<float, 256>(buf, hy, n, yb);
 }
 
-static void launch_softmax_short_lds(const float* x, float* y, int64_t M, int N, hipStream_t s) {
+static void launch_softmax_short_lds(const float* x, float* y, int64_t M, int N, const SoftmaxStats& st,
+                                     hipStream_t s) {
   int g = 1;
   while (4 * g < N) g *= 2;
   const int rows = kShortRpt * (256 / g);
   const dim3 grid(static_cast<unsigned>((M + rows - 1) / rows)), block(256);
   switch (g) {
-    case 1: softmax_rows_f32_short_lds<1><<<grid, block, 0, s>>>(x, y, M, N); break;
-    case 2: softmax_rows_f32_short_lds<2><<<grid, block, 0, s>>>(x, y, M, N); break;
-    case 4: softmax_rows_f32_short_lds<4><<<grid, block, 0, s>>>(x, y, M, N); break;
-    case 8: softmax_rows_f32_short_lds<8><<<grid, block, 0, s>>>(x, y, M, N); break;
-    case 16: softmax_rows_f32_short_lds<16><<<grid, block, 0, s>>>(x, y, M, N); break;
-    default: softmax_rows_f32_short_lds<32><<<grid, block, 0, s>>>(x, y, M, N); break;
+    case 1: softmax_rows_f32_short_lds<1><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    case 2: softmax_rows_f32_short_lds<2><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    case 4: softmax_rows_f32_short_lds<4><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    case 8: softmax_rows_f32_short_lds<8><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    case 16: softmax_rows_f32_short_lds<16><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    default: softmax_rows_f32_short_lds<32><<<grid, block, 0, s>>>(x, y, M, N, st); break;
   }
 }
 
-static void launch_softmax_grouped_any(const float* x, float* y, int64_t M, int64_t N, hipStream_t s) {
+static void launch_softmax_grouped_any(const float* x, float* y, int64_t M, int64_t N, const SoftmaxStats& st,
+                                      hipStream_t s) {
   int g = 1;
   while (4 * g < N) g *= 2;
   const dim3 grid(static_cast<unsigned>((M * g + 255) / 256)), block(256);
   switch (g) {
-    case 1: softmax_rows_f32_grouped_any<1><<<grid, block, 0, s>>>(x, y, M, N); break;
-    case 2: softmax_rows_f32_grouped_any<2><<<grid, block, 0, s>>>(x, y, M, N); break;
-    case 4: softmax_rows_f32_grouped_any<4><<<grid, block, 0, s>>>(x, y, M, N); break;
-    case 8: softmax_rows_f32_grouped_any<8><<<grid, block, 0, s>>>(x, y, M, N); break;
-    case 16: softmax_rows_f32_grouped_any<16><<<grid, block, 0, s>>>(x, y, M, N); break;
-    default: softmax_rows_f32_grouped_any<32><<<grid, block, 0, s>>>(x, y, M, N); break;
+    case 1: softmax_rows_f32_grouped_any<1><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    case 2: softmax_rows_f32_grouped_any<2><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    case 4: softmax_rows_f32_grouped_any<4><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    case 8: softmax_rows_f32_grouped_any<8><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    case 16: softmax_rows_f32_grouped_any<16><<<grid, block, 0, s>>>(x, y, M, N, st); break;
+    default: softmax_rows_f32_grouped_any<32><<<grid, block, 0, s>>>(x, y, M, N, st); break;
   }
 }
 
-static void launch_softmax_grouped(const f32x4* x4, f32x4* y4, int64_t M, int n4, hipStream_t s) {
+static void launch_softmax_grouped(const f32x4* x4, f32x4* y4, int64_t M, int n4, const SoftmaxStats& st,
+                                   hipStream_t s) {
   int g = 1;
   while (g < n4) g *= 2;
   const dim3 grid(static_cast<unsigned>((M * g + 255) / 256)), block(256);
   switch (g) {
-    case 1: softmax_rows_f32_grouped<1><<<grid, block, 0, s>>>(x4, y4, M, n4); break;
-    case 2: softmax_rows_f32_grouped<2><<<grid, block, 0, s>>>(x4, y4, M, n4); break;
-    case 4: softmax_rows_f32_grouped<4><<<grid, block, 0, s>>>(x4, y4, M, n4); break;
-    case 8: softmax_rows_f32_grouped<8><<<grid, block, 0, s>>>(x4, y4, M, n4); break;
-    case 16: softmax_rows_f32_grouped<16><<<grid, block, 0, s>>>(x4, y4, M, n4); break;
-    default: softmax_rows_f32_grouped<32><<<grid, block, 0, s>>>(x4, y4, M, n4); break;
+    case 1: softmax_rows_f32_grouped<1><<<grid, block, 0, s>>>(x4, y4, M, n4, st); break;
+    case 2: softmax_rows_f32_grouped<2><<<grid, block, 0, s>>>(x4, y4, M, n4, st); break;
+    case 4: softmax_rows_f32_grouped<4><<<grid, block, 0, s>>>(x4, y4, M, n4, st); break;
+    case 8: softmax_rows_f32_grouped<8><<<grid, block, 0, s>>>(x4, y4, M, n4, st); break;
+    case 16: softmax_rows_f32_grouped<16><<<grid, block, 0, s>>>(x4, y4, M, n4, st); break;
+    default: softmax_rows_f32_grouped<32><<<grid, block, 0, s>>>(x4, y4, M, n4, st); break;
   }
 }
 
 // rows: rows per workgroup, 1, 2 or 4 (the kernel reads its waves from blockDim).  Four rows of
 // at most 1024 floats run as two waves of two rows each, otherwise one wave per row.
 template <int kVpl>
-static void launch_softmax_reg(const f32x4* x4, f32x4* y4, int64_t M, int n4, int rows, hipStream_t s) {
+static void launch_softmax_reg(const f32x4* x4, f32x4* y4, int64_t M, int n4, int rows, const SoftmaxStats& st,
+                               hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((M + rows - 1) / rows));
   const bool full = n4 == kVpl * kWave;
   if (kVpl <= 4 && rows == 4) {
     if (full)
-      softmax_rows_f32_reg<kVpl, true, 2><<<grid, dim3(128), 0, s>>>(x4, y4, M, n4);
+      softmax_rows_f32_reg<kVpl, true, 2><<<grid, dim3(128), 0, s>>>(x4, y4, M, n4, st);
     else
-      softmax_rows_f32_reg<kVpl, false, 2><<<grid, dim3(128), 0, s>>>(x4, y4, M, n4);
+      softmax_rows_f32_reg<kVpl, false, 2><<<grid, dim3(128), 0, s>>>(x4, y4, M, n4, st);
   } else if (full) {
-    softmax_rows_f32_reg<kVpl, true, 1><<<grid, dim3(64 * rows), 0, s>>>(x4, y4, M, n4);
+    softmax_rows_f32_reg<kVpl, true, 1><<<grid, dim3(64 * rows), 0, s>>>(x4, y4, M, n4, st);
   } else {
-    softmax_rows_f32_reg<kVpl, false, 1><<<grid, dim3(64 * rows), 0, s>>>(x4, y4, M, n4);
+    softmax_rows_f32_reg<kVpl, false, 1><<<grid, dim3(64 * rows), 0, s>>>(x4, y4, M, n4, st);
   }
 }
 
@@ -1201,19 +1219,21 @@ bool softmax_rows_per_wg_form(const float* x, const float* y, int64_t N) {
 // rows_per_wg: 0 = automatic (4), else 1, 2 or 4 for the one-wave-per-row form.  part: workspace
 // of 2 * M * softmax_split_plan(M, N).S floats, or null: rows longer than 65536 floats are then
 // split over several workgroups each (16-byte aligned rows, or rows at the same offset modulo 16
-// bytes in x and y), else they take the workgroup-per-row kernel.
+// bytes in x and y), else they take the workgroup-per-row kernel.  row_max, row_sum: per-row
+// outputs of the maximum and of the sum of exp(x - max), or null (every form writes them).
 hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, int rows_per_wg, hipStream_t s,
-                                   float* part) {
-  if (M == 0 || N == 0) return hipSuccess;
+                                   float* part, float* row_max, float* row_sum) {
+  if (M == 0 || N == 0) return hipSuccess;  // (statistics of empty rows are rejected by the caller)
+  const SoftmaxStats st{row_max, row_sum};
   if (part != nullptr) {
     const SoftmaxSplit p = softmax_split_plan(M, N);
     const uintptr_t xa = reinterpret_cast<uintptr_t>(x), ya = reinterpret_cast<uintptr_t>(y);
     if (p.S > 0 && N % 4 == 0 && ((xa | ya) & 15) == 0) {
-      launch_softmax_split<false>(x, y, M, N, p, part, s);
+      launch_softmax_split<false>(x, y, M, N, p, part, st, s);
       return hipGetLastError();
     }
     if (p.S > 0 && ((xa | ya) & 3) == 0 && ((xa ^ ya) & 15) == 0) {
-      launch_softmax_split<true>(x, y, M, N, p, part, s);
+      launch_softmax_split<true>(x, y, M, N, p, part, st, s);
       return hipGetLastError();
     }
   }
@@ -1228,56 +1248,56 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
   f32x4* y4 = reinterpret_cast<f32x4*>(y);
   const int n4i = static_cast<int>(n4 < 0x7fffffff ? n4 : 0x7fffffff);
   if (vec && n4 <= 32 && rows_per_wg == 0)  // short rows: several per wave (a rows knob keeps a wave per row)
-    launch_softmax_grouped(x4, y4, M, n4i, s);
+    launch_softmax_grouped(x4, y4, M, n4i, st, s);
   else if (vec && n4 <= 64)
-    launch_softmax_reg<1>(x4, y4, M, n4i, rows, s);
+    launch_softmax_reg<1>(x4, y4, M, n4i, rows, st, s);
   else if (vec && n4 <= 128)
-    launch_softmax_reg<2>(x4, y4, M, n4i, rows, s);
+    launch_softmax_reg<2>(x4, y4, M, n4i, rows, st, s);
   else if (vec && n4 <= 256)
-    launch_softmax_reg<4>(x4, y4, M, n4i, rows, s);
+    launch_softmax_reg<4>(x4, y4, M, n4i, rows, st, s);
   else if (vec && n4 <= 512)
-    launch_softmax_reg<8>(x4, y4, M, n4i, rows, s);
+    launch_softmax_reg<8>(x4, y4, M, n4i, rows, st, s);
   else if (vec && n4 <= 1024)
-    launch_softmax_reg<16>(x4, y4, M, n4i, rows, s);
+    launch_softmax_reg<16>(x4, y4, M, n4i, rows, st, s);
   else if (vec && n4 <= 2048)
-    softmax_rows_f32_multi<16, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x4, y4, M, n4i);
+    softmax_rows_f32_multi<16, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x4, y4, M, n4i, st);
   else if (vec && n4 <= 4096)
-    softmax_rows_f32_multi<16, 4><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x4, y4, M, n4i);
+    softmax_rows_f32_multi<16, 4><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x4, y4, M, n4i, st);
   else if (vec && n4 <= 8192)
-    softmax_rows_f32_multi<16, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x4, y4, M, n4i);
+    softmax_rows_f32_multi<16, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x4, y4, M, n4i, st);
   else if (vec && n4 <= 16384)
-    softmax_rows_f32_multi<16, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x4, y4, M, n4i);
+    softmax_rows_f32_multi<16, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x4, y4, M, n4i, st);
   else if (!vec && N <= 128 && rows_per_wg == 0 &&
            ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 3) == 0)
-    launch_softmax_short_lds(x, y, M, static_cast<int>(N), s);  // short rows at any length: staged in LDS
+    launch_softmax_short_lds(x, y, M, static_cast<int>(N), st, s);  // short rows at any length: staged in LDS
   else if (!vec && N <= 128 && rows_per_wg == 0)  // short rows at any alignment: several per wave
-    launch_softmax_grouped_any(x, y, M, N, s);
+    launch_softmax_grouped_any(x, y, M, N, st, s);
   else if (!vec && N <= 64 * 16)
-    softmax_rows_f32_regs<16, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_regs<16, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N, st);
   else if (skew && N <= 4096)
-    softmax_rows_f32_skew<16, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_skew<16, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N, st);
   else if (skew && N <= 4096 * 2)
-    softmax_rows_f32_skew<16, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_skew<16, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x, y, M, N, st);
   else if (skew && N <= 4096 * 4)
-    softmax_rows_f32_skew<16, 4><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_skew<16, 4><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, M, N, st);
   else if (skew && N <= 4096 * 8)
-    softmax_rows_f32_skew<16, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_skew<16, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x, y, M, N, st);
   else if (skew && N <= 4096 * 16)
-    softmax_rows_f32_skew<16, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_skew<16, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, M, N, st);
   else if (!vec && N <= 64 * 64)
-    softmax_rows_f32_regs<64, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_regs<64, 1><<<dim3(static_cast<unsigned>(M)), dim3(64), 0, s>>>(x, y, M, N, st);
   else if (!vec && N <= 64 * 64 * 2)
-    softmax_rows_f32_regs<64, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_regs<64, 2><<<dim3(static_cast<unsigned>(M)), dim3(128), 0, s>>>(x, y, M, N, st);
   else if (!vec && N <= 64 * 64 * 4)
-    softmax_rows_f32_regs<64, 4><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_regs<64, 4><<<dim3(static_cast<unsigned>(M)), dim3(256), 0, s>>>(x, y, M, N, st);
   else if (!vec && N <= 64 * 64 * 8)
-    softmax_rows_f32_regs<64, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_regs<64, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x, y, M, N, st);
   else if (!vec && N <= 64 * 64 * 16)
-    softmax_rows_f32_regs<64, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, M, N);
+    softmax_rows_f32_regs<64, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, M, N, st);
   else if (skew || vec)
-    softmax_rows_f32_online<true><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, N);
+    softmax_rows_f32_online<true><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, N, st);
   else
-    softmax_rows_f32_online<false><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, N);
+    softmax_rows_f32_online<false><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, N, st);
   return hipGetLastError();
 }
 

@@ -6,7 +6,10 @@ per chain (backends/cuda/codegen/intentir_to_cuda.py:229-534).  This backend
 runs every such chain on one precompiled gfx950 kernel and passes the chain
 as a short program: a DAG of the outputs' expression trees (common
 subexpressions shared), scheduled in Sethi-Ullman order and given registers
-by last use, so a chain needs at most ``MAX_REGS`` live values at once.
+by last use.  A chain within the interpreter kernel's limits (``MAX_*``: 64
+instructions, 8 live values, 8 inputs, 4 outputs) runs in every execution
+mode; a larger one is compiled for the native form's limits (``NATIVE_MAX_*``)
+and runs only as hiprtc-compiled code.
 
 Index maps: broadcasts, transposes and kept unit dims of the expression trees
 (``patterns.py``) are pushed down to the leaves, so every input is read
@@ -20,6 +23,9 @@ from dataclasses import dataclass
 from typing import Any, Dict, List, Mapping, Optional, Sequence, Tuple
 
 MAX_CODE, MAX_REGS, MAX_INPUTS, MAX_OUTPUTS, MAX_RANK = 64, 8, 8, 4, 4
+# The native (hiprtc) form's limits, include/intentir_hip.h IHIP_EW_NATIVE_MAX_*: a program
+# over the interpreter limits above runs only as native code.
+NATIVE_MAX_CODE, NATIVE_MAX_REGS, NATIVE_MAX_INPUTS, NATIVE_MAX_OUTPUTS = 1024, 255, 32, 8
 
 # Opcodes of include/intentir_hip.h.
 OP = {
@@ -46,6 +52,10 @@ CAST_OP = {"f16": "cast_f16", "bf16": "cast_f16", "f32": None, "f64": None, "boo
 
 class EwCompileError(ValueError):
     """The trees are not an element-wise chain the program kernel runs."""
+
+
+class EwLimitError(EwCompileError):
+    """The chain is element-wise but exceeds the limits it was compiled for."""
 
 
 @dataclass(frozen=True)
@@ -102,7 +112,8 @@ class _Dag:
 
 class _Builder:
     def __init__(self, shape: Tuple[int, ...], decl: Mapping[str, Tuple[int, ...]],
-                 units: Mapping[str, Tuple[int, ...]]):
+                 units: Mapping[str, Tuple[int, ...]], max_inputs: int = MAX_INPUTS):
+        self.max_inputs = max_inputs
         self.shape = shape
         self.rank = len(shape)
         self.decl = decl
@@ -118,6 +129,8 @@ class _Builder:
             raise EwCompileError(f"input {name} has no resolved shape")
         shp = self.decl[name]
         unit = self.units.get(name, ())
+        if len(shp) == 0:  # a rank-0 tensor: one element, broadcast over every axis (stride 0)
+            amap = ()
         if len(shp) != len(amap):
             # a value with kept unit dims ([M,1]) is placed by its other axes only
             if len(shp) - len(unit) != len(amap):
@@ -134,8 +147,8 @@ class _Builder:
             st4[self._pad(ax)] += cs
         key = (name, tuple(st4))
         if key not in self.inputs:
-            if len(self.inputs) == MAX_INPUTS:
-                raise EwCompileError(f"more than {MAX_INPUTS} distinct input views")
+            if len(self.inputs) == self.max_inputs:
+                raise EwLimitError(f"more than {self.max_inputs} distinct input views")
             self.inputs.append(key)
         return self.dag.add("load", self.inputs.index(key))
 
@@ -178,6 +191,14 @@ class _Builder:
         raise EwCompileError(f"{k} is not element-wise")
 
 
+def fits_interpreter(prog: EwProgram) -> bool:
+    """True when the program runs on the interpreter kernel too (every mode); else it needs
+    the native form (capi.hip fits_interpreter)."""
+    regs = [d for op, d, *_ in prog.code if op != OP["store"]]
+    return (len(prog.code) <= MAX_CODE and len(prog.inputs) <= MAX_INPUTS and len(prog.outputs) <= MAX_OUTPUTS
+            and (max(regs) if regs else 0) < MAX_REGS)
+
+
 def _schedule(dag: _Dag, roots: Sequence[int]) -> List[int]:
     """Post-order over the DAG, children needing more registers first (Sethi-Ullman)."""
     need: Dict[int, int] = {}
@@ -210,16 +231,22 @@ def _schedule(dag: _Dag, roots: Sequence[int]) -> List[int]:
 
 def compile_elementwise(out_trees: Sequence[Tuple[str, Any]], shape: Tuple[int, ...],
                         decl: Mapping[str, Tuple[int, ...]],
-                        units: Optional[Mapping[str, Tuple[int, ...]]] = None) -> EwProgram:
+                        units: Optional[Mapping[str, Tuple[int, ...]]] = None, native: bool = False) -> EwProgram:
     """``out_trees``: (output name, expression tree at the iteration rank), in output order;
     ``shape``: the iteration shape; ``decl``: resolved shape of every input tensor;
     ``units``: per input, the declared size-1 axes the expression trees broadcast along
-    (``patterns.Val.unit``)."""
+    (``patterns.Val.unit``).  ``native``: compile for the native form's limits instead of
+    the interpreter kernel's (the program then runs only as native code)."""
+    max_code, max_regs, max_inputs, max_outputs = ((NATIVE_MAX_CODE, NATIVE_MAX_REGS, NATIVE_MAX_INPUTS,
+                                                    NATIVE_MAX_OUTPUTS) if native
+                                                   else (MAX_CODE, MAX_REGS, MAX_INPUTS, MAX_OUTPUTS))
     if len(shape) > MAX_RANK:
         raise EwCompileError(f"rank {len(shape)} exceeds {MAX_RANK}")
-    if not 1 <= len(out_trees) <= MAX_OUTPUTS:
-        raise EwCompileError(f"need 1..{MAX_OUTPUTS} outputs")
-    b = _Builder(tuple(int(d) for d in shape), decl, units or {})
+    if not out_trees:
+        raise EwCompileError("need at least one output")
+    if len(out_trees) > max_outputs:
+        raise EwLimitError(f"{len(out_trees)} outputs exceed {max_outputs}")
+    b = _Builder(tuple(int(d) for d in shape), decl, units or {}, max_inputs)
     ident = tuple(range(len(shape)))
     roots = [b.node(t, ident) for _, t in out_trees]
     order = _schedule(b.dag, roots)
@@ -232,7 +259,7 @@ def compile_elementwise(out_trees: Sequence[Tuple[str, Any]], shape: Tuple[int, 
         stores.setdefault(r, []).append(k)
         uses[r] = uses.get(r, 0) + 1
     reg_of: Dict[int, int] = {}
-    free = list(range(MAX_REGS - 1, -1, -1))
+    free = list(range(max_regs - 1, -1, -1))
     code: List[Tuple[int, int, int, int, int, float]] = []
     for n in order:
         kind, payload, kids = b.dag.nodes[n]
@@ -242,7 +269,7 @@ def compile_elementwise(out_trees: Sequence[Tuple[str, Any]], shape: Tuple[int, 
             if uses[c] == 0:
                 free.append(reg_of[c])
         if not free:
-            raise EwCompileError(f"chain needs more than {MAX_REGS} live values")
+            raise EwLimitError(f"chain needs more than {max_regs} live values")
         d = free.pop()
         reg_of[n] = d
         a, bb, c = (src + [0, 0, 0])[:3]
@@ -259,10 +286,11 @@ def compile_elementwise(out_trees: Sequence[Tuple[str, Any]], shape: Tuple[int, 
             uses[n] -= 1
             if uses[n] == 0:
                 free.append(d)
-    if len(code) > MAX_CODE:
-        raise EwCompileError(f"program of {len(code)} instructions exceeds {MAX_CODE}")
+    if len(code) > max_code:
+        raise EwLimitError(f"program of {len(code)} instructions exceeds {max_code}")
     return EwProgram(tuple(code), tuple(b.inputs), tuple(n for n, _ in out_trees), tuple(int(d) for d in shape))
 
 
-__all__ = ["EwProgram", "EwCompileError", "compile_elementwise", "OP", "DTYPE_CODE",
-           "MAX_CODE", "MAX_REGS", "MAX_INPUTS", "MAX_OUTPUTS", "MAX_RANK"]
+__all__ = ["EwProgram", "EwCompileError", "EwLimitError", "compile_elementwise", "OP", "DTYPE_CODE",
+           "MAX_CODE", "MAX_REGS", "MAX_INPUTS", "MAX_OUTPUTS", "MAX_RANK", "NATIVE_MAX_CODE", "NATIVE_MAX_REGS",
+           "NATIVE_MAX_INPUTS", "NATIVE_MAX_OUTPUTS", "fits_interpreter"]

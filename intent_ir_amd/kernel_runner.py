@@ -5,6 +5,8 @@
     python -m intent_ir_amd.kernel_runner --ew-chain all --launches 20
     python -m intent_ir_amd.kernel_runner --row-reduce sum --bindings M=64,N=1048576 --launches 20
     python -m intent_ir_amd.kernel_runner --gather --bindings M=8192,N=8192,L=16777216 --launches 20
+    python -m intent_ir_amd.kernel_runner --f32 matmul --launches 10        # 8192^3 on the fp32 matrix cores
+    python -m intent_ir_amd.kernel_runner --f32 layernorm --launches 20     # [8192, 4096] f32
 
 ``--ew-chain`` runs generic element-wise programs (ihip_elementwise_program, native code)
 on 8192 x 8192 operands and prints each chain's rate: per launch, every input's bytes
@@ -171,6 +173,63 @@ def run_row_reduce(kind, bindings, launches, torch) -> int:
     return 0
 
 
+def run_f32(family, bindings, launches, torch) -> int:
+    """The reference's own f32 IR of a family (matmul_bias_relu2d, pipeline/tilelang/core.py:886-910,
+    on ihip_gemm_f32_bias_relu; layer_norm_persistent, :1322-1384, on ihip_layernorm_rows_f32),
+    timed as the other legs: median of 5 rounds of ``launches`` launches (HIP events), the
+    LayerNorm's buffer sets rotated over >= 640 MiB.  Prints TFLOP/s against the 157.3 TFLOP/s
+    dense fp32 matrix peak (2*M*N*K flops) or TB/s against 8 TB/s (x and y 4 bytes per element,
+    w and b 4 bytes per column, mean and rstd 4 bytes per row)."""
+    import statistics  # noqa: PLC0415
+
+    from . import lower_intent_to_hip_kernel  # noqa: PLC0415
+    from .configs import layer_norm_persistent_ir, matmul_bias_relu2d_ir  # noqa: PLC0415
+    from .runtime import launch_lowered  # noqa: PLC0415
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(17)
+    if family == "matmul":
+        b = {"M": 8192, "N": 8192, "K": 8192, **bindings}
+        M, N, K = b["M"], b["N"], b["K"]
+        ir = matmul_bias_relu2d_ir("f32")
+        work, unit, peak = 2 * M * N * K, "TFLOP/s", 157.3e12
+        nsets = 1
+        mk = lambda: {"A": torch.randn((M, K), generator=g, device="cuda") / math.sqrt(K),  # noqa: E731
+                      "B": torch.randn((K, N), generator=g, device="cuda"),
+                      "bias": torch.randn((N,), generator=g, device="cuda") * 0.1,
+                      "C": torch.empty((M, N), device="cuda")}
+    else:
+        b = {"M": 8192, "N": 4096, **bindings}
+        M, N = b["M"], b["N"]
+        ir = layer_norm_persistent_ir("f32")
+        work, unit, peak = 8 * M * N + 8 * N + 8 * M, "TB/s", 8e12
+        nsets = max(2, math.ceil(ROTATE_MIN_BYTES / work))
+        mk = lambda: {"in_ptr": torch.randn((M, N), generator=g, device="cuda"),  # noqa: E731
+                      "weight_ptr": 1 + 0.1 * torch.randn((N,), generator=g, device="cuda"),
+                      "bias_ptr": 0.1 * torch.randn((N,), generator=g, device="cuda"),
+                      "out_ptr": torch.empty((M, N), device="cuda"), "out_mean_ptr": torch.empty(M, device="cuda"),
+                      "out_rstd_ptr": torch.empty(M, device="cuda")}
+    k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    sets = [mk() for _ in range(nsets)]
+    for i in range(nsets):
+        launch_lowered(k, sets[i])
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(5):
+        t0.record()
+        for i in range(launches):
+            launch_lowered(k, sets[i % nsets])
+        t1.record()
+        torch.cuda.synchronize()
+        times.append(t0.elapsed_time(t1) / launches)
+    ms = statistics.median(times)
+    rate = work / (ms * 1e-3)
+    print(f"[runner] f32 {family} {b}: {k.kernel_id}, {ms * 1e3:.1f} us/launch, {rate / 1e12:.2f} {unit} "
+          f"({100 * rate / peak:.1f}% of peak)", flush=True)
+    return 0
+
+
 def run_gather(bindings, launches, torch) -> int:
     """gather(inp [M, N] f32, row [L] i32, col [L] i32) -> out [L] (ihip_gather2d_f32) with
     uniformly random in-range indices; algorithmic bytes 16 per element (two indices, one inp
@@ -218,6 +277,8 @@ def main(argv=None) -> int:
                     help="time a generic element-wise program chain (or all of them)")
     ap.add_argument("--row-reduce", choices=["sum", "max"], help="time a row reduction (f32 [M, N], --bindings)")
     ap.add_argument("--gather", action="store_true", help="time gather2d (inp f32 [M, N], L random index pairs)")
+    ap.add_argument("--f32", choices=["matmul", "layernorm"],
+                    help="time the reference's f32 IR of a family (default 8192^3 / [8192, 4096], --bindings)")
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--copy-mib", type=int, default=0)
     ap.add_argument("--bindings", default="", help="comma-separated SYMBOL=VALUE overrides, e.g. M=1000,N=4096")
@@ -226,8 +287,8 @@ def main(argv=None) -> int:
                     help="pass an empty workspace (a GEMM that would be packed runs the guarded kernel, a long-row "
                          "softmax the workgroup-per-row kernel)")
     args = ap.parse_args(argv)
-    if sum(x is not None for x in (args.config, args.ew_chain, args.row_reduce)) + args.gather != 1:
-        ap.error("give exactly one of --config, --ew-chain, --row-reduce and --gather")
+    if sum(x is not None for x in (args.config, args.ew_chain, args.row_reduce, args.f32)) + args.gather != 1:
+        ap.error("give exactly one of --config, --ew-chain, --row-reduce, --f32 and --gather")
     if args.transpose_b and args.config != "matmul":
         ap.error("--transpose-b applies to --config matmul only")
 
@@ -235,8 +296,10 @@ def main(argv=None) -> int:
 
     if args.ew_chain:
         return run_ew_chains(sorted(EW_CHAINS) if args.ew_chain == "all" else [args.ew_chain], args.launches, torch)
-    if args.row_reduce or args.gather:
+    if args.row_reduce or args.gather or args.f32:
         rb = {n: int(v) for n, _, v in (item.partition("=") for item in filter(None, args.bindings.split(",")))}
+        if args.f32:
+            return run_f32(args.f32, rb, args.launches, torch)
         if args.gather:
             return run_gather(rb, args.launches, torch)
         return run_row_reduce(args.row_reduce, rb, args.launches, torch)

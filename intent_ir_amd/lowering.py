@@ -35,7 +35,7 @@ from .ir import IntentFunction, ScheduleSketch, as_intent, resolve_shape
 from .macros import GELU_CUBIC, GELU_NEG_2_SQRT_2_OVER_PI, expand_macros
 from .opset import HIP_SUPPORTED_OPS
 from .ewprogram import BINARY as EW_BINARY, DTYPE_CODE as EW_DTYPE_CODE, UNARY as EW_UNARY
-from .ewprogram import EwCompileError, compile_elementwise
+from .ewprogram import EwCompileError, EwLimitError, compile_elementwise
 from .patterns import ExprBuilder, PatternError, close, unify
 
 
@@ -91,7 +91,7 @@ def _normalize_bindings(shape_bindings: Mapping[str, Any]) -> Dict[str, Any]:
 # Knobs carried in the bindings and the values each accepts (None: any 0/1 flag).
 KNOBS: Dict[str, Optional[Tuple[int, ...]]] = {
     "HIP_RESPECT_SCHEDULE": None,
-    "HIP_GEMM_TILE": (128, 256),
+    "HIP_GEMM_TILE": (64, 128, 256),
     "HIP_ROWS_PER_WG": (1, 2, 4),
     # 1: an element-wise chain that has a specialised kernel (bias + GELU + axpy) runs as a
     # generic element-wise program instead (the role of INTENTIR_CUDA_CODEGEN's choice of
@@ -140,16 +140,24 @@ class _Knobs:
                                        f"(choices: {[a for a in allowed[f] if a is not None]})")
         self.used |= set(allowed)
 
-    def gemm_tile(self) -> int:
-        """C tile extent the GEMM must use: 0 = the kernel's own choice, else 128 or 256."""
+    def gemm_tile(self, f32: bool = False) -> int:
+        """C tile extent the GEMM must use: 0 = the kernel's own choice, else 128 or 256 (bf16)
+        or 64 or 128 (f32)."""
         self.used.add("HIP_GEMM_TILE")
         knob = self.values.get("HIP_GEMM_TILE")
-        allowed: Dict[str, Tuple[Optional[int], ...]] = {"tile_k": (32,), "pipeline_depth": (4,), "vec_width": (8,)}
+        tiles = (64, 128) if f32 else (128, 256)
+        if knob is not None and knob not in tiles:
+            raise HipLoweringError(f"HIP_GEMM_TILE={knob} is not available for the {'f32' if f32 else 'bf16'} GEMM "
+                                   f"(choices: {list(tiles)})")
+        allowed: Dict[str, Tuple[Optional[int], ...]] = (
+            {"tile_k": (32,), "pipeline_depth": (2,), "vec_width": (4,)} if f32
+            else {"tile_k": (32,), "pipeline_depth": (4,), "vec_width": (8,)})
         if knob is None:
-            allowed.update(tile_m=(128, 256), tile_n=(128, 256))
+            allowed.update(tile_m=tiles, tile_n=tiles)
         else:  # the binding knob overrides the schedule's tile (as SOFTMAX_THREADS does in the reference)
             self.used |= {"tile_m", "tile_n"}
-        self._fields(allowed, "the GEMM (K slices of 32, 16-byte copies)")
+        self._fields(allowed, "the f32 GEMM (k steps of 32, double-buffered, 16-byte copies)" if f32
+                     else "the GEMM (K slices of 32, 16-byte copies)")
         if knob is not None:
             return knob
         tm, tn = self.sched.get("tile_m"), self.sched.get("tile_n")
@@ -233,9 +241,10 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
         return None
     ta, tb = bool(env["ta"]), bool(env["tb"])
     a, b = env["A"][1], env["B"][1]
-    for n in (a, b, oname):
-        if c.dtype(n) != "bf16":
-            raise HipLoweringError(f"HIP GEMM takes bf16 A, B and C; {n} is {c.dtype(n)}")
+    dts = {c.dtype(n) for n in (a, b, oname)}
+    if dts not in ({"bf16"}, {"f32"}):
+        raise HipLoweringError(f"HIP GEMM takes A, B and C all bf16 or all f32; got A {c.dtype(a)}, "
+                               f"B {c.dtype(b)}, C {c.dtype(oname)}")
     sa, sb, so = c.shape(a), c.shape(b), c.shape(oname)
     if len(sa) != 2 or len(sb) != 2:
         raise HipLoweringError(f"HIP GEMM takes rank-2 operands: A{sa} B{sb}")
@@ -247,6 +256,8 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
         bn = env["bias"][1]
         if c.dtype(bn) != "f32" or c.shape(bn) != (N,):
             raise HipLoweringError(f"GEMM bias must be f32 [{N}]")
+    if dts == {"f32"}:
+        return _gemm_f32(c, a, b, env["bias"][1] if has_bias else None, oname, M, N, K, ta, tb, relu, names)
     tile = c.knobs.gemm_tile()
     args = [("tensor", a), ("tensor", b), ("tensor", env["bias"][1]) if has_bias else ("null", None),
             ("tensor", oname), ("i64", M), ("i64", N), ("i64", K)]
@@ -283,6 +294,26 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     kid = ("ihip_gemm_bf16_bias_relu_ex" if tile else "ihip_gemm_bf16_bias_relu_t" if (ta or tb)
            else "ihip_gemm_bf16_bias_relu")
     return HipLoweredKernel(c.fn.name, kid, c.io(names), launch, [oname], dict(c.b), tuple(args))
+
+
+def gemm_f32_tile_extent(M: int, N: int) -> int:
+    """gemm_f32.hip gemm_f32_tile_extent: 128x128 tiles, 64x64 when fewer than 256 tiles of
+    128x128 (the CU count) would run."""
+    return 64 if _cdiv(M, 128) * _cdiv(N, 128) < 256 else 128
+
+
+def _gemm_f32(c: "_Ctx", a: str, b: str, bias: Optional[str], oname: str, M: int, N: int, K: int, ta: bool,
+              tb: bool, relu: bool, names: List[str]) -> HipLoweredKernel:
+    """The reference's own matmul IR (f32 A, B, C: intentir_to_cuda.py:537-985, with the bias +
+    ReLU epilogue of pipeline/tilelang/core.py:886-910) on the fp32 matrix cores."""
+    tile = c.knobs.gemm_tile(f32=True)
+    t = tile or gemm_f32_tile_extent(M, N)
+    lds = {128: 71680, 64: 36864}[t]  # the [row][k] / [k][row] double buffers of gemm_f32.hip
+    launch = HipLaunch((max(1, _cdiv(M, t) * _cdiv(N, t)), 1, 1), (256, 1, 1), lds)
+    args = (("tensor", a), ("tensor", b), ("tensor", bias) if bias else ("null", None), ("tensor", oname),
+            ("i64", M), ("i64", N), ("i64", K), ("i32", int(ta)), ("i32", int(tb)), ("i32", int(relu)),
+            ("i32", tile))
+    return HipLoweredKernel(c.fn.name, "ihip_gemm_f32_bias_relu", c.io(names), launch, [oname], dict(c.b), args)
 
 
 def _gemm_fast_fits(M: int, N: int, K: int, ta: bool, tb: bool, packed: bool = False) -> bool:
@@ -447,27 +478,76 @@ def _softmax_templates(rank: int):
     return [("softmax", X, last), ("div", E, ("bcast", ("rsum", E, (last,)), lead, rank))]
 
 
+def _softmax_stat_templates(rank: int):
+    """The row statistics a softmax IR may also return (pipeline/cuda/core.py:453-493): the
+    row maximum and the sum of exp(x - max)."""
+    last = rank - 1
+    lead = tuple(range(last))
+    X = ("?in", "x")
+    E = ("exp", ("sub", X, ("bcast", ("rmax", X, (last,)), lead, rank)))
+    return (("max", ("rmax", X, (last,))), ("sum", ("rsum", E, (last,))))
+
+
 def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
-    if len(c.outs) != 1:
-        return None
-    (oname, ov), = c.outs.items()
-    if ov.rank < 1:
-        return None
-    env = None
-    for t in _softmax_templates(ov.rank):
-        env = unify(ov.tree, t, {})
-        if env is not None:
+    oname = env = None
+    for name, v in c.outs.items():
+        if v.rank < 1:
+            continue
+        for t in _softmax_templates(v.rank):
+            env = unify(v.tree, t, {})
+            if env is not None:
+                oname = name
+                break
+        if oname is not None:
             break
-    if env is None:
+    if oname is None:
         return None
+    ov = c.outs[oname]
+    stats: Dict[str, str] = {}  # "max" / "sum" -> output name
+    for name, v in c.outs.items():
+        if name == oname:
+            continue
+        for role, t in _softmax_stat_templates(ov.rank):
+            if role not in stats and unify(v.tree, t, dict(env)) is not None:
+                stats[role] = name
+                break
+        else:
+            return None  # an output that is neither the softmax nor one of its statistics
     x = env["x"][1]
-    if c.dtype(x) != "f32" or c.dtype(oname) != "f32":
-        raise HipLoweringError("HIP softmax takes f32 input and output")
+    if c.dtype(x) != "f32" or c.dtype(oname) != "f32" or any(c.dtype(n) != "f32" for n in stats.values()):
+        raise HipLoweringError("HIP softmax takes f32 input and outputs")
     M, N = c.rows(x)
+    if stats:
+        if N == 0:
+            raise HipLoweringError("softmax statistics of rows of length 0 (no maximum)")
+        segs, _ = softmax_split_plan(M, N)
+        st = lambda r: ("tensor", stats[r]) if r in stats else ("null", None)  # noqa: E731
+        args = (("tensor", x), ("tensor", oname), st("max"), st("sum"), ("i64", M), ("i64", N))
+        args += (("workspace", 8 * M * segs),) if segs else (("null", None), ("i64", 0))
+        launch = HipLaunch((M * segs, 1, 1), (256, 1, 1), 32) if segs else _softmax_launch(M, N, 0)
+        names = [x, oname] + [stats[r] for r in ("max", "sum") if r in stats]
+        return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32_stats", c.io(names), launch, list(c.fn.outputs),
+                                dict(c.b), args)
     rows = c.knobs.rows_per_wg()
     if rows > 1 and not (N % 4 == 0 and N <= 4096):
         raise HipLoweringError(f"{rows} rows per workgroup needs the one-wave-per-row softmax (N % 4 == 0, "
                                f"N <= 4096); N = {N} runs one row per workgroup")
+    launch = _softmax_launch(M, N, rows)
+    args = (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N))
+    if rows:
+        return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32_ex", c.io([x, oname]), launch, [oname], dict(c.b),
+                                args + (("i32", rows),))
+    segs, _ = softmax_split_plan(M, N)
+    if segs:  # rows longer than 65536 floats: S workgroups per row, two floats of partials each
+        launch = HipLaunch((M * segs, 1, 1), (256, 1, 1), 32)
+        return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32_ws", c.io([x, oname]), launch, [oname], dict(c.b),
+                                args + (("workspace", 8 * M * segs),))
+    return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b), args)
+
+
+def _softmax_launch(M: int, N: int, rows: int) -> HipLaunch:
+    """The unsplit launch rows.hip plans for 16-byte aligned x and y (rows: the rows-per-workgroup
+    knob, 0 = automatic)."""
     if 0 < N <= 128 and N % 4 == 0 and not rows:  # short rows: g lanes per row (one vector each)
         g = 1
         while g < N // 4:
@@ -492,17 +572,8 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
         kw = next(w for w in (1, 2, 4, 8, 16) if N <= 4096 * w)
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw if (kw > 1 or N > 1024) else 0)
     else:
-        launch = HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
-    args = (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N))
-    if rows:
-        return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32_ex", c.io([x, oname]), launch, [oname], dict(c.b),
-                                args + (("i32", rows),))
-    segs, _ = softmax_split_plan(M, N)
-    if segs:  # rows longer than 65536 floats: S workgroups per row, two floats of partials each
-        launch = HipLaunch((M * segs, 1, 1), (256, 1, 1), 32)
-        return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32_ws", c.io([x, oname]), launch, [oname], dict(c.b),
-                                args + (("workspace", 8 * M * segs),))
-    return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b), args)
+        launch = HipLaunch((max(1, M), 1, 1), (1024, 1, 1), 128)
+    return launch
 
 
 def softmax_split_plan(M: int, N: int) -> Tuple[int, int]:
@@ -564,25 +635,38 @@ def _match_gather(fn: IntentFunction, b: Dict[str, Any]) -> Optional[HipLoweredK
                              ("i64", N), ("i64", L), ("f32", other)))
 
 
-def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
+def _layernorm_templates():
+    """(mean, var) written as sum / N (div{divisor}) or as reduce_sum{scale: 1/N} (a sum times
+    a constant, interpreter.py:646-673), in the four combinations the reference builders use
+    (pipeline/tilelang/core.py:1322-1384 divides, pipeline/cuda/core.py:496-546 scales)."""
     X = ("?in", "x")
-    MEAN = ("div", ("rsum", X, (1,)), ("?c", "n1"))
-    D = ("sub", X, ("bcast", MEAN, (0,), 2))
-    VAR = ("div", ("rsum", ("mul", D, D), (1,)), ("?c", "n2"))
-    R = ("rsqrt", ("add", VAR, ("?c", "eps")))
-    Y = ("add", ("mul", ("mul", D, ("bcast", R, (0,), 2)), ("bcast", ("?in", "w"), (1,), 2)),
-         ("bcast", ("?in", "b"), (1,), 2))
-    roles: Dict[str, str] = {}
-    env: Dict[str, Any] = {}
-    for name, v in c.outs.items():
-        for role, t in (("y", Y), ("mean", MEAN), ("rstd", R)):
-            e = unify(v.tree, t, env)
-            if e is not None and role not in roles.values():
-                env, roles[name] = e, role
+    for mean_op in ("div", "mul"):
+        for var_op in ("div", "mul"):
+            MEAN = (mean_op, ("rsum", X, (1,)), ("?c", "n1"))
+            D = ("sub", X, ("bcast", MEAN, (0,), 2))
+            VAR = (var_op, ("rsum", ("mul", D, D), (1,)), ("?c", "n2"))
+            R = ("rsqrt", ("add", VAR, ("?c", "eps")))
+            Y = ("add", ("mul", ("mul", D, ("bcast", R, (0,), 2)), ("bcast", ("?in", "w"), (1,), 2)),
+                 ("bcast", ("?in", "b"), (1,), 2))
+            yield (mean_op, var_op), (("y", Y), ("mean", MEAN), ("rstd", R))
+
+
+def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
+    for forms, templates in _layernorm_templates():
+        roles: Dict[str, str] = {}
+        env: Dict[str, Any] = {}
+        for name, v in c.outs.items():
+            for role, t in templates:
+                e = unify(v.tree, t, env)
+                if e is not None and role not in roles.values():
+                    env, roles[name] = e, role
+                    break
+            else:
                 break
         else:
-            return None
-    if "y" not in roles.values():
+            if "y" in roles.values():
+                break
+    else:
         return None
     inv = {r: n for n, r in roles.items()}
     x, w, b = env["x"][1], env["w"][1], env["b"][1]
@@ -590,11 +674,14 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     M, N = c.rows(x)
     if c.fn.tensors[x].rank != 2:
         return None
-    if not (close(env["n1"][1], N) and close(env["n2"][1], N)):
-        raise HipLoweringError("LayerNorm chain divides by something other than the row length")
-    for n in (x, w, b, y):
-        if c.dtype(n) != "f16":
-            raise HipLoweringError(f"HIP LayerNorm takes f16 x, w, b, y; {n} is {c.dtype(n)}")
+    for key, op in zip(("n1", "n2"), forms):
+        if not (close(env[key][1], N) if op == "div" else close(env[key][1] * N, 1.0)):
+            raise HipLoweringError("LayerNorm chain takes its mean or variance over something other than the row "
+                                   f"length ({'divides by' if op == 'div' else 'scales by'} {env[key][1]}, N = {N})")
+    dt = {c.dtype(n) for n in (x, w, b, y)}
+    if dt not in ({"f16"}, {"f32"}):
+        raise HipLoweringError("HIP LayerNorm takes x, w, b, y all f16 or all f32; got "
+                               + ", ".join(f"{n} {c.dtype(n)}" for n in (x, w, b, y)))
     for n in (w, b):  # the kernel reads N elements of each; a [1] weight would broadcast in numpy
         if c.shape(n) != (N,):
             raise HipLoweringError(f"HIP LayerNorm takes w and b of shape [{N}]; {n} is {list(c.shape(n))}")
@@ -606,6 +693,9 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
     args = (("tensor", x), ("tensor", w), ("tensor", b), ("tensor", y), stat("mean"), stat("rstd"), ("i64", M),
             ("i64", N), ("f32", float(env["eps"][1])))
     names = [x, w, b, y] + [inv[r] for r in ("mean", "rstd") if r in inv]
+    if dt == {"f32"}:
+        return HipLoweredKernel(c.fn.name, "ihip_layernorm_rows_f32", c.io(names), _layernorm_f32_launch(M, N),
+                                list(c.fn.outputs), dict(c.b), args)
     if N % 8 == 0 and 0 < N <= 256:  # short rows: g lanes per row (one 16-byte vector each), 2 rows per group
         g = 1
         while g < N // 8:
@@ -636,6 +726,21 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
         launch = HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
     return HipLoweredKernel(c.fn.name, "ihip_layernorm_rows_f16", c.io(names), launch, list(c.fn.outputs),
                             dict(c.b), args)
+
+
+def _layernorm_f32_launch(M: int, N: int) -> HipLaunch:
+    """The launch ihip_layernorm_rows_f32 plans for 16-byte aligned tensors
+    (layernorm_f32.hip): N % 4 == 0 and N <= 4096: a wave per row, 16 rows per 1024-thread
+    workgroup, w and b staged in LDS; N % 4 == 0 and N <= 65536: 2-16 waves per row, one row
+    per workgroup; otherwise a 256-thread workgroup per row."""
+    n4 = N // 4
+    if N % 4 == 0 and 0 < N <= 4096:
+        kvpl = next(v for v in (1, 2, 4, 8, 16) if n4 <= 64 * v)
+        return HipLaunch((max(1, _cdiv(M, 16)), 1, 1), (1024, 1, 1), 2 * 16 * 64 * kvpl)
+    if N % 4 == 0 and 0 < N <= 65536:
+        kw = next(w for w in (2, 4, 8, 16) if n4 <= 1024 * w)
+        return HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
+    return HipLaunch((max(1, M), 1, 1), (256, 1, 1), 16)
 
 
 def _match_gelu_axpy(c: _Ctx) -> Optional[HipLoweredKernel]:
@@ -677,10 +782,15 @@ def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
     if len(c.outs) != 1:
         return None
     (oname, ov), = c.outs.items()
-    kind = ov.tree[0] if isinstance(ov.tree, tuple) else None
+    tree, scale = ov.tree, None
+    # reduce_sum{scale}: the sum times a constant (interpreter.py:487, :646-673)
+    env = unify(tree, ("mul", ("rsum", ("?", "x"), ("?", "ax")), ("?c", "s")), {})
+    if env is not None:
+        tree, scale = ("rsum", env["x"], env["ax"]), float(env["s"][1])
+    kind = tree[0] if isinstance(tree, tuple) else None
     if kind not in ("rsum", "rmax"):
         return None
-    env = unify(ov.tree, (kind, ("?in", "x"), ("?", "ax")), {})
+    env = unify(tree, (kind, ("?in", "x"), ("?", "ax")), {})
     if env is None:
         return None
     x = env["x"][1]
@@ -691,10 +801,15 @@ def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
     M, N = c.rows(x)
     args = (("tensor", x), ("tensor", oname), ("i64", M), ("i64", N), ("i32", 0 if kind == "rsum" else 1))
     segs = reduce_rows_segments(M, N)
+    kid = "ihip_reduce_rows_f32"
+    if scale is not None:  # out = sum * scale: the _ex entry, with the split workspace when the rule splits
+        kid = "ihip_reduce_rows_f32_ex"
+        args += (("f32", scale),) + ((("workspace", 4 * M * segs),) if segs > 1 else (("null", None), ("i64", 0)))
     if segs > 1:  # rows too few for the CUs: S workgroups of 16 waves per row, partials in a workspace
         launch = HipLaunch((M * segs, 1, 1), (1024, 1, 1), 64)
-        return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32_ws", c.io([x, oname]), launch, [oname], dict(c.b),
-                                args + (("workspace", 4 * M * segs),))
+        if scale is None:
+            kid, args = "ihip_reduce_rows_f32_ws", args + (("workspace", 4 * M * segs),)
+        return HipLoweredKernel(c.fn.name, kid, c.io([x, oname]), launch, [oname], dict(c.b), args)
     if 0 < N and N // 4 <= 128:  # short rows: g lanes per row (two to four vectors each), several per wave
         g = 1
         while g < 32 and 2 * g < N // 4:
@@ -706,7 +821,7 @@ def _match_row_reduce(c: _Ctx) -> Optional[HipLoweredKernel]:
         launch = HipLaunch((max(1, M), 1, 1), (1024 if few_long else 64, 1, 1), 64 if few_long else 0)
     else:
         launch = _row_launch(M)
-    return HipLoweredKernel(c.fn.name, "ihip_reduce_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b), args)
+    return HipLoweredKernel(c.fn.name, kid, c.io([x, oname]), launch, [oname], dict(c.b), args)
 
 
 def reduce_rows_segments(M: int, N: int) -> int:
@@ -764,9 +879,13 @@ def _match_elementwise(c: _Ctx) -> Optional[HipLoweredKernel]:
     for n in names + outs:
         if c.dtype(n) not in EW_DTYPE_CODE:
             raise HipLoweringError(f"element-wise program does not take {c.dtype(n)} ({n})")
+    trees = [(o, c.outs[o].tree) for o in outs]
+    decl, units = {n: c.shape(n) for n in names}, {n: c.eb.get(n).unit for n in names}
     try:
-        prog = compile_elementwise([(o, c.outs[o].tree) for o in outs], shp, {n: c.shape(n) for n in names},
-                                   {n: c.eb.get(n).unit for n in names})
+        try:
+            prog = compile_elementwise(trees, shp, decl, units)
+        except EwLimitError:  # beyond the interpreter kernel: the native form's limits
+            prog = compile_elementwise(trees, shp, decl, units, native=True)
     except EwCompileError as e:
         raise HipLoweringError(f"element-wise chain of {c.fn.name}: {e}") from e
     used = []

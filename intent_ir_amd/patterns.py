@@ -26,7 +26,9 @@ kept unit dims (keepdims reductions, [M,1] tensors) broadcast along themselves.
 
 from __future__ import annotations
 
+import ast
 import math
+import operator
 from dataclasses import dataclass
 from typing import Any, Dict, List, Mapping, Optional, Sequence, Tuple
 
@@ -68,6 +70,49 @@ def _num(v: Any, bindings: Mapping[str, Any]) -> Optional[float]:
         except ValueError:
             return 1e-5 if v == "eps" else None
     return None
+
+
+_SCALE_BINOPS = {ast.Add: operator.add, ast.Sub: operator.sub, ast.Mult: operator.mul, ast.Div: operator.truediv,
+                 ast.Pow: operator.pow, ast.FloorDiv: operator.floordiv, ast.Mod: operator.mod}
+
+
+def reduce_scale_factor(scale: Any, bindings: Mapping[str, Any]) -> float:
+    """The factor of reduce_sum{scale} as the interpreter resolves it (verify/interpreter.py:646-673):
+    a number; a binding name; or an arithmetic expression over numbers and bindings (such as
+    "1.0/N"), with num_elements = group_size * HW when both are bound.  The interpreter hands
+    the expression to Python's eval; here it is parsed and only numbers, bound names, + - * /
+    // % ** and parentheses are accepted, so an unresolvable scale raises PatternError."""
+    if isinstance(scale, bool) or not isinstance(scale, (int, float, str)):
+        raise PatternError(f"unsupported reduce scale {scale!r}")
+    if not isinstance(scale, str):
+        return float(scale)
+    names = dict(bindings)
+    if "num_elements" not in names and isinstance(names.get("group_size"), int) and isinstance(names.get("HW"), int):
+        names["num_elements"] = names["group_size"] * names["HW"]
+    if scale in names:
+        return float(names[scale])
+
+    def ev(node: ast.AST) -> Any:
+        if isinstance(node, ast.Expression):
+            return ev(node.body)
+        if isinstance(node, ast.Constant) and isinstance(node.value, (int, float)) and not isinstance(node.value, bool):
+            return node.value
+        if isinstance(node, ast.Name) and isinstance(names.get(node.id), (int, float)):
+            return names[node.id]
+        if isinstance(node, ast.BinOp) and type(node.op) in _SCALE_BINOPS:
+            lhs, rhs = ev(node.left), ev(node.right)
+            if isinstance(node.op, ast.Pow) and abs(rhs) > 64:
+                raise PatternError(f"reduce scale {scale!r}: exponent {rhs} out of range")
+            return _SCALE_BINOPS[type(node.op)](lhs, rhs)
+        if isinstance(node, ast.UnaryOp) and isinstance(node.op, (ast.USub, ast.UAdd)):
+            v = ev(node.operand)
+            return -v if isinstance(node.op, ast.USub) else v
+        raise PatternError(f"unresolved reduce scale {scale!r}")
+
+    try:
+        return float(ev(ast.parse(scale.strip(), mode="eval")))
+    except (SyntaxError, ZeroDivisionError, OverflowError, ValueError) as e:
+        raise PatternError(f"unresolved reduce scale {scale!r}: {e}") from e
 
 
 class ExprBuilder:
@@ -240,9 +285,10 @@ class ExprBuilder:
             kind = {"reduce_sum": "rsum", "reduce_max": "rmax", "reduce_any": "rany"}[name]
             if name == "reduce_sum" and at.get("reduction_type") == "any":
                 kind = "rany"
-            if name == "reduce_sum" and at.get("scale") is not None:
-                raise PatternError("reduce_sum with scale is not lowered")
             tree = (kind, a.full(), axes)
+            if name == "reduce_sum" and kind == "rsum" and at.get("scale") is not None:
+                # the sum times the scale factor (interpreter.py:487, :646-673)
+                tree = ("mul", tree, ("const", reduce_scale_factor(at["scale"], self.b)))
             if at.get("keepdims"):
                 return Val(tree, a.rank, axes)
             return Val(tree, a.rank - len(axes))
@@ -335,4 +381,4 @@ def close(a: float, b: float, rel: float = 1e-6) -> bool:
     return math.isclose(float(a), float(b), rel_tol=rel, abs_tol=0.0)
 
 
-__all__ = ["ExprBuilder", "Val", "PatternError", "unify", "close", "COMMUTATIVE"]
+__all__ = ["ExprBuilder", "Val", "PatternError", "unify", "close", "COMMUTATIVE", "reduce_scale_factor"]

@@ -43,17 +43,21 @@ SIGNATURES: Dict[str, Tuple[Any, Tuple[Any, ...]]] = {
     "ihip_reduce_rows_f32": (_I32, (_P, _P, _I64, _I64, _I32, _P)),
     "ihip_reduce_rows_f32_workspace_size": (_I64, (_I64, _I64)),
     "ihip_reduce_rows_f32_ws": (_I32, (_P, _P, _I64, _I64, _I32, _P, _I64, _P)),
+    "ihip_reduce_rows_f32_ex": (_I32, (_P, _P, _I64, _I64, _I32, _F32, _P, _I64, _P)),
     "ihip_reduce_rows_f32_noalloc": (_I32, (_P, _P, _I64, _I64, _I32, _P)),
     "ihip_softmax_rows_f32": (_I32, (_P, _P, _I64, _I64, _P)),
     "ihip_softmax_rows_f32_ex": (_I32, (_P, _P, _I64, _I64, _I32, _P)),
     "ihip_softmax_rows_f32_workspace_size": (_I64, (_I64, _I64)),
     "ihip_softmax_rows_f32_ws": (_I32, (_P, _P, _I64, _I64, _P, _I64, _P)),
+    "ihip_softmax_rows_f32_stats": (_I32, (_P, _P, _P, _P, _I64, _I64, _P, _I64, _P)),
     "ihip_layernorm_rows_f16": (_I32, (_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _P)),
+    "ihip_layernorm_rows_f32": (_I32, (_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _P)),
     "ihip_bias_gelu_tanh_axpy_bf16": (_I32, (_P, _P, _P, _I64, _I64, _F32, _P)),
     "ihip_gather2d_f32": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _F32, _P)),
     "ihip_gemm_bf16_bias_relu": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _P)),
     "ihip_gemm_bf16_bias_relu_t": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _P)),
     "ihip_gemm_bf16_bias_relu_ex": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P)),
+    "ihip_gemm_f32_bias_relu": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P)),
     "ihip_gemm_workspace_size": (_I64, (_I64, _I64, _I64, _I32, _I32)),
     "ihip_gemm_bf16_bias_relu_ws": (_I32, (_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _I64, _P)),
     "ihip_gemm_splitk_workspace_size": (_I64, (_I64, _I64, _I64, _I32)),
@@ -119,7 +123,7 @@ def ew_program_args(prog, ptrs: Mapping[str, int], dtypes: Mapping[str, str]) ->
             (code, ins, outs, shape)]
 
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -166,7 +166,7 @@ static void program_checker() {
   } bad[] = {
       {{ins(99, 0, 0)}, "unknown opcode"},
       {{ins(IHIP_EW_LOAD, 0, 5), ins(IHIP_EW_STORE, 0, 0)}, "load of a missing input"},
-      {{ins(IHIP_EW_LOAD, 9, 0), ins(IHIP_EW_STORE, 0, 9)}, "register out of range"},
+      {{ins(IHIP_EW_LOAD, 255, 0), ins(IHIP_EW_STORE, 0, 255)}, "register out of range"},
       {{ins(IHIP_EW_ADD, 0, 1, 2), ins(IHIP_EW_STORE, 0, 0)}, "reads unwritten registers"},
       {{ins(IHIP_EW_LOAD, 0, 0)}, "output never stored"},
       {{ins(IHIP_EW_LOAD, 0, 0), ins(IHIP_EW_STORE, 0, 0), ins(IHIP_EW_STORE, 0, 0)}, "output stored twice"},
@@ -177,9 +177,16 @@ static void program_checker() {
   for (auto& b : bad)
     EXPECT(ihip_elementwise_program(b.code.data(), (int)b.code.size(), in, 2, out, 1, shape, 2, nullptr) ==
                IHIP_ERR_INVALID_ARG, "%s accepted", b.what);
-  std::vector<ihip_ew_instr> big(IHIP_EW_MAX_CODE + 1, ins(IHIP_EW_IMM, 0, 0));
+  std::vector<ihip_ew_instr> big(IHIP_EW_NATIVE_MAX_CODE + 1, ins(IHIP_EW_IMM, 0, 0));
   EXPECT(ihip_elementwise_program(big.data(), (int)big.size(), in, 2, out, 1, shape, 2, nullptr) ==
              IHIP_ERR_INVALID_ARG, "too many instructions");
+  {  // past the interpreter kernel's register file: refused in INTERP mode before any launch
+    const int prev = ihip_elementwise_mode(IHIP_EW_MODE_INTERP);
+    ihip_ew_instr wide[] = {ins(IHIP_EW_LOAD, 9, 0), ins(IHIP_EW_STORE, 0, 9)};
+    EXPECT(ihip_elementwise_program(wide, 2, in, 2, out, 1, shape, 2, nullptr) == IHIP_ERR_INVALID_ARG,
+           "register 9 accepted by the interpreter");
+    ihip_elementwise_mode(prev);
+  }
   ihip_ew_instr ok[] = {ins(IHIP_EW_LOAD, 0, 0), ins(IHIP_EW_STORE, 0, 0)};
   const int64_t shape5[5] = {1, 1, 1, 1, 1};
   EXPECT(ihip_elementwise_program(ok, 2, in, 2, out, 1, shape5, 5, nullptr) == IHIP_ERR_INVALID_ARG, "rank 5");
@@ -197,14 +204,17 @@ static void program_checker() {
                      IHIP_EW_CAST_F16, IHIP_EW_CAST_BF16, IHIP_EW_CAST_BOOL, IHIP_EW_CAST_I32, IHIP_EW_LOAD};
   int accepted = 0, sourced = 0;
   for (int t = 0; t < 20000; ++t) {
-    const int n = 2 + (int)(rnd() % (IHIP_EW_MAX_CODE - 2));
+    // every fourth program runs past the interpreter limits (native form: more registers and
+    // instructions, so the generator's register array and fusion planner see larger programs)
+    const bool wide = t % 4 == 0;
+    const int n = 2 + (int)(rnd() % ((wide ? 3 * IHIP_EW_MAX_CODE : IHIP_EW_MAX_CODE) - 2));
     std::vector<ihip_ew_instr> code;
     std::vector<int> live = {0};  // registers that hold values
     const auto pick = [&]() { return live[rnd() % live.size()]; };
     code.push_back(ins(IHIP_EW_LOAD, 0, 0));
     for (int k = 1; k + 1 < n; ++k) {
       const int op = ops[rnd() % (sizeof(ops) / sizeof(ops[0]))];
-      const int dst = (int)(rnd() % IHIP_EW_MAX_REGS);
+      const int dst = (int)(rnd() % (wide ? 5 * IHIP_EW_MAX_REGS : IHIP_EW_MAX_REGS));
       ihip_ew_instr c = ins(op, dst, pick(), pick(), pick(), (rnd() % 4 == 0) ? 1.0f : (float)(int)(rnd() % 9) - 4.f);
       if (op == IHIP_EW_LOAD) c.a = (uint8_t)(rnd() % 2);
       if (op == IHIP_EW_IOTA) c.a = (uint8_t)(rnd() % 4);

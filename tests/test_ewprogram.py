@@ -20,6 +20,7 @@ from intent_ir_amd import HipLoweringError, lower_intent_to_hip_kernel
 from intent_ir_amd.dtypes import bf16_bits_to_f32, round_to_bf16, to_compute_f32, to_storage
 from intent_ir_amd.ewprogram import MAX_REGS, OP, EwCompileError, compile_elementwise
 from intent_ir_amd.ir import as_intent
+from intent_ir_amd.runtime import EW_MODE_INTERP, load_library
 from oracle.compare import compare_outputs
 from oracle.interpreter import execute_intent
 from tests.ew_cases import CASES, TOL
@@ -204,18 +205,35 @@ def _prog_call(lib, code, n_in=1, n_out=1, in_dt=0, out_dt=0, rank=2, shape=(4, 
     ([(OP["load"], 0, 1, 0, 0), (OP["store"], 0, 0, 0, 0)], {}, "loads input 1"),
     ([(OP["load"], 0, 0, 0, 0), (OP["store"], 0, 0, 0, 0), (OP["store"], 0, 0, 0, 0)], {}, "stored 2 times"),
     ([(OP["load"], 0, 0, 0, 0)], {}, "stored 0 times"),
-    ([(OP["load"], 9, 0, 0, 0), (OP["store"], 0, 9, 0, 0)], {}, "writes register 9"),
+    ([(OP["load"], 255, 0, 0, 0), (OP["store"], 0, 255, 0, 0)], {}, "writes register 255"),
     ([(OP["iota"], 0, 4, 0, 0), (OP["store"], 0, 0, 0, 0)], {}, "iota axis 4"),
     ([(OP["load"], 0, 0, 0, 0), (OP["store"], 0, 0, 0, 0)], {"in_dt": 7}, "unknown dtype 7"),
     ([(OP["load"], 0, 0, 0, 0), (OP["store"], 0, 0, 0, 0)], {"rank": 5, "shape": (1, 2, 3, 4, 5)}, "rank 5"),
     ([(OP["load"], 0, 0, 0, 0), (OP["store"], 0, 0, 0, 0)], {"shape": (-1, 8)}, "invalid shape"),
-    ([], {}, "need 1..64 instructions"),
+    ([], {}, "need 1..1024 instructions"),
 ])
 def test_c_abi_rejects_bad_programs(code, kw, msg):
     from intent_ir_amd.runtime import load_library
 
     st, err = _prog_call(load_library(), code, **kw)
     assert st == -1 and msg in err, err
+
+
+def test_programs_beyond_the_interpreter_limits_need_native_code():
+    """Register 9 (or more than 64 instructions, 8 inputs, 4 outputs) is past the interpreter
+    kernel's register file: in INTERP mode the call is refused before any launch, with the
+    reason; in AUTO / NATIVE mode such a program runs as native code (GPU tests)."""
+    lib = load_library()
+    prev = lib.ihip_elementwise_mode(EW_MODE_INTERP)
+    try:
+        st, msg = _prog_call(lib, [(OP["load"], 9, 0, 0, 0), (OP["store"], 0, 9, 0, 0)])
+        assert st == -1 and "exceed the interpreter kernel's limits" in msg
+        code = [(OP["load"], 0, 0, 0, 0)] + [(OP["add"], 0, 0, 0, 0)] * 70 + [(OP["store"], 0, 0, 0, 0)]
+        st, msg = _prog_call(lib, code)
+        assert st == -1 and "72 instructions" in msg
+    finally:
+        lib.ihip_elementwise_mode(prev)
+
 
 
 @pytest.mark.parametrize("name,ir,bindings,gen", CASES, ids=[c[0] for c in CASES])

@@ -32,8 +32,10 @@ def test_gemm_tile_binding_knob():
     assert k.launch.grid[0] == 16 and k.launch.lds_bytes == 163840
     k = lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 128})
     assert k.call_args[-1] == ("i32", 128) and k.launch.grid[0] == 64 and k.launch.lds_bytes == 81920
-    with pytest.raises(HipLoweringError, match="is not one of"):
+    with pytest.raises(HipLoweringError, match="not available for the bf16 GEMM"):
         lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 64})
+    with pytest.raises(HipLoweringError, match="is not one of"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={**GEMM_B, "HIP_GEMM_TILE": 32})
 
 
 def test_gemm_tile_from_an_authoritative_schedule():

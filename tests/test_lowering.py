@@ -196,9 +196,14 @@ def test_gemm_forms_and_errors():
     assert k.kernel_id == "ihip_gemm_bf16_bias_relu_t" and k.call_args[-3:] == (("i32", 0), ("i32", 1), ("i32", 1))
     with pytest.raises(HipLoweringError, match="transpose_b=True"):
         lower_intent_to_hip_kernel(ir, shape_bindings=b | {"N": 128})
-    f32 = matmul_bias_relu2d_ir("f32")
-    with pytest.raises(HipLoweringError, match="bf16"):
-        lower_intent_to_hip_kernel(f32, shape_bindings=b)
+    f32 = matmul_bias_relu2d_ir("f32")  # the reference builder's own dtype: the fp32-MFMA kernel
+    k = lower_intent_to_hip_kernel(f32, shape_bindings=b)
+    assert k.kernel_id == "ihip_gemm_f32_bias_relu" and k.call_args[-4:] == (("i32", 0), ("i32", 0), ("i32", 1),
+                                                                              ("i32", 0))
+    mixed = matmul_bias_relu2d_ir()
+    mixed["tensors"]["C"]["dtype"] = "f32"
+    with pytest.raises(HipLoweringError, match="all bf16 or all f32"):
+        lower_intent_to_hip_kernel(mixed, shape_bindings=b)
     # max(x, 0) is ReLU too
     ir = matmul_bias_relu2d_ir()
     ir["tensors"]["zero"] = {"dtype": "f32", "shape": []}
@@ -327,7 +332,7 @@ def test_library_exports_every_declared_symbol():
     for sym in _header_symbols():
         assert hasattr(lib, sym), sym
     lib.ihip_abi_version.restype = ctypes.c_int
-    assert lib.ihip_abi_version() == 2
+    assert lib.ihip_abi_version() == 3
     lib.ihip_last_error.restype = ctypes.c_char_p
     # the message is per thread and survives until the next call: other tests in this process
     # may have left one, and a successful call (an empty softmax needs no device) clears it
