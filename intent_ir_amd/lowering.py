@@ -281,7 +281,10 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     # be busy (gemm_fast_tile_extent)
     t = tile or _gemm_tile_extent(M, N)
     grid = (max(1, _cdiv(M, t) * _cdiv(N, t)) * S, 1, 1)  # a split: tiles x segments workgroups
-    if full or packed:
+    if full and S == 1 and t == 256 and _gemm_db64_fits(M, N, K, ta):
+        # whole 256x256 tiles, K in 64-k slices: gemm_db.hip (three A and two B slices of 32 KiB)
+        launch = HipLaunch(grid, (256, 1, 1), 163840)
+    elif full or packed:
         launch = HipLaunch(grid, (256, 1, 1), _gemm_fast_lds(t, ta2 if packed else ta))
     else:  # guarded kernel: the same tile choice, a double-buffered {A, Bt} tile pair of 64-k slices
         launch = HipLaunch(grid, (256, 1, 1), 147456 if t == 256 else 73728)
@@ -323,6 +326,12 @@ def _gemm_fast_fits(M: int, N: int, K: int, ta: bool, tb: bool, packed: bool = F
     ragged_k_ok = K % 32 == 0 or (M * K * 2 < (1 << 31) and K * N * 2 < (1 << 31))
     return (M > 0 and N > 0 and K > 0 and (N % 8 == 0 or tb) and K % 8 == 0 and (not ta or M % 8 == 0)
             and K * 512 < lim and N * 128 < lim and M * 128 < lim and ragged_k_ok)
+
+
+def _gemm_db64_fits(M: int, N: int, K: int, ta: bool) -> bool:
+    """gemm_db.hip gemm_db64_fits for 16-byte aligned tensors (C aligned too)."""
+    return (not ta and M > 0 and N > 0 and K >= 64 and M % 256 == 0 and N % 256 == 0 and K % 64 == 0
+            and K * 512 < (1 << 32) and N * 128 < (1 << 32))
 
 
 def _gemm_fast_lds(tile: int, ta: bool) -> int:
