@@ -7,6 +7,7 @@
     python -m intent_ir_amd.kernel_runner --gather --bindings M=8192,N=8192,L=16777216 --launches 20
     python -m intent_ir_amd.kernel_runner --f32 matmul --launches 10        # 8192^3 on the fp32 matrix cores
     python -m intent_ir_amd.kernel_runner --f32 layernorm --launches 20     # [8192, 4096] f32
+    python -m intent_ir_amd.kernel_runner --sweep softmax --launches 100    # fixed cost vs a copy
 
 ``--ew-chain`` runs generic element-wise programs (ihip_elementwise_program, native code)
 on 8192 x 8192 operands and prints each chain's rate: per launch, every input's bytes
@@ -230,6 +231,108 @@ def run_f32(family, bindings, launches, torch) -> int:
     return 0
 
 
+def _graph_time(launch, nsets, steps, torch) -> float:
+    """Median over 5 replays of a graph of `steps` launches (launch(i) uses buffer set i % nsets),
+    in ms per launch: the bench's timing, without launch gaps from the host."""
+    import statistics  # noqa: PLC0415
+
+    for i in range(max(nsets, 10)):
+        launch(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph.capture_begin()
+        for i in range(steps):
+            launch(i)
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(5):
+        t0.record()
+        graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        times.append(t0.elapsed_time(t1) / steps)
+    return statistics.median(times)
+
+
+def run_sweep(family, launches, torch) -> int:
+    """Fixed cost and asymptotic rate of the softmax kernel against a plain copy of the same
+    bytes.  For M = 2048 .. 65536 rows of 1024 f32 (read + write 8 KiB per row), both are timed
+    like bench.py (graph replays of `launches` launches, buffer sets rotated over >= 640 MiB,
+    median of 5) and each fitted as t = t0 + bytes / R by least squares: t0 is the per-launch
+    cost that does not scale with the data (ramp-up of the first loads, drain of the last
+    workgroups), R the streaming rate.  The copy is the identity element-wise program
+    (ihip_elementwise_program, native code: one 16-byte load and store per lane)."""
+    from . import lower_intent_to_hip_kernel  # noqa: PLC0415
+    from .configs import softmax_inner_ir  # noqa: PLC0415
+    from .runtime import ew_program_args, load_library  # noqa: PLC0415
+
+    if family != "softmax":
+        raise SystemExit(f"--sweep {family}: only softmax")
+    import ctypes  # noqa: PLC0415
+
+    lib = load_library()
+    copy_ir = {"name": "copy2d", "tensors": {"x": _t("f32", "M", "N"), "y": _t("f32", "M", "N")},
+               "ops": [_op("identity", ["x"], "y")], "outputs": ["y"]}
+    rows = (2048, 4096, 8192, 16384, 32768, 65536)
+    fits = {}
+    for name, ir, xn, yn in (("softmax", softmax_inner_ir(), "input_ptr", "output_ptr"), ("copy", copy_ir, "x", "y")):
+        pts = []
+        for M in rows:
+            b = {"M": M, "N": 1024}
+            k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+            byt = 2 * 4 * M * 1024
+            nsets = max(2, math.ceil(ROTATE_MIN_BYTES / byt))
+            g = torch.Generator(device="cuda")
+            g.manual_seed(M)
+            sets = [(torch.randn((M, 1024), generator=g, device="cuda") * 2, torch.empty((M, 1024), device="cuda"))
+                    for _ in range(nsets)]
+            fn = getattr(lib, k.kernel_id)
+            if k.kernel_id == "ihip_elementwise_program":
+                prog = k.call_args[0][1]
+                argv = []
+                for x, y in sets:
+                    a = ew_program_args(prog, {xn: x.data_ptr(), yn: y.data_ptr()}, {xn: "f32", yn: "f32"})
+                    argv.append(a)
+            else:
+                argv = [[ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()), ctypes.c_int64(M),
+                         ctypes.c_int64(1024)] for x, y in sets]
+
+            def launch(i, fn=fn, argv=argv):
+                a = argv[i % len(argv)]
+                st = fn(*a[:8] if len(a) == 9 else a, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                if st != 0:
+                    raise RuntimeError(lib.ihip_last_error().decode())
+
+            ms = _graph_time(launch, nsets, launches, torch)
+            pts.append((byt, ms * 1e-3))
+            print(f"[runner] sweep {name} M={M}: {ms * 1e3:.2f} us, {byt / (ms * 1e-3) / 1e12:.2f} TB/s "
+                  f"({100 * byt / (ms * 1e-3) / 8e12:.1f}% of 8 TB/s)", flush=True)
+            del sets
+            torch.cuda.empty_cache()
+        n = len(pts)
+        sx = sum(x for x, _ in pts)
+        sy = sum(y for _, y in pts)
+        sxx = sum(x * x for x, _ in pts)
+        sxy = sum(x * y for x, y in pts)
+        slope = (n * sxy - sx * sy) / (n * sxx - sx * sx)
+        t0 = (sy - slope * sx) / n
+        fits[name] = (t0, 1.0 / slope)
+        print(f"[runner] sweep {name}: fixed {t0 * 1e6:.2f} us per launch, streaming rate {1e-12 / slope:.2f} TB/s "
+              f"({100 / slope / 8e12:.1f}% of 8 TB/s)", flush=True)
+    (t0s, rs), (t0c, rc) = fits["softmax"], fits["copy"]
+    byt = 2 * 4 * 16384 * 1024
+    print(f"[runner] at [16384, 1024]: softmax {1e6 * (t0s + byt / rs):.2f} us, copy {1e6 * (t0c + byt / rc):.2f} us; "
+          f"without the fixed cost softmax would run at {100 * rs / 8e12:.1f}% of 8 TB/s", flush=True)
+    return 0
+
+
 def run_gather(bindings, launches, torch) -> int:
     """gather(inp [M, N] f32, row [L] i32, col [L] i32) -> out [L] (ihip_gather2d_f32) with
     uniformly random in-range indices; algorithmic bytes 16 per element (two indices, one inp
@@ -277,6 +380,8 @@ def main(argv=None) -> int:
                     help="time a generic element-wise program chain (or all of them)")
     ap.add_argument("--row-reduce", choices=["sum", "max"], help="time a row reduction (f32 [M, N], --bindings)")
     ap.add_argument("--gather", action="store_true", help="time gather2d (inp f32 [M, N], L random index pairs)")
+    ap.add_argument("--sweep", choices=["softmax"],
+                    help="fixed cost and streaming rate of the softmax kernel against a copy of the same bytes")
     ap.add_argument("--f32", choices=["matmul", "layernorm"],
                     help="time the reference's f32 IR of a family (default 8192^3 / [8192, 4096], --bindings)")
     ap.add_argument("--launches", type=int, default=20)
@@ -287,13 +392,15 @@ def main(argv=None) -> int:
                     help="pass an empty workspace (a GEMM that would be packed runs the guarded kernel, a long-row "
                          "softmax the workgroup-per-row kernel)")
     args = ap.parse_args(argv)
-    if sum(x is not None for x in (args.config, args.ew_chain, args.row_reduce, args.f32)) + args.gather != 1:
-        ap.error("give exactly one of --config, --ew-chain, --row-reduce, --f32 and --gather")
+    if sum(x is not None for x in (args.config, args.ew_chain, args.row_reduce, args.f32, args.sweep)) + args.gather != 1:
+        ap.error("give exactly one of --config, --ew-chain, --row-reduce, --f32, --sweep and --gather")
     if args.transpose_b and args.config != "matmul":
         ap.error("--transpose-b applies to --config matmul only")
 
     import torch
 
+    if args.sweep:
+        return run_sweep(args.sweep, args.launches, torch)
     if args.ew_chain:
         return run_ew_chains(sorted(EW_CHAINS) if args.ew_chain == "all" else [args.ew_chain], args.launches, torch)
     if args.row_reduce or args.gather or args.f32:

@@ -910,8 +910,8 @@ def _ew_launch(prog, dtype_of) -> HipLaunch:
     """The launch ihip_elementwise_program plans (ewjit.hip plan_jit) for dense 16-byte aligned
     outputs: lanes own 8 elements when every operand is 16-bit or narrower, else 4.  Inputs read
     across their unit-stride axis (axis 2 contiguous, axis 3 strided; up to 4) select the
-    LDS-tiled form: one workgroup per 64 x 64 tile, a 64 x 65 f32 tile each.  Otherwise a few
-    thousand 256-lane workgroups stride over rows and vectors."""
+    LDS-tiled form: one workgroup per 64 x 64 tile, a 64 x 65 f32 tile each.  Otherwise up to
+    16384 256-lane workgroups stride over groups of U rows and over vectors."""
     sh = [1] * (4 - len(prog.shape)) + [int(d) for d in prog.shape]
     narrow = all(dtype_of(n) in ("f16", "bf16", "bool", "i1", "u8") for n in [i for i, _ in prog.inputs] + list(prog.outputs))
     v = 8 if narrow else 4
@@ -925,7 +925,12 @@ def _ew_launch(prog, dtype_of) -> HipLaunch:
         return HipLaunch((max(1, min(tx, 65535)), max(1, min(ty, 65535)), 1), (256, 1, 1), tiled * 64 * 65 * 4)
     rows = sh[0] * sh[1] * sh[2]
     gx = max(1, min(1024, _cdiv(_cdiv(sh[3], v), 256)))
-    return HipLaunch((gx, max(1, min(rows, 65535, _cdiv(4096, gx))), 1), (256, 1, 1), 0)
+    # a lane takes U rows per trip, U = 64 // (row-varying loads x elements per lane) in 1..4
+    # (ew_jit_rows_per_trip); inputs with zero stride or extent 1 on axes 0-2 do not count
+    rowinv = [all(st[d] == 0 or sh[d] == 1 for d in range(3)) for _, st in prog.inputs]
+    loads = sum(1 for ins in prog.code if ins[0] == 1 and not rowinv[ins[2]])
+    U = 4 if loads == 0 else max(1, min(4, 64 // (loads * v)))
+    return HipLaunch((gx, max(1, min(_cdiv(rows, U), 65535, _cdiv(16384, gx))), 1), (256, 1, 1), 0)
 
 
 def call_args_to_json(call_args) -> List[Dict[str, Any]]:

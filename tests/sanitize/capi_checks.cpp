@@ -278,7 +278,7 @@ static void source_generator() {
         EXPECT(ihip_elementwise_source(code.data(), (int)code.size(), in, 2, out, 1, shape, 2, small, 17, nullptr) ==
                    IHIP_OK && strlen(small) == 16, "source truncated");
         generated += len > 0;
-        fused += strstr(buf.data(), "ew_logistic_div_fast(x, u, bad)") != nullptr;
+        fused += strstr(buf.data(), "ew_logistic_div_fast(r[") != nullptr;
       }
   EXPECT(generated == 36 && fused == 36, "generated %d, fused %d of 36", generated, fused);
   const int in_dt[2] = {IHIP_DT_BF16, IHIP_DT_BF16}, out_dt[1] = {IHIP_DT_BF16};

@@ -8,14 +8,16 @@ whether the fusion fired and that the result still compiles."""
 from __future__ import annotations
 
 import copy
+import re
 
+import numpy as np
 import pytest
 
 from intent_ir_amd import lower_intent_to_hip_kernel
 from intent_ir_amd.runtime import elementwise_source, ew_program_args, load_library
 from tests.ew_cases import CASES, T, op
 
-FUSED = "ew_logistic_div_fast(x, u, bad)"
+FUSED = "ew_logistic_div_fast(r["  # a fused step (the prelude defines the function)
 
 
 def _source(ir, bindings):
@@ -42,6 +44,28 @@ def test_logistic_shapes_are_fused(name):
     src = _source(ir, b)
     assert src.count(FUSED) == 1
     assert "ew_exp(x)" not in src.split("ihip_ew_jit")[-1]  # the exp is not emitted on its own
+
+
+def _bits(v: float) -> str:
+    return f"__builtin_bit_cast(float, {int(np.float32(v).view(np.uint32))}u)"
+
+
+def test_constant_multiplies_fold_into_the_exponent():
+    """u = x * k feeds the fused step as t = x * (k log2 e); GELU-tanh's
+    u = (z + 0.044715 z^3) * k as t = z * fma(z * z, 0.044715 k log2 e, k log2 e), each
+    constant rounded once from the double product of the program's f32 constants."""
+    log2e = 1.4426950408889634
+    ir, b = _case("logistic_special")
+    src = _source(ir, b)
+    assert re.search(r"ew_logistic_div_fast\(r\[\d+\]\[j\], s\d+_\d+\[j\] \* " + re.escape(_bits(float(np.float32(-1.7)) * log2e)), src)
+    ir, b = _case("gelu_f32_chain")
+    src = _source(ir, b)
+    k = -2.0 * np.sqrt(2.0 / np.pi)  # the macro's exp(-2 sqrt(2/pi) w) form
+    fold = re.search(r"s(\d+)_(\d+)\[j\] \* __builtin_fmaf\(s\1_\2\[j\] \* s\1_\2\[j\], "
+                     r"__builtin_bit_cast\(float, (\d+)u\), __builtin_bit_cast\(float, (\d+)u\)\)", src)
+    assert fold, src
+    got = [np.uint32(int(g)).view(np.float32) for g in fold.groups()[2:]]
+    np.testing.assert_allclose(got, [0.044715 * k * log2e, k * log2e], rtol=2e-7)
 
 
 def test_exp_with_another_use_is_not_fused():

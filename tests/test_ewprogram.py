@@ -300,8 +300,8 @@ def test_c_abi_accepts_empty_iteration_space_without_a_device():
 @pytest.mark.parametrize("name,bindings,launch", [
     ("transpose_add", {"M": 8192, "N": 8192}, ((128, 128, 1), 16640)),          # LDS-tiled: 64 x 64 tiles
     ("transpose_batched_3d", {"A": 4, "M": 256, "N": 520}, ((4, 36, 1), 16640)),
-    ("half_inputs_bf16_out", {"M": 8192, "N": 8192}, ((4, 1024, 1), 0)),       # 16-bit operands: 8 per lane
-    ("add_bias_relu", {"M": 8192, "N": 8192}, ((8, 512, 1), 0)),               # f32: 4 per lane
+    ("half_inputs_bf16_out", {"M": 8192, "N": 8192}, ((4, 2048, 1), 0)),       # 16-bit operands: 8 per lane
+    ("add_bias_relu", {"M": 8192, "N": 8192}, ((8, 2048, 1), 0)),              # f32: 4 per lane, 4 rows a trip
 ])
 def test_launch_descriptor_follows_the_native_plan(name, bindings, launch):
     """The lowering's launch plan is the one ihip_elementwise_program uses for dense aligned operands."""
