@@ -15,7 +15,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libintentir_hip.so"
 SOURCES = ["capi.hip", "rows.hip", "elementwise.hip", "gather.hip", "gemm.hip", "gemm_fast.hip", "gemm_pack.hip",
-           "gemm_db.hip", "gemm_f32.hip", "layernorm_f32.hip", "ewprog.hip", "ewjit.hip"]
+           "gemm_m16.hip", "gemm_f32.hip", "layernorm_f32.hip", "ewprog.hip", "ewjit.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

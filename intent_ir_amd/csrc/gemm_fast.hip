@@ -926,9 +926,9 @@ int gemm_fast_tile_extent(int64_t M, int64_t N) {
   return (tiles256 <= kSmallGridTiles && !one_full_row) || (M <= kSkinnyRows && tiles256 > 256) ? 128 : 256;
 }
 
-bool gemm_db64_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, const void* A, const void* B, const void* C);
-hipError_t launch_gemm_db64(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
-                            int64_t K, bool transpose_b, int relu, hipStream_t s);
+bool gemm_m16_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, const void* A, const void* B, const void* C);
+hipError_t launch_gemm_m16(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
+                           int64_t K, bool transpose_b, int relu, hipStream_t s);
 
 template <int TILE, bool CU>
 static void launch_tiles(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
@@ -961,10 +961,10 @@ hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* b
                             int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s,
                             bool c_unaligned) {
   const bool small = (tile == 0 ? gemm_fast_tile_extent(M, N) : tile) == 128, cu = N % 8 != 0 || c_unaligned;
-  // whole 256x256 tiles and K in 64-k slices: the double-buffered 64-k kernel (gemm_db.hip),
-  // same MFMAs in the same k order, so the same results
-  if (!small && !cu && gemm_db64_fits(M, N, K, transpose_a, A, B, C))
-    return launch_gemm_db64(A, B, bias, C, M, N, K, transpose_b, relu, s);
+  // whole 256x256 tiles and K in 64-k slices: the 16x16x32 kernel (gemm_m16.hip), whose sums
+  // are bit-identical to this file's
+  if (!small && !cu && gemm_m16_fits(M, N, K, transpose_a, A, B, C))
+    return launch_gemm_m16(A, B, bias, C, M, N, K, transpose_b, relu, s);
   if (small && cu)
     launch_tiles<128, true>(A, B, bias, C, M, N, K, transpose_a, transpose_b, relu, s);
   else if (small)

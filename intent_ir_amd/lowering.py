@@ -281,8 +281,8 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     # be busy (gemm_fast_tile_extent)
     t = tile or _gemm_tile_extent(M, N)
     grid = (max(1, _cdiv(M, t) * _cdiv(N, t)) * S, 1, 1)  # a split: tiles x segments workgroups
-    if full and S == 1 and t == 256 and _gemm_db64_fits(M, N, K, ta):
-        # whole 256x256 tiles, K in 64-k slices: gemm_db.hip (three A and two B slices of 32 KiB)
+    if full and S == 1 and t == 256 and _gemm_m16_fits(M, N, K, ta):
+        # whole 256x256 tiles, K in 64-k slices: gemm_m16.hip (three A and two B slices of 32 KiB)
         launch = HipLaunch(grid, (256, 1, 1), 163840)
     elif full or packed:
         launch = HipLaunch(grid, (256, 1, 1), _gemm_fast_lds(t, ta2 if packed else ta))
@@ -328,8 +328,8 @@ def _gemm_fast_fits(M: int, N: int, K: int, ta: bool, tb: bool, packed: bool = F
             and K * 512 < lim and N * 128 < lim and M * 128 < lim and ragged_k_ok)
 
 
-def _gemm_db64_fits(M: int, N: int, K: int, ta: bool) -> bool:
-    """gemm_db.hip gemm_db64_fits for 16-byte aligned tensors (C aligned too)."""
+def _gemm_m16_fits(M: int, N: int, K: int, ta: bool) -> bool:
+    """gemm_m16.hip gemm_m16_fits for 16-byte aligned tensors (C aligned too)."""
     return (not ta and M > 0 and N > 0 and K >= 64 and M % 256 == 0 and N % 256 == 0 and K % 64 == 0
             and K * 512 < (1 << 32) and N * 128 < (1 << 32))
 

@@ -322,13 +322,14 @@ def test_elementwise_programs_past_the_interpreter_limits(hip, make, arg):
         hip.ihip_elementwise_mode(prev)
 
 
-# ------------------------------------------------------------------ bf16 GEMM: 64-k double-buffered kernel
+# ------------------------------------------------------------------ bf16 GEMM: 16x16x32 whole-tile kernel
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (256, 512, 128), (512, 768, 192), (1024, 1024, 1024),
                                    (2048, 1536, 4096), (256, 4096, 320)])
-def test_gemm_db64_matches_the_ring_kernel_bit_for_bit(hip, M, N, K):
-    """Whole 256x256 tiles with K % 64 == 0 run gemm_db.hip; a C base 2 bytes off a 16-byte
-    boundary (B given as [N, K]) sends the same product to gemm_fast.hip's ring kernel (2-byte
-    stores).  Both issue the same MFMAs in the same k order: identical bits (1, 2, 3 and more
+@pytest.mark.parametrize("relu", [1, 0])
+def test_gemm_m16_matches_the_ring_kernel_bit_for_bit(hip, M, N, K, relu):
+    """Whole 256x256 tiles with K % 64 == 0 run gemm_m16.hip (16x16x32 MFMAs); a C base 2 bytes
+    off a 16-byte boundary (B given as [N, K]) sends the same product to gemm_fast.hip's ring
+    kernel (32x32x16 MFMAs, 2-byte stores).  The sums are identical bits (1, 2, 3 and more
     64-k slices, so the prologue, the last two slices and the steady loop are all covered)."""
     torch = _torch()
     g = torch.Generator(device="cuda")
@@ -339,14 +340,14 @@ def test_gemm_db64_matches_the_ring_kernel_bit_for_bit(hip, M, N, K):
     c1 = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
     cbuf = torch.empty(M * N + 8, device="cuda", dtype=torch.bfloat16)
     c2 = cbuf[1:1 + M * N]
-    print(f"[case] gemm db64 vs ring M={M} N={N} K={K}", flush=True)
+    print(f"[case] gemm m16 vs ring M={M} N={N} K={K} relu={relu}", flush=True)
     for c in (c1, c2):
         _ok(hip, hip.ihip_gemm_bf16_bias_relu_t(P(a.data_ptr()), P(bt.data_ptr()), P(bias.data_ptr()),
-                                                P(c.data_ptr()), M, N, K, 0, 1, 1, _stream()))
+                                                P(c.data_ptr()), M, N, K, 0, 1, relu, _stream()))
     b = bt.t().contiguous()  # the same product with B as [K, N]: the K-major form of the kernel
     c3 = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
     _ok(hip, hip.ihip_gemm_bf16_bias_relu_t(P(a.data_ptr()), P(b.data_ptr()), P(bias.data_ptr()), P(c3.data_ptr()),
-                                            M, N, K, 0, 0, 1, _stream()))
+                                            M, N, K, 0, 0, relu, _stream()))
     torch.cuda.synchronize()
     assert torch.equal(c1.view(torch.int16), c2.view(torch.int16).reshape(M, N))
     assert torch.equal(c1.view(torch.int16), c3.view(torch.int16))
