@@ -207,7 +207,8 @@ int ihip_gemm_bf16_bias_relu_t(const uint16_t* A, const uint16_t* B, const float
  * tile_m / tile_n (backends/cuda/codegen/intentir_to_cuda.py:659-664, 2074-2097): tile = 0
  * chooses automatically (256x256 C tiles, 128x128 when at most 128 tiles of 256x256 would
  * run); 128 or 256 fixes the tile extent, of the tiled and of the guarded kernel alike.  Every
- * tile extent accumulates in the same order, so C does not depend on tile. */
+ * tile extent accumulates in the same order, so C does not depend on tile (the workspace
+ * entries below may split a 128 x 128 grid along K, which changes the f32 summation order). */
 int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                                 int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
                                 void* stream);
@@ -217,10 +218,11 @@ int ihip_gemm_bf16_bias_relu_ex(const uint16_t* A, const uint16_t* B, const floa
  *  - K-contiguous copies, K rounded up to 8, of the operands whose rows cannot start 16-byte
  *    aligned (K % 8 != 0, N % 8 != 0 with B given as [K, N], M % 8 != 0 with A given as
  *    [K, M]);
- *  - split-K partials, S x M x (N rounded up to 4) floats, when the output has fewer than 128
- *    tiles (256 x 256 tiles, or 128 x 128 tiles when at most 128 of 256 x 256 would be busy):
- *    S = min(256 / tiles, K8 / 512) segments of a whole number of 64-k steps, K8 = K rounded
- *    up to 8.
+ *  - split-K partials, S x M x (N rounded up to 4) floats, when the split rule cuts K into
+ *    S > 1 segments: only grids of 128 x 128 tiles (the automatic choice when at most 128
+ *    tiles of 256 x 256 would be busy) are split, into the S (segments of whole 64-k steps, at
+ *    least 512 k each, at most 512 workgroups) of least estimated time on K8 = K rounded up
+ *    to 8 (gemm_pack.hip split_plan).
  * Same shapes and layouts as the entries above (the reference allocates nothing for matmul:
  * its kernels take any shape in place, intentir_to_cuda.py:537-985). */
 int64_t ihip_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int transpose_a, int transpose_b);
@@ -235,7 +237,8 @@ int64_t ihip_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int transpose_
  *  - a grid of too few tiles (ihip_gemm_workspace_size) is split along K: each segment's
  *    f32 sums go to the workspace and a second kernel adds the segments in order, then bias
  *    and activation.  Deterministic; it differs from the unsplit result only by f32
- *    summation order.  Without room for the partials the launch is unsplit.
+ *    summation order.  Without room for the partials the launch is unsplit, and so is a
+ *    launch with tile = 256 (the rule splits 128 x 128 tiles only).
  * The workspace must stay untouched until the launch completes on the stream. */
 int ihip_gemm_bf16_bias_relu_ws(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M,
                                 int64_t N, int64_t K, int transpose_a, int transpose_b, int relu, int tile,
@@ -245,7 +248,8 @@ int ihip_gemm_bf16_bias_relu_ws(const uint16_t* A, const uint16_t* B, const floa
  * ihip_gemm_workspace_size; 1: none), for operands read in place. */
 int64_t ihip_gemm_splitk_workspace_size(int64_t M, int64_t N, int64_t K, int splits);
 
-/* ihip_gemm_bf16_bias_relu_ex split into `splits` K segments (0: the split rule; 1: unsplit;
+/* ihip_gemm_bf16_bias_relu_ex split into `splits` K segments (0: the split rule, which leaves
+ * 256 x 256 tiles unsplit; 1: unsplit;
  * at most one per 64 k and at most 1024), for operands the tiled kernel reads in place (K % 8 == 0, M % 8 == 0
  * with A given as [K, M], N % 8 == 0 with B given as [K, N], A and B 16-byte aligned; any C
  * alignment), K > 0; IHIP_ERR_INVALID_ARG otherwise or when the workspace (256-byte aligned)

@@ -26,7 +26,7 @@
 // loads (global_load_lds_dwordx4: lane l of a wave writes 16 bytes at m0 + 16 l), so bank
 // conflicts are avoided by choosing which global chunk a lane fetches (XOR swizzles over the
 // 64 banks): a 128-byte row r holds logical 16-byte chunk c in slot c ^ ((r / 2) % 8); a 512-byte
-// k-row holds logical n-chunk c in slot c ^ 2 (k & 3) ^ 8 ((c / 2) & 1).
+// k-row holds logical n-chunk c in slot c ^ 2 (k & 3) ^ 8 ((c / 2) & 1) ^ 8 ((k / 8) & 1).
 // Fragments of 16x16x32: lane l holds row (or column) l & 15 and k 8 (l >> 4) .. +7 of a 32-k
 // step; A (and a K-contiguous B) with ds_read_b128, a K-major B with two ds_read_b64_tr_b16 per
 // block (each 16-lane group reads a 4 k x 16 n block; lane i receives column i).
@@ -65,9 +65,14 @@ constexpr int kLdsBytes = kTile * kCPitch + kTile * 4 > kRing ? kTile * kCPitch 
 static_assert(kLdsBytes <= 160 * 1024, "LDS");
 
 __device__ __forceinline__ int row_slot(int c, int r) { return c ^ ((r >> 1) & 7); }
-__device__ __forceinline__ int kmaj_slot(int c, int k) { return c ^ ((k & 3) << 1) ^ (((c >> 1) & 1) << 3); }
+// K-major slot: bit 3 also follows bit 3 of k, so that the two 16-lane groups one tr read
+// serves together (k rows 8 apart, same columns) land on different halves of the banks.
+__device__ __forceinline__ int kmaj_slot(int c, int k) {
+  return c ^ ((k & 3) << 1) ^ (((c >> 1) & 1) << 3) ^ (((k >> 3) & 1) << 3);
+}
+// Inverse of kmaj_slot in c for a fixed k.
 __device__ __forceinline__ int kmaj_logical(int p, int k) {
-  const int x = p ^ ((k & 3) << 1);
+  const int x = p ^ ((k & 3) << 1) ^ (((k >> 3) & 1) << 3);
   return x ^ (((x >> 1) & 1) << 3);
 }
 

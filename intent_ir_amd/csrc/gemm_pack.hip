@@ -81,17 +81,18 @@ struct SplitPlan {
 };
 
 // splits: 0 = by the rule above, else the number asked for (at most one per 64 k, and at
-// most kSplitMax).
+// most kSplitMax).  tile: the C tile the launch uses (0: gemm_fast_tile_extent's choice); the
+// rule splits grids of 128x128 tiles only.
 SplitPlan plan_of(int64_t K, int64_t S) {
   S = std::max<int64_t>(1, std::min<int64_t>({S, (K + 63) / 64, kSplitMax}));
   const int64_t kseg = ((K + S - 1) / S + 63) / 64 * 64;
   return {static_cast<int>((K + kseg - 1) / kseg), kseg};
 }
 
-SplitPlan split_plan(int64_t M, int64_t N, int64_t K, int splits) {
+SplitPlan split_plan(int64_t M, int64_t N, int64_t K, int splits, int tile) {
   if (K <= 0) return {1, K};
   if (splits > 0) return plan_of(K, splits);
-  if (gemm_fast_tile_extent(M, N) != 128) return {1, K};
+  if ((tile == 0 ? gemm_fast_tile_extent(M, N) : tile) != 128) return {1, K};
   const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
   const int64_t smax = std::max<int64_t>(1, std::min({K / kSplitMinK, kSplitMax, kSplitMaxGrid / tiles}));
   SplitPlan best = {1, K};
@@ -222,13 +223,13 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, bool ta, bool tb) 
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const int64_t K8 = round8(K);
   return (shape_packs_a(M, K, ta) ? align_up(M * K8 * 2) : 0) + (shape_packs_b(N, K, tb) ? align_up(N * K8 * 2) : 0) +
-         split_bytes(M, N, split_plan(M, N, K8, 0).S);
+         split_bytes(M, N, split_plan(M, N, K8, 0, 0).S);
 }
 
 // Workspace bytes of a split into `splits` segments (0: by the split rule).
 int64_t gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return split_bytes(M, N, split_plan(M, N, K, splits).S);
+  return split_bytes(M, N, split_plan(M, N, K, splits, 0).S);
 }
 
 // The tiled kernel split into `splits` segments (1: unsplit; 0: by the split rule) on
@@ -240,7 +241,7 @@ hipError_t launch_gemm_split(const uint16_t* A, const uint16_t* B, const float* 
                              int64_t ws_bytes, hipStream_t s) {
   if (!gemm_fast_fits(M, N, K, ta, tb, A, B, A)) return hipErrorNotSupported;  // C checked below
   const bool c_unaligned = (reinterpret_cast<uintptr_t>(C) & 15) != 0;
-  const SplitPlan plan = split_plan(M, N, K, splits);
+  const SplitPlan plan = split_plan(M, N, K, splits, tile);
   if (plan.S > 1 && (ws == nullptr || (reinterpret_cast<uintptr_t>(ws) & (kWsAlign - 1)) != 0 ||
                      split_bytes(M, N, plan.S) > ws_bytes))
     return hipErrorNotSupported;
@@ -277,7 +278,7 @@ hipError_t launch_gemm_packed(const uint16_t* A, const uint16_t* B, const float*
   if (pa) e = pack(A, a_ws, M, K, ta, s);
   if (e == hipSuccess && pb) e = pack(B, b_ws, N, K, !tb, s);
   if (e != hipSuccess) return e;
-  return launch_tiled(A2, B2, bias, C, M, N, K8, ta2, tb2, relu, tile, c_unaligned, split_plan(M, N, K8, 0),
+  return launch_tiled(A2, B2, bias, C, M, N, K8, ta2, tb2, relu, tile, c_unaligned, split_plan(M, N, K8, 0, tile),
                       static_cast<char*>(ws) + a_bytes + b_bytes, ws_bytes - a_bytes - b_bytes, s);
 }
 

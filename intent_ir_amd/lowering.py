@@ -100,6 +100,49 @@ KNOBS: Dict[str, Optional[Tuple[int, ...]]] = {
 }
 _SCHED_FIELDS = ("tile_m", "tile_n", "tile_k", "vec_width", "pipeline_depth")
 
+# The reference CUDA backend's own binding knobs (backends/cuda/codegen/intentir_to_cuda.py:577,
+# 600-844,1012-1041,1175-1202,1357-1392; cpp_codegen/intentir_cuda_codegen.cpp:598,1764,4866)
+# and the value at which each requests nothing.  CUDA_RESPECT_SCHEDULE means what
+# HIP_RESPECT_SCHEDULE means; ALLOW_TF32 only permits reduced precision, which the exact f32
+# GEMM never uses; every other knob tunes a CUDA launch shape or code path that has no HIP
+# counterpart, so a value other than its no-request value raises HipLoweringError.
+REFERENCE_KNOBS: Dict[str, Any] = {
+    "CUDA_SPECIALIZE_DIMS": 0, "CUDA_AUTO_SPECIALIZE_DIMS": 0, "CUDA_MAX_SMEM_OPTIN": 0, "CUDA_DROPOUT_VEC4": 1,
+    "SOFTMAX_THREADS": 0, "SOFTMAX_MAX_EPT": 16, "SOFTMAX_USE_EXP2": 0,
+    "DROPOUT_THREADS": 0, "DROPOUT_EPT": 0,
+    "ROPE_HEADS_PER_BLOCK": 1, "ROPE_VEC": 4, "ROPE_THREADS": 0,
+    "WMMA_WARPS_M": 0, "WMMA_WARPS_N": 0, "WMMA_FRAG_M": 1, "WMMA_FRAG_N": 1, "WMMA_STAGE_K": 0,
+    "WMMA_CP_A_POLICY": "", "WMMA_CP_B_POLICY": "", "WMMA_USE_CP_ASYNC": -1, "WMMA_PIPE_STAGES": 0,
+    "WMMA_AS_PAD": 8, "WMMA_BS_PAD": 8, "WMMA_DISABLE_FASTPATH": 0, "WMMA_TINY_SEARCH": 1,
+}
+_HIP_ALTERNATIVE = {"SOFTMAX_THREADS": "; the HIP softmax runs a wave per row of up to 4096 floats "
+                                       "(HIP_ROWS_PER_WG chooses rows per workgroup)",
+                    "WMMA_": "; HIP_GEMM_TILE chooses the GEMM's C tile"}
+
+
+def _reference_knobs(raw: Mapping[str, Any], bindings: Dict[str, Any]) -> None:
+    """Honour or reject the reference's own knobs in ``raw`` (the caller's bindings), updating
+    the normalised ``bindings`` in place."""
+    if "CUDA_RESPECT_SCHEDULE" in raw:
+        v = bindings.pop("CUDA_RESPECT_SCHEDULE", raw["CUDA_RESPECT_SCHEDULE"])
+        if v not in (0, 1):
+            raise HipLoweringError(f"CUDA_RESPECT_SCHEDULE={v!r} is not one of (0, 1)")
+        if bindings.get("HIP_RESPECT_SCHEDULE", v) != v:
+            raise HipLoweringError("CUDA_RESPECT_SCHEDULE and HIP_RESPECT_SCHEDULE disagree")
+        bindings["HIP_RESPECT_SCHEDULE"] = v
+    if "ALLOW_TF32" in raw:
+        v = bindings.pop("ALLOW_TF32", raw["ALLOW_TF32"])
+        if v not in (0, 1):
+            raise HipLoweringError(f"ALLOW_TF32={v!r} is not one of (0, 1)")
+    for k, idle in REFERENCE_KNOBS.items():
+        if k not in raw:
+            continue
+        v = bindings.pop(k, raw[k])  # the normalised value where there is one ("16" -> 16)
+        if v is None or v == idle or (isinstance(idle, str) and str(v).strip().lower() == idle):
+            continue
+        hint = _HIP_ALTERNATIVE.get(k) or next((h for p, h in _HIP_ALTERNATIVE.items() if k.startswith(p)), "")
+        raise HipLoweringError(f"{k}={v!r} tunes the reference CUDA backend and has no HIP counterpart{hint}")
+
 
 class _Knobs:
     """Launch-variant requests: binding knobs, and the schedule when it is authoritative.
@@ -275,7 +318,7 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     km_copy = (ta and not ta2) or (not tb and tb2)  # a transposing copy: (K8 / 64)-tile grid rows
     packed = (pack_ws > 0 and _gemm_fast_fits(M, N, K8, ta2, tb2, packed=True)
               and not (km_copy and _cdiv(K8, 64) > 65535))
-    S = gemm_split_plan(M, N, K8)[0] if (full or packed) else 1
+    S = gemm_split_plan(M, N, K8, tile=tile)[0] if (full or packed) else 1
     ws = pack_ws + _gemm_split_bytes(M, N, S) if (full or packed) else 0
     # 256x256 tiles, or 128x128 tiles when at most 128 tiles of 256x256 (half the CUs) would
     # be busy (gemm_fast_tile_extent)
@@ -389,18 +432,18 @@ def _split_plan_of(K: int, S: int) -> Tuple[int, int]:
     return _cdiv(K, kseg), kseg
 
 
-def gemm_split_plan(M: int, N: int, K: int, splits: int = 0) -> Tuple[int, int]:
+def gemm_split_plan(M: int, N: int, K: int, splits: int = 0, tile: int = 0) -> Tuple[int, int]:
     """(S, kseg) of gemm_pack.hip split_plan.  splits > 0: that many segments (at most one per
     64 k and at most 1024), each but the last of kseg k, a multiple of 64.  splits = 0: grids
-    of 256x256 tiles stay unsplit; for 128x128 tiles, the S (segments of at least 512 k, at
-    most 512 workgroups) of least estimated time: tile-steps over the measured rate at
-    tiles x S workgroups, plus the reduce launch and the partials' round trip; ties go to the
-    smaller S."""
+    of 256x256 tiles (``tile``, or the automatic choice when it is 0) stay unsplit; for
+    128x128 tiles, the S (segments of at least 512 k, at most 512 workgroups) of least
+    estimated time: tile-steps over the measured rate at tiles x S workgroups, plus the reduce
+    launch and the partials' round trip; ties go to the smaller S."""
     if K <= 0:
         return 1, K
     if splits > 0:
         return _split_plan_of(K, splits)
-    if _gemm_tile_extent(M, N) != 128:
+    if (tile or _gemm_tile_extent(M, N)) != 128:
         return 1, K
     tiles = _cdiv(M, 128) * _cdiv(N, 128)
     smax = max(1, min(K // 512, 1024, 512 // tiles))
@@ -981,6 +1024,7 @@ def lower_intent_to_hip_kernel(intent, *, shape_bindings: Mapping[str, Any],
     or a reference ``IntentFunction`` (anything with ``to_json_dict()``).  Raises
     ``HipLoweringError`` when no kernel family matches."""
     bindings = _normalize_bindings(shape_bindings)
+    _reference_knobs(shape_bindings, bindings)
     bindings.setdefault("HIP_RESPECT_SCHEDULE", 1 if schedule_override is not None else 0)
     fn = as_intent(intent)
     if schedule_override is not None:

@@ -723,7 +723,8 @@ def test_gemm_split_k(hip, M, N, K, splits, ta, tb):
     sums written to the workspace, then added in segment order with bias and ReLU.  Judged
     against the oracle, against the unsplit tiled kernel (equal up to f32 summation order),
     run to run (bit for bit), across the 128 and 256 tile knobs (bit for bit: the same
-    segments in the same MFMA order) and with a 2-byte aligned C (bit for bit)."""
+    segments in the same MFMA order; under the rule a forced 256x256 tile runs unsplit) and
+    with a 2-byte aligned C (bit for bit)."""
     w = WORKLOADS["matmul"]
     b = {"M": M, "N": N, "K": K}
     inp = w.gen(b, seed=M + 5 * N + 7 * K + splits, sigma=1.0)
@@ -742,6 +743,11 @@ def test_gemm_split_k(hip, M, N, K, splits, ta, tb):
     assert np.array_equal(split, _gemm_splitk(hip, A, B, inp["bias"], M, N, K, ta, tb, splits)), "run to run"
     for tile in (128, 256):
         other = _gemm_splitk(hip, A, B, inp["bias"], M, N, K, ta, tb, splits, tile=tile)
+        if splits == 0 and tile == 256 and gemm_split_plan(M, N, K, 0, tile=256)[0] == 1:
+            # the rule splits grids of 128x128 tiles only: 256x256 tiles on request run unsplit
+            other_ref = _gemm_splitk(hip, A, B, inp["bias"], M, N, K, ta, tb, 1, tile=256)
+            assert np.array_equal(other, other_ref), "tile 256 under the rule is the unsplit kernel"
+            continue
         assert np.array_equal(split, other), f"tile {tile}: {int((split != other).sum())} elements differ"
     assert np.array_equal(split, _gemm_splitk(hip, A, B, inp["bias"], M, N, K, ta, tb, splits, c_offset=1))
     if splits == 0:  # the workspace entry applies the same rule

@@ -175,3 +175,65 @@ def test_elementwise_program_knob():
     assert k.kernel_id == "ihip_elementwise_program"
     with pytest.raises(HipLoweringError, match="does not apply"):
         lower_intent_to_hip_kernel(WORKLOADS["softmax"].ir(), shape_bindings={**b, "HIP_ELEMENTWISE_PROGRAM": 1})
+
+
+def test_reference_cuda_knobs_are_honoured_or_rejected():
+    """The reference's own binding knobs (intentir_to_cuda.py:577,1012,1175-1190 and the WMMA
+    and launch knobs) either mean something here or raise: CUDA_RESPECT_SCHEDULE is
+    HIP_RESPECT_SCHEDULE, ALLOW_TF32 only permits reduced precision (never used), a knob at the
+    value where it requests nothing passes, any other request raises HipLoweringError."""
+    ir = WORKLOADS["softmax"].ir()
+    b = {"M": 64, "N": 1024}
+    ir_s = dict(ir, schedule={"tile_m": 2})
+    # CUDA_RESPECT_SCHEDULE=1 makes the IR's own schedule authoritative, as HIP_RESPECT_SCHEDULE=1 does
+    k_cuda = lower_intent_to_hip_kernel(ir_s, shape_bindings={**b, "CUDA_RESPECT_SCHEDULE": 1})
+    k_hip = lower_intent_to_hip_kernel(ir_s, shape_bindings={**b, "HIP_RESPECT_SCHEDULE": 1})
+    assert k_cuda.call_args == k_hip.call_args and k_cuda.bindings["HIP_RESPECT_SCHEDULE"] == 1
+    assert "CUDA_RESPECT_SCHEDULE" not in k_cuda.bindings
+    k0 = lower_intent_to_hip_kernel(ir_s, shape_bindings={**b, "CUDA_RESPECT_SCHEDULE": 0})
+    assert k0.call_args == lower_intent_to_hip_kernel(ir_s, shape_bindings=b).call_args
+    with pytest.raises(HipLoweringError, match="disagree"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={**b, "CUDA_RESPECT_SCHEDULE": 1, "HIP_RESPECT_SCHEDULE": 0})
+    with pytest.raises(HipLoweringError, match="is not one of"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={**b, "CUDA_RESPECT_SCHEDULE": 2})
+    # launch-shape knobs: the no-request value passes, a request raises and names the HIP knob
+    base = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    for idle in ({"SOFTMAX_THREADS": 0}, {"SOFTMAX_MAX_EPT": 16}, {"SOFTMAX_MAX_EPT": "16"}, {"WMMA_CP_A_POLICY": ""}):
+        k = lower_intent_to_hip_kernel(ir, shape_bindings={**b, **idle})
+        assert k.call_args == base.call_args and not set(idle) & set(k.bindings)
+    with pytest.raises(HipLoweringError, match="SOFTMAX_THREADS=128 .*HIP_ROWS_PER_WG"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={**b, "SOFTMAX_THREADS": 128})
+    with pytest.raises(HipLoweringError, match="SOFTMAX_MAX_EPT=8"):
+        lower_intent_to_hip_kernel(ir, shape_bindings={**b, "SOFTMAX_MAX_EPT": 8})
+    mm = WORKLOADS["matmul"].ir()
+    with pytest.raises(HipLoweringError, match="WMMA_WARPS_M=2 .*HIP_GEMM_TILE"):
+        lower_intent_to_hip_kernel(mm, shape_bindings={**GEMM_B, "WMMA_WARPS_M": 2})
+    with pytest.raises(HipLoweringError, match="WMMA_CP_A_POLICY='cg'"):
+        lower_intent_to_hip_kernel(mm, shape_bindings={**GEMM_B, "WMMA_CP_A_POLICY": "cg"})
+    # ALLOW_TF32 permits a reduced-precision path; the exact f32 GEMM honours both values
+    f32 = json.loads(json.dumps(mm))
+    for t in ("A", "B", "C"):
+        f32["tensors"][t]["dtype"] = "f32"
+    for v in (0, 1):
+        k = lower_intent_to_hip_kernel(f32, shape_bindings={**GEMM_B, "ALLOW_TF32": v})
+        assert k.kernel_id == "ihip_gemm_f32_bias_relu" and "ALLOW_TF32" not in k.bindings
+    with pytest.raises(HipLoweringError, match="ALLOW_TF32"):
+        lower_intent_to_hip_kernel(f32, shape_bindings={**GEMM_B, "ALLOW_TF32": 3})
+
+
+def test_gemm_split_rule_follows_the_forced_tile():
+    """gemm_pack.hip split_plan sizes its segments for 128x128 tiles; with 256x256 tiles on
+    request (the tile knob) the rule leaves the grid unsplit, and the lowering's workspace
+    holds no partials for it."""
+    from intent_ir_amd.lowering import gemm_split_plan
+
+    M, N, K = 1024, 1024, 8192  # 64 tiles of 128x128: the rule splits into 4
+    assert gemm_split_plan(M, N, K)[0] == 4 and gemm_split_plan(M, N, K, tile=128)[0] == 4
+    assert gemm_split_plan(M, N, K, tile=256) == (1, K)
+    assert gemm_split_plan(M, N, K, 3, tile=256)[0] == 3  # an explicit count is taken as asked
+    ir = WORKLOADS["matmul"].ir()
+    b = {"M": M, "N": N, "K": K}
+    auto = lower_intent_to_hip_kernel(ir, shape_bindings=b)
+    assert auto.kernel_id == "ihip_gemm_bf16_bias_relu_ws" and auto.launch.grid[0] == 64 * 4
+    big = lower_intent_to_hip_kernel(ir, shape_bindings={**b, "HIP_GEMM_TILE": 256})
+    assert big.kernel_id == "ihip_gemm_bf16_bias_relu_ex" and big.launch.grid[0] == 16
