@@ -11,8 +11,9 @@
 
 ``--ew-chain`` runs generic element-wise programs (ihip_elementwise_program, native code)
 on 8192 x 8192 operands and prints each chain's rate: per launch, every input's bytes
-read once and every output's written once, over the median of 5 timed rounds of
-``--launches`` launches (HIP events, after a compile-and-warm-up launch).  ``--row-reduce``
+read once and every output's written once, timed like bench.py (median of 5 graph replays
+of ``--launches`` launches after a compile-and-warm-up launch, buffer sets rotated over
+>= 640 MiB).  ``--row-reduce``
 times reduce_sum / reduce_max over the last axis of an f32 [M, N] tensor the same way
 (rotating buffer sets over > 640 MiB), default [64, 1048576]: few long rows, which the
 library splits over several workgroups per row with partial results in a workspace.
@@ -107,8 +108,6 @@ def _ew_inputs(k, torch, g):
 
 
 def run_ew_chains(names, launches, torch) -> int:
-    import statistics  # noqa: PLC0415
-
     from . import lower_intent_to_hip_kernel  # noqa: PLC0415
     from .runtime import launch_lowered  # noqa: PLC0415
 
@@ -119,22 +118,18 @@ def run_ew_chains(names, launches, torch) -> int:
         k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
         assert k.kernel_id == "ihip_elementwise_program", k.kernel_id
         bufs, nbytes = _ew_inputs(k, torch, g)
+        sets = [bufs] + [_ew_inputs(k, torch, g)[0] for _ in range(max(2, math.ceil(ROTATE_MIN_BYTES / nbytes)) - 1)]
         launch_lowered(k, bufs)  # compiles the native code, warms up
-        torch.cuda.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        times = []
-        for _ in range(5):
-            t0.record()
-            for _ in range(launches):
-                launch_lowered(k, bufs)
-            t1.record()
-            torch.cuda.synchronize()
-            times.append(t0.elapsed_time(t1) / launches)
-        ms = statistics.median(times)
+
+        def launch(i, k=k, sets=sets):
+            launch_lowered(k, sets[i % len(sets)])
+
+        ms = _graph_time(launch, len(sets), launches, torch)
         prog = k.call_args[0][1]
         print(f"[runner] ew {name}: {len(prog.code)} instructions, {nbytes / 2**20:.0f} MiB/launch, "
-              f"{ms * 1e3:.1f} us/launch, {nbytes / (ms * 1e-3) / 1e12:.2f} TB/s", flush=True)
-        del bufs
+              f"{len(sets)} buffer sets, {ms * 1e3:.1f} us/launch, {nbytes / (ms * 1e-3) / 1e12:.2f} TB/s "
+              f"({100 * nbytes / (ms * 1e-3) / 8e12:.1f}% of 8 TB/s)", flush=True)
+        del bufs, sets
         torch.cuda.empty_cache()
     return 0
 
@@ -177,12 +172,10 @@ def run_row_reduce(kind, bindings, launches, torch) -> int:
 def run_f32(family, bindings, launches, torch) -> int:
     """The reference's own f32 IR of a family (matmul_bias_relu2d, pipeline/tilelang/core.py:886-910,
     on ihip_gemm_f32_bias_relu; layer_norm_persistent, :1322-1384, on ihip_layernorm_rows_f32),
-    timed as the other legs: median of 5 rounds of ``launches`` launches (HIP events), the
-    LayerNorm's buffer sets rotated over >= 640 MiB.  Prints TFLOP/s against the 157.3 TFLOP/s
+    timed like bench.py (median of 5 graph replays of ``launches`` launches), the LayerNorm's
+    buffer sets rotated over >= 640 MiB.  Prints TFLOP/s against the 157.3 TFLOP/s
     dense fp32 matrix peak (2*M*N*K flops) or TB/s against 8 TB/s (x and y 4 bytes per element,
     w and b 4 bytes per column, mean and rstd 4 bytes per row)."""
-    import statistics  # noqa: PLC0415
-
     from . import lower_intent_to_hip_kernel  # noqa: PLC0415
     from .configs import layer_norm_persistent_ir, matmul_bias_relu2d_ir  # noqa: PLC0415
     from .runtime import launch_lowered  # noqa: PLC0415
@@ -212,19 +205,11 @@ def run_f32(family, bindings, launches, torch) -> int:
                       "out_rstd_ptr": torch.empty(M, device="cuda")}
     k = lower_intent_to_hip_kernel(ir, shape_bindings=b)
     sets = [mk() for _ in range(nsets)]
-    for i in range(nsets):
-        launch_lowered(k, sets[i])
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    times = []
-    for _ in range(5):
-        t0.record()
-        for i in range(launches):
-            launch_lowered(k, sets[i % nsets])
-        t1.record()
-        torch.cuda.synchronize()
-        times.append(t0.elapsed_time(t1) / launches)
-    ms = statistics.median(times)
+
+    def launch(i):
+        launch_lowered(k, sets[i % nsets])
+
+    ms = _graph_time(launch, nsets, launches, torch)
     rate = work / (ms * 1e-3)
     print(f"[runner] f32 {family} {b}: {k.kernel_id}, {ms * 1e3:.1f} us/launch, {rate / 1e12:.2f} {unit} "
           f"({100 * rate / peak:.1f}% of peak)", flush=True)
