@@ -8,6 +8,8 @@
     python -m intent_ir_amd.kernel_runner --f32 matmul --launches 10        # 8192^3 on the fp32 matrix cores
     python -m intent_ir_amd.kernel_runner --f32 layernorm --launches 20     # [8192, 4096] f32
     python -m intent_ir_amd.kernel_runner --sweep softmax --launches 100    # fixed cost vs a copy
+    python -m intent_ir_amd.kernel_runner --sweep gemm-tile --launches 10   # the GEMM tile rule
+    python -m intent_ir_amd.kernel_runner --sweep gemm-split --launches 10  # the split-K rule
 
 ``--ew-chain`` runs generic element-wise programs (ihip_elementwise_program, native code)
 on 8192 x 8192 operands and prints each chain's rate: per launch, every input's bytes
@@ -318,6 +320,104 @@ def run_sweep(family, launches, torch) -> int:
     return 0
 
 
+# Shapes behind the GEMM's shipped rules (M, N, K, B given as [N, K]).
+GEMM_TILE_SHAPES = [
+    (1000, 4096, 4096, False), (512, 8192, 8192, False), (2048, 2048, 8192, False), (1024, 1024, 8192, False),
+    (256, 4096, 4096, False), (4096, 2048, 8192, False), (2048, 3072, 4096, False), (1536, 2048, 4096, True),
+    (2304, 2816, 4096, True), (3072, 3072, 4096, False), (4096, 4096, 4096, True), (200, 32000, 4096, True),
+    (32, 128256, 4096, True), (128, 128256, 4096, True), (16, 50257, 4096, True),
+]
+GEMM_SPLIT_SHAPES = [
+    (1024, 1024, 8192, False), (512, 512, 16384, False), (768, 768, 16384, True), (256, 4096, 8192, False),
+    (2048, 1024, 8192, False), (1000, 1000, 3000, False), (1536, 1280, 4096, False), (1024, 1024, 2048, False),
+    (2048, 2048, 4096, False),
+]
+GEMM_SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
+
+
+def _gemm_operands(M, N, K, tb, torch, g):
+    a = (torch.randn((M, K), generator=g, device="cuda") / math.sqrt(K)).bfloat16()
+    b = torch.randn((N, K) if tb else (K, N), generator=g, device="cuda").bfloat16()
+    bias = torch.randn((N,), generator=g, device="cuda") * 0.1
+    c = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+    return a, b, bias, c
+
+
+def run_gemm_sweep(family, launches, torch) -> int:
+    """The measurements behind two GEMM rules the library and the lowering ship, timed like
+    bench.py (graph replays of ``launches`` launches, median of 5):
+
+    gemm-tile: gemm_fast_tile_extent's choice between 256x256 and 128x128 C tiles, on grids of
+    16-1024 tiles of 256x256 and on skinny vocabulary-width products; each shape runs with
+    both tile knobs (ihip_gemm_bf16_bias_relu_ex, no workspace, so no split) and prints the
+    rule's pick and the faster one.
+
+    gemm-split: split_plan's segment count, on small grids; each shape runs unsplit and split
+    into S = 2 .. 16 K segments (ihip_gemm_bf16_bias_relu_splitk) and prints the time of
+    every S, the rule's S and the best S."""
+    import ctypes  # noqa: PLC0415
+
+    from .lowering import _gemm_tile_extent, gemm_split_plan  # noqa: PLC0415
+    from .runtime import load_library  # noqa: PLC0415
+
+    lib = load_library()
+    P = ctypes.c_void_p
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2024)
+
+    def stream():
+        return P(torch.cuda.current_stream().cuda_stream)
+
+    def check(st):
+        if st != 0:
+            raise RuntimeError(lib.ihip_last_error().decode())
+
+    if family == "gemm-tile":
+        agree = 0
+        for M, N, K, tb in GEMM_TILE_SHAPES:
+            a, b, bias, c = _gemm_operands(M, N, K, tb, torch, g)
+            us = {}
+            for tile in (256, 128):
+                def launch(i, tile=tile):
+                    check(lib.ihip_gemm_bf16_bias_relu_ex(P(a.data_ptr()), P(b.data_ptr()), P(bias.data_ptr()),
+                                                          P(c.data_ptr()), M, N, K, 0, int(tb), 1, tile, stream()))
+                us[tile] = 1e3 * _graph_time(launch, 1, launches, torch)
+            rule = _gemm_tile_extent(M, N)
+            best = min(us, key=us.get)
+            agree += rule == best
+            t256 = -(-M // 256) * -(-N // 256)
+            print(f"[runner] gemm-tile {M}x{N}x{K} B as {'[N, K]' if tb else '[K, N]'} ({t256} tiles of 256): "
+                  f"256 {us[256]:.1f} us ({2 * M * N * K / us[256] / 1e6:.0f} TFLOP/s), 128 {us[128]:.1f} us "
+                  f"({2 * M * N * K / us[128] / 1e6:.0f} TFLOP/s); rule {rule}, faster {best}", flush=True)
+            del a, b, bias, c
+        print(f"[runner] gemm-tile: the rule picks the faster tile on {agree} of {len(GEMM_TILE_SHAPES)} shapes",
+              flush=True)
+        return 0
+    if family == "gemm-split":
+        for M, N, K, tb in GEMM_SPLIT_SHAPES:
+            a, b, bias, c = _gemm_operands(M, N, K, tb, torch, g)
+            need = max(lib.ihip_gemm_splitk_workspace_size(M, N, K, S) for S in (*GEMM_SPLITS, 0))
+            ws = torch.empty(max(1, need), dtype=torch.uint8, device="cuda")
+            us = {}
+            rule = gemm_split_plan(M, N, K)[0]
+            for S in sorted(set(GEMM_SPLITS) | {rule}):
+                if gemm_split_plan(M, N, K, S)[0] != S:
+                    continue  # more segments than 64-k steps
+
+                def launch(i, S=S):
+                    check(lib.ihip_gemm_bf16_bias_relu_splitk(P(a.data_ptr()), P(b.data_ptr()), P(bias.data_ptr()),
+                                                              P(c.data_ptr()), M, N, K, 0, int(tb), 1, 0, S,
+                                                              P(ws.data_ptr()), need, stream()))
+                us[S] = 1e3 * _graph_time(launch, 1, launches, torch)
+            best = min(us, key=us.get)
+            row = ", ".join(f"S={S} {t:.1f}" for S, t in us.items())
+            print(f"[runner] gemm-split {M}x{N}x{K} B as {'[N, K]' if tb else '[K, N]'}: {row} us; rule S={rule} "
+                  f"({us.get(rule, float('nan')):.1f} us), best S={best} ({us[best]:.1f} us)", flush=True)
+            del a, b, bias, c, ws
+        return 0
+    raise SystemExit(f"--sweep {family}: unknown")
+
+
 def run_gather(bindings, launches, torch) -> int:
     """gather(inp [M, N] f32, row [L] i32, col [L] i32) -> out [L] (ihip_gather2d_f32) with
     uniformly random in-range indices; algorithmic bytes 16 per element (two indices, one inp
@@ -365,8 +465,9 @@ def main(argv=None) -> int:
                     help="time a generic element-wise program chain (or all of them)")
     ap.add_argument("--row-reduce", choices=["sum", "max"], help="time a row reduction (f32 [M, N], --bindings)")
     ap.add_argument("--gather", action="store_true", help="time gather2d (inp f32 [M, N], L random index pairs)")
-    ap.add_argument("--sweep", choices=["softmax"],
-                    help="fixed cost and streaming rate of the softmax kernel against a copy of the same bytes")
+    ap.add_argument("--sweep", choices=["softmax", "gemm-tile", "gemm-split"],
+                    help="softmax: fixed cost and streaming rate against a copy of the same bytes; gemm-tile, "
+                         "gemm-split: the measurements behind the GEMM's tile and split-K rules")
     ap.add_argument("--f32", choices=["matmul", "layernorm"],
                     help="time the reference's f32 IR of a family (default 8192^3 / [8192, 4096], --bindings)")
     ap.add_argument("--launches", type=int, default=20)
@@ -385,6 +486,8 @@ def main(argv=None) -> int:
     import torch
 
     if args.sweep:
+        if args.sweep.startswith("gemm"):
+            return run_gemm_sweep(args.sweep, args.launches, torch)
         return run_sweep(args.sweep, args.launches, torch)
     if args.ew_chain:
         return run_ew_chains(sorted(EW_CHAINS) if args.ew_chain == "all" else [args.ew_chain], args.launches, torch)
