@@ -10,8 +10,10 @@
 // 32x32x16 form (`rocm-smi -c` during back-to-back launches).  The sums come out bit-identical
 // to the 32x32x16 kernels' (same k order over 16-k halves, f32 accumulation).
 //
-// Tile schedule: one 256x256 tile per workgroup of four waves (2 x 2), each wave a 128x128
-// block held as 8 x 8 accumulators of 16x16 (256 AGPRs, one wave per SIMD).  K runs in 64-k
+// Tile schedule: 256x256 tiles, each computed by a workgroup of four waves (2 x 2), each wave a
+// 128x128 block held as 8 x 8 accumulators of 16x16 (256 AGPRs, one wave per SIMD).  The grid
+// is persistent, one workgroup per CU taking tiles in turn (a tile's stores drain while the
+// next tile's first slices load, and no workgroup is launched per tile).  K runs in 64-k
 // slices; LDS holds three A slices and two B slices (5 x 32 KiB); one barrier per slice.
 // A slice is two 32-k steps of 64 MFMAs; a step's fragments (8 A blocks, 8 B blocks) are read
 // during the previous step, in its first six quarters (a quarter = 8 MFMAs), so that the last
@@ -35,6 +37,7 @@
 // (v_accvgpr_read/write pairs and wait states inside the loop).
 #include "common.hpp"
 
+#include <atomic>
 #include <type_traits>
 
 namespace ihip {
@@ -184,17 +187,9 @@ void gemm_bf16_m16_kernel(const uint16_t* __restrict__ A, const uint16_t* __rest
   const lds_char_t* lds = (const lds_char_t*)lds_raw;
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
 
-  const int bid = xcd_contiguous(blockIdx.x, gridDim.x);
-  const int per_group = kGroupRows * tiles_n;
-  const int grp = bid / per_group, first_m = grp * kGroupRows;
-  const int gsz = (tiles_m - first_m) < kGroupRows ? (tiles_m - first_m) : kGroupRows;
-  const int tm = first_m + (bid % per_group) % gsz, tn = (bid % per_group) / gsz;
-  const int64_t m0 = static_cast<int64_t>(tm) * kTile, n0 = static_cast<int64_t>(tn) * kTile;
-
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave & 1, wn = wave >> 1;
-  const float bias_v = threadIdx.x < kTile && bias != nullptr ? bias[n0 + threadIdx.x] : 0.0f;
 
   uint32_t ca[kCopies], cb[kCopies];
   copy_offsets<false>(K, wave, lane, ca);
@@ -206,159 +201,189 @@ void gemm_bf16_m16_kernel(const uint16_t* __restrict__ A, const uint16_t* __rest
   else
     kc_offsets(wn * 128, lane, obc);
 
-  const uint16_t* const a_rows = A + m0 * K;
-  const uint16_t* const b_base = BKM ? B + n0 : B + n0 * K;
-  auto copy_a = [&](int s, int ra, int c) {
-    dma16(a_rows + static_cast<int64_t>(s) * kDK, ca[c], lds_addr + ra * kOpBytes + (4 * c + wave) * 1024);
-  };
-  auto copy_b = [&](int s, int c) {
-    const int64_t k0 = static_cast<int64_t>(s) * kDK;
-    dma16(BKM ? b_base + k0 * N : b_base + k0, cb[c], lds_addr + kOffB + (s & 1) * kOpBytes + (4 * c + wave) * 1024);
-  };
+  // Persistent grid: workgroup b takes virtual tiles b, b + G, b + 2G, ...; a virtual tile v runs
+  // on XCD v % 8 as a non-persistent launch's block v would, and maps to the same tile.
+  const int tiles = tiles_m * tiles_n;
+  for (int v = blockIdx.x; v < tiles; v += gridDim.x) {
+    const int bid = xcd_contiguous(v, tiles);
+    const int per_group = kGroupRows * tiles_n;
+    const int grp = bid / per_group, first_m = grp * kGroupRows;
+    const int gsz = (tiles_m - first_m) < kGroupRows ? (tiles_m - first_m) : kGroupRows;
+    const int tm = first_m + (bid % per_group) % gsz, tn = (bid % per_group) / gsz;
+    const int64_t m0 = static_cast<int64_t>(tm) * kTile, n0 = static_cast<int64_t>(tn) * kTile;
+    const float bias_v = threadIdx.x < kTile && bias != nullptr ? bias[n0 + threadIdx.x] : 0.0f;
 
-  f32x4_t acc[8][8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{};
-  acc_fence<true>(acc[0]);
-#pragma unroll
-  for (int i = 1; i < 8; ++i) acc_fence<false>(acc[i]);
+    const uint16_t* const a_rows = A + m0 * K;
+    const uint16_t* const b_base = BKM ? B + n0 : B + n0 * K;
+    auto copy_a = [&](int s, int ra, int c) {
+      dma16(a_rows + static_cast<int64_t>(s) * kDK, ca[c], lds_addr + ra * kOpBytes + (4 * c + wave) * 1024);
+    };
+    auto copy_b = [&](int s, int c) {
+      const int64_t k0 = static_cast<int64_t>(s) * kDK;
+      dma16(BKM ? b_base + k0 * N : b_base + k0, cb[c], lds_addr + kOffB + (s & 1) * kOpBytes + (4 * c + wave) * 1024);
+    };
 
-  const int KT = static_cast<int>(K / kDK);
+    f32x4_t acc[8][8];
 #pragma unroll
-  for (int c = 0; c < kCopies; ++c) copy_a(0, 0, c);
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-  for (int c = 0; c < kCopies; ++c) copy_b(0, c);
-  if (KT > 1) {
+      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{};
+    acc_fence<true>(acc[0]);
 #pragma unroll
-    for (int c = 0; c < kCopies; ++c) copy_a(1, 1, c);
-#pragma unroll
-    for (int c = 0; c < kCopies; ++c) copy_b(1, c);
-    wait_vm<2 * kCopies>();
-  } else {
-    wait_vm<0>();
-  }
-  __syncthreads();
-  Frag f[2];
-#pragma unroll
-  for (int sl = 0; sl < kSlots; ++sl) read_slot<BKM>(lds, lds + kOffB, 0, oa, obc, obk, f[0], sl);
+    for (int i = 1; i < 8; ++i) acc_fence<false>(acc[i]);
 
-  // Copy schedule per slice kt (16 quarters of 8 MFMAs): quarters 0-7 copy A slice kt+2 into
-  // the region slice kt-1 used; quarters 8-15, after the barrier that closes slice kt (start of
-  // quarter 8), copy B slice kt+2 into the stage slice kt used.  The barrier waits for A and B
-  // of slice kt+1 (issued during slice kt-1): only A slice kt+2's copies were issued since.
-  auto slice = [&](int kt, int ra, auto more_tag, auto more2_tag) {
-    constexpr bool kMore = decltype(more_tag)::value;
-    constexpr bool kMore2 = decltype(more2_tag)::value;
-    const int ra1 = ra == kRegionsA - 1 ? 0 : ra + 1, ra2 = ra1 == kRegionsA - 1 ? 0 : ra1 + 1;
-    const lds_char_t* sa = lds + ra * kOpBytes;
-    const lds_char_t* sb = lds + kOffB + (kt & 1) * kOpBytes;
-    const lds_char_t* na = lds + ra1 * kOpBytes;
-    const lds_char_t* nb = lds + kOffB + ((kt + 1) & 1) * kOpBytes;
+    const int KT = static_cast<int>(K / kDK);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      Frag& cur = f[s];
-      Frag& nxt = f[s ^ 1];
-      const bool last = s == 1;
-      const bool rd = !last || kMore;
-      const lds_char_t* rda = last ? na : sa;
-      const lds_char_t* rdb = last ? nb : sb;
-      const int rs = last ? 0 : 1;
+    for (int c = 0; c < kCopies; ++c) copy_a(0, 0, c);
+#pragma unroll
+    for (int c = 0; c < kCopies; ++c) copy_b(0, c);
+    if (KT > 1) {
+#pragma unroll
+      for (int c = 0; c < kCopies; ++c) copy_a(1, 1, c);
+#pragma unroll
+      for (int c = 0; c < kCopies; ++c) copy_b(1, c);
+      wait_vm<2 * kCopies>();
+    } else {
+      wait_vm<0>();
+    }
+    __syncthreads();
+    Frag f[2];
+#pragma unroll
+    for (int sl = 0; sl < kSlots; ++sl) read_slot<BKM>(lds, lds + kOffB, 0, oa, obc, obk, f[0], sl);
+
+    // Copy schedule per slice kt (16 quarters of 8 MFMAs): quarters 0-7 copy A slice kt+2 into
+    // the region slice kt-1 used; quarters 8-15, after the barrier that closes slice kt (start of
+    // quarter 8), copy B slice kt+2 into the stage slice kt used.  The barrier waits for A and B
+    // of slice kt+1 (issued during slice kt-1): only A slice kt+2's copies were issued since.
+    auto slice = [&](int kt, int ra, auto more_tag, auto more2_tag) {
+      constexpr bool kMore = decltype(more_tag)::value;
+      constexpr bool kMore2 = decltype(more2_tag)::value;
+      const int ra1 = ra == kRegionsA - 1 ? 0 : ra + 1, ra2 = ra1 == kRegionsA - 1 ? 0 : ra1 + 1;
+      const lds_char_t* sa = lds + ra * kOpBytes;
+      const lds_char_t* sb = lds + kOffB + (kt & 1) * kOpBytes;
+      const lds_char_t* na = lds + ra1 * kOpBytes;
+      const lds_char_t* nb = lds + kOffB + ((kt + 1) & 1) * kOpBytes;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        Frag& cur = f[s];
+        Frag& nxt = f[s ^ 1];
+        const bool last = s == 1;
+        const bool rd = !last || kMore;
+        const lds_char_t* rda = last ? na : sa;
+        const lds_char_t* rdb = last ? nb : sb;
+        const int rs = last ? 0 : 1;
+#pragma unroll
+        for (int mi = 0; mi < 8; ++mi) {
+          __builtin_amdgcn_sched_barrier(0);
+          const bool pre = last && mi == 0 && kMore;
+          if (pre) {
+#pragma unroll
+            for (int q = 0; q < kPre; ++q)
+              mfma16(acc[mi][q], cur.b[q], cur.a[mi]);
+            if constexpr (kMore2)
+              wait_vm<kCopies>();
+            else
+              wait_vm<0>();
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          const int from = pre ? kPre : 0;
+          // fixed order: MFMA, LDS read, MFMA, LDS read, ..., each fenced so that the scheduler
+          // keeps one live range per accumulator
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            if (q >= from) {
+              mfma16(acc[mi][q], cur.b[q], cur.a[mi]);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            const int r = q - from;
+            const int lo = mi < kReadQ ? mi * kSlots / kReadQ : kSlots;
+            const int hi = mi < kReadQ ? (mi + 1) * kSlots / kReadQ : kSlots;
+            if (rd && r >= 0 && lo + r < hi) {
+              read_slot<BKM>(rda, rdb, rs, oa, obc, obk, nxt, lo + r);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+          const int qi = s * 8 + mi;
+          if (kMore2) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (qi < 8)
+              copy_a(kt + 2, ra2, qi);
+            else
+              copy_b(kt + 2, qi - 8);
+          }
+        }
+      }
+    };
+    int kt = 0, ra = 0;
+    for (; kt + 2 < KT; ++kt) {
+      slice(kt, ra, std::true_type{}, std::true_type{});
+      ra = ra == kRegionsA - 1 ? 0 : ra + 1;
+    }
+    if (kt + 1 < KT) {
+      slice(kt, ra, std::true_type{}, std::false_type{});
+      ++kt;
+      ra = ra == kRegionsA - 1 ? 0 : ra + 1;
+    }
+    slice(kt, ra, std::false_type{}, std::false_type{});
+
+    // epilogue: bias + activation, the tile staged in LDS as bf16 rows, written out in 512-byte rows
+    acc_fence<true>(acc[0]);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) acc_fence<false>(acc[i]);
+    __syncthreads();
+    float* bias_lds = reinterpret_cast<float*>(lds_raw + kTile * kCPitch);
+    if (threadIdx.x < kTile) bias_lds[threadIdx.x] = bias_v;
+    __syncthreads();
+    typedef __attribute__((address_space(3))) char lds_wchar_t;
+    lds_wchar_t* ct = (lds_wchar_t*)lds_raw;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int nl = wn * 128 + q * 16 + (lane >> 4) * 4;
+      const f32x4_t bv = *reinterpret_cast<const f32x4_t*>(&bias_lds[nl]);
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
-        __builtin_amdgcn_sched_barrier(0);
-        const bool pre = last && mi == 0 && kMore;
-        if (pre) {
+        const int ml = wm * 128 + mi * 16 + (lane & 15);
+        float v[4];
 #pragma unroll
-          for (int q = 0; q < kPre; ++q)
-            mfma16(acc[mi][q], cur.b[q], cur.a[mi]);
-          if constexpr (kMore2)
-            wait_vm<kCopies>();
-          else
-            wait_vm<0>();
-          __syncthreads();
-          __builtin_amdgcn_sched_barrier(0);
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[mi][q][e] + bv[e];
+          if constexpr (RELU) v[e] = __builtin_elementwise_maximum(v[e], 0.0f);
         }
-        const int from = pre ? kPre : 0;
-        // fixed order: MFMA, LDS read, MFMA, LDS read, ..., each fenced so that the scheduler
-        // keeps one live range per accumulator
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          if (q >= from) {
-            mfma16(acc[mi][q], cur.b[q], cur.a[mi]);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          const int r = q - from;
-          const int lo = mi < kReadQ ? mi * kSlots / kReadQ : kSlots;
-          const int hi = mi < kReadQ ? (mi + 1) * kSlots / kReadQ : kSlots;
-          if (rd && r >= 0 && lo + r < hi) {
-            read_slot<BKM>(rda, rdb, rs, oa, obc, obk, nxt, lo + r);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-        }
-        const int qi = s * 8 + mi;
-        if (kMore2) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (qi < 8)
-            copy_a(kt + 2, ra2, qi);
-          else
-            copy_b(kt + 2, qi - 8);
-        }
+        const bf16x2_t lo = {static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1])};
+        const bf16x2_t hi = {static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
+        const u32x2 pk = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        *(lds_u32x2_t*)(ct + ml * kCPitch + nl * 2) = pk;
       }
+      asm volatile("" ::: "memory");
     }
-  };
-  int kt = 0, ra = 0;
-  for (; kt + 2 < KT; ++kt) {
-    slice(kt, ra, std::true_type{}, std::true_type{});
-    ra = ra == kRegionsA - 1 ? 0 : ra + 1;
-  }
-  if (kt + 1 < KT) {
-    slice(kt, ra, std::true_type{}, std::false_type{});
-    ++kt;
-    ra = ra == kRegionsA - 1 ? 0 : ra + 1;
-  }
-  slice(kt, ra, std::false_type{}, std::false_type{});
-
-  // epilogue: bias + activation, the tile staged in LDS as bf16 rows, written out in 512-byte rows
-  acc_fence<true>(acc[0]);
-#pragma unroll
-  for (int i = 1; i < 8; ++i) acc_fence<false>(acc[i]);
-  __syncthreads();
-  float* bias_lds = reinterpret_cast<float*>(lds_raw + kTile * kCPitch);
-  if (threadIdx.x < kTile) bias_lds[threadIdx.x] = bias_v;
-  __syncthreads();
-  typedef __attribute__((address_space(3))) char lds_wchar_t;
-  lds_wchar_t* ct = (lds_wchar_t*)lds_raw;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int nl = wn * 128 + q * 16 + (lane >> 4) * 4;
-    const f32x4_t bv = *reinterpret_cast<const f32x4_t*>(&bias_lds[nl]);
-#pragma unroll
-    for (int mi = 0; mi < 8; ++mi) {
-      const int ml = wm * 128 + mi * 16 + (lane & 15);
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = acc[mi][q][e] + bv[e];
-        if constexpr (RELU) v[e] = __builtin_elementwise_maximum(v[e], 0.0f);
-      }
-      const bf16x2_t lo = {static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1])};
-      const bf16x2_t hi = {static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
-      const u32x2 pk = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
-      *(lds_u32x2_t*)(ct + ml * kCPitch + nl * 2) = pk;
-    }
-    asm volatile("" ::: "memory");
-  }
-  __syncthreads();
-  constexpr int kLanesPerRow = kTile / 8, kRowsPerStore = 64 / kLanesPerRow;
-  const int chunk = lane % kLanesPerRow;
+    __syncthreads();
+    constexpr int kLanesPerRow = kTile / 8, kRowsPerStore = 64 / kLanesPerRow;
+    const int chunk = lane % kLanesPerRow;
 #pragma unroll 4
-  for (int i = 0; i < kTile / (4 * kRowsPerStore); ++i) {
-    const int row = (i * 4 + wave) * kRowsPerStore + lane / kLanesPerRow;
-    const u32x4 v = *(const lds_u32x4_t*)(ct + row * kCPitch + chunk * 16);
-    *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + chunk * 8) = v;
+    for (int i = 0; i < kTile / (4 * kRowsPerStore); ++i) {
+      const int row = (i * 4 + wave) * kRowsPerStore + lane / kLanesPerRow;
+      const u32x4 v = *(const lds_u32x4_t*)(ct + row * kCPitch + chunk * 16);
+      *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + chunk * 8) = v;
+    }
+    // every wave has read its rows of the staged tile before the next tile's copies land in LDS
+    __syncthreads();
   }
+}
+
+// Compute units of the current device, looked up once per device.
+int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
+  return cus;
 }
 
 }  // namespace m16
@@ -376,7 +401,11 @@ bool gemm_m16_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, const void
 hipError_t launch_gemm_m16(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
                            int64_t K, bool transpose_b, int relu, hipStream_t s) {
   const int tm = static_cast<int>(M / m16::kTile), tn = static_cast<int>(N / m16::kTile);
-  const dim3 grid(static_cast<unsigned>(tm) * static_cast<unsigned>(tn)), block(256);
+  const int64_t tiles = static_cast<int64_t>(tm) * tn;
+  const int cus = m16::device_cus();
+  if (cus <= 0) return hipErrorInvalidDevice;
+  // one workgroup per CU (the kernel holds all of a CU's LDS and registers)
+  const dim3 grid(static_cast<unsigned>(tiles < cus ? tiles : cus)), block(256);
   if (transpose_b) {
     if (relu)
       m16::gemm_bf16_m16_kernel<false, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, tm, tn);

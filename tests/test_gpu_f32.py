@@ -324,13 +324,16 @@ def test_elementwise_programs_past_the_interpreter_limits(hip, make, arg):
 
 # ------------------------------------------------------------------ bf16 GEMM: 16x16x32 whole-tile kernel
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (256, 512, 128), (512, 768, 192), (1024, 1024, 1024),
-                                   (2048, 1536, 4096), (256, 4096, 320)])
+                                   (2048, 1536, 4096), (256, 4096, 320), (4352, 4096, 128), (4096, 4352, 192),
+                                   (8192, 8192, 64)])
 @pytest.mark.parametrize("relu", [1, 0])
 def test_gemm_m16_matches_the_ring_kernel_bit_for_bit(hip, M, N, K, relu):
     """Whole 256x256 tiles with K % 64 == 0 run gemm_m16.hip (16x16x32 MFMAs); a C base 2 bytes
     off a 16-byte boundary (B given as [N, K]) sends the same product to gemm_fast.hip's ring
     kernel (32x32x16 MFMAs, 2-byte stores).  The sums are identical bits (1, 2, 3 and more
-    64-k slices, so the prologue, the last two slices and the steady loop are all covered)."""
+    64-k slices, so the prologue, the last two slices and the steady loop are all covered).  The
+    grid is one workgroup per CU: 272 and 1024 tiles make workgroups take several tiles each, in
+    uneven numbers for 272."""
     torch = _torch()
     g = torch.Generator(device="cuda")
     g.manual_seed(M + N + K)
