@@ -25,6 +25,10 @@ HIPCC_FLAGS = [
     "-shared",
     # Keep the compiler from forming packed-FP32 (v_pk_*_f32) instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # The first kernel arguments arrive in SGPRs at wave launch (gfx950 kernarg preloading; code
+    # objects keep a loading prologue for firmware without it): the row kernels issue their first
+    # loads without waiting on an argument load.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-function",
 ]

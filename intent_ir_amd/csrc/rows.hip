@@ -489,11 +489,13 @@ hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t
 // of a plain copy of the same bytes).  The loads are unconditional: a wave whose second row
 // is past the last re-reads the last row and stores nothing for it (loads under a row guard
 // cost 4%).
-template <int kVpl, bool kFull, int kR>
+// kWaves: waves per workgroup (a constant, so that the kernel reads no hidden argument before
+// its first loads).
+template <int kVpl, bool kFull, int kR, int kWaves>
 __global__ __launch_bounds__(256) void softmax_rows_f32_reg(const f32x4* __restrict__ x, f32x4* __restrict__ y,
                                                             int64_t M, int n4, SoftmaxStats st) {
   const int lane = threadIdx.x & 63;
-  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * kR;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6)) * kR;
   if (row0 >= M) return;
   const float ninf = -__builtin_inff();
   f32x4 v[kR][kVpl];
@@ -1190,22 +1192,40 @@ static void launch_softmax_grouped(const f32x4* x4, f32x4* y4, int64_t M, int n4
   }
 }
 
-// rows: rows per workgroup, 1, 2 or 4 (the kernel reads its waves from blockDim).  Four rows of
-// at most 1024 floats run as two waves of two rows each, otherwise one wave per row.
+template <int kVpl, bool kFull, int kWaves>
+static void launch_softmax_reg_waves(const f32x4* x4, f32x4* y4, int64_t M, int n4, const SoftmaxStats& st,
+                                     hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((M + kWaves - 1) / kWaves));
+  softmax_rows_f32_reg<kVpl, kFull, 1, kWaves><<<grid, dim3(64 * kWaves), 0, s>>>(x4, y4, M, n4, st);
+}
+
+// rows: rows per workgroup, 1, 2 or 4.  Four rows of at most 1024 floats run as two waves of
+// two rows each, otherwise one wave per row.
 template <int kVpl>
 static void launch_softmax_reg(const f32x4* x4, f32x4* y4, int64_t M, int n4, int rows, const SoftmaxStats& st,
                                hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((M + rows - 1) / rows));
   const bool full = n4 == kVpl * kWave;
   if (kVpl <= 4 && rows == 4) {
+    const dim3 grid(static_cast<unsigned>((M + 3) / 4));
     if (full)
-      softmax_rows_f32_reg<kVpl, true, 2><<<grid, dim3(128), 0, s>>>(x4, y4, M, n4, st);
+      softmax_rows_f32_reg<kVpl, true, 2, 2><<<grid, dim3(128), 0, s>>>(x4, y4, M, n4, st);
     else
-      softmax_rows_f32_reg<kVpl, false, 2><<<grid, dim3(128), 0, s>>>(x4, y4, M, n4, st);
-  } else if (full) {
-    softmax_rows_f32_reg<kVpl, true, 1><<<grid, dim3(64 * rows), 0, s>>>(x4, y4, M, n4, st);
-  } else {
-    softmax_rows_f32_reg<kVpl, false, 1><<<grid, dim3(64 * rows), 0, s>>>(x4, y4, M, n4, st);
+      softmax_rows_f32_reg<kVpl, false, 2, 2><<<grid, dim3(128), 0, s>>>(x4, y4, M, n4, st);
+    return;
+  }
+  switch (rows) {
+    case 1:
+      full ? launch_softmax_reg_waves<kVpl, true, 1>(x4, y4, M, n4, st, s)
+           : launch_softmax_reg_waves<kVpl, false, 1>(x4, y4, M, n4, st, s);
+      break;
+    case 2:
+      full ? launch_softmax_reg_waves<kVpl, true, 2>(x4, y4, M, n4, st, s)
+           : launch_softmax_reg_waves<kVpl, false, 2>(x4, y4, M, n4, st, s);
+      break;
+    default:
+      full ? launch_softmax_reg_waves<kVpl, true, 4>(x4, y4, M, n4, st, s)
+           : launch_softmax_reg_waves<kVpl, false, 4>(x4, y4, M, n4, st, s);
+      break;
   }
 }
 
@@ -1328,9 +1348,11 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 // masks.
 constexpr int kLnRows = 16;
 template <int kVpl, bool kExact>
+// Argument order: what the first loads need comes first (the first 56 bytes of arguments arrive
+// preloaded in SGPRs), rstd_out and eps, needed last, after.
 __global__ __launch_bounds__(64 * kLnRows) void layernorm_rows_f16_wave(
     const u32x4* __restrict__ x, const u32x4* __restrict__ w, const u32x4* __restrict__ b, u32x4* __restrict__ y,
-    float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t M, int n8, int N, float eps) {
+    int n8, int N, int64_t M, float* __restrict__ mean_out, float* __restrict__ rstd_out, float eps) {
   static_assert(kVpl * kWave <= 64 * kLnRows, "one staging load per thread");
   __shared__ u32x4 w_lds[kVpl * kWave], b_lds[kVpl * kWave];
   const int lane = threadIdx.x & 63;
@@ -2142,9 +2164,9 @@ static void launch_layernorm_wave(const u32x4* x8, const u32x4* w8, const u32x4*
                                   int64_t M, int n8, int N, float eps, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((M + kLnRows - 1) / kLnRows)), block(64 * kLnRows);
   if (n8 == kVpl * kWave && M % kLnRows == 0)
-    layernorm_rows_f16_wave<kVpl, true><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, N, eps);
+    layernorm_rows_f16_wave<kVpl, true><<<grid, block, 0, s>>>(x8, w8, b8, y8, n8, N, M, mean, rstd, eps);
   else
-    layernorm_rows_f16_wave<kVpl, false><<<grid, block, 0, s>>>(x8, w8, b8, y8, mean, rstd, M, n8, N, eps);
+    layernorm_rows_f16_wave<kVpl, false><<<grid, block, 0, s>>>(x8, w8, b8, y8, n8, N, M, mean, rstd, eps);
 }
 
 template <int kVpl, int kW, int kWaves>
