@@ -58,19 +58,40 @@ __device__ __forceinline__ uint32_t bf16x2_apply(uint32_t xw, float b0, float b1
 // of fewer than 256 vectors n8 rounded up to a power of two, so that 256 / lanes rows share the
 // workgroup instead of leaving most threads idle: N = 64 ran at 17% of HBM peak); thread t takes
 // column t % lanes of rows (t / lanes) + r * (256 / lanes), r < kRows, of its row block.
-template <int kRows, bool kFolded>
+// kExact: the grid tiles the tensor exactly (one row block per grid row, every column and row in
+// range), so the rows need no guards and their addresses are one per-lane offset from a uniform
+// base and stride (0.6% faster at [32768, 8192] than 64-bit addresses per row).
+template <int kRows, bool kFolded, bool kExact>
 __global__ __launch_bounds__(256) void bias_gelu_axpy_bf16_vec(const u32x4* __restrict__ x, const u32x4* __restrict__ bias,
                                                                u32x4* __restrict__ y, int64_t M, int64_t n8, float a,
                                                                int lanes) {
   const int64_t col = static_cast<int64_t>(blockIdx.x) * lanes + (threadIdx.x & (lanes - 1));
   const int64_t sub = threadIdx.x / lanes, per = 256 / lanes;  // row within a group of per rows
-  if (col >= n8) return;
+  if (!kExact && col >= n8) return;
   const u32x4 bw = bias[col];
   float bf[8];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     bf[2 * j] = __uint_as_float(bw[j] << 16);
     bf[2 * j + 1] = __uint_as_float(bw[j] & 0xffff0000u);
+  }
+  if constexpr (kExact) {
+    const int64_t row0 = static_cast<int64_t>(blockIdx.y) * kRows * per;
+    const u32x4* const xb = x + row0 * n8;
+    u32x4* const yb = y + row0 * n8;
+    const uint32_t off = static_cast<uint32_t>(sub * n8 + col);  // vectors; the launcher checks the range
+    const int64_t rs = per * n8;
+    u32x4 v[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) v[r] = __builtin_nontemporal_load(xb + r * rs + off);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = bf16x2_apply<kFolded>(v[r][j], bf[2 * j], bf[2 * j + 1], a);
+      __builtin_nontemporal_store(o, yb + r * rs + off);
+    }
+    return;
   }
   for (int64_t row0 = static_cast<int64_t>(blockIdx.y) * kRows * per + sub; row0 < M;
        row0 += static_cast<int64_t>(gridDim.y) * kRows * per) {
@@ -121,10 +142,21 @@ hipError_t launch_bias_gelu_axpy_bf16(const uint16_t* x, const uint16_t* bias, u
     const u32x4* b8 = reinterpret_cast<const u32x4*>(bias);
     u32x4* y8 = reinterpret_cast<u32x4*>(y);
     const float ia = 1.0f / alpha;
-    if (alpha != 0.0f && __builtin_isfinite(ia) && __builtin_isfinite(alpha))
-      bias_gelu_axpy_bf16_vec<kRows, true><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, ia, lanes);
-    else
-      bias_gelu_axpy_bf16_vec<kRows, false><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, alpha, lanes);
+    // exact tiling: every row block and column block full, one row block per grid row, and the
+    // per-lane offset (rows of the group times n8, plus the column) below 2^32 vectors
+    const bool exact = M % (kRows * per) == 0 && n8 % lanes == 0 && row_blocks * kRows * per == M &&
+                       (per - 1) * n8 + n8 < (int64_t(1) << 32);
+    if (alpha != 0.0f && __builtin_isfinite(ia) && __builtin_isfinite(alpha)) {
+      if (exact)
+        bias_gelu_axpy_bf16_vec<kRows, true, true><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, ia, lanes);
+      else
+        bias_gelu_axpy_bf16_vec<kRows, true, false><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, ia, lanes);
+    } else {
+      if (exact)
+        bias_gelu_axpy_bf16_vec<kRows, false, true><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, alpha, lanes);
+      else
+        bias_gelu_axpy_bf16_vec<kRows, false, false><<<grid, dim3(256), 0, s>>>(x8, b8, y8, M, n8, alpha, lanes);
+    }
   } else {
     const int64_t total = M * N;
     int64_t blocks = (total + 255) / 256;

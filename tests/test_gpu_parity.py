@@ -482,6 +482,23 @@ def test_gelu_short_and_ragged_rows(hip, M, N):
     check(out, ref, ["y"], TOL["gelu_strict"], f"gelu strict {b}")
 
 
+@pytest.mark.parametrize("M,N", [(72, 2048), (256, 64), (64, 8)])
+def test_gelu_exact_tiling_matches_the_guarded_path(hip, M, N):
+    """When the grid tiles the tensor exactly the kernel drops its row guards and addresses rows
+    from a uniform base; one more row sends the same rows through the guarded loop.  Both
+    against the oracle, and bit for bit against each other on the shared rows."""
+    w = WORKLOADS["gelu"]
+    big = {"M": M + 1, "N": N}
+    inp = w.gen(big, seed=M * 7 + N)
+    sub = {"x": inp["x"][:M], "bias": inp["bias"]}
+    b = {"M": M, "N": N}
+    out_exact = run_case(w.ir(), sub, b)["y"]
+    out_guarded = run_case(w.ir(), inp, big)["y"]
+    assert np.array_equal(out_exact, out_guarded[:M])
+    ref = oracle_outputs(w.ir(), sub, b)
+    check({"y": out_exact}, ref, ["y"], TOL["gelu_strict"], f"gelu exact {b}")
+
+
 def test_gelu_full_config(hip):
     import torch
 
