@@ -389,13 +389,14 @@ int device_cus() {
 }  // namespace m16
 
 // True when this kernel takes the launch: whole tiles, K a multiple of 64, A given as [M, K],
-// 16-byte aligned tensors, 32-bit copy offsets.
+// 16-byte aligned tensors, 32-bit copy offsets, and at most 2^30 tiles (the persistent loop's
+// tile index plus the grid size stays within int).
 bool gemm_m16_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, const void* A, const void* B, const void* C) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
   const int64_t lim = int64_t(1) << 32;
   return !transpose_a && M > 0 && N > 0 && K >= m16::kDK && M % m16::kTile == 0 && N % m16::kTile == 0 &&
          K % m16::kDK == 0 && (al & 15) == 0 && K * 512 < lim && N * 128 < lim &&
-         (M / m16::kTile) * (N / m16::kTile) <= 0x7fffffffLL;
+         (M / m16::kTile) * (N / m16::kTile) <= (int64_t(1) << 30);
 }
 
 hipError_t launch_gemm_m16(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
