@@ -1036,20 +1036,31 @@ __global__ __launch_bounds__(256) void softmax_rows_f32_grouped_any(const float*
 // ---------------------------------------------------------------- LDS-staged short rows
 // A block of consecutive short rows is one contiguous run of n elements in memory, whatever the
 // row length.  stage_in copies it to LDS with 16-byte loads: element e goes to dst[h + e], where
-// h = (address of src & 15) / sizeof(T), so src's 16-byte boundaries fall on 16-byte boundaries
-// of dst and every whole vector moves with one load and one ds_write_b128; the at most two
-// partial vectors at the ends move element by element.  stage_out is the reverse.  src and dst
-// must be aligned to their element size.
+// h = (address of src & 127) / sizeof(T) (stage_offset), so src's 128-byte lines fall on 128-byte
+// boundaries of dst: a wave's 1 KiB of vectors covers whole lines, and every whole vector moves
+// with one load and one ds_write_b128 (a plain copy whose 1 KiB store runs start 16 bytes past a
+// line boundary ran 17% slower than an aligned one: the lines split between two stores are
+// written twice).  Vectors wholly outside the run are skipped; the at most two partial vectors at
+// its ends move element by element.  stage_out is the reverse.  src and dst must be aligned to
+// their element size; dst (src for stage_out) holds at least kStageSlack<T> elements past the run.
+constexpr int kStageAlign = 128;
+template <typename T>
+constexpr int kStageSlack = kStageAlign / sizeof(T) + 16 / sizeof(T);
+template <typename T>
+__device__ __forceinline__ int stage_offset(const T* p) {
+  return static_cast<int>((reinterpret_cast<uintptr_t>(p) & (kStageAlign - 1)) / sizeof(T));
+}
 template <typename T, int kT>
 __device__ __forceinline__ void stage_in(const T* __restrict__ src, int n, T* dst, int h) {
   constexpr int kE = 16 / sizeof(T);
-  const u32x4* base = reinterpret_cast<const u32x4*>(reinterpret_cast<uintptr_t>(src) & ~uintptr_t{15});
+  const u32x4* base =
+      reinterpret_cast<const u32x4*>(reinterpret_cast<uintptr_t>(src) & ~uintptr_t{kStageAlign - 1});
   const int nv = (h + n + kE - 1) / kE;
   for (int v = threadIdx.x; v < nv; v += kT) {
     const int e0 = v * kE - h;
     if (e0 >= 0 && e0 + kE <= n) {
       reinterpret_cast<u32x4*>(dst)[v] = __builtin_nontemporal_load(base + v);
-    } else {  // every load issued before the first is used: clamped indices, no branches
+    } else if (e0 + kE > 0) {  // every load issued before the first is used: clamped indices, no branches
       T t[kE];
 #pragma unroll
       for (int k = 0; k < kE; ++k) t[k] = src[min(max(e0 + k, 0), n - 1)];
@@ -1063,13 +1074,13 @@ __device__ __forceinline__ void stage_in(const T* __restrict__ src, int n, T* ds
 template <typename T, int kT>
 __device__ __forceinline__ void stage_out(const T* src, int h, int n, T* __restrict__ dst) {
   constexpr int kE = 16 / sizeof(T);
-  u32x4* base = reinterpret_cast<u32x4*>(reinterpret_cast<uintptr_t>(dst) & ~uintptr_t{15});
+  u32x4* base = reinterpret_cast<u32x4*>(reinterpret_cast<uintptr_t>(dst) & ~uintptr_t{kStageAlign - 1});
   const int nv = (h + n + kE - 1) / kE;
   for (int v = threadIdx.x; v < nv; v += kT) {
     const int e0 = v * kE - h;
     if (e0 >= 0 && e0 + kE <= n) {
       __builtin_nontemporal_store(reinterpret_cast<const u32x4*>(src)[v], base + v);
-    } else {  // the slot's LDS words read together (v * kE + kE <= the buffer's size)
+    } else if (e0 + kE > 0) {  // the slot's LDS words read together (v * kE + kE <= the buffer's size)
       T t[kE];
 #pragma unroll
       for (int k = 0; k < kE; ++k) t[k] = src[v * kE + k];
@@ -1090,20 +1101,20 @@ constexpr int kLnShortRpt = 4;
 // (softmax_rows_f32_grouped_any's per-element 4-byte accesses of rows that straddle vectors
 // ran at 55-66% of HBM peak), then each group of G lanes takes a row with
 // softmax_rows_f32_grouped_any's element mapping and arithmetic, so the results are identical.
-// y goes back into the same LDS slots when x and y share their offset modulo 16 bytes (each
+// y goes back into the same LDS slots when x and y share their offset modulo 128 bytes (each
 // lane rewrites only the slots it read), after a barrier otherwise.
 template <int G>
 __global__ __launch_bounds__(256) void softmax_rows_f32_short_lds(const float* __restrict__ x, float* __restrict__ y,
                                                                   int64_t M, int N, SoftmaxStats st) {
   constexpr int kRows = kShortRpt * (256 / G);
-  __shared__ __align__(16) float buf[kRows * 4 * G + 4];
+  __shared__ __align__(16) float buf[kRows * 4 * G + kStageSlack<float>];
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
   const int rows = static_cast<int>(M - r0 < kRows ? M - r0 : kRows);
   const int n = rows * N;
   const float* xb = x + r0 * N;
   float* yb = y + r0 * N;
-  const int hx = static_cast<int>((reinterpret_cast<uintptr_t>(xb) & 15) >> 2);
-  const int hy = static_cast<int>((reinterpret_cast<uintptr_t>(yb) & 15) >> 2);
+  const int hx = stage_offset(xb);
+  const int hy = stage_offset(yb);
   stage_in<float, 256>(xb, n, buf, hx);
   __syncthreads();
   const int lig = threadIdx.x & (G - 1);
@@ -2013,15 +2024,15 @@ __global__ __launch_bounds__(256) void layernorm_rows_f16_short_lds(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b,
     uint16_t* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t M, int N, float eps) {
   constexpr int kRows = kLnShortRpt * (256 / G);
-  __shared__ __align__(16) uint16_t buf[kRows * K * G + 8];
+  __shared__ __align__(16) uint16_t buf[kRows * K * G + kStageSlack<uint16_t>];
   __shared__ float wl[8 * G], bl[8 * G];
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
   const int rows = static_cast<int>(M - r0 < kRows ? M - r0 : kRows);
   const int n = rows * N;
   const uint16_t* xb = x + r0 * N;
   uint16_t* yb = y + r0 * N;
-  const int hx = static_cast<int>((reinterpret_cast<uintptr_t>(xb) & 15) >> 1);
-  const int hy = static_cast<int>((reinterpret_cast<uintptr_t>(yb) & 15) >> 1);
+  const int hx = stage_offset(xb);
+  const int hy = stage_offset(yb);
   if (static_cast<int>(threadIdx.x) < N) {  // N <= 256 = blockDim.x
     wl[threadIdx.x] = f16_to_f32(w[threadIdx.x]);
     bl[threadIdx.x] = f16_to_f32(b[threadIdx.x]);
