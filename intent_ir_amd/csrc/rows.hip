@@ -485,8 +485,8 @@ hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t
 // About 14 VALU instructions per element, so the kernel stays HBM-bound.
 // kVpl: f32x4 vectors held per lane; kFull: n4 == 64 * kVpl; kR: consecutive rows per wave,
 // all loaded before the first is reduced (with rows of at most 1024 floats, two rows per wave
-// and two waves per workgroup ran [16384, 1024] 2.8% faster than a wave per row, at the rate
-// of a plain copy of the same bytes).  The loads are unconditional: a wave whose second row
+// ran [16384, 1024] 2.8% faster than a wave per row, and four such waves per workgroup 2.6%
+// faster again than two).  The loads are unconditional: a wave whose second row
 // is past the last re-reads the last row and stores nothing for it (loads under a row guard
 // cost 4%).
 // kWaves: waves per workgroup (a constant, so that the kernel reads no hidden argument before
@@ -1210,12 +1210,23 @@ static void launch_softmax_reg_waves(const f32x4* x4, f32x4* y4, int64_t M, int 
   softmax_rows_f32_reg<kVpl, kFull, 1, kWaves><<<grid, dim3(64 * kWaves), 0, s>>>(x4, y4, M, n4, st);
 }
 
-// rows: rows per workgroup, 1, 2 or 4.  Four rows of at most 1024 floats run as two waves of
-// two rows each, otherwise one wave per row.
+// rows: rows per workgroup, 1, 2 or 4, or 0 (automatic: 4, except that rows of at most 1024
+// floats run as four waves of two rows each, eight rows per workgroup, measured 2.6% ahead of
+// two waves of two rows at [16384, 1024] on two boxes).  Four rows of at most 1024 floats run as
+// two waves of two rows each, otherwise one wave per row.
 template <int kVpl>
 static void launch_softmax_reg(const f32x4* x4, f32x4* y4, int64_t M, int n4, int rows, const SoftmaxStats& st,
                                hipStream_t s) {
   const bool full = n4 == kVpl * kWave;
+  if (kVpl <= 4 && rows == 0) {
+    const dim3 grid(static_cast<unsigned>((M + 7) / 8));
+    if (full)
+      softmax_rows_f32_reg<kVpl, true, 2, 4><<<grid, dim3(256), 0, s>>>(x4, y4, M, n4, st);
+    else
+      softmax_rows_f32_reg<kVpl, false, 2, 4><<<grid, dim3(256), 0, s>>>(x4, y4, M, n4, st);
+    return;
+  }
+  if (rows == 0) rows = 4;
   if (kVpl <= 4 && rows == 4) {
     const dim3 grid(static_cast<unsigned>((M + 3) / 4));
     if (full)
@@ -1268,7 +1279,7 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
       return hipGetLastError();
     }
   }
-  const int rows = rows_per_wg > 0 ? rows_per_wg : 4;
+  const int rows = rows_per_wg > 0 ? rows_per_wg : 0;  // 0: the register kernels choose
   if (M > 0x7fffffffLL) return hipErrorInvalidValue;  // grid.x limit of the row-per-workgroup fallback
   const bool vec = (N % 4 == 0) && (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0);
   // rows of a non-vector shape split at the same 16-byte boundaries in x and y

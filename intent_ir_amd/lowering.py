@@ -610,15 +610,18 @@ def _softmax_launch(M: int, N: int, rows: int) -> HipLaunch:
             g *= 2
         launch = HipLaunch((max(1, _cdiv(M * g, 256)), 1, 1), (256, 1, 1), 0)
     elif 0 < N <= 128 and not rows:  # short rows, N % 4 != 0: g lanes per row, up to 4 elements
-        # each, 2 rows per group; the workgroup's rows staged in LDS (8 KiB + 16 B)
+        # each, 2 rows per group; the workgroup's rows staged in LDS (8 KiB + 144 B: the run's
+        # offset in its 128-byte line and one vector of slack)
         g = 1
         while 4 * g < N:
             g *= 2
-        launch = HipLaunch((max(1, _cdiv(M * g, 512)), 1, 1), (256, 1, 1), 4 * (2048 + 4))
+        launch = HipLaunch((max(1, _cdiv(M * g, 512)), 1, 1), (256, 1, 1), 4 * (2048 + 36))
     elif N % 4 == 0 and N <= 4096:  # 4 rows per workgroup unless a knob says otherwise: a wave per
-        # row, or for N <= 1024 and 4 rows two waves of two rows each
+        # row, or for N <= 1024 two rows per wave: four waves (8 rows) by default, two for a knob of 4
         launch = _row_launch(M, rows or 4)
-        if N <= 1024 and (rows or 4) == 4:
+        if N <= 1024 and not rows:
+            launch = HipLaunch((max(1, _cdiv(M, 8)), 1, 1), (256, 1, 1), 0)
+        elif N <= 1024 and rows == 4:
             launch = HipLaunch(launch.grid, (128, 1, 1), 0)
     elif N % 4 == 0 and N <= 65536:  # kW waves per row, one row per workgroup, partials in LDS
         kw = next(w for w in (2, 4, 8, 16) if N // 4 <= 1024 * w)
@@ -771,7 +774,7 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
         while 8 * g < N:
             g *= 2
         slots = 5 if N <= 5 * g else 8
-        launch = HipLaunch((max(1, _cdiv(M * g, 1024)), 1, 1), (256, 1, 1), 2 * (1024 * slots + 8) + 2 * 4 * 8 * g)
+        launch = HipLaunch((max(1, _cdiv(M * g, 1024)), 1, 1), (256, 1, 1), 2 * (1024 * slots + 72) + 2 * 4 * 8 * g)
     elif 0 < N <= 4096 + 7:  # N % 8 != 0: 8 row classes x J workgroups of 4 waves, w and b per class in LDS
         J = min(128, _cdiv(_cdiv(M, 8), 4))
         launch = HipLaunch((8 * max(1, J), 1, 1), (256, 1, 1), 2 * 512 * 16)

@@ -367,7 +367,7 @@ def test_library_rejects_bad_arguments_without_a_device():
 
 
 @pytest.mark.parametrize("M,N,grid,block,lds", [
-    (8192, 4099, 1024, 256, 16384), (3, 1029, 8, 256, 16384), (64, 7, 1, 256, 16464), (1000, 100, 16, 256, 17424), (1000, 33, 8, 256, 10768),
+    (8192, 4099, 1024, 256, 16384), (3, 1029, 8, 256, 16384), (64, 7, 1, 256, 16592), (1000, 100, 16, 256, 17552), (1000, 33, 8, 256, 10896),
     (1000, 256, 63, 256, 0), (1000, 64, 16, 256, 0), (1000, 257, 256, 256, 16384),
     (8192, 4104, 1024, 1024, 128), (8192, 8191, 8192, 128, 16), (5, 65537, 5, 1024, 128), (5, 65545, 5, 256, 16)])
 def test_layernorm_launch_descriptor(M, N, grid, block, lds):
@@ -395,12 +395,13 @@ def test_reduce_any_launch_descriptor(dt, M, N, grid, block):
 
 
 @pytest.mark.parametrize("M,N,grid,block,lds", [
-    (1000, 31, 16, 256, 8208), (1000, 127, 63, 256, 8208), (5, 1, 1, 256, 8208), (1000, 32, 32, 256, 0),
+    (1000, 31, 16, 256, 8336), (1000, 127, 63, 256, 8336), (5, 1, 1, 256, 8336), (1000, 32, 32, 256, 0),
     (1000, 128, 125, 256, 0), (1000, 129, 1000, 64, 0)])
 def test_softmax_short_row_launch_descriptor(M, N, grid, block, lds):
     """Short rows (up to 128 floats) run several per wave: N / 4 lanes per row rounded up to a
     power of two for aligned rows; for the others one lane per 4 elements, two rows per group and
-    the workgroup's rows staged in LDS (8 KiB + 16 B).  Longer rows not 16-byte aligned take a
+    the workgroup's rows staged in LDS (8 KiB + 144 B: the run's offset in its 128-byte line,
+    one vector of slack).  Longer rows not 16-byte aligned take a
     wave per row."""
     k = lower_intent_to_hip_kernel(WORKLOADS["softmax"].ir(), shape_bindings={"M": M, "N": N})
     assert (k.launch.grid[0], k.launch.block[0], k.launch.lds_bytes) == (grid, block, lds)
