@@ -961,8 +961,8 @@ hipError_t launch_gemm_fast(const uint16_t* A, const uint16_t* B, const float* b
                             int64_t K, bool transpose_a, bool transpose_b, int relu, int tile, hipStream_t s,
                             bool c_unaligned) {
   const bool small = (tile == 0 ? gemm_fast_tile_extent(M, N) : tile) == 128, cu = N % 8 != 0 || c_unaligned;
-  // whole 256x256 tiles and K in 64-k slices: the 16x16x32 kernel (gemm_m16.hip), whose sums
-  // are bit-identical to this file's
+  // 256x256 tiles and K in 64-k slices: the 16x16x32 kernel (gemm_m16.hip), whose sums are
+  // bit-identical to this file's
   if (!small && !cu && gemm_m16_fits(M, N, K, transpose_a, A, B, C))
     return launch_gemm_m16(A, B, bias, C, M, N, K, transpose_b, relu, s);
   if (small && cu)

@@ -1,4 +1,4 @@
-// bf16 GEMM for whole 256x256 tiles on v_mfma_f32_16x16x32_bf16 (C = act(A @ B + bias),
+// bf16 GEMM in 256x256 tiles on v_mfma_f32_16x16x32_bf16 (C = act(A @ B + bias),
 // A [M, K] row-major, B [K, N] or, transposed, [N, K]; f32 accumulation; C bf16, round to
 // nearest even).
 //
@@ -19,9 +19,10 @@
 // during the previous step, in its first six quarters (a quarter = 8 MFMAs), so that the last
 // read has landed before the barrier that opens the next slice.
 //
-// Shapes: M % 256 == 0, N % 256 == 0, K % 64 == 0 (K >= 64), A, B and C 16-byte aligned, and
-// the 32-bit per-lane copy offsets in range (K * 512 and N * 128 below 2^32); the dispatcher
-// sends everything else to gemm_fast.hip.
+// Shapes: any M, N % 8 == 0, K % 64 == 0 (K >= 64), A, B and C 16-byte aligned, and the 32-bit
+// per-lane copy offsets in range (K * 512 and N * 128 below 2^32); the dispatcher sends
+// everything else to gemm_fast.hip.  M or N not a multiple of 256 leaves edge tiles, which copy
+// through range-checked descriptors and mask their stores (the EDGE kernel below).
 //
 // Layout in a stage: A as [256 rows][64 k], 128-byte rows; B given as [K, N] as [64 k][256 n],
 // 512-byte rows; B given as [N, K] as [256 n][64 k] like A.  Copies are gfx950 direct-to-LDS
@@ -44,6 +45,7 @@ namespace ihip {
 namespace m16 {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x8_t __attribute__((ext_vector_type(8)));
@@ -81,6 +83,21 @@ __device__ __forceinline__ int kmaj_logical(int p, int k) {
 
 __device__ __forceinline__ void dma16(const uint16_t* sbase, uint32_t voff, uint32_t lds_addr) {
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
+}
+
+// Raw buffer descriptor over [base, end): loads at byte offsets past end - base return zero.
+__device__ __forceinline__ i32x4_t rsrc_of(const uint16_t* base, const uint16_t* end) {
+  const int64_t left = (end - base) * 2;
+  const uint32_t records = left <= 0 ? 0u : left >= 0xffffffffll ? 0xffffffffu : static_cast<uint32_t>(left);
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  // word1: base address bits 47:32, stride 0; word3: 32-bit data format, raw (untyped) access
+  return i32x4_t{static_cast<int>(addr & 0xffffffffu), static_cast<int>((addr >> 32) & 0xffffu),
+                 static_cast<int>(records), 0x00020000};
+}
+
+// The direct-to-LDS copy through a descriptor, for tiles that reach past a tensor's last row.
+__device__ __forceinline__ void dma16(const i32x4_t& rsrc, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds_addr) : "memory");
 }
 
 template <int n>
@@ -175,7 +192,11 @@ __device__ __forceinline__ void read_slot(const lds_char_t* sa, const lds_char_t
   }
 }
 
-template <bool BKM, bool RELU>
+// EDGE: M or N not a multiple of 256.  Tiles that reach past the last row or column copy A and B
+// through descriptors that end at the tensor (rows past it read zeros; B columns past N, within
+// the tensor, read other columns' values, which only reach outputs that are not stored) and
+// mask their stores; the other tiles run the plain copies.
+template <bool BKM, bool RELU, bool EDGE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_m16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                           const float* __restrict__ bias, uint16_t* __restrict__ C, int64_t M, int64_t N, int64_t K,
@@ -211,16 +232,30 @@ void gemm_bf16_m16_kernel(const uint16_t* __restrict__ A, const uint16_t* __rest
     const int gsz = (tiles_m - first_m) < kGroupRows ? (tiles_m - first_m) : kGroupRows;
     const int tm = first_m + (bid % per_group) % gsz, tn = (bid % per_group) / gsz;
     const int64_t m0 = static_cast<int64_t>(tm) * kTile, n0 = static_cast<int64_t>(tn) * kTile;
-    const float bias_v = threadIdx.x < kTile && bias != nullptr ? bias[n0 + threadIdx.x] : 0.0f;
+    const float bias_v = threadIdx.x < kTile && bias != nullptr && (!EDGE || n0 + threadIdx.x < N)
+                             ? bias[n0 + threadIdx.x]
+                             : 0.0f;
 
     const uint16_t* const a_rows = A + m0 * K;
     const uint16_t* const b_base = BKM ? B + n0 : B + n0 * K;
+    auto tile = [&](auto edge_tag) {
+    constexpr bool kEdge = decltype(edge_tag)::value;
     auto copy_a = [&](int s, int ra, int c) {
-      dma16(a_rows + static_cast<int64_t>(s) * kDK, ca[c], lds_addr + ra * kOpBytes + (4 * c + wave) * 1024);
+      const uint16_t* const base = a_rows + static_cast<int64_t>(s) * kDK;
+      const uint32_t dst = lds_addr + ra * kOpBytes + (4 * c + wave) * 1024;
+      if constexpr (kEdge)
+        dma16(rsrc_of(base, A + M * K), ca[c], dst);
+      else
+        dma16(base, ca[c], dst);
     };
     auto copy_b = [&](int s, int c) {
       const int64_t k0 = static_cast<int64_t>(s) * kDK;
-      dma16(BKM ? b_base + k0 * N : b_base + k0, cb[c], lds_addr + kOffB + (s & 1) * kOpBytes + (4 * c + wave) * 1024);
+      const uint16_t* const base = BKM ? b_base + k0 * N : b_base + k0;
+      const uint32_t dst = lds_addr + kOffB + (s & 1) * kOpBytes + (4 * c + wave) * 1024;
+      if constexpr (kEdge)
+        dma16(rsrc_of(base, B + K * N), cb[c], dst);
+      else
+        dma16(base, cb[c], dst);
     };
 
     f32x4_t acc[8][8];
@@ -364,7 +399,17 @@ void gemm_bf16_m16_kernel(const uint16_t* __restrict__ A, const uint16_t* __rest
     for (int i = 0; i < kTile / (4 * kRowsPerStore); ++i) {
       const int row = (i * 4 + wave) * kRowsPerStore + lane / kLanesPerRow;
       const u32x4 v = *(const lds_u32x4_t*)(ct + row * kCPitch + chunk * 16);
-      *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + chunk * 8) = v;
+      if (!kEdge || (m0 + row < M && n0 + chunk * 8 < N))
+        *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + chunk * 8) = v;
+    }
+    };
+    if constexpr (EDGE) {
+      if (m0 + kTile > M || n0 + kTile > N)
+        tile(std::true_type{});
+      else
+        tile(std::false_type{});
+    } else {
+      tile(std::false_type{});
     }
     // every wave has read its rows of the staged tile before the next tile's copies land in LDS
     __syncthreads();
@@ -388,36 +433,40 @@ int device_cus() {
 
 }  // namespace m16
 
-// True when this kernel takes the launch: whole tiles, K a multiple of 64, A given as [M, K],
-// 16-byte aligned tensors, 32-bit copy offsets, and at most 2^30 tiles (the persistent loop's
-// tile index plus the grid size stays within int).
+// True when this kernel takes the launch: K a multiple of 64, N of 8 (16-byte rows of B and C),
+// A given as [M, K], 16-byte aligned tensors, 32-bit copy offsets, and at most 2^30 tiles (the
+// persistent loop's tile index plus the grid size stays within int).
 bool gemm_m16_fits(int64_t M, int64_t N, int64_t K, bool transpose_a, const void* A, const void* B, const void* C) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C);
   const int64_t lim = int64_t(1) << 32;
-  return !transpose_a && M > 0 && N > 0 && K >= m16::kDK && M % m16::kTile == 0 && N % m16::kTile == 0 &&
-         K % m16::kDK == 0 && (al & 15) == 0 && K * 512 < lim && N * 128 < lim &&
-         (M / m16::kTile) * (N / m16::kTile) <= (int64_t(1) << 30);
+  const int64_t tm = (M + m16::kTile - 1) / m16::kTile, tn = (N + m16::kTile - 1) / m16::kTile;
+  return !transpose_a && M > 0 && N > 0 && K >= m16::kDK && N % 8 == 0 && K % m16::kDK == 0 && (al & 15) == 0 &&
+         K * 512 < lim && N * 128 < lim && tm * tn <= (int64_t(1) << 30);
 }
 
 hipError_t launch_gemm_m16(const uint16_t* A, const uint16_t* B, const float* bias, uint16_t* C, int64_t M, int64_t N,
                            int64_t K, bool transpose_b, int relu, hipStream_t s) {
-  const int tm = static_cast<int>(M / m16::kTile), tn = static_cast<int>(N / m16::kTile);
+  const int tm = static_cast<int>((M + m16::kTile - 1) / m16::kTile), tn = static_cast<int>((N + m16::kTile - 1) / m16::kTile);
+  const bool edge = M % m16::kTile != 0 || N % m16::kTile != 0;
   const int64_t tiles = static_cast<int64_t>(tm) * tn;
   const int cus = m16::device_cus();
   if (cus <= 0) return hipErrorInvalidDevice;
   // one workgroup per CU (the kernel holds all of a CU's LDS and registers)
   const dim3 grid(static_cast<unsigned>(tiles < cus ? tiles : cus)), block(256);
+#define IHIP_M16_LAUNCH(BKM, RELU, EDGE) \
+  m16::gemm_bf16_m16_kernel<BKM, RELU, EDGE><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, tm, tn)
   if (transpose_b) {
     if (relu)
-      m16::gemm_bf16_m16_kernel<false, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, tm, tn);
+      edge ? IHIP_M16_LAUNCH(false, true, true) : IHIP_M16_LAUNCH(false, true, false);
     else
-      m16::gemm_bf16_m16_kernel<false, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, tm, tn);
+      edge ? IHIP_M16_LAUNCH(false, false, true) : IHIP_M16_LAUNCH(false, false, false);
   } else {
     if (relu)
-      m16::gemm_bf16_m16_kernel<true, true><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, tm, tn);
+      edge ? IHIP_M16_LAUNCH(true, true, true) : IHIP_M16_LAUNCH(true, true, false);
     else
-      m16::gemm_bf16_m16_kernel<true, false><<<grid, block, 0, s>>>(A, B, bias, C, M, N, K, tm, tn);
+      edge ? IHIP_M16_LAUNCH(true, false, true) : IHIP_M16_LAUNCH(true, false, false);
   }
+#undef IHIP_M16_LAUNCH
   return hipGetLastError();
 }
 

@@ -328,8 +328,8 @@ def _match_gemm(c: _Ctx) -> Optional[HipLoweredKernel]:
     t = tile or _gemm_tile_extent(M, N)
     grid = (max(1, _cdiv(M, t) * _cdiv(N, t)) * S, 1, 1)  # a split: tiles x segments workgroups
     if full and S == 1 and t == 256 and _gemm_m16_fits(M, N, K, ta):
-        # whole 256x256 tiles, K in 64-k slices: gemm_m16.hip (three A and two B slices of 32 KiB),
-        # a persistent grid of one workgroup per CU (MI355X: 256) taking the tiles in turn
+        # 256x256 tiles, K in 64-k slices: gemm_m16.hip (three A and two B slices of 32 KiB), a
+        # persistent grid of one workgroup per CU (MI355X: 256) taking the tiles in turn
         launch = HipLaunch((min(grid[0], MI355X_CUS), 1, 1), (256, 1, 1), 163840)
     elif full or packed:
         launch = HipLaunch(grid, (256, 1, 1), _gemm_fast_lds(t, ta2 if packed else ta))
@@ -377,8 +377,8 @@ def _gemm_fast_fits(M: int, N: int, K: int, ta: bool, tb: bool, packed: bool = F
 
 def _gemm_m16_fits(M: int, N: int, K: int, ta: bool) -> bool:
     """gemm_m16.hip gemm_m16_fits for 16-byte aligned tensors (C aligned too)."""
-    return (not ta and M > 0 and N > 0 and K >= 64 and M % 256 == 0 and N % 256 == 0 and K % 64 == 0
-            and K * 512 < (1 << 32) and N * 128 < (1 << 32) and (M // 256) * (N // 256) <= (1 << 30))
+    return (not ta and M > 0 and N > 0 and K >= 64 and N % 8 == 0 and K % 64 == 0
+            and K * 512 < (1 << 32) and N * 128 < (1 << 32) and _cdiv(M, 256) * _cdiv(N, 256) <= (1 << 30))
 
 
 def _gemm_fast_lds(tile: int, ta: bool) -> int:

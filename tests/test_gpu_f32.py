@@ -323,6 +323,40 @@ def test_elementwise_programs_past_the_interpreter_limits(hip, make, arg):
 
 
 # ------------------------------------------------------------------ bf16 GEMM: 16x16x32 whole-tile kernel
+@pytest.mark.parametrize("M,N,K", [(1000, 4096, 256), (4096, 1000, 320), (1000, 1000, 64), (8000, 8192, 512),
+                                   (300, 264, 128), (257, 8, 64), (256, 264, 64), (513, 520, 192), (1, 2048, 128)])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_gemm_m16_edge_tiles_match_the_ring_kernel_bit_for_bit(hip, M, N, K, tb):
+    """M or N not a multiple of 256 (N % 8 == 0, K % 64 == 0) with 256x256 tiles: the 16x16x32
+    kernel copies edge tiles through descriptors that end at the tensor and masks their stores.
+    A C base 2 bytes off a 16-byte boundary sends the same product to the ring kernel; the two
+    agree bit for bit, and nothing past C's last element is written."""
+    torch = _torch()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(M * 7 + N + K + tb)
+    a = torch.randn((M, K), device="cuda", generator=g).bfloat16()
+    b = torch.randn((N, K) if tb else (K, N), device="cuda", generator=g).bfloat16()
+    bias = torch.randn((N,), device="cuda", generator=g)
+    sentinel = -12345
+    for relu in (1, 0):
+        c1buf = torch.full((M * N + 64,), sentinel, device="cuda", dtype=torch.int16)
+        c2buf = torch.full((M * N + 72,), sentinel, device="cuda", dtype=torch.int16)
+        c1, c2 = c1buf[:M * N], c2buf[1:1 + M * N]
+        print(f"[case] gemm m16 edge vs ring M={M} N={N} K={K} tb={tb} relu={relu}", flush=True)
+        for c in (c1, c2):
+            _ok(hip, hip.ihip_gemm_bf16_bias_relu_ex(P(a.data_ptr()), P(b.data_ptr()), P(bias.data_ptr()),
+                                                     P(c.data_ptr()), M, N, K, 0, tb, relu, 256, _stream()))
+        torch.cuda.synchronize()
+        assert torch.equal(c1, c2)
+        assert bool((c1buf[M * N:] == sentinel).all()) and bool((c2buf[1 + M * N:] == sentinel).all())
+        assert int(c2buf[0]) == sentinel
+        if M * N <= 1 << 22:  # and against a float32 evaluation (bf16 output rounding)
+            ref = a.float() @ (b.float().t() if tb else b.float()) + bias
+            ref = torch.relu(ref) if relu else ref
+            got = c1.view(torch.bfloat16).reshape(M, N).float()
+            assert torch.allclose(got, ref, rtol=2e-2, atol=2e-2)
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (256, 512, 128), (512, 768, 192), (1024, 1024, 1024),
                                    (2048, 1536, 4096), (256, 4096, 320), (4352, 4096, 128), (4096, 4352, 192),
                                    (8192, 8192, 64)])
