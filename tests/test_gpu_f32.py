@@ -329,8 +329,9 @@ def test_elementwise_programs_past_the_interpreter_limits(hip, make, arg):
 def test_gemm_m16_edge_tiles_match_the_ring_kernel_bit_for_bit(hip, M, N, K, tb):
     """M or N not a multiple of 256 (N % 8 == 0, K % 64 == 0) with 256x256 tiles: the 16x16x32
     kernel copies edge tiles through descriptors that end at the tensor and masks their stores.
-    A C base 2 bytes off a 16-byte boundary sends the same product to the ring kernel; the two
-    agree bit for bit, and nothing past C's last element is written."""
+    A C base 2 bytes off a 16-byte boundary sends the same product to the guarded kernel
+    (gemm.hip), and tile knob 128 to the ring kernel; the three agree bit for bit, and nothing
+    past C's last element is written."""
     torch = _torch()
     g = torch.Generator(device="cuda")
     g.manual_seed(M * 7 + N + K + tb)
@@ -341,13 +342,14 @@ def test_gemm_m16_edge_tiles_match_the_ring_kernel_bit_for_bit(hip, M, N, K, tb)
     for relu in (1, 0):
         c1buf = torch.full((M * N + 64,), sentinel, device="cuda", dtype=torch.int16)
         c2buf = torch.full((M * N + 72,), sentinel, device="cuda", dtype=torch.int16)
-        c1, c2 = c1buf[:M * N], c2buf[1:1 + M * N]
-        print(f"[case] gemm m16 edge vs ring M={M} N={N} K={K} tb={tb} relu={relu}", flush=True)
-        for c in (c1, c2):
+        c3buf = torch.full((M * N + 64,), sentinel, device="cuda", dtype=torch.int16)
+        c1, c2, c3 = c1buf[:M * N], c2buf[1:1 + M * N], c3buf[:M * N]
+        print(f"[case] gemm m16 edge vs guarded and ring M={M} N={N} K={K} tb={tb} relu={relu}", flush=True)
+        for c, tile in ((c1, 256), (c2, 256), (c3, 128)):
             _ok(hip, hip.ihip_gemm_bf16_bias_relu_ex(P(a.data_ptr()), P(b.data_ptr()), P(bias.data_ptr()),
-                                                     P(c.data_ptr()), M, N, K, 0, tb, relu, 256, _stream()))
+                                                     P(c.data_ptr()), M, N, K, 0, tb, relu, tile, _stream()))
         torch.cuda.synchronize()
-        assert torch.equal(c1, c2)
+        assert torch.equal(c1, c2) and torch.equal(c1, c3)
         assert bool((c1buf[M * N:] == sentinel).all()) and bool((c2buf[1 + M * N:] == sentinel).all())
         assert int(c2buf[0]) == sentinel
         if M * N <= 1 << 22:  # and against a float32 evaluation (bf16 output rounding)
@@ -362,10 +364,11 @@ def test_gemm_m16_edge_tiles_match_the_ring_kernel_bit_for_bit(hip, M, N, K, tb)
                                    (8192, 8192, 64)])
 @pytest.mark.parametrize("relu", [1, 0])
 def test_gemm_m16_matches_the_ring_kernel_bit_for_bit(hip, M, N, K, relu):
-    """Whole 256x256 tiles with K % 64 == 0 run gemm_m16.hip (16x16x32 MFMAs); a C base 2 bytes
-    off a 16-byte boundary (B given as [N, K]) sends the same product to gemm_fast.hip's ring
-    kernel (32x32x16 MFMAs, 2-byte stores).  The sums are identical bits (1, 2, 3 and more
-    64-k slices, so the prologue, the last two slices and the steady loop are all covered).  The
+    """Whole 256x256 tiles with K % 64 == 0 (tile knob 256) run gemm_m16.hip (16x16x32 MFMAs);
+    tile knob 128 sends the same product to gemm_fast.hip's ring kernel (32x32x16 MFMAs), and a
+    C base 2 bytes off a 16-byte boundary to the guarded kernel (gemm.hip, 2-byte stores).  The
+    three agree bit for bit, with B given as [N, K] and as [K, N] (1, 2, 3 and more 64-k slices,
+    so the prologue, the last two slices and the steady loop are all covered).  The 16x16x32
     grid is one workgroup per CU: 272 and 1024 tiles make workgroups take several tiles each, in
     uneven numbers for 272."""
     torch = _torch()
@@ -373,18 +376,17 @@ def test_gemm_m16_matches_the_ring_kernel_bit_for_bit(hip, M, N, K, relu):
     g.manual_seed(M + N + K)
     a = torch.randn((M, K), device="cuda", generator=g).bfloat16()
     bt = torch.randn((N, K), device="cuda", generator=g).bfloat16()
+    b = bt.t().contiguous()  # the same product with B as [K, N]: the K-major form of the kernels
     bias = torch.randn((N,), device="cuda", generator=g)
-    c1 = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
-    cbuf = torch.empty(M * N + 8, device="cuda", dtype=torch.bfloat16)
-    c2 = cbuf[1:1 + M * N]
-    print(f"[case] gemm m16 vs ring M={M} N={N} K={K} relu={relu}", flush=True)
-    for c in (c1, c2):
-        _ok(hip, hip.ihip_gemm_bf16_bias_relu_t(P(a.data_ptr()), P(bt.data_ptr()), P(bias.data_ptr()),
-                                                P(c.data_ptr()), M, N, K, 0, 1, relu, _stream()))
-    b = bt.t().contiguous()  # the same product with B as [K, N]: the K-major form of the kernel
-    c3 = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
-    _ok(hip, hip.ihip_gemm_bf16_bias_relu_t(P(a.data_ptr()), P(b.data_ptr()), P(bias.data_ptr()), P(c3.data_ptr()),
-                                            M, N, K, 0, 0, relu, _stream()))
+    print(f"[case] gemm m16 vs ring vs guarded M={M} N={N} K={K} relu={relu}", flush=True)
+    outs = []
+    for tb, bx in ((1, bt), (0, b)):
+        for tile, off in ((256, 0), (128, 0), (0, 1)):
+            cbuf = torch.empty(M * N + 8, device="cuda", dtype=torch.bfloat16)
+            c = cbuf[off:off + M * N]
+            _ok(hip, hip.ihip_gemm_bf16_bias_relu_ex(P(a.data_ptr()), P(bx.data_ptr()), P(bias.data_ptr()),
+                                                     P(c.data_ptr()), M, N, K, 0, tb, relu, tile, _stream()))
+            outs.append(c)
     torch.cuda.synchronize()
-    assert torch.equal(c1.view(torch.int16), c2.view(torch.int16).reshape(M, N))
-    assert torch.equal(c1.view(torch.int16), c3.view(torch.int16))
+    for c in outs[1:]:
+        assert torch.equal(outs[0].view(torch.int16), c.view(torch.int16))
