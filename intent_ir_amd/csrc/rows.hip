@@ -1768,7 +1768,10 @@ __global__ __launch_bounds__(64 * kLnLdsWaves) __attribute__((amdgpu_waves_per_e
           const float d = __builtin_fmaf(static_cast<float>(xv[i][e]), unit2, -mean);
           o[e] = static_cast<_Float16>(__builtin_fmaf(d * rstd, static_cast<float>(wv[e]), static_cast<float>(bv[e])));
         }
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), yb + i * kWave);
+        // an ordinary store: the row's 128-byte lines are shared with the stores of the next
+        // instruction and of the neighbouring rows, which the L2 can then merge (2.5% faster
+        // than non-temporal stores at [8192, 4099])
+        yb[i * kWave] = __builtin_bit_cast(u32x4, o);
       }
     }
     if (lane < head) yr[lane] = f32_to_f16_rne(__builtin_fmaf((hx - mean) * rstd, hw, hb));
