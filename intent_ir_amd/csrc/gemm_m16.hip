@@ -239,169 +239,169 @@ void gemm_bf16_m16_kernel(const uint16_t* __restrict__ A, const uint16_t* __rest
     const uint16_t* const a_rows = A + m0 * K;
     const uint16_t* const b_base = BKM ? B + n0 : B + n0 * K;
     auto tile = [&](auto edge_tag) {
-    constexpr bool kEdge = decltype(edge_tag)::value;
-    auto copy_a = [&](int s, int ra, int c) {
-      const uint16_t* const base = a_rows + static_cast<int64_t>(s) * kDK;
-      const uint32_t dst = lds_addr + ra * kOpBytes + (4 * c + wave) * 1024;
-      if constexpr (kEdge)
-        dma16(rsrc_of(base, A + M * K), ca[c], dst);
-      else
-        dma16(base, ca[c], dst);
-    };
-    auto copy_b = [&](int s, int c) {
-      const int64_t k0 = static_cast<int64_t>(s) * kDK;
-      const uint16_t* const base = BKM ? b_base + k0 * N : b_base + k0;
-      const uint32_t dst = lds_addr + kOffB + (s & 1) * kOpBytes + (4 * c + wave) * 1024;
-      if constexpr (kEdge)
-        dma16(rsrc_of(base, B + K * N), cb[c], dst);
-      else
-        dma16(base, cb[c], dst);
-    };
+      constexpr bool kEdge = decltype(edge_tag)::value;
+      auto copy_a = [&](int s, int ra, int c) {
+        const uint16_t* const base = a_rows + static_cast<int64_t>(s) * kDK;
+        const uint32_t dst = lds_addr + ra * kOpBytes + (4 * c + wave) * 1024;
+        if constexpr (kEdge)
+          dma16(rsrc_of(base, A + M * K), ca[c], dst);
+        else
+          dma16(base, ca[c], dst);
+      };
+      auto copy_b = [&](int s, int c) {
+        const int64_t k0 = static_cast<int64_t>(s) * kDK;
+        const uint16_t* const base = BKM ? b_base + k0 * N : b_base + k0;
+        const uint32_t dst = lds_addr + kOffB + (s & 1) * kOpBytes + (4 * c + wave) * 1024;
+        if constexpr (kEdge)
+          dma16(rsrc_of(base, B + K * N), cb[c], dst);
+        else
+          dma16(base, cb[c], dst);
+      };
 
-    f32x4_t acc[8][8];
+      f32x4_t acc[8][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{};
-    acc_fence<true>(acc[0]);
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{};
+      acc_fence<true>(acc[0]);
 #pragma unroll
-    for (int i = 1; i < 8; ++i) acc_fence<false>(acc[i]);
+      for (int i = 1; i < 8; ++i) acc_fence<false>(acc[i]);
 
-    const int KT = static_cast<int>(K / kDK);
+      const int KT = static_cast<int>(K / kDK);
 #pragma unroll
-    for (int c = 0; c < kCopies; ++c) copy_a(0, 0, c);
+      for (int c = 0; c < kCopies; ++c) copy_a(0, 0, c);
 #pragma unroll
-    for (int c = 0; c < kCopies; ++c) copy_b(0, c);
-    if (KT > 1) {
+      for (int c = 0; c < kCopies; ++c) copy_b(0, c);
+      if (KT > 1) {
 #pragma unroll
-      for (int c = 0; c < kCopies; ++c) copy_a(1, 1, c);
+        for (int c = 0; c < kCopies; ++c) copy_a(1, 1, c);
 #pragma unroll
-      for (int c = 0; c < kCopies; ++c) copy_b(1, c);
-      wait_vm<2 * kCopies>();
-    } else {
-      wait_vm<0>();
-    }
-    __syncthreads();
-    Frag f[2];
+        for (int c = 0; c < kCopies; ++c) copy_b(1, c);
+        wait_vm<2 * kCopies>();
+      } else {
+        wait_vm<0>();
+      }
+      __syncthreads();
+      Frag f[2];
 #pragma unroll
-    for (int sl = 0; sl < kSlots; ++sl) read_slot<BKM>(lds, lds + kOffB, 0, oa, obc, obk, f[0], sl);
+      for (int sl = 0; sl < kSlots; ++sl) read_slot<BKM>(lds, lds + kOffB, 0, oa, obc, obk, f[0], sl);
 
-    // Copy schedule per slice kt (16 quarters of 8 MFMAs): quarters 0-7 copy A slice kt+2 into
-    // the region slice kt-1 used; quarters 8-15, after the barrier that closes slice kt (start of
-    // quarter 8), copy B slice kt+2 into the stage slice kt used.  The barrier waits for A and B
-    // of slice kt+1 (issued during slice kt-1): only A slice kt+2's copies were issued since.
-    auto slice = [&](int kt, int ra, auto more_tag, auto more2_tag) {
-      constexpr bool kMore = decltype(more_tag)::value;
-      constexpr bool kMore2 = decltype(more2_tag)::value;
-      const int ra1 = ra == kRegionsA - 1 ? 0 : ra + 1, ra2 = ra1 == kRegionsA - 1 ? 0 : ra1 + 1;
-      const lds_char_t* sa = lds + ra * kOpBytes;
-      const lds_char_t* sb = lds + kOffB + (kt & 1) * kOpBytes;
-      const lds_char_t* na = lds + ra1 * kOpBytes;
-      const lds_char_t* nb = lds + kOffB + ((kt + 1) & 1) * kOpBytes;
+      // Copy schedule per slice kt (16 quarters of 8 MFMAs): quarters 0-7 copy A slice kt+2 into
+      // the region slice kt-1 used; quarters 8-15, after the barrier that closes slice kt (start of
+      // quarter 8), copy B slice kt+2 into the stage slice kt used.  The barrier waits for A and B
+      // of slice kt+1 (issued during slice kt-1): only A slice kt+2's copies were issued since.
+      auto slice = [&](int kt, int ra, auto more_tag, auto more2_tag) {
+        constexpr bool kMore = decltype(more_tag)::value;
+        constexpr bool kMore2 = decltype(more2_tag)::value;
+        const int ra1 = ra == kRegionsA - 1 ? 0 : ra + 1, ra2 = ra1 == kRegionsA - 1 ? 0 : ra1 + 1;
+        const lds_char_t* sa = lds + ra * kOpBytes;
+        const lds_char_t* sb = lds + kOffB + (kt & 1) * kOpBytes;
+        const lds_char_t* na = lds + ra1 * kOpBytes;
+        const lds_char_t* nb = lds + kOffB + ((kt + 1) & 1) * kOpBytes;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        Frag& cur = f[s];
-        Frag& nxt = f[s ^ 1];
-        const bool last = s == 1;
-        const bool rd = !last || kMore;
-        const lds_char_t* rda = last ? na : sa;
-        const lds_char_t* rdb = last ? nb : sb;
-        const int rs = last ? 0 : 1;
+        for (int s = 0; s < 2; ++s) {
+          Frag& cur = f[s];
+          Frag& nxt = f[s ^ 1];
+          const bool last = s == 1;
+          const bool rd = !last || kMore;
+          const lds_char_t* rda = last ? na : sa;
+          const lds_char_t* rdb = last ? nb : sb;
+          const int rs = last ? 0 : 1;
+#pragma unroll
+          for (int mi = 0; mi < 8; ++mi) {
+            __builtin_amdgcn_sched_barrier(0);
+            const bool pre = last && mi == 0 && kMore;
+            if (pre) {
+#pragma unroll
+              for (int q = 0; q < kPre; ++q)
+                mfma16(acc[mi][q], cur.b[q], cur.a[mi]);
+              if constexpr (kMore2)
+                wait_vm<kCopies>();
+              else
+                wait_vm<0>();
+              __syncthreads();
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            const int from = pre ? kPre : 0;
+            // fixed order: MFMA, LDS read, MFMA, LDS read, ..., each fenced so that the scheduler
+            // keeps one live range per accumulator
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              if (q >= from) {
+                mfma16(acc[mi][q], cur.b[q], cur.a[mi]);
+                __builtin_amdgcn_sched_barrier(0);
+              }
+              const int r = q - from;
+              const int lo = mi < kReadQ ? mi * kSlots / kReadQ : kSlots;
+              const int hi = mi < kReadQ ? (mi + 1) * kSlots / kReadQ : kSlots;
+              if (rd && r >= 0 && lo + r < hi) {
+                read_slot<BKM>(rda, rdb, rs, oa, obc, obk, nxt, lo + r);
+                __builtin_amdgcn_sched_barrier(0);
+              }
+            }
+            const int qi = s * 8 + mi;
+            if (kMore2) {
+              __builtin_amdgcn_sched_barrier(0);
+              if (qi < 8)
+                copy_a(kt + 2, ra2, qi);
+              else
+                copy_b(kt + 2, qi - 8);
+            }
+          }
+        }
+      };
+      int kt = 0, ra = 0;
+      for (; kt + 2 < KT; ++kt) {
+        slice(kt, ra, std::true_type{}, std::true_type{});
+        ra = ra == kRegionsA - 1 ? 0 : ra + 1;
+      }
+      if (kt + 1 < KT) {
+        slice(kt, ra, std::true_type{}, std::false_type{});
+        ++kt;
+        ra = ra == kRegionsA - 1 ? 0 : ra + 1;
+      }
+      slice(kt, ra, std::false_type{}, std::false_type{});
+
+      // epilogue: bias + activation, the tile staged in LDS as bf16 rows, written out in 512-byte rows
+      acc_fence<true>(acc[0]);
+#pragma unroll
+      for (int i = 1; i < 8; ++i) acc_fence<false>(acc[i]);
+      __syncthreads();
+      float* bias_lds = reinterpret_cast<float*>(lds_raw + kTile * kCPitch);
+      if (threadIdx.x < kTile) bias_lds[threadIdx.x] = bias_v;
+      __syncthreads();
+      typedef __attribute__((address_space(3))) char lds_wchar_t;
+      lds_wchar_t* ct = (lds_wchar_t*)lds_raw;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int nl = wn * 128 + q * 16 + (lane >> 4) * 4;
+        const f32x4_t bv = *reinterpret_cast<const f32x4_t*>(&bias_lds[nl]);
 #pragma unroll
         for (int mi = 0; mi < 8; ++mi) {
-          __builtin_amdgcn_sched_barrier(0);
-          const bool pre = last && mi == 0 && kMore;
-          if (pre) {
+          const int ml = wm * 128 + mi * 16 + (lane & 15);
+          float v[4];
 #pragma unroll
-            for (int q = 0; q < kPre; ++q)
-              mfma16(acc[mi][q], cur.b[q], cur.a[mi]);
-            if constexpr (kMore2)
-              wait_vm<kCopies>();
-            else
-              wait_vm<0>();
-            __syncthreads();
-            __builtin_amdgcn_sched_barrier(0);
+          for (int e = 0; e < 4; ++e) {
+            v[e] = acc[mi][q][e] + bv[e];
+            if constexpr (RELU) v[e] = __builtin_elementwise_maximum(v[e], 0.0f);
           }
-          const int from = pre ? kPre : 0;
-          // fixed order: MFMA, LDS read, MFMA, LDS read, ..., each fenced so that the scheduler
-          // keeps one live range per accumulator
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            if (q >= from) {
-              mfma16(acc[mi][q], cur.b[q], cur.a[mi]);
-              __builtin_amdgcn_sched_barrier(0);
-            }
-            const int r = q - from;
-            const int lo = mi < kReadQ ? mi * kSlots / kReadQ : kSlots;
-            const int hi = mi < kReadQ ? (mi + 1) * kSlots / kReadQ : kSlots;
-            if (rd && r >= 0 && lo + r < hi) {
-              read_slot<BKM>(rda, rdb, rs, oa, obc, obk, nxt, lo + r);
-              __builtin_amdgcn_sched_barrier(0);
-            }
-          }
-          const int qi = s * 8 + mi;
-          if (kMore2) {
-            __builtin_amdgcn_sched_barrier(0);
-            if (qi < 8)
-              copy_a(kt + 2, ra2, qi);
-            else
-              copy_b(kt + 2, qi - 8);
-          }
+          const bf16x2_t lo = {static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1])};
+          const bf16x2_t hi = {static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
+          const u32x2 pk = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+          *(lds_u32x2_t*)(ct + ml * kCPitch + nl * 2) = pk;
         }
+        asm volatile("" ::: "memory");
       }
-    };
-    int kt = 0, ra = 0;
-    for (; kt + 2 < KT; ++kt) {
-      slice(kt, ra, std::true_type{}, std::true_type{});
-      ra = ra == kRegionsA - 1 ? 0 : ra + 1;
-    }
-    if (kt + 1 < KT) {
-      slice(kt, ra, std::true_type{}, std::false_type{});
-      ++kt;
-      ra = ra == kRegionsA - 1 ? 0 : ra + 1;
-    }
-    slice(kt, ra, std::false_type{}, std::false_type{});
-
-    // epilogue: bias + activation, the tile staged in LDS as bf16 rows, written out in 512-byte rows
-    acc_fence<true>(acc[0]);
-#pragma unroll
-    for (int i = 1; i < 8; ++i) acc_fence<false>(acc[i]);
-    __syncthreads();
-    float* bias_lds = reinterpret_cast<float*>(lds_raw + kTile * kCPitch);
-    if (threadIdx.x < kTile) bias_lds[threadIdx.x] = bias_v;
-    __syncthreads();
-    typedef __attribute__((address_space(3))) char lds_wchar_t;
-    lds_wchar_t* ct = (lds_wchar_t*)lds_raw;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int nl = wn * 128 + q * 16 + (lane >> 4) * 4;
-      const f32x4_t bv = *reinterpret_cast<const f32x4_t*>(&bias_lds[nl]);
-#pragma unroll
-      for (int mi = 0; mi < 8; ++mi) {
-        const int ml = wm * 128 + mi * 16 + (lane & 15);
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = acc[mi][q][e] + bv[e];
-          if constexpr (RELU) v[e] = __builtin_elementwise_maximum(v[e], 0.0f);
-        }
-        const bf16x2_t lo = {static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1])};
-        const bf16x2_t hi = {static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
-        const u32x2 pk = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
-        *(lds_u32x2_t*)(ct + ml * kCPitch + nl * 2) = pk;
-      }
-      asm volatile("" ::: "memory");
-    }
-    __syncthreads();
-    constexpr int kLanesPerRow = kTile / 8, kRowsPerStore = 64 / kLanesPerRow;
-    const int chunk = lane % kLanesPerRow;
+      __syncthreads();
+      constexpr int kLanesPerRow = kTile / 8, kRowsPerStore = 64 / kLanesPerRow;
+      const int chunk = lane % kLanesPerRow;
 #pragma unroll 4
-    for (int i = 0; i < kTile / (4 * kRowsPerStore); ++i) {
-      const int row = (i * 4 + wave) * kRowsPerStore + lane / kLanesPerRow;
-      const u32x4 v = *(const lds_u32x4_t*)(ct + row * kCPitch + chunk * 16);
-      if (!kEdge || (m0 + row < M && n0 + chunk * 8 < N))
-        *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + chunk * 8) = v;
-    }
+      for (int i = 0; i < kTile / (4 * kRowsPerStore); ++i) {
+        const int row = (i * 4 + wave) * kRowsPerStore + lane / kLanesPerRow;
+        const u32x4 v = *(const lds_u32x4_t*)(ct + row * kCPitch + chunk * 16);
+        if (!kEdge || (m0 + row < M && n0 + chunk * 8 < N))
+          *reinterpret_cast<u32x4*>(C + (m0 + row) * N + n0 + chunk * 8) = v;
+      }
     };
     if constexpr (EDGE) {
       if (m0 + kTile > M || n0 + kTile > N)
