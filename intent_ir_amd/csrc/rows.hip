@@ -1369,9 +1369,9 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 // live across the reduction).  kExact (n8 == 64 * kVpl and M % kLnRows == 0) drops the tail
 // masks.
 constexpr int kLnRows = 16;
-template <int kVpl, bool kExact>
 // Argument order: what the first loads need comes first (the first 56 bytes of arguments arrive
 // preloaded in SGPRs), rstd_out and eps, needed last, after.
+template <int kVpl, bool kExact>
 __global__ __launch_bounds__(64 * kLnRows) void layernorm_rows_f16_wave(
     const u32x4* __restrict__ x, const u32x4* __restrict__ w, const u32x4* __restrict__ b, u32x4* __restrict__ y,
     int n8, int N, int64_t M, float* __restrict__ mean_out, float* __restrict__ rstd_out, float eps) {
