@@ -789,13 +789,13 @@ def _match_layernorm(c: _Ctx) -> Optional[HipLoweredKernel]:
 
 def _layernorm_f32_launch(M: int, N: int) -> HipLaunch:
     """The launch ihip_layernorm_rows_f32 plans for 16-byte aligned tensors
-    (layernorm_f32.hip): N % 4 == 0 and N <= 4096: a wave per row, 16 rows per 1024-thread
+    (layernorm_f32.hip): N % 4 == 0 and N <= 4096: a wave per row, 4 rows per 256-thread
     workgroup, w and b staged in LDS; N % 4 == 0 and N <= 65536: 2-16 waves per row, one row
     per workgroup; otherwise a 256-thread workgroup per row."""
     n4 = N // 4
     if N % 4 == 0 and 0 < N <= 4096:
         kvpl = next(v for v in (1, 2, 4, 8, 16) if n4 <= 64 * v)
-        return HipLaunch((max(1, _cdiv(M, 16)), 1, 1), (1024, 1, 1), 2 * 16 * 64 * kvpl)
+        return HipLaunch((max(1, _cdiv(M, 4)), 1, 1), (256, 1, 1), 2 * 16 * 64 * kvpl)
     if N % 4 == 0 and 0 < N <= 65536:
         kw = next(w for w in (2, 4, 8, 16) if n4 <= 1024 * w)
         return HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw)
