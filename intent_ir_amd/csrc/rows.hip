@@ -805,6 +805,130 @@ __global__ __launch_bounds__(1024) void softmax_rows_f32_online(const float* __r
   }
 }
 
+// Rows of 65536 < N <= 4 * kResMaxVecs floats (N % 4 == 0, x and y 16-byte aligned; vocabulary-
+// width rows): one 1024-thread workgroup per row, and the whole row held on the CU, so x is read
+// from HBM once where the two-pass kernel above reads it twice.  The first kResVpl * 1024
+// 16-byte vectors sit in registers (vector t + i * 1024 in thread t; 96 VGPRs); the rest, up to
+// kResLdsVecs vectors, is copied straight into LDS by direct-to-LDS loads (global_load_lds_
+// dwordx4: lane l of a wave writes its 16 bytes at m0 + 16 l, so wave v's copy b covers LDS
+// vectors 64 (16 b + v) ..., with no VGPR on the way), issued before the register loads, and
+// thread t works the LDS vectors t + u * 1024.
+// One workgroup fills the CU, so nothing else hides its arithmetic, and about 12 VALU slots per
+// element would otherwise sit between the loads and the stores.  So each group of kResGroup
+// register vectors is reduced as it arrives, under the loads of the later ones: its maximum g,
+// e = exp(x - g) in place of x, and the sum of e folded into the thread's running (maximum,
+// sum) as the two-pass kernel folds; the thread's LDS vectors form one more group.  After the
+// workgroup's fold (fixed order) every output is one multiply, e * (exp(g - max) / sum), under
+// the stores.  Against exp(x - max) / sum that adds two roundings (a few ulp); special values
+// follow numpy: a group of -inf only holds e = 0, a NaN or +inf makes the row NaN, and a row
+// of -inf gives NaN.
+// kFull: the row fills the registers (n4 >= kResVpl * 1024), so their loads and stores need no
+// guard; only such rows have an LDS part.
+constexpr int kResT = 1024, kResW = kResT / kWave, kResVpl = 24, kResGroup = 4;
+// LDS: the part of the row past the registers plus the two 16-float partial arrays, 160 KiB
+constexpr int kResLdsVecs = (160 * 1024 - 2 * kResW * 4) / 16;
+constexpr int kResLdsIters = (kResLdsVecs + kResT - 1) / kResT;
+constexpr int64_t kResMaxVecs = static_cast<int64_t>(kResVpl) * kResT + kResLdsVecs;
+static_assert(kResVpl % kResGroup == 0, "whole groups");
+
+__device__ __forceinline__ void lds_copy16(const float* sbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
+}
+
+__device__ __forceinline__ float max4(f32x4 q) { return max_nan(max_nan(q.x, q.y), max_nan(q.z, q.w)); }
+__device__ __forceinline__ f32x4 exp4(f32x4 q, float g) {
+  return f32x4{exp_nonpos(q.x - g), exp_nonpos(q.y - g), exp_nonpos(q.z - g), exp_nonpos(q.w - g)};
+}
+
+template <bool kFull>
+__global__ __launch_bounds__(kResT) void softmax_rows_f32_resident(const f32x4* __restrict__ x, f32x4* __restrict__ y,
+                                                                  int n4, SoftmaxStats st) {
+  typedef __attribute__((address_space(3))) f32x4 lds_f32x4_t;
+  __shared__ __attribute__((aligned(16))) f32x4 rest_raw[kResLdsVecs];
+  __shared__ float part_m[kResW], part_s[kResW];
+  lds_f32x4_t* rest = (lds_f32x4_t*)rest_raw;
+  const int tid = threadIdx.x, v = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const f32x4* xr = x + row * n4;
+  f32x4* yr = y + row * n4;
+  const float ninf = -__builtin_inff();
+  const int nl = n4 - kResVpl * kResT;  // vectors past the registers (uniform; > 0 only when kFull)
+  if constexpr (kFull) {
+    if (nl > 0) {
+      const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(rest));
+      const float* sbase = reinterpret_cast<const float*>(xr + kResVpl * kResT);
+      const int vs = __builtin_amdgcn_readfirstlane(v);  // the wave index in a scalar register, for m0
+#pragma unroll
+      for (int b = 0; b < kResLdsIters; ++b) {
+        const int first = (b * kResW + vs) * kWave;
+        const int lane = tid & 63;
+        if (first < nl && first + lane < nl)
+          lds_copy16(sbase, static_cast<uint32_t>(first + lane) * 16u, lds_base + static_cast<uint32_t>(first) * 16u);
+      }
+    }
+  }
+  f32x4 xv[kResVpl];
+#pragma unroll
+  for (int i = 0; i < kResVpl; ++i) {
+    xv[i] = kFull || tid + i * kResT < n4 ? __builtin_nontemporal_load(xr + tid + i * kResT)
+                                          : f32x4{ninf, ninf, ninf, ninf};
+    __builtin_amdgcn_sched_barrier(0);  // issue order = use order, so each group waits only for its own loads
+  }
+  float m = ninf, s = 0.f, lg = ninf;
+  if constexpr (kFull) {
+    if (nl > 0) {
+      // the copies were issued before the kResVpl register loads: once at most that many loads
+      // are outstanding, this wave's copies have landed; the barrier waits for every wave's
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kResVpl) : "memory");
+      __syncthreads();
+      for (int u = 0; u < kResLdsIters; ++u)
+        if (tid + u * kResT < nl) lg = max_nan(lg, max4(rest[tid + u * kResT]));
+      float ls = 0.f;
+      for (int u = 0; u < kResLdsIters; ++u) {
+        const int j = tid + u * kResT;
+        if (j < nl) {
+          const f32x4 e = lg == ninf ? f32x4{0.f, 0.f, 0.f, 0.f} : exp4(rest[j], lg);
+          ls += (e.x + e.y) + (e.z + e.w);
+          rest[j] = e;
+        }
+      }
+      softmax_fold(m, s, lg, ls);
+    }
+  }
+  float gmax[kResVpl / kResGroup];
+#pragma unroll
+  for (int g = 0; g < kResVpl / kResGroup; ++g) {
+    float gm = ninf;
+#pragma unroll
+    for (int i = g * kResGroup; i < (g + 1) * kResGroup; ++i) gm = max_nan(gm, max4(xv[i]));
+    float gs = 0.f;
+#pragma unroll
+    for (int i = g * kResGroup; i < (g + 1) * kResGroup; ++i) {
+      xv[i] = gm == ninf ? f32x4{0.f, 0.f, 0.f, 0.f} : exp4(xv[i], gm);
+      gs += (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+    }
+    softmax_fold(m, s, gm, gs);
+    gmax[g] = gm;
+  }
+  block_softmax_fold<kResW>(m, s, part_m, part_s);
+  if (tid == 0) put_softmax_stats(st, row, m, s);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int g = 0; g < kResVpl / kResGroup; ++g) {
+    const float c = exp_nonpos(gmax[g] - m) * inv;
+#pragma unroll
+    for (int i = g * kResGroup; i < (g + 1) * kResGroup; ++i)
+      if (kFull || tid + i * kResT < n4) __builtin_nontemporal_store(xv[i] * c, yr + tid + i * kResT);
+  }
+  if constexpr (kFull) {
+    const float c = exp_nonpos(lg - m) * inv;
+    for (int u = 0; u < kResLdsIters; ++u) {
+      const int j = tid + u * kResT;
+      if (j < nl) __builtin_nontemporal_store(rest[j] * c, yr + kResVpl * kResT + j);
+    }
+  }
+}
+
 // ------------------------------------------------------------- long rows, split over workgroups
 // Rows longer than 65536 floats are cut into S segments of kSplitThreads * kVpl 16-byte vectors
 // of the row's body, one workgroup each, and run in two launches:
@@ -1336,6 +1460,10 @@ hipError_t launch_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t 
     softmax_rows_f32_regs<64, 8><<<dim3(static_cast<unsigned>(M)), dim3(512), 0, s>>>(x, y, M, N, st);
   else if (!vec && N <= 64 * 64 * 16)
     softmax_rows_f32_regs<64, 16><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, M, N, st);
+  else if (vec && n4 >= kResVpl * kResT && n4 <= kResMaxVecs)  // vocabulary-width rows, read once
+    softmax_rows_f32_resident<true><<<dim3(static_cast<unsigned>(M)), dim3(kResT), 0, s>>>(x4, y4, n4i, st);
+  else if (vec && n4 <= kResMaxVecs)
+    softmax_rows_f32_resident<false><<<dim3(static_cast<unsigned>(M)), dim3(kResT), 0, s>>>(x4, y4, n4i, st);
   else if (skew || vec)
     softmax_rows_f32_online<true><<<dim3(static_cast<unsigned>(M)), dim3(1024), 0, s>>>(x, y, N, st);
   else

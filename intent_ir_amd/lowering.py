@@ -601,6 +601,11 @@ def _match_softmax(c: _Ctx) -> Optional[HipLoweredKernel]:
     return HipLoweredKernel(c.fn.name, "ihip_softmax_rows_f32", c.io([x, oname]), launch, [oname], dict(c.b), args)
 
 
+# Longest vector row (16-byte vectors) the workgroup-per-row softmax holds on the CU (rows.hip
+# kResMaxVecs): 24 * 1024 in registers plus (160 KiB - 128 B) / 16 in LDS.
+SOFTMAX_RESIDENT_MAX_VECS = 24 * 1024 + (160 * 1024 - 128) // 16
+
+
 def _softmax_launch(M: int, N: int, rows: int) -> HipLaunch:
     """The unsplit launch rows.hip plans for 16-byte aligned x and y (rows: the rows-per-workgroup
     knob, 0 = automatic)."""
@@ -630,7 +635,10 @@ def _softmax_launch(M: int, N: int, rows: int) -> HipLaunch:
         # head and tail around a 16-byte aligned body (partials in LDS even for one wave)
         kw = next(w for w in (1, 2, 4, 8, 16) if N <= 4096 * w)
         launch = HipLaunch((max(1, M), 1, 1), (64 * kw, 1, 1), 8 * kw if (kw > 1 or N > 1024) else 0)
-    else:
+    elif N % 4 == 0 and N <= 4 * SOFTMAX_RESIDENT_MAX_VECS:  # vocabulary-width rows held on the CU:
+        # 24 vectors per lane in registers, the rest of the row and the partials in 160 KiB of LDS
+        launch = HipLaunch((max(1, M), 1, 1), (1024, 1, 1), 160 * 1024)
+    else:  # two passes over x, one workgroup per row
         launch = HipLaunch((max(1, M), 1, 1), (1024, 1, 1), 128)
     return launch
 
