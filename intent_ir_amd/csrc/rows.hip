@@ -483,10 +483,11 @@ hipError_t launch_reduce_rows_f32(const float* x, float* out, int64_t M, int64_t
 // reciprocal adds at most one rounding (|rel. diff| < 2.4e-7).  max propagates
 // NaN (v_maximum3_f32), so a row holding a NaN comes out all NaN, as in numpy.
 // About 14 VALU instructions per element, so the kernel stays HBM-bound.
-// kVpl: f32x4 vectors held per lane; kFull: n4 == 64 * kVpl; kR: consecutive rows per wave,
-// all loaded before the first is reduced (with rows of at most 1024 floats, two rows per wave
-// ran [16384, 1024] 2.8% faster than a wave per row, and four such waves per workgroup 2.6%
-// faster again than two).  The loads are unconditional: a wave whose second row
+// kVpl: f32x4 vectors held per lane; kFull: n4 == 64 * kVpl; kR: consecutive rows per wave
+// (with rows of at most 1024 floats, two rows per wave ran [16384, 1024] 2.8% faster than a
+// wave per row, and four such waves per workgroup 2.6% faster again than two).  The compiler
+// issues the second row's loads after the first row's maximum; pinned ahead of it (all loads
+// first) the kernel ran 2% slower.  The loads are unconditional: a wave whose second row
 // is past the last re-reads the last row and stores nothing for it (loads under a row guard
 // cost 4%).
 // kWaves: waves per workgroup (a constant, so that the kernel reads no hidden argument before
