@@ -100,7 +100,8 @@ int ihip_softmax_rows_f32(const float* x, float* y, int64_t M, int64_t N, void* 
 
 /* The same with a launch-shape knob, the role of the reference's SOFTMAX_THREADS binding
  * (backends/cuda/codegen/intentir_to_cuda.py:1175-1200): rows_per_wg = 0 chooses
- * automatically (rows of at most 1024 floats: 8 per workgroup, two per wave); 1, 2 or 4 sets
+ * automatically (rows of exactly 1024 floats: 8 per workgroup, two per wave; at most 256: 4, two
+ * per wave; other rows of at most 1024 floats: 2, one per wave; longer: 4, one per wave); 1, 2 or 4 sets
  * how many rows (one wave each; 4 rows of at most 1024 floats: two waves of two) share a
  * workgroup.  Only the
  * one-wave-per-row form (N % 4 == 0, N <= 4096, 16-byte aligned x and y) has that choice;

@@ -1335,22 +1335,25 @@ static void launch_softmax_reg_waves(const f32x4* x4, f32x4* y4, int64_t M, int 
   softmax_rows_f32_reg<kVpl, kFull, 1, kWaves><<<grid, dim3(64 * kWaves), 0, s>>>(x4, y4, M, n4, st);
 }
 
-// rows: rows per workgroup, 1, 2 or 4, or 0 (automatic: 4, except that rows of at most 1024
-// floats run as four waves of two rows each, eight rows per workgroup, measured 2.6% ahead of
-// two waves of two rows at [16384, 1024] on two boxes).  Four rows of at most 1024 floats run as
-// two waves of two rows each, otherwise one wave per row.
+// rows: rows per workgroup, 1, 2 or 4, or 0 (automatic).  Four rows of at most 1024 floats run
+// as two waves of two rows each, otherwise one wave per row.  The automatic choice
+// (`kernel_runner --sweep softmax-rows`, graph replays, us against the next best): rows of
+// exactly 1024 floats run as four waves of two rows each, eight rows per workgroup (23.7
+// against 24.0); rows of at most 256 floats as two waves of two rows (N = 200: 19.9 against
+// 20.6 for eight); the other rows of at most 1024 floats as two waves of one row (N = 512: 23.2
+// against 24.7 for eight, N = 768: 23.7 against 25.8; with a lane's last vector partly past
+// the row, two rows per wave lose more than they gain); longer rows four waves of one row.
 template <int kVpl>
 static void launch_softmax_reg(const f32x4* x4, f32x4* y4, int64_t M, int n4, int rows, const SoftmaxStats& st,
                                hipStream_t s) {
   const bool full = n4 == kVpl * kWave;
-  if (kVpl <= 4 && rows == 0) {
-    const dim3 grid(static_cast<unsigned>((M + 7) / 8));
-    if (full)
-      softmax_rows_f32_reg<kVpl, true, 2, 4><<<grid, dim3(256), 0, s>>>(x4, y4, M, n4, st);
-    else
-      softmax_rows_f32_reg<kVpl, false, 2, 4><<<grid, dim3(256), 0, s>>>(x4, y4, M, n4, st);
+  if (kVpl == 4 && full && rows == 0) {
+    softmax_rows_f32_reg<kVpl, true, 2, 4><<<dim3(static_cast<unsigned>((M + 7) / 8)), dim3(256), 0, s>>>(x4, y4, M, n4,
+                                                                                                         st);
     return;
   }
+  if (kVpl == 1 && rows == 0) rows = 4;
+  if (kVpl <= 4 && rows == 0) rows = 2;
   if (rows == 0) rows = 4;
   if (kVpl <= 4 && rows == 4) {
     const dim3 grid(static_cast<unsigned>((M + 3) / 4));

@@ -8,6 +8,7 @@
     python -m intent_ir_amd.kernel_runner --f32 matmul --launches 10        # 8192^3 on the fp32 matrix cores
     python -m intent_ir_amd.kernel_runner --f32 layernorm --launches 20     # [8192, 4096] f32
     python -m intent_ir_amd.kernel_runner --sweep softmax --launches 100    # fixed cost vs a copy
+    python -m intent_ir_amd.kernel_runner --sweep softmax-rows --launches 20  # rows per workgroup
     python -m intent_ir_amd.kernel_runner --sweep gemm-tile --launches 10   # the GEMM tile rule
     python -m intent_ir_amd.kernel_runner --sweep gemm-split --launches 10  # the split-K rule
 
@@ -320,6 +321,47 @@ def run_sweep(family, launches, torch) -> int:
     return 0
 
 
+# Row lengths behind the softmax's default rows per workgroup (rows.hip launch_softmax_reg).
+SOFTMAX_ROWS_SHAPES = [(65536, 200), (65536, 256), (49152, 300), (43690, 384), (32768, 512), (21845, 768), (16777, 1000), (16384, 1024), (8192, 2048), (4096, 4096)]
+
+
+def run_softmax_rows_sweep(launches, torch) -> int:
+    """The measurement behind the softmax's default rows per workgroup: for rows held by one
+    wave (N <= 4096), ihip_softmax_rows_f32_ex with rows_per_wg = 0 (the default: for N <= 1024
+    four waves of two rows each, else four waves of one row) against the knob's 1, 2 and 4,
+    timed like bench.py (graph replays of ``launches`` launches, buffer sets rotated over
+    >= 640 MiB, median of 5)."""
+    import ctypes  # noqa: PLC0415
+
+    from .runtime import load_library  # noqa: PLC0415
+
+    lib = load_library()
+    P = ctypes.c_void_p
+    for M, N in SOFTMAX_ROWS_SHAPES:
+        byt = 2 * 4 * M * N
+        nsets = max(2, math.ceil(ROTATE_MIN_BYTES / byt))
+        g = torch.Generator(device="cuda")
+        g.manual_seed(M + N)
+        sets = [(torch.randn((M, N), generator=g, device="cuda") * 2, torch.empty((M, N), device="cuda"))
+                for _ in range(nsets)]
+        us = {}
+        for rows in (0, 1, 2, 4):
+            def launch(i, rows=rows):
+                x, y = sets[i % nsets]
+                st = lib.ihip_softmax_rows_f32_ex(P(x.data_ptr()), P(y.data_ptr()), M, N, rows,
+                                                   P(torch.cuda.current_stream().cuda_stream))
+                if st != 0:
+                    raise RuntimeError(lib.ihip_last_error().decode())
+            us[rows] = 1e3 * _graph_time(launch, nsets, launches, torch)
+        best = min(us, key=us.get)
+        row = ", ".join(f"{'default' if r == 0 else r} {t:.2f}" for r, t in us.items())
+        print(f"[runner] softmax-rows [{M}, {N}]: {row} us; default {100 * byt / (us[0] * 1e-6) / 8e12:.1f}% of "
+              f"8 TB/s, fastest {'default' if best == 0 else best}", flush=True)
+        del sets
+        torch.cuda.empty_cache()
+    return 0
+
+
 # Shapes behind the GEMM's shipped rules (M, N, K, B given as [N, K]).
 GEMM_TILE_SHAPES = [
     (1000, 4096, 4096, False), (512, 8192, 8192, False), (2048, 2048, 8192, False), (1024, 1024, 8192, False),
@@ -465,7 +507,7 @@ def main(argv=None) -> int:
                     help="time a generic element-wise program chain (or all of them)")
     ap.add_argument("--row-reduce", choices=["sum", "max"], help="time a row reduction (f32 [M, N], --bindings)")
     ap.add_argument("--gather", action="store_true", help="time gather2d (inp f32 [M, N], L random index pairs)")
-    ap.add_argument("--sweep", choices=["softmax", "gemm-tile", "gemm-split"],
+    ap.add_argument("--sweep", choices=["softmax", "softmax-rows", "gemm-tile", "gemm-split"],
                     help="softmax: fixed cost and streaming rate against a copy of the same bytes; gemm-tile, "
                          "gemm-split: the measurements behind the GEMM's tile and split-K rules")
     ap.add_argument("--f32", choices=["matmul", "layernorm"],
@@ -488,6 +530,8 @@ def main(argv=None) -> int:
     if args.sweep:
         if args.sweep.startswith("gemm"):
             return run_gemm_sweep(args.sweep, args.launches, torch)
+        if args.sweep == "softmax-rows":
+            return run_softmax_rows_sweep(args.launches, torch)
         return run_sweep(args.sweep, args.launches, torch)
     if args.ew_chain:
         return run_ew_chains(sorted(EW_CHAINS) if args.ew_chain == "all" else [args.ew_chain], args.launches, torch)

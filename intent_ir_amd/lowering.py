@@ -621,10 +621,13 @@ def _softmax_launch(M: int, N: int, rows: int) -> HipLaunch:
         while 4 * g < N:
             g *= 2
         launch = HipLaunch((max(1, _cdiv(M * g, 512)), 1, 1), (256, 1, 1), 4 * (2048 + 36))
-    elif N % 4 == 0 and N <= 4096:  # 4 rows per workgroup unless a knob says otherwise: a wave per
-        # row, or for N <= 1024 two rows per wave: four waves (8 rows) by default, two for a knob of 4
-        launch = _row_launch(M, rows or 4)
-        if N <= 1024 and not rows:
+    elif N % 4 == 0 and N <= 4096:  # a wave per row, or for N <= 1024 two rows per wave with 4 rows
+        # per workgroup (two waves); automatic: N == 1024 four waves of two rows (8 per workgroup),
+        # N <= 256 two waves of two rows, other N <= 1024 two waves of one row, longer rows four waves
+        if not rows:
+            rows = 8 if N == 1024 else 4 if N <= 256 else 2 if N <= 1024 else 4
+        launch = _row_launch(M, rows)
+        if rows == 8:
             launch = HipLaunch((max(1, _cdiv(M, 8)), 1, 1), (256, 1, 1), 0)
         elif N <= 1024 and rows == 4:
             launch = HipLaunch(launch.grid, (128, 1, 1), 0)

@@ -397,6 +397,8 @@ def test_reduce_any_launch_descriptor(dt, M, N, grid, block):
 @pytest.mark.parametrize("M,N,grid,block,lds", [
     (1000, 31, 16, 256, 8336), (1000, 127, 63, 256, 8336), (5, 1, 1, 256, 8336), (1000, 32, 32, 256, 0),
     (1000, 128, 125, 256, 0), (1000, 129, 1000, 64, 0),
+    (1000, 200, 250, 128, 0), (1000, 256, 250, 128, 0), (1000, 512, 500, 128, 0), (1000, 768, 500, 128, 0),
+    (1000, 1024, 125, 256, 0), (1000, 2048, 250, 256, 0), (1000, 4096, 250, 256, 0),
     (1024, 128256, 1024, 1024, 163840), (1000, 65540, 1000, 1024, 163840), (1000, 139232, 1000, 1024, 163840),
     (1000, 139236, 1000, 1024, 128), (1000, 128255, 1000, 1024, 128)])
 def test_softmax_short_row_launch_descriptor(M, N, grid, block, lds):
@@ -404,7 +406,9 @@ def test_softmax_short_row_launch_descriptor(M, N, grid, block, lds):
     power of two for aligned rows; for the others one lane per 4 elements, two rows per group and
     the workgroup's rows staged in LDS (8 KiB + 144 B: the run's offset in its 128-byte line,
     one vector of slack).  Longer rows not 16-byte aligned take a
-    wave per row.  Vector rows longer than 65536 floats, up to 139232, are held on the CU (all
+    wave per row.  Vector rows up to 4096 floats: two waves of two rows for N <= 256, two waves of
+    one row up to 1020, four waves of two rows at 1024, four waves of one row beyond (the
+    library's automatic choice, from kernel_runner --sweep softmax-rows).  Vector rows longer than 65536 floats, up to 139232, are held on the CU (all
     160 KiB of LDS); longer or unaligned ones run the two-pass kernel (128 B of partials)."""
     k = lower_intent_to_hip_kernel(WORKLOADS["softmax"].ir(), shape_bindings={"M": M, "N": N})
     assert (k.launch.grid[0], k.launch.block[0], k.launch.lds_bytes) == (grid, block, lds)
